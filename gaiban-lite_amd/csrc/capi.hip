@@ -1,0 +1,356 @@
+// extern "C" entry points of include/dsv4moe.h: argument validation (before
+// any launch), dispatch to the kernels, and the thread-local error message.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <vector>
+
+#include "common.h"
+#include "../../include/dsv4moe.h"
+
+namespace dsv4host {
+
+static thread_local char g_error[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_error[0] = '\0'; }
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("%s: %s", what, hipGetErrorString(err));
+    return DSV4MOE_EHIP;
+  }
+  return DSV4MOE_OK;
+}
+
+// Profiling state: one event per (call, stamp); a call is one layer/experts
+// invocation, counted when its last stamp is recorded.  Process-global and
+// not thread-safe: profile from one host thread.
+struct ProfileState {
+  std::vector<hipEvent_t> events;
+  int max_calls = 0;
+  int call = 0;
+  bool active = false;
+};
+static ProfileState g_prof;
+
+void prof_stamp(int stamp, hipStream_t stream) {
+  if (!g_prof.active || g_prof.call >= g_prof.max_calls) return;
+  hipEventRecord(g_prof.events[(size_t)g_prof.call * kNumStamps + stamp], stream);
+  if (stamp == kNumStamps - 1) ++g_prof.call;
+}
+
+static void prof_release() {
+  for (hipEvent_t e : g_prof.events) hipEventDestroy(e);
+  g_prof.events.clear();
+  g_prof.active = false;
+  g_prof.call = 0;
+  g_prof.max_calls = 0;
+}
+
+}  // namespace dsv4host
+
+// kernel launchers (one per translation unit)
+int dsv4_launch_route_topk(const float*, const float*, int64_t, int32_t, int32_t, int32_t, float,
+                           int32_t*, float*, float*, int32_t*, float*, hipStream_t);
+int dsv4_launch_route_hash(const float*, const int64_t*, int64_t, const int64_t*, int64_t, int32_t,
+                           int32_t, float, int32_t*, float*, float*, hipStream_t);
+int dsv4_launch_gate_logits(const uint16_t*, const uint16_t*, int64_t, int, int, float*,
+                            hipStream_t);
+int dsv4_launch_align(const int32_t*, int64_t, int32_t, int32_t, int32_t*, int64_t, int32_t*,
+                      int64_t, int32_t*, hipStream_t);
+int dsv4_launch_pack(const uint8_t*, const uint16_t*, int64_t, int64_t, int64_t, uint8_t*,
+                     uint16_t*, hipStream_t);
+size_t dsv4_experts_workspace_bytes(int64_t, int, int, int, int);
+int dsv4_launch_experts_w4a16(const uint16_t*, int64_t, int, int, int, int, const uint8_t*,
+                              const uint16_t*, const uint8_t*, const uint16_t*, int, const float*,
+                              const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
+                              uint16_t*, void*, hipStream_t);
+
+using dsv4host::clear_error;
+using dsv4host::set_error;
+
+static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+static int64_t max_padded(int64_t a, int32_t e, int32_t bs) {
+  if (a <= 0 || e <= 0 || bs <= 0) return -1;
+  int64_t m = a + (int64_t)e * (bs - 1);
+  if (a < e) {
+    const int64_t alt = a * bs;
+    if (alt < m) m = alt;
+  }
+  return m;
+}
+
+static bool valid_block_size(int32_t bs) {
+  return bs == 8 || bs == 16 || bs == 32 || bs == 48 || bs == 64;
+}
+
+extern "C" {
+
+const char* dsv4moe_last_error(void) { return dsv4host::g_error; }
+
+int32_t dsv4moe_abi_version(void) { return 1; }
+
+int dsv4moe_profile_begin(int32_t max_calls) {
+  clear_error();
+  DSV4_REQUIRE(max_calls > 0 && max_calls <= 100000, "profile_begin: max_calls must be in [1, 100000]");
+  dsv4host::prof_release();
+  dsv4host::g_prof.events.resize((size_t)max_calls * dsv4host::kNumStamps);
+  for (auto& e : dsv4host::g_prof.events) {
+    if (hipEventCreate(&e) != hipSuccess) {
+      e = nullptr;
+      dsv4host::prof_release();
+      set_error("profile_begin: hipEventCreate failed");
+      return DSV4MOE_EHIP;
+    }
+  }
+  dsv4host::g_prof.max_calls = max_calls;
+  dsv4host::g_prof.call = 0;
+  dsv4host::g_prof.active = true;
+  return DSV4MOE_OK;
+}
+
+int dsv4moe_profile_end(float* mean_ms, int32_t n_intervals, int32_t* calls_recorded) {
+  clear_error();
+  using dsv4host::g_prof;
+  using dsv4host::kNumStamps;
+  DSV4_REQUIRE(g_prof.active, "profile_end: profiling is not active");
+  DSV4_REQUIRE(mean_ms && n_intervals == kNumStamps - 1, "profile_end: need %d output slots",
+               kNumStamps - 1);
+  const int calls = g_prof.call;
+  for (int i = 0; i < kNumStamps - 1; ++i) mean_ms[i] = 0.0f;
+  int rc = DSV4MOE_OK;
+  if (calls > 0 && hipEventSynchronize(g_prof.events[(size_t)calls * kNumStamps - 1]) != hipSuccess) {
+    set_error("profile_end: hipEventSynchronize failed");
+    rc = DSV4MOE_EHIP;
+  }
+  for (int c = 0; c < calls && rc == DSV4MOE_OK; ++c) {
+    for (int i = 1; i < kNumStamps; ++i) {
+      float ms = 0.0f;
+      if (hipEventElapsedTime(&ms, g_prof.events[(size_t)c * kNumStamps + i - 1],
+                              g_prof.events[(size_t)c * kNumStamps + i]) != hipSuccess) {
+        set_error("profile_end: hipEventElapsedTime failed");
+        rc = DSV4MOE_EHIP;
+        break;
+      }
+      mean_ms[i - 1] += ms / (float)calls;
+    }
+  }
+  if (calls_recorded) *calls_recorded = calls;
+  dsv4host::prof_release();
+  return rc;
+}
+
+int32_t dsv4moe_block_size_m(int64_t rows, int32_t topk, int32_t experts, int32_t act_itemsize) {
+  if (rows <= 0 || topk <= 0 || experts <= 0) return -1;
+  int32_t selected = 64;
+  const int32_t cands[5] = {8, 16, 32, 48, 64};
+  for (int i = 0; i < 5; ++i) {
+    // rows*topk/experts/candidate < 0.9, evaluated as the reference's float division
+    const double ratio = (double)rows * (double)topk / (double)experts / (double)cands[i];
+    if (ratio < 0.9) {
+      selected = cands[i];
+      break;
+    }
+  }
+  if (act_itemsize == 1 && selected < 16) selected = 16;
+  return selected;
+}
+
+int64_t dsv4moe_max_padded_tokens(int64_t num_assignments, int32_t num_experts, int32_t block_size) {
+  return max_padded(num_assignments, num_experts, block_size);
+}
+
+int dsv4moe_route_topk(const float* logits, const float* bias, int64_t tokens, int32_t experts,
+                       int32_t topk, int32_t score_func, float route_scale, int32_t* ids,
+                       float* weights, float* margin, int32_t* selection_ids,
+                       float* selection_scores, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(tokens >= 0, "route_topk: tokens must be >= 0");
+  DSV4_REQUIRE(experts >= 1 && experts <= 1024, "route_topk: experts must be in [1, 1024]");
+  DSV4_REQUIRE(topk >= 1 && topk <= experts && topk <= 16,
+               "route_topk: topk must be in [1, min(experts, 16)]");
+  DSV4_REQUIRE(score_func == DSV4MOE_SCORE_SIGMOID || score_func == DSV4MOE_SCORE_SOFTMAX ||
+                   score_func == DSV4MOE_SCORE_SQRTSOFTPLUS,
+               "route_topk: unknown score_func %d", score_func);
+  DSV4_REQUIRE(route_scale > 0.0f && route_scale < 3.0e38f, "route_topk: route_scale must be finite and positive");
+  if (tokens == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(logits && ids && weights, "route_topk: null logits/ids/weights");
+  return dsv4_launch_route_topk(logits, bias, tokens, experts, topk, score_func, route_scale, ids,
+                                weights, margin, selection_ids, selection_scores,
+                                static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_route_hash(const float* logits, const int64_t* tid2eid, int64_t vocab,
+                       const int64_t* input_ids, int64_t tokens, int32_t experts, int32_t topk,
+                       float route_scale, int32_t* ids, float* weights,
+                       float* selected_scores, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(tokens >= 0 && vocab > 0, "route_hash: bad tokens/vocab");
+  DSV4_REQUIRE(experts >= 1 && experts <= 1024, "route_hash: experts must be in [1, 1024]");
+  DSV4_REQUIRE(topk >= 1 && topk < experts && topk <= 16, "route_hash: topk must be in [1, experts)");
+  DSV4_REQUIRE(route_scale > 0.0f && route_scale < 3.0e38f, "route_hash: route_scale must be finite and positive");
+  if (tokens == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(logits && tid2eid && input_ids && ids && weights, "route_hash: null pointer");
+  return dsv4_launch_route_hash(logits, tid2eid, vocab, input_ids, tokens, experts, topk,
+                                route_scale, ids, weights, selected_scores,
+                                static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_gate_logits(const uint16_t* x, const uint16_t* wg, int64_t tokens, int32_t hidden,
+                        int32_t experts, float* logits, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(tokens >= 0, "gate_logits: tokens must be >= 0");
+  DSV4_REQUIRE(hidden > 0 && hidden % 32 == 0, "gate_logits: hidden must be a positive multiple of 32");
+  DSV4_REQUIRE(experts > 0 && experts <= 65535 * 64, "gate_logits: bad experts");
+  if (tokens == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(x && wg && logits, "gate_logits: null pointer");
+  DSV4_REQUIRE(aligned(x, 16) && aligned(wg, 16), "gate_logits: x and wg must be 16-byte aligned");
+  return dsv4_launch_gate_logits(x, wg, tokens, hidden, experts, logits,
+                                 static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_align(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts,
+                  int32_t block_size, int32_t* sorted_token_ids, int64_t capacity,
+                  int32_t* expert_ids, int64_t num_blocks, int32_t* num_tokens_post_padded,
+                  void* stream) {
+  clear_error();
+  DSV4_REQUIRE(tokens > 0 && topk > 0, "align: route ids must be non-empty [tokens, topk]");
+  DSV4_REQUIRE(experts >= 1 && experts <= 1024, "align: experts must be in [1, 1024]");
+  DSV4_REQUIRE(block_size > 0 && block_size <= 1024, "align: bad block_size %d", block_size);
+  const int64_t a = tokens * topk;
+  DSV4_REQUIRE(a <= 0x7FFFFFFFLL, "align: assignments exceed int32");
+  const int64_t cap = max_padded(a, experts, block_size);
+  DSV4_REQUIRE(cap <= 0x7FFFFFFFLL, "align: capacity exceeds int32");
+  DSV4_REQUIRE(capacity == cap, "align: capacity %lld != max_padded_tokens %lld",
+               (long long)capacity, (long long)cap);
+  DSV4_REQUIRE(num_blocks == (cap + block_size - 1) / block_size, "align: expert_ids length mismatch");
+  DSV4_REQUIRE(ids && sorted_token_ids && expert_ids && num_tokens_post_padded, "align: null pointer");
+  return dsv4_launch_align(ids, a, experts, block_size, sorted_token_ids, capacity, expert_ids,
+                           num_blocks, num_tokens_post_padded, static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, int64_t batch,
+                           int64_t n, int64_t k, uint8_t* packed, uint16_t* packed_scales,
+                           void* stream) {
+  clear_error();
+  DSV4_REQUIRE(batch >= 0 && n >= 0 && k >= 0, "pack: negative size");
+  DSV4_REQUIRE(n % 16 == 0, "pack: n=%lld must be a multiple of 16", (long long)n);
+  DSV4_REQUIRE(k % DSV4MOE_GROUP == 0, "pack: k=%lld must be a multiple of 128", (long long)k);
+  if (batch == 0 || n == 0 || k == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(canon && canon_scales && packed && packed_scales, "pack: null pointer");
+  DSV4_REQUIRE(aligned(canon, 4) && aligned(packed, 16), "pack: canon 4-byte / packed 16-byte alignment required");
+  return dsv4_launch_pack(canon, canon_scales, batch, n, k, packed, packed_scales,
+                          static_cast<hipStream_t>(stream));
+}
+
+size_t dsv4moe_experts_workspace_bytes(int64_t tokens, int32_t topk, int32_t hidden,
+                                       int32_t inter, int32_t has_shared) {
+  if (tokens < 0 || topk <= 0 || hidden <= 0 || inter <= 0) return 0;
+  return dsv4_experts_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0);
+}
+
+static int validate_experts(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
+                            int32_t experts, int32_t topk, const uint8_t* w13q,
+                            const uint16_t* w13s, const uint8_t* w2q, const uint16_t* w2s,
+                            int64_t capacity, int32_t block_size, uint16_t* out, void* workspace,
+                            size_t workspace_bytes, int32_t has_shared, const char* who) {
+  DSV4_REQUIRE(tokens >= 0, "%s: tokens must be >= 0", who);
+  DSV4_REQUIRE(hidden > 0 && hidden % 128 == 0, "%s: hidden=%d must be a positive multiple of 128", who, hidden);
+  DSV4_REQUIRE(inter > 0 && inter % 128 == 0, "%s: inter=%d must be a positive multiple of 128", who, inter);
+  DSV4_REQUIRE(experts >= 1 && experts <= 1024, "%s: experts must be in [1, 1024]", who);
+  DSV4_REQUIRE(topk >= 1 && topk <= experts, "%s: topk must be in [1, experts]", who);
+  DSV4_REQUIRE(valid_block_size(block_size), "%s: block_size %d not in {8,16,32,48,64}", who, block_size);
+  if (tokens == 0) return DSV4MOE_OK;
+  const int64_t cap = max_padded(tokens * topk, experts, block_size);
+  DSV4_REQUIRE(capacity == cap, "%s: capacity %lld != max_padded_tokens %lld", who,
+               (long long)capacity, (long long)cap);
+  DSV4_REQUIRE(x && w13q && w13s && w2q && w2s && out && workspace, "%s: null pointer", who);
+  DSV4_REQUIRE(aligned(x, 16) && aligned(w13q, 16) && aligned(w2q, 16) && aligned(w13s, 8) &&
+                   aligned(w2s, 8) && aligned(out, 8) && aligned(workspace, 256),
+               "%s: alignment (x/w*q 16 B, scales/out 8 B, workspace 256 B)", who);
+  const size_t need = dsv4_experts_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0);
+  DSV4_REQUIRE(workspace_bytes >= need, "%s: workspace %zu bytes < required %zu", who,
+               workspace_bytes, need);
+  const int64_t blocks = (cap + block_size - 1) / block_size;
+  const int64_t shared_blocks = has_shared ? (tokens + block_size - 1) / block_size : 0;
+  const int64_t tiles = (int64_t)(hidden > inter ? hidden : inter) / 128;
+  DSV4_REQUIRE((blocks + shared_blocks) * tiles < 0x7FFFFFFFLL, "%s: grid too large", who);
+  return DSV4MOE_OK;
+}
+
+int dsv4moe_experts_w4a16(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
+                          int32_t experts, int32_t topk, const uint8_t* w13q,
+                          const uint16_t* w13s, const uint8_t* w2q, const uint16_t* w2s,
+                          int32_t has_shared, const float* weights,
+                          const int32_t* sorted_token_ids, int64_t capacity,
+                          const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                          int32_t block_size, float clamp_limit, uint16_t* out,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = validate_experts(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+                            capacity, block_size, out, workspace, workspace_bytes, has_shared,
+                            "experts_w4a16");
+  if (rc != DSV4MOE_OK || tokens == 0) return rc;
+  DSV4_REQUIRE(weights && sorted_token_ids && expert_ids && num_tokens_post_padded,
+               "experts_w4a16: null route/alignment pointer");
+  DSV4_REQUIRE(!(clamp_limit < 0.0f) && clamp_limit < 3.0e38f, "experts_w4a16: clamp_limit must be >= 0 and finite");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dsv4host::prof_stamp(dsv4host::kStampBegin, s);
+  dsv4host::prof_stamp(dsv4host::kStampRoute, s);
+  dsv4host::prof_stamp(dsv4host::kStampAlign, s);
+  return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+                                   has_shared ? 1 : 0, weights, sorted_token_ids, capacity,
+                                   expert_ids, num_tokens_post_padded, block_size, clamp_limit,
+                                   out, workspace, static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bias,
+                        int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
+                        int32_t topk, int32_t score_func, float route_scale,
+                        const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
+                        const uint16_t* w2s, int32_t has_shared, float clamp_limit,
+                        int32_t block_size, int32_t* ids, float* weights, float* margin,
+                        int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                        int32_t* num_tokens_post_padded, uint16_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = validate_experts(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+                            capacity, block_size, out, workspace, workspace_bytes, has_shared,
+                            "layer_w4a16");
+  if (rc != DSV4MOE_OK || tokens == 0) return rc;
+  DSV4_REQUIRE(topk <= 16, "layer_w4a16: topk must be <= 16");
+  DSV4_REQUIRE(score_func == DSV4MOE_SCORE_SIGMOID || score_func == DSV4MOE_SCORE_SOFTMAX ||
+                   score_func == DSV4MOE_SCORE_SQRTSOFTPLUS,
+               "layer_w4a16: unknown score_func %d", score_func);
+  DSV4_REQUIRE(route_scale > 0.0f && route_scale < 3.0e38f, "layer_w4a16: route_scale must be finite and positive");
+  DSV4_REQUIRE(!(clamp_limit < 0.0f) && clamp_limit < 3.0e38f, "layer_w4a16: clamp_limit must be >= 0 and finite");
+  DSV4_REQUIRE(logits && ids && weights && sorted_token_ids && expert_ids && num_tokens_post_padded,
+               "layer_w4a16: null route/alignment pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dsv4host::prof_stamp(dsv4host::kStampBegin, s);
+  rc = dsv4_launch_route_topk(logits, bias, tokens, experts, topk, score_func, route_scale, ids,
+                              weights, margin, nullptr, nullptr, s);
+  if (rc != DSV4MOE_OK) return rc;
+  dsv4host::prof_stamp(dsv4host::kStampRoute, s);
+  const int64_t nblocks = (capacity + block_size - 1) / block_size;
+  rc = dsv4_launch_align(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity,
+                         expert_ids, nblocks, num_tokens_post_padded, s);
+  if (rc != DSV4MOE_OK) return rc;
+  dsv4host::prof_stamp(dsv4host::kStampAlign, s);
+  return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+                                   has_shared ? 1 : 0, weights, sorted_token_ids, capacity,
+                                   expert_ids, num_tokens_post_padded, block_size, clamp_limit,
+                                   out, workspace, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,101 @@
+// Shared device helpers and host error plumbing for the gfx950 MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+namespace dsv4 {
+
+// ---------------------------------------------------------------- vector types
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;   // MFMA 16x16x32 operand
+typedef __attribute__((ext_vector_type(4))) float f32x4;     // MFMA 16x16 accumulator
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr int kGroup = 128;      // int4 quantisation group along K
+constexpr int kTileBytes = 1024; // one packed tile: 16 rows x 128 K int4
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 helpers
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even float -> bf16 bits (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t float_to_bf16_bits(float v) {
+  __bf16 b = (__bf16)v;
+  return (uint32_t)__builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return float_to_bf16_bits(lo) | (float_to_bf16_bits(hi) << 16);
+}
+
+// ---------------------------------------------------------------- int4 dequant
+// A packed dword holds 8 offset-binary nibbles u = q + 8 of one row: nibble
+// slot j (bits 4j..4j+3) is K offset 2j, slot 4+j (bits 16+4j..) is K offset
+// 2j+1, j = 0..3.  OR-ing a nibble into the mantissa of bf16 128.0 (0x4300)
+// gives exactly 128 + u = q + 136; the kernels remove the 136*sum(x) term with
+// the per-group activation sums.
+__device__ __forceinline__ bf16x8 dequant_biased(uint32_t w) {
+  u32x4 p;
+  p[0] = (w & 0x000F000Fu) | 0x43004300u;
+  p[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  p[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  p[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  return __builtin_bit_cast(bf16x8, p);
+}
+constexpr float kDequantBias = 136.0f;
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x4 load16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+__device__ __forceinline__ float silu_f(float g) {
+  return g / (1.0f + __expf(-g));
+}
+
+}  // namespace dsv4
+
+// ------------------------------------------------------------------ host side
+namespace dsv4host {
+void set_error(const char* fmt, ...);
+void clear_error();
+int check_launch(const char* what);
+
+// Optional per-kernel timing (dsv4moe_profile_begin/_end): stamp points of
+// one layer call, recorded as HIP events on the launch stream.
+enum Stamp {
+  kStampBegin = 0,
+  kStampRoute,
+  kStampAlign,
+  kStampRowSum,
+  kStampStage1,
+  kStampStage2,
+  kStampCombine,
+  kNumStamps
+};
+void prof_stamp(int stamp, hipStream_t stream);
+}  // namespace dsv4host
+
+#define DSV4_REQUIRE(cond, ...)            \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::dsv4host::set_error(__VA_ARGS__);   \
+      return DSV4MOE_EINVAL;                \
+    }                                       \
+  } while (0)
+
+#define DSV4_CHECK_LAUNCH(what)                          \
+  do {                                                   \
+    int _rc = ::dsv4host::check_launch(what);            \
+    if (_rc != DSV4MOE_OK) return _rc;                   \
+  } while (0)

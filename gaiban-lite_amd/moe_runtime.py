@@ -1,0 +1,752 @@
+"""Single-GPU MoE layer with the ``TP4MoE`` call signature.
+
+Drop-in for ``runtime/dsv4_direct/moe_runtime.py:TP4MoE`` at world size 1: the
+whole unsharded layer (all routed experts plus the shared expert) is resident
+on one MI355X, so the all_gather / reduce_scatter of the reference
+(``moe_runtime.py:1699,1893``) are identities and the stage markers around
+them fire back to back.  The compute between them -- gate, alignment, grouped
+experts, top-k combine, shared expert and add (``moe_runtime.py:1714-1888``)
+-- runs in the HIP kernels behind ``include/dsv4moe.h``.
+
+Kept from the reference: constructor keywords, per-(rows, slot) preallocated
+buffers with the ``free -> in_flight -> free | poisoned`` lifecycle and a
+per-slot completion event, route override validation
+(``moe_runtime.py:418-476``), the alignment-provider protocol
+(``:631-666,1812-1828``), stage markers, ``MoETrace``, ``forward_tensor``,
+route observation and the slot-status introspection used by graph callers.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+from contextlib import contextmanager
+from dataclasses import dataclass
+from typing import Any, Callable, Iterable, Iterator
+
+import torch
+
+from . import ops
+from .deterministic_moe_align import (
+    DeterministicMoEAlignment,
+    allocate_deterministic_moe_alignment,
+)
+from .weights import ResidentInt4MoEWeights
+
+SCORE_FUNCS = ("sigmoid", "softmax", "sqrtsoftplus")
+
+
+@dataclass(frozen=True)
+class TP4MoEConfig:
+    """Layer geometry and routing contract.
+
+    The reference pins the Flash geometry and TP world 4
+    (``moe_runtime.py:35-67``); this build runs the whole layer on one GPU
+    (``world_size`` 1) and accepts any geometry the kernels support.
+    ``FLASH_CONFIG`` is the DeepSeek-V4-Flash contract.
+    """
+
+    hidden_size: int = 4096
+    intermediate_size: int = 2048
+    experts: int = 256
+    topk: int = 6
+    route_scale: float = 1.5
+    clamp_limit: float = 10.0
+    world_size: int = 1
+    score_func: str = "sqrtsoftplus"
+    shared_experts: int = 1
+
+    @property
+    def local_intermediate(self) -> int:
+        return self.intermediate_size // self.world_size
+
+    def validate(self) -> None:
+        if self.world_size != 1:
+            raise ValueError(
+                "this build keeps the whole MoE layer on one GPU: world_size must be 1"
+            )
+        for name in ("hidden_size", "intermediate_size"):
+            value = getattr(self, name)
+            if not isinstance(value, int) or value <= 0 or value % 128:
+                raise ValueError(f"{name} must be a positive multiple of 128")
+        if not isinstance(self.experts, int) or not 1 <= self.experts <= 1024:
+            raise ValueError("experts must be in [1, 1024]")
+        if not isinstance(self.topk, int) or not 1 <= self.topk < self.experts or self.topk > 16:
+            raise ValueError("topk must be in [1, min(experts - 1, 16)]")
+        if not math.isfinite(self.route_scale) or self.route_scale <= 0:
+            raise ValueError("route_scale must be finite and positive")
+        if not math.isfinite(self.clamp_limit) or self.clamp_limit < 0:
+            raise ValueError("clamp_limit must be finite and >= 0 (0 disables the clamp)")
+        if self.score_func not in SCORE_FUNCS:
+            raise ValueError(f"score_func must be one of {SCORE_FUNCS}")
+        if self.shared_experts not in (0, 1):
+            raise ValueError("shared_experts must be 0 or 1")
+
+
+FLASH_CONFIG = TP4MoEConfig()
+
+
+@dataclass
+class ResidentGateWeights:
+    """Gate parameters (``runtime/dsv4_direct/block_weights.py:135-150``).
+
+    ``weight`` bf16 [E, H]; ``bias`` fp32 [E] (selection shift) or None;
+    ``tid2eid`` int64 [vocab, k] for hash layers.  A hash gate has no bias.
+    """
+
+    weight: torch.Tensor
+    bias: torch.Tensor | None = None
+    layer_id: int | None = None
+    rank: int | None = None
+    world_size: int | None = None
+    checkpoint_id: str | None = None
+    tid2eid: torch.Tensor | None = None
+
+    def __post_init__(self) -> None:
+        if self.tid2eid is not None and self.bias is not None:
+            raise ValueError("a hash gate (tid2eid) forbids a bias")
+
+    @property
+    def route_kind(self) -> str:
+        return "hash" if self.tid2eid is not None else "learned"
+
+
+@dataclass(frozen=True)
+class MoETrace:
+    local_input_shape: tuple[int, ...]
+    gathered_shape: tuple[int, ...]
+    partial_shape: tuple[int, ...]
+    local_output_shape: tuple[int, ...]
+    route_ids_row_zero: tuple[int, ...]
+    route_weights_row_zero: tuple[float, ...]
+    route_margin_min: float | None
+    route_digest: str
+    stage_digests: dict[str, str]
+    buffer_slot: int
+    shared_path: str = "int4_g128_fused_grouped"
+    route_source: str = "native"
+
+
+@dataclass(frozen=True)
+class MoERouteOverride:
+    """Explicit full route (ids int32 [rows, k], weights fp32 [rows, k])."""
+
+    ids: torch.Tensor
+    weights: torch.Tensor
+
+
+@dataclass(frozen=True)
+class MoERouteTensors:
+    weights: torch.Tensor
+    ids: torch.Tensor
+    margin: torch.Tensor | None
+    selection_ids: torch.Tensor | None
+    selection_scores: torch.Tensor | None
+    local_input: torch.Tensor | None = None
+    gate_logits: torch.Tensor | None = None
+    route_source: str = "native"
+
+
+@dataclass
+class _LayerBuffers:
+    workspace: torch.Tensor
+    logits: torch.Tensor
+    route_ids: torch.Tensor
+    route_weights: torch.Tensor
+    margin: torch.Tensor
+    output: torch.Tensor
+    alignment: DeterministicMoEAlignment
+    block_size_m: int
+    ready_event: Any
+    gathered_input_ids: torch.Tensor | None = None
+    has_completion_event: bool = False
+    state: str = "free"
+
+
+def _tensor_digest(*tensors: torch.Tensor) -> str:
+    digest = hashlib.sha256()
+    for tensor in tensors:
+        digest.update(f"{list(tensor.shape)}|{tensor.dtype}|".encode())
+        digest.update(tensor.detach().contiguous().view(torch.uint8).cpu().numpy().tobytes())
+    return digest.hexdigest()
+
+
+def _snapshot_route_override(
+    value: MoERouteOverride, *, rows: int, config: TP4MoEConfig, device: torch.device
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Validate and own an injected route (``moe_runtime.py:418-476``)."""
+
+    if not isinstance(value, MoERouteOverride):
+        raise TypeError("route_override must be a MoERouteOverride")
+    ids, weights = value.ids, value.weights
+    if not isinstance(ids, torch.Tensor) or not isinstance(weights, torch.Tensor):
+        raise TypeError("route override IDs and weights must be tensors")
+    shape = (rows, config.topk)
+    if tuple(ids.shape) != shape or tuple(weights.shape) != shape:
+        raise ValueError(f"route override IDs/weights must have shape {shape}")
+    if ids.dtype != torch.int32 or weights.dtype != torch.float32:
+        raise TypeError("route override requires INT32 IDs and FP32 weights")
+    if ids.device != device or weights.device != device:
+        raise ValueError("route override tensors must use the configured device")
+    if not ids.is_contiguous() or not weights.is_contiguous():
+        raise ValueError("route override tensors must be contiguous")
+    if ids.requires_grad or weights.requires_grad:
+        raise ValueError("route override tensors must not require gradients")
+    ids = ids.detach().clone(memory_format=torch.contiguous_format)
+    weights = weights.detach().clone(memory_format=torch.contiguous_format)
+    if not bool(torch.isfinite(weights).all().item()):
+        raise ValueError("route override weights must be finite")
+    if bool((weights <= 0).any().item()):
+        raise ValueError("route override weights must be strictly positive")
+    minimum, maximum = int(ids.min().item()), int(ids.max().item())
+    if minimum < 0 or maximum >= config.experts:
+        raise ValueError(
+            f"route override expert range [{minimum}, {maximum}] is outside [0, {config.experts})"
+        )
+    ordered = ids.sort(dim=1).values
+    if bool((ordered[:, 1:] == ordered[:, :-1]).any().item()):
+        raise ValueError("route override rows must contain unique expert IDs")
+    if config.score_func != "softmax":
+        row_sums = weights.sum(dim=1)
+        err = float((row_sums - float(config.route_scale)).abs().max().item())
+        tol = 8.0 * torch.finfo(torch.float32).eps * max(1.0, abs(float(config.route_scale)))
+        if err > tol:
+            raise ValueError(
+                "route override weights must sum to route_scale per row; "
+                f"max_abs_error={err}, tolerance={tol}"
+            )
+    return ids, weights
+
+
+class TP4MoE:
+    """Whole MoE layer resident on one GPU, ``TP4MoE``-compatible interface.
+
+    Slots isolate storage, not ordering: calls are expected from one scheduler
+    thread; every launch goes to the current stream of ``device``.
+    """
+
+    def __init__(
+        self,
+        *,
+        config: TP4MoEConfig,
+        resident: ResidentInt4MoEWeights,
+        gate: ResidentGateWeights,
+        rank: int = 0,
+        device: torch.device,
+        global_row_shapes: Iterable[int],
+        group: Any = None,
+        slots_per_shape: int = 1,
+        alignment_provider: Callable[..., object] | None = None,
+        marlin_input_dtype: torch.dtype | None = None,
+        buffer_donor: "TP4MoE | None" = None,
+    ) -> None:
+        config.validate()
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise ValueError("TP4MoE runs on a GPU device")
+        if rank != 0:
+            raise ValueError("single-GPU layer: rank must be 0")
+        if group is not None:
+            import torch.distributed as dist
+
+            if dist.is_initialized() and dist.get_world_size(group) != 1:
+                raise ValueError("single-GPU layer: the process group must have world size 1")
+        if marlin_input_dtype not in (None, torch.float8_e4m3fn):
+            raise ValueError(f"unsupported input dtype {marlin_input_dtype!r}")
+        if getattr(resident, "marlin_input_dtype", None) != marlin_input_dtype:
+            raise ValueError(
+                f"resident input dtype {getattr(resident, 'marlin_input_dtype', None)!r} "
+                f"does not match requested {marlin_input_dtype!r}"
+            )
+        if marlin_input_dtype is not None:
+            raise NotImplementedError("the W4A8 layer path is provided by experts_w4a8 (not yet wired)")
+        if not isinstance(resident, ResidentInt4MoEWeights):
+            raise TypeError("resident must be ResidentInt4MoEWeights")
+        resident.validate()
+        if (resident.experts, resident.hidden_size, resident.intermediate_size) != (
+            config.experts, config.hidden_size, config.intermediate_size
+        ):
+            raise ValueError("resident expert geometry does not match the config")
+        if resident.has_shared != bool(config.shared_experts):
+            raise ValueError("resident shared-expert presence does not match the config")
+        if resident.device != device:
+            raise ValueError("resident weights must live on the configured device")
+        if tuple(gate.weight.shape) != (config.experts, config.hidden_size):
+            raise ValueError("gate weight shape mismatch")
+        if gate.weight.device != device:
+            raise ValueError("gate weight must use the configured device")
+        if gate.bias is not None:
+            if tuple(gate.bias.shape) != (config.experts,) or gate.bias.device != device:
+                raise ValueError("gate bias must be [experts] on the configured device")
+        if gate.tid2eid is not None:
+            t = gate.tid2eid
+            if t.ndim != 2 or t.shape[1] != config.topk or t.dtype != torch.int64 or t.device != device:
+                raise ValueError(f"hash tid2eid must be int64 [vocab, {config.topk}] on the device")
+            lo, hi = int(t.min().item()), int(t.max().item())
+            if lo < 0 or hi >= config.experts:
+                raise ValueError(f"hash route table range [{lo}, {hi}] outside [0, {config.experts})")
+            ordered = t.sort(dim=1).values
+            if bool((ordered[:, 1:] == ordered[:, :-1]).any().item()):
+                raise ValueError("hash route table rows must contain unique expert IDs")
+        if resident.checkpoint_id is not None and gate.checkpoint_id is not None:
+            if resident.checkpoint_id != gate.checkpoint_id:
+                raise ValueError("gate and MoE weights come from different checkpoints")
+
+        self.config = config
+        self.resident = resident
+        self.gate = gate
+        self.layer_id = resident.layer_id
+        self.route_kind = gate.route_kind
+        self.rank = 0
+        self.device = device
+        self.group = group
+        self._marlin_input_dtype = marlin_input_dtype
+        self._gate_weight = gate.weight.to(torch.bfloat16).contiguous()
+        self._gate_bias = None if gate.bias is None else gate.bias.float().contiguous()
+        self.overlap_stats: dict[str, int] = {
+            "overlapped_calls": 0,
+            "overlapped_rows": 0,
+            "sequential_calls": 0,
+            "sequential_rows": 0,
+        }
+        self._route_tensor_observer: list[MoERouteTensors] | None = None
+        self._route_observer_captures_local_input = False
+        if alignment_provider is not None:
+            if self.route_kind != "learned":
+                raise ValueError("an injected alignment provider is only valid for learned routing")
+            if not callable(alignment_provider):
+                raise TypeError("alignment_provider must be callable")
+        self._owned_alignment_provider = alignment_provider
+        self._alignment_provider_poisoned = False
+        self._alignment_provider_tensors = self._snapshot_provider_tensors(alignment_provider)
+        if slots_per_shape < 1:
+            raise ValueError("slots_per_shape must be positive")
+        if buffer_donor is not None:
+            if not isinstance(buffer_donor, TP4MoE) or buffer_donor is self:
+                raise TypeError("buffer_donor must be a different TP4MoE")
+            if buffer_donor.config != self.config or buffer_donor.device != self.device:
+                raise ValueError("buffer_donor config/device differs")
+            if buffer_donor.route_kind != self.route_kind:
+                raise ValueError("buffer_donor route kind differs (input-ID storage shape)")
+            needed = {(int(r), s) for r in global_row_shapes for s in range(slots_per_shape)}
+            missing = needed - set(buffer_donor._buffers)
+            if missing:
+                raise ValueError(f"buffer_donor lacks registered shapes {sorted(missing)}")
+            self._buffers = buffer_donor._buffers
+        else:
+            self._buffers: dict[tuple[int, int], _LayerBuffers] = {}
+            for rows in global_row_shapes:
+                for slot in range(slots_per_shape):
+                    self._register_shape(int(rows), slot)
+        self._validate_provider_storage()
+
+    # ------------------------------------------------------------ buffers
+    def _register_shape(self, rows: int, slot: int) -> None:
+        cfg = self.config
+        if rows <= 0:
+            raise ValueError("MoE rows must be positive")
+        key = (rows, slot)
+        if key in self._buffers:
+            return
+        bs = ops.block_size_m(rows, cfg.topk, cfg.experts, 1 if self._marlin_input_dtype else 2)
+        template = torch.empty(rows, cfg.topk, dtype=torch.int32, device=self.device)
+        ws_bytes = ops.experts_workspace_bytes(
+            rows, cfg.topk, cfg.hidden_size, cfg.intermediate_size, bool(cfg.shared_experts)
+        )
+        self._buffers[key] = _LayerBuffers(
+            workspace=torch.empty(ws_bytes, dtype=torch.uint8, device=self.device),
+            logits=torch.empty(rows, cfg.experts, dtype=torch.float32, device=self.device),
+            route_ids=torch.empty(rows, cfg.topk, dtype=torch.int32, device=self.device),
+            route_weights=torch.empty(rows, cfg.topk, dtype=torch.float32, device=self.device),
+            margin=torch.empty(rows, dtype=torch.float32, device=self.device),
+            output=torch.empty(rows, cfg.hidden_size, dtype=torch.bfloat16, device=self.device),
+            alignment=allocate_deterministic_moe_alignment(template, block_size=bs, num_experts=cfg.experts),
+            block_size_m=bs,
+            ready_event=torch.cuda.Event(blocking=False),
+            gathered_input_ids=(
+                torch.empty(rows, dtype=torch.int64, device=self.device)
+                if self.route_kind == "hash" else None
+            ),
+        )
+
+    @property
+    def registered_global_rows(self) -> tuple[int, ...]:
+        return tuple(sorted({rows for rows, _ in self._buffers}))
+
+    @property
+    def registered_slots(self) -> dict[int, tuple[int, ...]]:
+        return {
+            rows: tuple(sorted(s for r, s in self._buffers if r == rows))
+            for rows in self.registered_global_rows
+        }
+
+    @property
+    def alignment_provider(self) -> Callable[..., object] | None:
+        return self._owned_alignment_provider
+
+    def block_size_for(self, rows: int, slot: int = 0) -> int:
+        return self._buffers[(rows, slot)].block_size_m
+
+    # ------------------------------------------------- alignment provider
+    def _snapshot_provider_tensors(self, provider) -> tuple[torch.Tensor, ...]:
+        if provider is None:
+            return ()
+        storage_tensors = getattr(provider, "storage_tensors", None)
+        if not callable(storage_tensors):
+            raise TypeError("alignment_provider must expose callable storage_tensors")
+        observed = storage_tensors()
+        if not isinstance(observed, tuple):
+            raise TypeError("alignment_provider.storage_tensors() must return a tuple")
+        pointers: set[int] = set()
+        for tensor in observed:
+            if not isinstance(tensor, torch.Tensor):
+                raise TypeError("alignment provider storage must contain only tensors")
+            if tensor.device != self.device:
+                raise ValueError("alignment provider storage device differs")
+            if tensor.numel() <= 0 or not tensor.is_contiguous():
+                raise ValueError("alignment provider storage must be nonempty and contiguous")
+            if tensor.requires_grad:
+                raise ValueError("alignment provider storage must not require gradients")
+            storage = tensor.untyped_storage()
+            if tensor.storage_offset() != 0 or storage.nbytes() != tensor.numel() * tensor.element_size():
+                raise ValueError("alignment provider tensors must own their complete storage")
+            pointer = int(storage.data_ptr())
+            if pointer in pointers:
+                raise ValueError("alignment provider storage tensors must not alias")
+            pointers.add(pointer)
+        return observed
+
+    def _runtime_storage_pointers(self) -> set[int]:
+        tensors = [self.resident.w13_q, self.resident.w13_s, self.resident.w2_q, self.resident.w2_s,
+                   self.gate.weight]
+        for b in self._buffers.values():
+            tensors += [b.workspace, b.logits, b.route_ids, b.route_weights, b.margin, b.output,
+                        b.alignment.sorted_token_ids, b.alignment.expert_ids,
+                        b.alignment.num_tokens_post_padded]
+        return {int(t.untyped_storage().data_ptr()) for t in tensors}
+
+    def _validate_provider_storage(self) -> None:
+        if self._owned_alignment_provider is None:
+            return
+        observed = self._snapshot_provider_tensors(self._owned_alignment_provider)
+        if len(observed) != len(self._alignment_provider_tensors) or any(
+            a is not b for a, b in zip(observed, self._alignment_provider_tensors)
+        ):
+            raise ValueError("alignment provider storage tensor identity drifted")
+        provider_ptrs = {int(t.untyped_storage().data_ptr()) for t in observed}
+        if provider_ptrs & self._runtime_storage_pointers():
+            raise ValueError("alignment provider storage aliases TP4MoE storage")
+
+    def _poison_alignment_runtime(self) -> None:
+        self._alignment_provider_poisoned = True
+        for b in self._buffers.values():
+            b.state = "poisoned"
+
+    # ----------------------------------------------------- lifecycle
+    def slot_completion_status(self, global_rows: int, slot: int) -> dict[str, Any]:
+        key = (global_rows, slot)
+        if key not in self._buffers:
+            raise ValueError(f"global row/slot {key} was not pre-registered")
+        b = self._buffers[key]
+        return {"state": b.state, "has_completion_event": b.has_completion_event}
+
+    def reset_free_slot_completion_event(self, global_rows: int, slot: int) -> None:
+        if self._alignment_provider_poisoned:
+            raise RuntimeError("MoE alignment-provider lifecycle is poisoned; restart required")
+        key = (global_rows, slot)
+        if key not in self._buffers:
+            raise ValueError(f"global row/slot {key} was not pre-registered")
+        b = self._buffers[key]
+        if b.state != "free":
+            raise RuntimeError(f"MoE buffer slot {key} is not free")
+        b.ready_event = torch.cuda.Event(blocking=False)
+        b.has_completion_event = False
+
+    def enable_collective_overlap(self, blocks: int) -> None:
+        """No collectives at world size 1: accepted and recorded, never engaged."""
+
+        if not isinstance(blocks, int) or blocks < 0:
+            raise ValueError("blocks must be a non-negative integer")
+        self._overlap_blocks = blocks
+
+    @contextmanager
+    def observe_route_tensors(self, *, capture_local_input: bool = False) -> Iterator[list[MoERouteTensors]]:
+        if not isinstance(capture_local_input, bool):
+            raise TypeError("capture_local_input must be bool")
+        if self._route_tensor_observer is not None:
+            raise RuntimeError("route tensor observation cannot be nested")
+        observed: list[MoERouteTensors] = []
+        self._route_tensor_observer = observed
+        self._route_observer_captures_local_input = capture_local_input
+        try:
+            yield observed
+        finally:
+            self._route_tensor_observer = None
+            self._route_observer_captures_local_input = False
+
+    # ------------------------------------------------------- forward
+    def __call__(
+        self,
+        hidden_local: torch.Tensor,
+        *,
+        input_ids_local: torch.Tensor | None = None,
+        route_override: MoERouteOverride | None = None,
+        router_logits: torch.Tensor | None = None,
+        local_step: Callable[[str, Callable[[], Any]], Any] | None = None,
+        slot: int = 0,
+        collect_trace: bool = True,
+        collect_stage_digests: bool = False,
+        stage_marker: Callable[[str], None] | None = None,
+    ) -> tuple[torch.Tensor, MoETrace | None]:
+        """One MoE layer forward (``moe_runtime.py:1565-1947``).
+
+        ``router_logits`` (fp32 [rows, E], optional) replaces the gate GEMM for
+        callers that already hold the logits; selection, weights and margin are
+        still computed from them with the configured score function.
+        """
+
+        cfg = self.config
+
+        def run_local(name: str, fn: Callable[[], Any]) -> Any:
+            return fn() if local_step is None else local_step(name, fn)
+
+        def mark(name: str) -> None:
+            if stage_marker is not None:
+                stage_marker(name)
+
+        def prepare_input():
+            if hidden_local.ndim != 3 or hidden_local.shape[-1] != cfg.hidden_size:
+                raise ValueError("MoE input must have shape [local_batch, sequence, hidden]")
+            if hidden_local.dtype != torch.bfloat16 or hidden_local.device != self.device:
+                raise ValueError("MoE input must use the configured device and BF16")
+            local_ids = None
+            if self.route_kind == "learned":
+                if input_ids_local is not None:
+                    raise ValueError("learned routing forbids input_ids_local")
+            else:
+                if route_override is not None:
+                    raise ValueError("hash routing forbids route_override")
+                if router_logits is not None:
+                    raise ValueError("hash routing computes its own logits")
+                if not isinstance(input_ids_local, torch.Tensor):
+                    raise ValueError("hash routing requires input_ids_local")
+                if tuple(input_ids_local.shape) != tuple(hidden_local.shape[:-1]):
+                    raise ValueError("input_ids_local shape must match hidden local row axes")
+                if input_ids_local.dtype != torch.int64 or input_ids_local.device != self.device:
+                    raise ValueError("input_ids_local must be int64 on the configured device")
+                if not input_ids_local.is_contiguous():
+                    raise ValueError("input_ids_local must be contiguous")
+                local_ids = input_ids_local.view(-1)
+            shape = tuple(hidden_local.shape)
+            flat = hidden_local.reshape(-1, cfg.hidden_size).contiguous()
+            rows = flat.shape[0]
+            override = None
+            if route_override is not None:
+                override = _snapshot_route_override(route_override, rows=rows, config=cfg, device=self.device)
+            if router_logits is not None:
+                if tuple(router_logits.shape) != (rows, cfg.experts) or router_logits.dtype != torch.float32:
+                    raise ValueError(f"router_logits must be fp32 [{rows}, {cfg.experts}]")
+                if router_logits.device != self.device or not router_logits.is_contiguous():
+                    raise ValueError("router_logits must be contiguous on the configured device")
+            key = (rows, slot)
+            if key not in self._buffers:
+                raise ValueError(
+                    f"global row/slot {key} was not pre-registered; registered={self.registered_slots}"
+                )
+            if self._alignment_provider_poisoned:
+                raise RuntimeError("MoE alignment-provider lifecycle is poisoned; restart required")
+            b = self._buffers[key]
+            if b.state != "free":
+                raise RuntimeError(
+                    f"MoE buffer slot {key} is {b.state}; worker restart is required after a poisoned slot"
+                )
+            return shape, flat, local_ids, override, b
+
+        shape, flat, local_ids, override, buffers = run_local("prepare MoE input", prepare_input)
+        buffers.state = "in_flight"
+        if buffers.has_completion_event:
+            torch.cuda.current_stream(self.device).wait_event(buffers.ready_event)
+        try:
+            self.overlap_stats["sequential_calls"] += 1
+            self.overlap_stats["sequential_rows"] += int(flat.shape[0])
+            mark("moe_inputs_ready")
+            mark("moe_hidden_all_gather_done")
+            if local_ids is not None and buffers.gathered_input_ids is not None:
+                buffers.gathered_input_ids.copy_(local_ids)
+            mark("moe_ids_all_gather_done")
+
+            def compute_partial():
+                route_source = "native"
+                margin = None
+                a = buffers.alignment
+                fused = (
+                    self.route_kind == "learned"
+                    and override is None
+                    and self._owned_alignment_provider is None
+                    and self._route_tensor_observer is None
+                    and stage_marker is None
+                )
+                if self.route_kind == "learned" and router_logits is None:
+                    ops.gate_logits_into(flat, self._gate_weight, buffers.logits)
+                logits = router_logits if router_logits is not None else buffers.logits
+                if fused:
+                    # route -> align -> experts -> combine in one C-ABI call
+                    ops.layer_w4a16_into(
+                        flat, logits, self._gate_bias, topk=cfg.topk, score_func=cfg.score_func,
+                        route_scale=cfg.route_scale, w13q=self.resident.w13_q,
+                        w13s=self.resident.w13_s, w2q=self.resident.w2_q, w2s=self.resident.w2_s,
+                        experts=cfg.experts, inter=cfg.intermediate_size,
+                        has_shared=bool(cfg.shared_experts), clamp_limit=cfg.clamp_limit,
+                        block_size=buffers.block_size_m, ids=buffers.route_ids,
+                        weights=buffers.route_weights, margin=buffers.margin,
+                        sorted_token_ids=a.sorted_token_ids, expert_ids=a.expert_ids,
+                        num_tokens_post_padded=a.num_tokens_post_padded, out=buffers.output,
+                        workspace=buffers.workspace,
+                    )
+                    return buffers.route_weights, buffers.route_ids, buffers.margin, {}
+                sel_ids = sel_scores = None
+                if self.route_kind == "hash":
+                    ops.gate_logits_into(flat, self._gate_weight, buffers.logits)
+                    ops.route_hash_into(
+                        buffers.logits, self.gate.tid2eid, buffers.gathered_input_ids,
+                        route_scale=cfg.route_scale, ids=buffers.route_ids,
+                        weights=buffers.route_weights,
+                    )
+                    route_ids, route_weights = buffers.route_ids, buffers.route_weights
+                else:
+                    if self._route_tensor_observer is not None:
+                        depth = min(cfg.topk + 1, cfg.experts)
+                        sel_ids = torch.empty(flat.shape[0], depth, dtype=torch.int32, device=self.device)
+                        sel_scores = torch.empty(flat.shape[0], depth, dtype=torch.float32, device=self.device)
+                    ops.route_topk_into(
+                        logits, self._gate_bias, topk=cfg.topk, score_func=cfg.score_func,
+                        route_scale=cfg.route_scale, ids=buffers.route_ids,
+                        weights=buffers.route_weights, margin=buffers.margin,
+                        selection_ids=sel_ids, selection_scores=sel_scores,
+                    )
+                    margin = buffers.margin
+                    route_ids, route_weights = buffers.route_ids, buffers.route_weights
+                    if override is not None:
+                        route_ids, route_weights = override
+                        route_source = "explicit_global"
+                mark("moe_route_done")
+                if self._route_tensor_observer is not None:
+                    self._route_tensor_observer.append(
+                        MoERouteTensors(
+                            weights=route_weights, ids=route_ids, margin=margin,
+                            selection_ids=sel_ids, selection_scores=sel_scores,
+                            local_input=flat.detach().clone() if self._route_observer_captures_local_input else None,
+                            gate_logits=logits if self.route_kind == "learned" else buffers.logits,
+                            route_source=route_source,
+                        )
+                    )
+                provider = self._owned_alignment_provider
+                if provider is None:
+                    ops.align_into(
+                        route_ids, block_size=buffers.block_size_m, num_experts=cfg.experts,
+                        sorted_token_ids=a.sorted_token_ids, expert_ids=a.expert_ids,
+                        num_tokens_post_padded=a.num_tokens_post_padded,
+                    )
+                else:
+                    try:
+                        aligned = provider(route_ids, block_size=buffers.block_size_m,
+                                           num_experts=cfg.experts, output=a, slot=slot)
+                    except BaseException:
+                        self._poison_alignment_runtime()
+                        raise
+                    if aligned is not a:
+                        self._poison_alignment_runtime()
+                        raise RuntimeError("alignment provider must return the caller-owned output")
+                ops.experts_w4a16_into(
+                    flat, w13q=self.resident.w13_q, w13s=self.resident.w13_s,
+                    w2q=self.resident.w2_q, w2s=self.resident.w2_s, experts=cfg.experts,
+                    inter=cfg.intermediate_size, has_shared=bool(cfg.shared_experts),
+                    route_weights=route_weights, sorted_token_ids=a.sorted_token_ids,
+                    expert_ids=a.expert_ids, num_tokens_post_padded=a.num_tokens_post_padded,
+                    block_size=buffers.block_size_m, clamp_limit=cfg.clamp_limit,
+                    out=buffers.output, workspace=buffers.workspace,
+                )
+                # routed experts, shared expert and the add run in the same fused launch chain
+                mark("moe_routed_done")
+                mark("moe_shared_done")
+                mark("moe_combine_done")
+                digests = {}
+                if collect_stage_digests:
+                    digests = {
+                        "gathered_input": _tensor_digest(flat),
+                        "combined_partial": _tensor_digest(buffers.output),
+                    }
+                return route_weights, route_ids, margin, digests
+
+            route_weights, route_ids, margin, digests = run_local("compute MoE partial", compute_partial)
+            mark("moe_reduce_scatter_done")
+
+            def finish():
+                out = buffers.output.reshape(shape).clone()
+                trace = None
+                if collect_trace:
+                    if collect_stage_digests:
+                        digests["reduce_scatter_output"] = _tensor_digest(buffers.output)
+                    trace = MoETrace(
+                        local_input_shape=shape,
+                        gathered_shape=tuple(flat.shape),
+                        partial_shape=tuple(buffers.output.shape),
+                        local_output_shape=tuple(out.shape),
+                        route_ids_row_zero=tuple(int(v) for v in route_ids[0].cpu()),
+                        route_weights_row_zero=tuple(float(v) for v in route_weights[0].cpu()),
+                        route_margin_min=None if margin is None else float(margin.min().item()),
+                        route_digest=_tensor_digest(route_ids, route_weights),
+                        stage_digests=digests,
+                        buffer_slot=slot,
+                        route_source="explicit_global" if override is not None else "native",
+                    )
+                buffers.ready_event.record(torch.cuda.current_stream(self.device))
+                buffers.has_completion_event = True
+                buffers.state = "free"
+                return out, trace
+
+            result = run_local("finalize MoE trace", finish)
+            mark("moe_finalize_done")
+            return result
+        except BaseException:
+            buffers.state = "poisoned"
+            raise
+
+    def forward_tensor(
+        self,
+        hidden_local: torch.Tensor,
+        *,
+        input_ids_local: torch.Tensor | None = None,
+        route_override: MoERouteOverride | None = None,
+        router_logits: torch.Tensor | None = None,
+        slot: int = 0,
+        stage_marker: Callable[[str], None] | None = None,
+    ) -> torch.Tensor:
+        """Owning output without host-side trace extraction (``moe_runtime.py:1949-1970``)."""
+
+        out, trace = self(
+            hidden_local,
+            input_ids_local=input_ids_local,
+            route_override=route_override,
+            router_logits=router_logits,
+            slot=slot,
+            collect_trace=False,
+            stage_marker=stage_marker,
+        )
+        if trace is not None:
+            raise AssertionError("trace-free MoE path unexpectedly produced a trace")
+        return out
+
+
+MoELayer = TP4MoE
+
+__all__ = [
+    "FLASH_CONFIG",
+    "MoELayer",
+    "MoERouteOverride",
+    "MoERouteTensors",
+    "MoETrace",
+    "ResidentGateWeights",
+    "TP4MoE",
+    "TP4MoEConfig",
+]

@@ -1,0 +1,267 @@
+"""Torch-tensor wrappers of the C ABI (device memory and streams only).
+
+Each wrapper checks dtype / device / shape / contiguity of caller-owned
+tensors, then launches on the current HIP stream of the tensors' device.  All
+arithmetic happens in the HIP kernels of ``libdsv4moe.so``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import SCORE_FUNCS, call, ptr
+
+GROUP = 128
+
+
+def _check(name, t, *, dtype, shape=None, device=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} shape must be {tuple(shape)}, got {tuple(t.shape)}")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device (cuda) tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+PROFILE_INTERVALS = ("route", "align", "row_sums", "stage1_w13", "stage2_w2", "combine")
+
+
+def profile_begin(max_calls: int) -> None:
+    """Start per-kernel HIP-event timing of the next ``max_calls`` layer calls."""
+
+    call("dsv4moe_profile_begin", int(max_calls))
+
+
+def profile_end() -> tuple[dict[str, float], int]:
+    """Stop timing; returns (mean ms per kernel interval, calls recorded)."""
+
+    import ctypes
+
+    out = (ctypes.c_float * len(PROFILE_INTERVALS))()
+    calls = ctypes.c_int32(0)
+    call("dsv4moe_profile_end", out, len(PROFILE_INTERVALS), ctypes.byref(calls))
+    return {k: float(out[i]) for i, k in enumerate(PROFILE_INTERVALS)}, int(calls.value)
+
+
+def score_func_id(score_func: str | int) -> int:
+    if isinstance(score_func, int):
+        if score_func not in SCORE_FUNCS.values():
+            raise ValueError(f"unknown score_func {score_func}")
+        return score_func
+    try:
+        return SCORE_FUNCS[score_func]
+    except KeyError as exc:
+        raise ValueError(f"unknown score_func {score_func!r}") from exc
+
+
+def block_size_m(rows: int, topk: int, experts: int, act_itemsize: int = 2) -> int:
+    bs = _lib.load().dsv4moe_block_size_m(rows, topk, experts, act_itemsize)
+    if bs < 0:
+        raise ValueError("rows, topk and experts must be positive")
+    return int(bs)
+
+
+def route_topk_into(
+    logits: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    topk: int,
+    score_func: str | int,
+    route_scale: float,
+    ids: torch.Tensor,
+    weights: torch.Tensor,
+    margin: torch.Tensor | None = None,
+    selection_ids: torch.Tensor | None = None,
+    selection_scores: torch.Tensor | None = None,
+) -> None:
+    if logits.ndim != 2:
+        raise ValueError("logits must be [tokens, experts]")
+    tokens, experts = logits.shape
+    dev = logits.device
+    _check("logits", logits, dtype=torch.float32, device=dev)
+    if bias is not None:
+        _check("bias", bias, dtype=torch.float32, shape=(experts,), device=dev)
+    _check("ids", ids, dtype=torch.int32, shape=(tokens, topk), device=dev)
+    _check("weights", weights, dtype=torch.float32, shape=(tokens, topk), device=dev)
+    if margin is not None:
+        _check("margin", margin, dtype=torch.float32, shape=(tokens,), device=dev)
+    depth = min(topk + 1, experts)
+    if selection_ids is not None:
+        _check("selection_ids", selection_ids, dtype=torch.int32, shape=(tokens, depth), device=dev)
+    if selection_scores is not None:
+        _check("selection_scores", selection_scores, dtype=torch.float32, shape=(tokens, depth), device=dev)
+    call(
+        "dsv4moe_route_topk", ptr(logits), ptr(bias), tokens, experts, topk,
+        score_func_id(score_func), float(route_scale), ptr(ids), ptr(weights), ptr(margin),
+        ptr(selection_ids), ptr(selection_scores), _lib.current_stream(dev),
+    )
+
+
+def route_hash_into(
+    logits: torch.Tensor,
+    tid2eid: torch.Tensor,
+    input_ids: torch.Tensor,
+    *,
+    route_scale: float,
+    ids: torch.Tensor,
+    weights: torch.Tensor,
+    selected_scores: torch.Tensor | None = None,
+) -> None:
+    tokens, experts = logits.shape
+    dev = logits.device
+    _check("logits", logits, dtype=torch.float32, device=dev)
+    _check("tid2eid", tid2eid, dtype=torch.int64, device=dev)
+    _check("input_ids", input_ids, dtype=torch.int64, shape=(tokens,), device=dev)
+    topk = tid2eid.shape[1]
+    _check("ids", ids, dtype=torch.int32, shape=(tokens, topk), device=dev)
+    _check("weights", weights, dtype=torch.float32, shape=(tokens, topk), device=dev)
+    if selected_scores is not None:
+        _check("selected_scores", selected_scores, dtype=torch.float32, shape=(tokens, topk), device=dev)
+    call(
+        "dsv4moe_route_hash", ptr(logits), ptr(tid2eid), tid2eid.shape[0], ptr(input_ids),
+        tokens, experts, topk, float(route_scale), ptr(ids), ptr(weights), ptr(selected_scores),
+        _lib.current_stream(dev),
+    )
+
+
+def gate_logits_into(x: torch.Tensor, weight: torch.Tensor, logits: torch.Tensor) -> None:
+    tokens, hidden = x.shape
+    experts = weight.shape[0]
+    dev = x.device
+    _check("x", x, dtype=torch.bfloat16, device=dev)
+    _check("weight", weight, dtype=torch.bfloat16, shape=(experts, hidden), device=dev)
+    _check("logits", logits, dtype=torch.float32, shape=(tokens, experts), device=dev)
+    call("dsv4moe_gate_logits", ptr(x), ptr(weight), tokens, hidden, experts, ptr(logits),
+         _lib.current_stream(dev))
+
+
+def align_into(
+    ids: torch.Tensor,
+    *,
+    block_size: int,
+    num_experts: int,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+) -> None:
+    tokens, topk = ids.shape
+    dev = ids.device
+    _check("topk_ids", ids, dtype=torch.int32, device=dev)
+    _check("sorted_token_ids", sorted_token_ids, dtype=torch.int32, device=dev)
+    _check("expert_ids", expert_ids, dtype=torch.int32, device=dev)
+    _check("num_tokens_post_padded", num_tokens_post_padded, dtype=torch.int32, shape=(1,), device=dev)
+    call(
+        "dsv4moe_align", ptr(ids), tokens, topk, num_experts, block_size, ptr(sorted_token_ids),
+        sorted_token_ids.numel(), ptr(expert_ids), expert_ids.numel(),
+        ptr(num_tokens_post_padded), _lib.current_stream(dev),
+    )
+
+
+def pack_int4_g128(canon: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Checkpoint-layout int4 [.., n, k/2] u8 + bf16 scales [.., n, k/128] ->
+    tiled (packed u8 [.., n*k/2], scales bf16 [.., n/16, k/128, 16])."""
+
+    if canon.ndim == 2:
+        canon = canon.unsqueeze(0)
+        scales = scales.unsqueeze(0)
+        squeeze = True
+    else:
+        squeeze = False
+    batch, n, half_k = canon.shape
+    k = half_k * 2
+    dev = canon.device
+    _check("canon", canon, dtype=torch.uint8, device=dev)
+    _check("scales", scales, dtype=torch.bfloat16, shape=(batch, n, k // GROUP), device=dev)
+    packed = torch.empty((batch, n * half_k), dtype=torch.uint8, device=dev)
+    packed_scales = torch.empty((batch, n // 16, k // GROUP, 16), dtype=torch.bfloat16, device=dev)
+    call("dsv4moe_pack_int4_g128", ptr(canon), ptr(scales), batch, n, k, ptr(packed),
+         ptr(packed_scales), _lib.current_stream(dev))
+    if squeeze:
+        return packed[0], packed_scales[0]
+    return packed, packed_scales
+
+
+def experts_workspace_bytes(tokens: int, topk: int, hidden: int, inter: int, has_shared: bool) -> int:
+    return int(_lib.load().dsv4moe_experts_workspace_bytes(tokens, topk, hidden, inter, int(bool(has_shared))))
+
+
+def experts_w4a16_into(
+    x: torch.Tensor,
+    *,
+    w13q, w13s, w2q, w2s,
+    experts: int,
+    inter: int,
+    has_shared: bool,
+    route_weights: torch.Tensor,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    block_size: int,
+    clamp_limit: float,
+    out: torch.Tensor,
+    workspace: torch.Tensor,
+) -> None:
+    tokens, hidden = x.shape
+    topk = route_weights.shape[1]
+    dev = x.device
+    _check("x", x, dtype=torch.bfloat16, device=dev)
+    _check("out", out, dtype=torch.bfloat16, shape=(tokens, hidden), device=dev)
+    _check("route_weights", route_weights, dtype=torch.float32, shape=(tokens, topk), device=dev)
+    _check("workspace", workspace, dtype=torch.uint8, device=dev)
+    call(
+        "dsv4moe_experts_w4a16", ptr(x), tokens, hidden, inter, experts, topk, ptr(w13q),
+        ptr(w13s), ptr(w2q), ptr(w2s), int(bool(has_shared)), ptr(route_weights),
+        ptr(sorted_token_ids), sorted_token_ids.numel(), ptr(expert_ids),
+        ptr(num_tokens_post_padded), block_size, float(clamp_limit), ptr(out), ptr(workspace),
+        workspace.numel(), _lib.current_stream(dev),
+    )
+
+
+def layer_w4a16_into(
+    x: torch.Tensor,
+    logits: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    topk: int,
+    score_func: str | int,
+    route_scale: float,
+    w13q, w13s, w2q, w2s,
+    experts: int,
+    inter: int,
+    has_shared: bool,
+    clamp_limit: float,
+    block_size: int,
+    ids: torch.Tensor,
+    weights: torch.Tensor,
+    margin: torch.Tensor | None,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    out: torch.Tensor,
+    workspace: torch.Tensor,
+) -> None:
+    tokens, hidden = x.shape
+    dev = x.device
+    _check("x", x, dtype=torch.bfloat16, device=dev)
+    _check("logits", logits, dtype=torch.float32, shape=(tokens, experts), device=dev)
+    _check("ids", ids, dtype=torch.int32, shape=(tokens, topk), device=dev)
+    _check("weights", weights, dtype=torch.float32, shape=(tokens, topk), device=dev)
+    _check("out", out, dtype=torch.bfloat16, shape=(tokens, hidden), device=dev)
+    _check("workspace", workspace, dtype=torch.uint8, device=dev)
+    if bias is not None:
+        _check("bias", bias, dtype=torch.float32, shape=(experts,), device=dev)
+    call(
+        "dsv4moe_layer_w4a16", ptr(x), ptr(logits), ptr(bias), tokens, hidden, inter, experts,
+        topk, score_func_id(score_func), float(route_scale), ptr(w13q), ptr(w13s), ptr(w2q),
+        ptr(w2s), int(bool(has_shared)), float(clamp_limit), block_size, ptr(ids), ptr(weights),
+        ptr(margin), ptr(sorted_token_ids), sorted_token_ids.numel(), ptr(expert_ids),
+        ptr(num_tokens_post_padded), ptr(out), ptr(workspace), workspace.numel(),
+        _lib.current_stream(dev),
+    )

@@ -1,0 +1,97 @@
+"""Seeded synthetic inputs and weights for the benchmark configurations.
+
+Distributions follow the benchmark definitions of this build (hidden states
+bf16 ~ N(0,1); router logits fp32 ~ N(0,1); int4 values uniform in [-8, 7];
+bf16 group scales ~ U(0.005, 0.02)) and the reference's routing pools
+(``experiments/A3F-marlin-moe-flash/common.py:198-211``: uniform, Zipf via
+Gumbel-top-k with p ~ rank^-alpha).  Generation runs with torch generators on
+the target device; it is input preparation, not part of any timed path.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+GROUP = 128
+
+
+@dataclass(frozen=True)
+class LayerShape:
+    experts: int
+    hidden: int
+    inter: int
+    topk: int
+    has_shared: bool
+
+    @property
+    def total_experts(self) -> int:
+        return self.experts + (1 if self.has_shared else 0)
+
+
+TINY = LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=False)
+FLASH = LayerShape(experts=256, hidden=4096, inter=2048, topk=6, has_shared=True)
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def make_checkpoint_experts(shape: LayerShape, *, seed: int = 0, device="cuda",
+                            experts: range | None = None):
+    """Checkpoint-layout int4-g128 weights for all (or a range of) experts.
+
+    Returns (w13_packed [n, 2I, H/2] u8, w13_scale [n, 2I, H/128] bf16,
+             w2_packed [n, H, I/2] u8, w2_scale [n, H, I/128] bf16).
+    Each expert index e is generated from its own seeded stream
+    (seed * 1_000_003 + e), so any subset reproduces the same bytes.
+    """
+
+    ids = range(shape.total_experts) if experts is None else experts
+    n = len(ids)
+    h, i = shape.hidden, shape.inter
+    w13 = torch.empty((n, 2 * i, h // 2), dtype=torch.uint8, device=device)
+    s13 = torch.empty((n, 2 * i, h // GROUP), dtype=torch.bfloat16, device=device)
+    w2 = torch.empty((n, h, i // 2), dtype=torch.uint8, device=device)
+    s2 = torch.empty((n, h, i // GROUP), dtype=torch.bfloat16, device=device)
+    for slot, e in enumerate(ids):
+        g = _gen(seed * 1_000_003 + e, device)
+        w13[slot] = torch.randint(0, 256, (2 * i, h // 2), dtype=torch.uint8, device=device, generator=g)
+        s13[slot] = (torch.rand((2 * i, h // GROUP), device=device, generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+        w2[slot] = torch.randint(0, 256, (h, i // 2), dtype=torch.uint8, device=device, generator=g)
+        s2[slot] = (torch.rand((h, i // GROUP), device=device, generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+    return w13, s13, w2, s2
+
+
+def make_hidden(tokens: int, hidden: int, *, seed: int = 1, device="cuda") -> torch.Tensor:
+    return torch.randn((tokens, hidden), device=device, generator=_gen(seed, device)).to(torch.bfloat16)
+
+
+def make_logits(tokens: int, experts: int, *, seed: int = 2, device="cuda") -> torch.Tensor:
+    return torch.randn((tokens, experts), device=device, generator=_gen(seed, device), dtype=torch.float32)
+
+
+def zipf_ids(tokens: int, experts: int, topk: int, *, alpha: float = 1.1, seed: int = 4,
+             device="cuda") -> torch.Tensor:
+    """Gumbel-top-k (Plackett-Luce without replacement) with p ~ rank^-alpha
+    (``common.py:202-206``); int32 [tokens, topk]."""
+
+    g = _gen(seed, device)
+    p = torch.arange(1, experts + 1, device=device, dtype=torch.float32) ** (-alpha)
+    u = torch.rand((tokens, experts), device=device, generator=g).clamp_min(1e-20)
+    logits = p.log() + (-torch.log(-torch.log(u)))
+    return logits.topk(topk, dim=-1)[1].to(torch.int32)
+
+
+__all__ = [
+    "FLASH",
+    "TINY",
+    "LayerShape",
+    "make_checkpoint_experts",
+    "make_hidden",
+    "make_logits",
+    "zipf_ids",
+]

@@ -1,0 +1,196 @@
+/*
+ * dsv4moe.h -- C ABI of the MI355X (gfx950) DeepSeek-V4-Flash MoE hot path.
+ *
+ * Every entry point is stream-ordered on the HIP stream passed as `stream`
+ * (a hipStream_t; NULL = the default stream), allocates no device memory,
+ * performs no host<->device synchronisation, and returns DSV4MOE_OK (0) or a
+ * nonzero status with a thread-local message in dsv4moe_last_error().
+ * Arguments are validated before any launch; on a validation error nothing is
+ * launched.  Device pointers are plain addresses of caller-owned buffers.
+ *
+ * Tensor conventions (row-major, contiguous):
+ *   bf16 values are passed as uint16_t bit patterns;
+ *   route ids int32 [T, k]; route weights fp32 [T, k];
+ *   int4 weights in the "tiled" layout produced by dsv4moe_pack_int4_g128.
+ *
+ * Reference interfaces replaced (gaiban-lite, paths from its repo root) are
+ * cited per entry point.
+ */
+#ifndef DSV4MOE_H
+#define DSV4MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSV4MOE_OK 0
+#define DSV4MOE_EINVAL 1   /* contract violation detected before launch */
+#define DSV4MOE_EHIP 2     /* HIP runtime error (launch / device state) */
+
+#define DSV4MOE_SCORE_SIGMOID 0
+#define DSV4MOE_SCORE_SOFTMAX 1
+#define DSV4MOE_SCORE_SQRTSOFTPLUS 2
+
+#define DSV4MOE_GROUP 128  /* int4 quantisation group along K */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* dsv4moe_last_error(void);
+
+/* ABI revision of this library. */
+int32_t dsv4moe_abi_version(void);
+
+/*
+ * Per-kernel timing of the next `max_calls` calls of dsv4moe_layer_w4a16 /
+ * dsv4moe_experts_w4a16, recorded with HIP events on the launch stream at 7
+ * stamps (begin, after route, after align, after row sums, after stage 1,
+ * after stage 2, after combine).  No counterpart in the reference (its benches
+ * time with CUDA events from Python, experiments/A3F-marlin-moe-flash/common.py:220-234).
+ * dsv4moe_profile_end synchronises on the last event and writes the mean
+ * duration in ms of the 6 intervals (route, align, row sums, stage 1, stage 2,
+ * combine) to mean_ms[6].  Process-global; use from one host thread.
+ */
+int dsv4moe_profile_begin(int32_t max_calls);
+int dsv4moe_profile_end(float* mean_ms, int32_t n_intervals, int32_t* calls_recorded);
+
+/*
+ * Block-size policy for the expert alignment.
+ * Replaces _marlin_block_size_m (runtime/dsv4_direct/moe_runtime.py:276-300):
+ * first of (8,16,32,48,64) with rows*topk/experts/bs < 0.9, else 64; at least
+ * 16 for 1-byte activations.  Returns -1 on invalid arguments.
+ */
+int32_t dsv4moe_block_size_m(int64_t rows, int32_t topk, int32_t experts, int32_t act_itemsize);
+
+/*
+ * Capacity of sorted_token_ids.
+ * Replaces max_padded_tokens (runtime/dsv4_direct/deterministic_moe_align.py:17-32).
+ * Returns -1 on invalid arguments.
+ */
+int64_t dsv4moe_max_padded_tokens(int64_t num_assignments, int32_t num_experts, int32_t block_size);
+
+/*
+ * Router: scores, top-(k+1) selection, renormalised weights, margin.
+ * Replaces the score/top-k half of gate_forward_with_boundary
+ * (runtime/dsv4_direct/moe_forward.py:52-94) and Gate.forward
+ * (reference/inference/model.py:564-584) for pre-computed logits.
+ *
+ *   logits   fp32 [tokens, experts]
+ *   bias     fp32 [experts] or NULL (shifts selection only)
+ *   ids      int32 [tokens, topk]      out
+ *   weights  fp32  [tokens, topk]      out (score/sum*route_scale; softmax: score*route_scale)
+ *   margin   fp32  [tokens] or NULL    out (sel[k-1]-sel[k]; 0 if topk == experts)
+ *   selection_ids    int32 [tokens, min(topk+1,experts)] or NULL   out
+ *   selection_scores fp32  [tokens, min(topk+1,experts)] or NULL   out
+ * Ordering: biased score descending, expert id ascending.  experts <= 1024,
+ * 1 <= topk <= min(experts, 16).
+ */
+int dsv4moe_route_topk(const float* logits, const float* bias, int64_t tokens, int32_t experts,
+                       int32_t topk, int32_t score_func, float route_scale, int32_t* ids,
+                       float* weights, float* margin, int32_t* selection_ids,
+                       float* selection_scores, void* stream);
+
+/*
+ * Hash router: ids = tid2eid[input_ids], weights from sqrt-softplus scores.
+ * Replaces hash_gate_forward (runtime/dsv4_direct/moe_forward.py:186-231).
+ *   tid2eid int64 [vocab, topk]; input_ids int64 [tokens].
+ *   selected_scores fp32 [tokens, topk] or NULL: the unnormalised gathered scores.
+ *   An id or token outside its table is written as expert id -1.
+ */
+int dsv4moe_route_hash(const float* logits, const int64_t* tid2eid, int64_t vocab,
+                       const int64_t* input_ids, int64_t tokens, int32_t experts, int32_t topk,
+                       float route_scale, int32_t* ids, float* weights,
+                       float* selected_scores, void* stream);
+
+/*
+ * Router logits from hidden states: logits = x . Wg^T with fp32 accumulation
+ * (bf16 products are exact in fp32).  Replaces F.linear(x.float(), W.float())
+ * (runtime/dsv4_direct/moe_forward.py:80; reference/inference/model.py:565).
+ *   x bf16 [tokens, hidden]; wg bf16 [experts, hidden]; logits fp32 [tokens, experts].
+ *   hidden % 32 == 0, experts % 16 == 0.
+ */
+int dsv4moe_gate_logits(const uint16_t* x, const uint16_t* wg, int64_t tokens, int32_t hidden,
+                        int32_t experts, float* logits, void* stream);
+
+/*
+ * Deterministic expert alignment.
+ * Replaces deterministic_moe_align_block_size
+ * (runtime/dsv4_direct/deterministic_moe_align.py:58-133) and the Triton
+ * fixed_b240_moe_align_block8 (runtime/dsv4_direct/fixed_moe_align.py:407-421).
+ *   ids int32 [tokens, topk], every id in [0, experts)
+ *   sorted_token_ids int32 [capacity]  out (capacity = dsv4moe_max_padded_tokens)
+ *   expert_ids int32 [ceil(capacity/block_size)]  out
+ *   num_tokens_post_padded int32 [1]  out; -1 if an id was out of range
+ * experts <= 1024.
+ */
+int dsv4moe_align(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts,
+                  int32_t block_size, int32_t* sorted_token_ids, int64_t capacity,
+                  int32_t* expert_ids, int64_t num_blocks, int32_t* num_tokens_post_padded,
+                  void* stream);
+
+/*
+ * Repack int4 group-128 weights from the checkpoint layout into the tiled
+ * layout the expert kernels stream.  Replaces the load-time Marlin repack
+ * (runtime/dsv4_direct/ops/marlin_moe.py:173-223).
+ *   canon        uint8 [batch, n, k/2]   (low nibble = even k, two's complement)
+ *   canon_scales bf16  [batch, n, k/128]
+ *   packed       uint8 [batch, n*k/2]     out (tiles of 16 rows x 128 k, 1 KiB each)
+ *   packed_scales bf16 [batch, n/16, k/128, 16]  out
+ * n % 16 == 0, k % 128 == 0.
+ */
+int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, int64_t batch,
+                           int64_t n, int64_t k, uint8_t* packed, uint16_t* packed_scales,
+                           void* stream);
+
+/*
+ * Workspace needed by dsv4moe_experts_w4a16 / _w4a8 (bytes).
+ */
+size_t dsv4moe_experts_workspace_bytes(int64_t tokens, int32_t topk, int32_t hidden,
+                                       int32_t inter, int32_t has_shared);
+
+/*
+ * Routed + shared experts with the fused combine, W4A16.
+ * Replaces the vLLM _fused_marlin_moe call (runtime/dsv4_direct/moe_runtime.py:1829-1856),
+ * the top-k sum (:1857), shared_bf16_partial (:246-263) and the combine add (:1873).
+ *   x        bf16 [tokens, hidden]
+ *   w13q/w13s  tiled int4 + scales, experts(+1 shared) x [2*inter, hidden]
+ *              (rows [0,inter) = gate w1, [inter,2*inter) = up w3)
+ *   w2q/w2s    tiled int4 + scales, experts(+1 shared) x [hidden, inter]
+ *   has_shared 1: expert index `experts` is the always-on shared expert
+ *   weights  fp32 [tokens, topk]  (route weights, applied to the w2 output)
+ *   sorted_token_ids / expert_ids / num_tokens_post_padded: dsv4moe_align output
+ *   clamp_limit > 0: gate = min(gate, L), up = clamp(up, -L, L) before SiLU(gate)*up
+ *   out      bf16 [tokens, hidden] = bf16( sum_j routed_j + shared ), fp32 accumulation
+ * hidden % 128 == 0, inter % 128 == 0, block_size in {8,16,32,48,64}.
+ */
+int dsv4moe_experts_w4a16(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
+                          int32_t experts, int32_t topk, const uint8_t* w13q,
+                          const uint16_t* w13s, const uint8_t* w2q, const uint16_t* w2s,
+                          int32_t has_shared, const float* weights,
+                          const int32_t* sorted_token_ids, int64_t capacity,
+                          const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                          int32_t block_size, float clamp_limit, uint16_t* out,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Whole MoE layer, W4A16: route (from logits) -> align -> experts -> combine.
+ * Replaces TP4MoE.compute_partial (runtime/dsv4_direct/moe_runtime.py:1714-1888)
+ * at world size 1.  Route and alignment outputs are caller-owned and written.
+ * bias may be NULL; margin may be NULL.
+ */
+int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bias,
+                        int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
+                        int32_t topk, int32_t score_func, float route_scale,
+                        const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
+                        const uint16_t* w2s, int32_t has_shared, float clamp_limit,
+                        int32_t block_size, int32_t* ids, float* weights, float* margin,
+                        int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                        int32_t* num_tokens_post_padded, uint16_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV4MOE_H */

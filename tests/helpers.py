@@ -1,0 +1,92 @@
+"""Shared test helpers: moving device data to the oracle, tolerances, layouts."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle as O
+
+# Parity bar for bf16 layer outputs against the fp32 dequant oracle (north
+# star: "within max relative error 1e-2 against an fp32 accumulation of the
+# same dequantized weights"): both the normwise max error max|d| / max|ref|
+# and the Frobenius relative error ||d|| / ||ref|| must be <= 1e-2.
+MOE_TOL = 1e-2
+
+
+def bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def to_np_f32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+class DeviceExpertSource(O.ExpertSource):
+    """Oracle accessor over device-resident checkpoint-layout experts; each
+    expert is copied to the host only when the oracle touches it."""
+
+    def __init__(self, w13, s13, w2, s2, group: int = 128):
+        super().__init__(w13, s13, w2, s2, group)
+        self._cache: dict[tuple[str, int], np.ndarray] = {}
+
+    def _get(self, which: str, e: int) -> np.ndarray:
+        key = (which, e)
+        if key not in self._cache:
+            if which == "w13":
+                v = O.dequant_int4_g128(self.w13_packed[e].cpu().numpy(), bf16_bits(self.w13_scale[e]), self.group)
+            else:
+                v = O.dequant_int4_g128(self.w2_packed[e].cpu().numpy(), bf16_bits(self.w2_scale[e]), self.group)
+            if len(self._cache) > 64:
+                self._cache.clear()
+            self._cache[key] = v
+        return self._cache[key]
+
+    def w13(self, e: int) -> np.ndarray:
+        return self._get("w13", e)
+
+    def w2(self, e: int) -> np.ndarray:
+        return self._get("w2", e)
+
+
+def moe_errors(out, ref) -> dict:
+    o = np.asarray(out, dtype=np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    d = o - r
+    return {
+        "max_rel": float(np.abs(d).max() / max(np.abs(r).max(), 1e-30)),
+        "rel_fro": float(np.linalg.norm(d) / max(np.linalg.norm(r), 1e-30)),
+        "max_abs": float(np.abs(d).max()),
+    }
+
+
+def assert_moe_close(out, ref, tol: float = MOE_TOL, what: str = "") -> dict:
+    err = moe_errors(out, ref)
+    assert np.isfinite(np.asarray(out, dtype=np.float64)).all(), f"{what}: non-finite output"
+    assert err["max_rel"] <= tol and err["rel_fro"] <= tol, f"{what}: {err}"
+    return err
+
+
+def np_tile_pack(canon: np.ndarray, scales_bits: np.ndarray):
+    """Independent numpy statement of the tiled int4 layout (see
+    gaiban-lite_amd/csrc/pack.hip): returns (packed bytes [n*k/2], scales [n/16, k/128, 16])."""
+
+    q = O.unpack_int4_rows(canon).astype(np.int32)  # [n, k]
+    n, k = q.shape
+    u = (q + 8).astype(np.uint32)
+    groups = k // 128
+    out = np.zeros((n // 16, groups, 64, 4), dtype=np.uint32)
+    lane = np.arange(64)
+    rows_in_strip = lane % 16
+    for s in range(n // 16):
+        for g in range(groups):
+            for d in range(4):
+                k0 = g * 128 + 32 * d + 8 * (lane // 16)
+                word = np.zeros(64, dtype=np.uint32)
+                for j in range(4):
+                    word |= u[s * 16 + rows_in_strip, k0 + 2 * j] << np.uint32(4 * j)
+                    word |= u[s * 16 + rows_in_strip, k0 + 2 * j + 1] << np.uint32(16 + 4 * j)
+                out[s, g, :, d] = word
+    packed = out.reshape(-1).view(np.uint8)
+    sc = scales_bits.reshape(n // 16, 16, groups).transpose(0, 2, 1).copy()
+    return packed, sc

@@ -1,0 +1,118 @@
+"""Grouped expert kernels (W4A16): bf16 layer output against the fp32 dequant
+oracle on the same seeded inputs, to max_rel and rel_fro <= 1e-2.
+
+Each token's output depends only on its own row, so full-size configurations
+are checked on a subset of token rows (routing, alignment and every kernel
+still run over all tokens).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gaiban_lite_amd import ResidentInt4MoEWeights, ops, route_from_logits, synthetic as S
+from gaiban_lite_amd.deterministic_moe_align import deterministic_moe_align_block_size
+from helpers import DeviceExpertSource, assert_moe_close, to_np_f32
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+_LAYERS: dict = {}
+
+
+def layer(shape: S.LayerShape, seed: int = 0):
+    key = (shape, seed)
+    if key not in _LAYERS:
+        if len(_LAYERS) >= 2:
+            _LAYERS.clear()
+            torch.cuda.empty_cache()
+        w13, s13, w2, s2 = S.make_checkpoint_experts(shape, seed=seed, device=DEV)
+        res = ResidentInt4MoEWeights.from_checkpoint_layout(
+            w13, s13, w2, s2, experts=shape.experts, has_shared=shape.has_shared)
+        _LAYERS[key] = (res, DeviceExpertSource(w13, s13, w2, s2))
+    return _LAYERS[key]
+
+
+def run_experts(shape, x, ids, weights, *, block_size=None, clamp=0.0):
+    res, _ = layer(shape)
+    t = x.shape[0]
+    bs = block_size or ops.block_size_m(t, shape.topk, shape.experts)
+    align = deterministic_moe_align_block_size(ids, block_size=bs, num_experts=shape.experts)
+    out = torch.empty((t, shape.hidden), dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(ops.experts_workspace_bytes(t, shape.topk, shape.hidden, shape.inter,
+                                                 shape.has_shared), dtype=torch.uint8, device=DEV)
+    ops.experts_w4a16_into(
+        x, w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, experts=shape.experts,
+        inter=shape.inter, has_shared=shape.has_shared, route_weights=weights,
+        sorted_token_ids=align.sorted_token_ids, expert_ids=align.expert_ids,
+        num_tokens_post_padded=align.num_tokens_post_padded, block_size=bs, clamp_limit=clamp,
+        out=out, workspace=ws)
+    torch.cuda.synchronize()
+    return out
+
+
+def check_layer(shape, t, *, rows=None, block_size=None, clamp=0.0, x_scale=1.0, seed=1,
+                score="sigmoid", ids=None):
+    print(f"[experts] E={shape.experts} H={shape.hidden} I={shape.inter} k={shape.topk} T={t} "
+          f"bs={block_size} clamp={clamp} x_scale={x_scale}", flush=True)
+    x = (S.make_hidden(t, shape.hidden, seed=seed, device=DEV).float() * x_scale).to(torch.bfloat16)
+    logits = S.make_logits(t, shape.experts, seed=seed + 1, device=DEV)
+    r = route_from_logits(logits, topk=shape.topk, score_func=score)
+    route_ids, route_w = r.routing_ids, r.routing_weights
+    if ids is not None:
+        route_ids = ids
+    out = run_experts(shape, x, route_ids, route_w, block_size=block_size, clamp=clamp)
+    _, src = layer(shape)
+    rows = np.arange(t) if rows is None else np.asarray(rows)
+    ref = O.moe_fp32(to_np_f32(x), route_ids.cpu().numpy(), route_w.cpu().numpy(), src,
+                     shared_index=shape.experts if shape.has_shared else None,
+                     clamp_limit=clamp, rows=rows)
+    got = to_np_f32(out)[rows]
+    err = assert_moe_close(got, ref, what=f"T={t}")
+    print(f"    {err}", flush=True)
+    return got, ref
+
+
+def test_tiny_config_full():
+    check_layer(S.TINY, 64)
+
+
+def test_tiny_config_matches_bf16_mirror_order_of_magnitude():
+    got, ref = check_layer(S.TINY, 64, seed=3)
+    x = S.make_hidden(64, S.TINY.hidden, seed=3, device=DEV)
+    r = route_from_logits(S.make_logits(64, S.TINY.experts, seed=4, device=DEV), topk=2)
+    mirror = O.moe_bf16_mirror(to_np_f32(x), r.routing_ids.cpu().numpy(),
+                               r.routing_weights.cpu().numpy(), layer(S.TINY)[1])
+    # the reference torch path itself sits at the same distance from the fp32 oracle
+    assert_moe_close(mirror, ref, what="bf16 mirror vs fp32 oracle")
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32, 48, 64])
+def test_every_block_size_kernel(bs):
+    check_layer(S.TINY, 200, block_size=bs, seed=5)
+
+
+@pytest.mark.parametrize("clamp,x_scale", [(10.0, 1.0), (10.0, 8.0), (2.0, 4.0)])
+def test_clamp(clamp, x_scale):
+    check_layer(S.TINY, 64, clamp=clamp, x_scale=x_scale, seed=7)
+
+
+def test_tiny_shared_expert_layout():
+    shape = S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True)
+    check_layer(shape, 50, seed=9)
+
+
+@pytest.mark.parametrize("t", [1, 8, 64, 256])
+def test_flash_decode(t):
+    rows = np.unique(np.r_[np.arange(min(t, 6)), t - 1])
+    check_layer(S.FLASH, t, rows=rows, seed=11 + t, clamp=10.0)
+
+
+def test_flash_prefill_2048_subset():
+    check_layer(S.FLASH, 2048, rows=[0, 1, 777, 2047], seed=13)
+
+
+def test_flash_zipf_routing_subset():
+    ids = S.zipf_ids(512, 256, 6, device=DEV)
+    check_layer(S.FLASH, 512, rows=[0, 5, 511], seed=15, ids=ids)
