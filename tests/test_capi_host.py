@@ -1,0 +1,128 @@
+"""CPU-side checks of the C ABI library and the host logic: the library loads
+and exports every function declared in include/dsv4moe.h; its host-only
+policy functions equal the oracle; validation rejects bad arguments before
+any launch; the Python boundary validates configs and route overrides."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gaiban_lite_amd import _lib, ops
+from gaiban_lite_amd import moe_runtime as R
+from gaiban_lite_amd import synthetic as S
+from gaiban_lite_amd.deterministic_moe_align import max_padded_tokens
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "dsv4moe.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsv4moe_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in dsv4moe.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.dsv4moe_abi_version() == 1
+
+
+def test_host_policy_functions_match_oracle():
+    lib = _lib.load()
+    for rows in (1, 4, 8, 64, 100, 256, 512, 1000, 1024, 2048, 4096, 8192, 32768):
+        for item in (1, 2):
+            assert lib.dsv4moe_block_size_m(rows, 6, 256, item) == O.marlin_block_size_m(rows, 6, 256, item)
+    for a, e, bs in ((24, 256, 8), (1440, 256, 8), (49152, 256, 64), (3, 8, 16), (7, 1024, 64)):
+        assert lib.dsv4moe_max_padded_tokens(a, e, bs) == O.max_padded_tokens(a, e, bs) == max_padded_tokens(a, e, bs)
+    assert lib.dsv4moe_block_size_m(0, 6, 256, 2) == -1
+    assert lib.dsv4moe_max_padded_tokens(0, 256, 8) == -1
+
+
+def _einval(name, *args):
+    rc = getattr(_lib.load(), name)(*args)
+    assert rc == _lib.DSV4MOE_EINVAL, (name, rc)
+    return _lib.last_error()
+
+
+def test_validation_rejects_before_launch():
+    fake = ctypes.c_void_p(0x1000)
+    assert "experts" in _einval("dsv4moe_route_topk", fake, None, 4, 0, 2, 0, 1.0, fake, fake, None, None, None, None)
+    assert "topk" in _einval("dsv4moe_route_topk", fake, None, 4, 8, 9, 0, 1.0, fake, fake, None, None, None, None)
+    assert "score_func" in _einval("dsv4moe_route_topk", fake, None, 4, 8, 2, 7, 1.0, fake, fake, None, None, None, None)
+    assert "capacity" in _einval("dsv4moe_align", fake, 4, 6, 256, 8, fake, 191, fake, 24, fake, None)
+    assert "multiple of 16" in _einval("dsv4moe_pack_int4_g128", fake, fake, 1, 24, 128, fake, fake, None)
+    assert "block_size" in _einval("dsv4moe_experts_w4a16", fake, 4, 4096, 2048, 256, 6, fake, fake, fake, fake,
+                                   1, fake, fake, 192, fake, fake, 12, 0.0, fake, fake, 1 << 30, None)
+    assert "hidden" in _einval("dsv4moe_experts_w4a16", fake, 4, 4000, 2048, 256, 6, fake, fake, fake, fake,
+                               1, fake, fake, 192, fake, fake, 8, 0.0, fake, fake, 1 << 30, None)
+    ws = ops.experts_workspace_bytes(4, 6, 4096, 2048, True)
+    assert "workspace" in _einval("dsv4moe_experts_w4a16", fake, 4, 4096, 2048, 256, 6, fake, fake, fake, fake,
+                                  1, fake, fake, 192, fake, fake, 8, 0.0, fake, ctypes.c_void_p(0x100000),
+                                  ws - 1, None)
+
+
+def test_workspace_formula():
+    # x row sums + h + h row sums + fp32 contributions, each 256-byte aligned
+    t, k, h, i = 64, 6, 4096, 2048
+    rows = t * k + t
+
+    def a(v):
+        return (v + 255) // 256 * 256
+
+    expect = a(4 * t * (h // 128)) + a(2 * rows * i) + a(4 * rows * (i // 128)) + a(4 * rows * h)
+    assert ops.experts_workspace_bytes(t, k, h, i, True) == expect
+
+
+def test_config_validation():
+    R.FLASH_CONFIG.validate()
+    with pytest.raises(ValueError):
+        R.TP4MoEConfig(world_size=4).validate()
+    with pytest.raises(ValueError):
+        R.TP4MoEConfig(hidden_size=4000).validate()
+    with pytest.raises(ValueError):
+        R.TP4MoEConfig(topk=17, experts=256).validate()
+    with pytest.raises(ValueError):
+        R.TP4MoEConfig(score_func="relu").validate()
+    with pytest.raises(ValueError):
+        R.TP4MoEConfig(clamp_limit=-1.0).validate()
+    with pytest.raises(ValueError):
+        R.ResidentGateWeights(weight=torch.zeros(4, 4), bias=torch.zeros(4), tid2eid=torch.zeros(2, 2, dtype=torch.int64))
+
+
+def test_route_override_validation_cpu():
+    cfg = R.TP4MoEConfig(experts=8, topk=2, route_scale=1.5, hidden_size=128, intermediate_size=128)
+    cpu = torch.device("cpu")
+    ids = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32)
+    w = torch.tensor([[0.75, 0.75], [1.0, 0.5]], dtype=torch.float32)
+    got_ids, got_w = R._snapshot_route_override(R.MoERouteOverride(ids, w), rows=2, config=cfg, device=cpu)
+    assert torch.equal(got_ids, ids) and got_ids.data_ptr() != ids.data_ptr()
+    bad = [
+        (torch.tensor([[0, 0], [2, 3]], dtype=torch.int32), w, "unique"),
+        (torch.tensor([[0, 9], [2, 3]], dtype=torch.int32), w, "outside"),
+        (ids, torch.tensor([[0.7, 0.7], [1.0, 0.5]]), "sum to route_scale"),
+        (ids, torch.tensor([[1.5, 0.0], [1.0, 0.5]]), "strictly positive"),
+        (ids.long(), w, "INT32"),
+    ]
+    for i, ww, msg in bad:
+        with pytest.raises((ValueError, TypeError), match=msg):
+            R._snapshot_route_override(R.MoERouteOverride(i, ww), rows=2, config=cfg, device=cpu)
+
+
+def test_synthetic_generators_are_seeded():
+    a = S.make_checkpoint_experts(S.TINY, seed=3, device="cpu", experts=range(2, 4))
+    b = S.make_checkpoint_experts(S.TINY, seed=3, device="cpu")
+    assert torch.equal(a[0][0], b[0][2]) and torch.equal(a[3][1], b[3][3])
+    s = a[1].float()
+    assert float(s.min()) >= 0.0049 and float(s.max()) <= 0.0201
+    ids = S.zipf_ids(8192, 256, 6, device="cpu")
+    counts = np.bincount(ids.numpy().reshape(-1), minlength=256)
+    assert counts.max() / counts.mean() > 10  # heavy skew (hottest expert >> mean)

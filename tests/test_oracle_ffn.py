@@ -1,0 +1,137 @@
+"""Pins the oracle's weight formats, expert FFN, W8A16 and split-K policy with
+known answers, scalar loops on tiny shapes and algebraic properties."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+
+def test_int4_pack_known_answer():
+    q = np.array([[0, 1, -1, 7, -8, 3, 2, -2]], dtype=np.int8)
+    p = O.pack_int4_rows(q)
+    # byte b: low nibble = k=2b, high nibble = k=2b+1, two's complement
+    np.testing.assert_array_equal(p, np.array([[0x10, 0x7F, 0x38, 0xE2]], dtype=np.uint8))
+    np.testing.assert_array_equal(O.unpack_int4_rows(p), q)
+
+
+def test_int4_roundtrip_and_group_indexing():
+    rng = np.random.default_rng(0)
+    q = rng.integers(-8, 8, size=(32, 512)).astype(np.int8)
+    p = O.pack_int4_rows(q)
+    np.testing.assert_array_equal(O.unpack_int4_rows(p), q)
+    s = O.bf16_round(rng.uniform(0.005, 0.02, size=(32, 4)).astype(np.float32))
+    w = O.dequant_int4_g128(p, O.bf16_to_bits(s))
+    for n in (0, 7, 31):
+        for k in (0, 127, 128, 300, 511):
+            assert w[n, k] == np.float32(q[n, k]) * s[n, k // 128]
+
+
+def test_fp4_table_and_e8m0_known_answers():
+    # moe_forward.py:23-40 (identical tables in convert.py:11-14, common.py:42-44)
+    assert O.FP4_VALUES == (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+                            0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)
+    # weight_only_linear.py:503-513: byte 0 -> 2^-127, b -> 2^(b-127)
+    codes = np.array([0, 1, 127, 128, 254], dtype=np.uint8)
+    np.testing.assert_array_equal(O.decode_e8m0(codes),
+                                  np.array([2.0 ** -127, 2.0 ** -126, 1.0, 2.0, 2.0 ** 127], dtype=np.float32))
+    with pytest.raises(ValueError):
+        O.decode_e8m0(np.array([255], dtype=np.uint8))
+    packed = np.array([[0x21, 0xF9] + [0] * 14], dtype=np.uint8)  # 32 values, one scale
+    w = O.dequant_mxfp4(packed, np.array([[128]], dtype=np.uint8))
+    np.testing.assert_array_equal(w[0, :4], np.array([1.0, 2.0, -1.0, -12.0], dtype=np.float32))
+
+
+def test_mxfp4_dequant_is_exact_in_bf16():
+    """c2f-dense-gate.json dequant_bf16_exact: E2M1 x E8M0 needs <= 3 significand bits."""
+
+    rng = np.random.default_rng(1)
+    packed = rng.integers(0, 256, size=(64, 128), dtype=np.uint8)
+    sc = rng.integers(100, 150, size=(64, 8), dtype=np.uint8)
+    w = O.dequant_mxfp4(packed, sc)
+    np.testing.assert_array_equal(O.bf16_round(w), w)
+
+
+def _tiny_source(rng, e, h, i):
+    w13 = rng.integers(0, 256, size=(e, 2 * i, h // 2), dtype=np.uint8)
+    s13 = O.bf16_to_bits(rng.uniform(0.005, 0.02, size=(e, 2 * i, h // 128)).astype(np.float32))
+    w2 = rng.integers(0, 256, size=(e, h, i // 2), dtype=np.uint8)
+    s2 = O.bf16_to_bits(rng.uniform(0.005, 0.02, size=(e, h, i // 128)).astype(np.float32))
+    return O.ExpertSource(w13, s13, w2, s2)
+
+
+@pytest.mark.parametrize("clamp", [0.0, 0.3])
+def test_moe_fp32_matches_scalar_loops(clamp):
+    rng = np.random.default_rng(2)
+    e, h, i, t, k = 3, 128, 128, 4, 2
+    src = _tiny_source(rng, e + 1, h, i)
+    x = O.bf16_round(rng.standard_normal((t, h)).astype(np.float32))
+    ids = np.array([[0, 2], [1, 0], [2, 1], [0, 1]])
+    w = rng.uniform(0.1, 1.0, size=(t, k)).astype(np.float32)
+    got = O.moe_fp32(x, ids, w, src, shared_index=e, clamp_limit=clamp)
+    ref = np.zeros((t, h), dtype=np.float64)
+
+    def ffn(tok, ex, weight):
+        w13 = src.w13(ex).astype(np.float64)
+        w2 = src.w2(ex).astype(np.float64)
+        act = np.zeros(i)
+        for n in range(i):
+            g = sum(x[tok, c] * w13[n, c] for c in range(h))
+            u = sum(x[tok, c] * w13[i + n, c] for c in range(h))
+            if clamp > 0:
+                g = min(g, clamp)
+                u = min(max(u, -clamp), clamp)
+            act[n] = g / (1 + np.exp(-g)) * u * weight
+        return np.array([sum(act[n] * w2[m, n] for n in range(i)) for m in range(h)])
+
+    for tok in range(t):
+        for j in range(k):
+            ref[tok] += ffn(tok, ids[tok, j], w[tok, j])
+        ref[tok] += ffn(tok, e, 1.0)
+    np.testing.assert_allclose(got, ref, rtol=2e-4, atol=2e-4 * np.abs(ref).max())
+
+
+def test_moe_fp32_linear_in_route_weights_and_row_subset():
+    rng = np.random.default_rng(3)
+    src = _tiny_source(rng, 4, 256, 128)
+    x = rng.standard_normal((10, 256)).astype(np.float32)
+    ids = np.argsort(rng.random((10, 4)), axis=1)[:, :2]
+    w = rng.uniform(0.1, 1.0, size=(10, 2)).astype(np.float32)
+    y1 = O.moe_fp32(x, ids, w, src)
+    y2 = O.moe_fp32(x, ids, 2 * w, src)
+    np.testing.assert_allclose(y2, 2 * y1, rtol=1e-5, atol=1e-5 * np.abs(y1).max())
+    sub = O.moe_fp32(x, ids, w, src, rows=[3, 7])
+    np.testing.assert_allclose(sub, y1[[3, 7]], rtol=1e-6, atol=1e-6)
+
+
+def test_bf16_mirror_close_to_fp32_oracle():
+    rng = np.random.default_rng(4)
+    src = _tiny_source(rng, 5, 512, 256)
+    x = rng.standard_normal((16, 512)).astype(np.float32)
+    ids = np.argsort(rng.random((16, 4)), axis=1)[:, :2]
+    w = rng.uniform(0.2, 0.8, size=(16, 2)).astype(np.float32)
+    a = O.moe_bf16_mirror(x, ids, w, src, shared_index=4)
+    b = O.moe_fp32(O.bf16_round(x), ids, w, src, shared_index=4)
+    assert O.rel_fro(a, b) < 1e-2
+    np.testing.assert_array_equal(O.bf16_round(a), a)
+    c = O.moe_bf16_mirror(x, ids, w, src, shared_index=4, workers=4)
+    np.testing.assert_array_equal(a, c)
+
+
+def test_w8a16_oracle_and_split_k_policy():
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((3, 256)).astype(np.float32)
+    q = rng.integers(-127, 128, size=(5, 256)).astype(np.int8)
+    s = O.bf16_round(rng.uniform(0.005, 0.02, size=5).astype(np.float32))
+    got = O.w8a16_linear_f32(a, q, O.bf16_to_bits(s))
+    ref = np.array([[sum(float(a[m, c]) * float(q[n, c]) * float(s[n]) for c in range(256))
+                     for n in range(5)] for m in range(3)])
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    # weight_only_linear.py:168-179 with block 32 x 64 (tiles = ceil(m/32)*ceil(n/64), kb = k/128)
+    assert O.automatic_split_k(1, 1024, 4096) == 4      # 16 tiles < 32, 32 K blocks
+    assert O.automatic_split_k(1, 4096, 4096) == 2      # 64 tiles < 96, >= 16 K blocks
+    assert O.automatic_split_k(64, 1024, 4096) == 2     # 32 tiles
+    assert O.automatic_split_k(1, 1024, 2048) == 2      # 16 K blocks only
+    assert O.automatic_split_k(1, 1024, 1024) == 1      # 8 K blocks
+    assert O.automatic_split_k(64, 16384, 4096) == 1
+    assert O.automatic_split_k(8192, 4096, 4096) == 1
