@@ -44,12 +44,13 @@ static ProfileState g_prof;
 
 void prof_stamp(int stamp, hipStream_t stream) {
   if (!g_prof.active || g_prof.call >= g_prof.max_calls) return;
-  hipEventRecord(g_prof.events[(size_t)g_prof.call * kNumStamps + stamp], stream);
+  (void)hipEventRecord(g_prof.events[(size_t)g_prof.call * kNumStamps + stamp], stream);
   if (stamp == kNumStamps - 1) ++g_prof.call;
 }
 
 static void prof_release() {
-  for (hipEvent_t e : g_prof.events) hipEventDestroy(e);
+  for (hipEvent_t e : g_prof.events)
+    if (e != nullptr) (void)hipEventDestroy(e);
   g_prof.events.clear();
   g_prof.active = false;
   g_prof.call = 0;
@@ -281,6 +282,9 @@ static int validate_experts(const uint16_t* x, int64_t tokens, int32_t hidden, i
   const size_t need = dsv4_experts_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0);
   DSV4_REQUIRE(workspace_bytes >= need, "%s: workspace %zu bytes < required %zu", who,
                workspace_bytes, need);
+  const int64_t act_rows = tokens * topk + (has_shared ? tokens : 0);
+  DSV4_REQUIRE(act_rows * (int64_t)(hidden > inter ? hidden : inter) * 4 < 0x7FFFFFFFLL,
+               "%s: activation / intermediate arrays exceed 2 GiB (split the batch)", who);
   const int64_t blocks = (cap + block_size - 1) / block_size;
   const int64_t shared_blocks = has_shared ? (tokens + block_size - 1) / block_size : 0;
   const int64_t tiles = (int64_t)(hidden > inter ? hidden : inter) / 128;

@@ -5,23 +5,34 @@
 // reference torch path (runtime/dsv4_direct/ops/dense_moe.py:336-354):
 //   stage 1: [g | u] = x[rows] . W13^T (fp32 accumulate), h = SiLU(min(g,L)) *
 //            clamp(u,-L,L) in fp32, h rounded to bf16;  also writes the fp32
-//            sum of each row's bf16 h over every 128-wide K group of stage 2;
+//            sum of each row's bf16 h over every 64-wide chunk of stage 2's K;
 //   stage 2: y = h . W2^T (fp32 accumulate) * route_weight, written fp32 per
 //            (token, k) slot (the shared expert uses weight 1);
 //   combine: out[t] = bf16( sum_j y[t*k+j] + y_shared[t] ), one rounding
 //            (moe_runtime.py:1857,1873 with a single fp32 accumulation).
 //
-// Work decomposition.  One workgroup (4 wavefronts) per (expert block of the
-// alignment, 128-row N tile).  The expert block supplies up to 16*C token
-// slots (the MFMA N dimension); each wavefront owns R strips of 16 weight
-// rows (the MFMA M dimension) and walks K one quantisation group at a time:
-// per strip one 16-byte load per lane brings a 16x128 int4 tile, per K step
-// of 32 the lane's dword is widened to 8 biased bf16 values in 5 ALU ops, and
-// the group's partial sums are scaled by the bf16 group scale in fp32.
+// Arithmetic per quantisation group g (128 K values) of weight row n and
+// token column t:  the MFMA sums (q + 136) * x (dequant_biased), the kernel
+// subtracts 136 * sum_g(x) (from the precomputed 64-wide row sums, added in a
+// fixed order) and accumulates s[n, g] * partial in fp32.
+//
+// Two kernels share this arithmetic:
+//  * expert_decode_kernel (alignment blocks of <= 16 token slots): one
+//    workgroup of 4 wavefronts per (expert block, N tile), two 16-row weight
+//    strips per wavefront, weights prefetched two groups ahead, the block's
+//    activations staged group by group in LDS one group ahead, loads issued in
+//    an order that never makes the in-order vmcnt wait on a prefetch;  padded
+//    token slots read zeros through out-of-range buffer loads (no branches in
+//    the K loop).  Shared-expert blocks carry 16 tokens.
+//  * expert_gemm_kernel (larger blocks): C column tiles of 16 tokens, R strips.
 #include "common.h"
 #include "../../include/dsv4moe.h"
 
 namespace dsv4 {
+
+constexpr int kSumChunk = 64;            // granularity of the activation row sums
+constexpr uint32_t kOobOffset = 0x80000000u;  // buffer offset past every resource
+constexpr int kRsrcFlags = 0x00020000;    // raw buffer, gfx950 dword3
 
 struct ExpertGemmParams {
   const uint8_t* wq;     // tiled int4, expert-major
@@ -31,11 +42,13 @@ struct ExpertGemmParams {
   int k_dim;             // K of the weight matrix
   int inter;             // stage 1: first up-projection row
   const uint16_t* act;   // stage 1: x [T][H]; stage 2: h [rows][I]
-  const float* act_gsum; // per-row sums over each K group of `act`
+  int64_t act_rows;      // rows of `act`
+  const float* act_sum;  // [act_rows][k_dim/64] row sums of `act`
   const int32_t* sorted;
   const int32_t* expert_ids;
   const int32_t* ntpp;
   int block_size;
+  int shared_block_size; // token slots per shared-expert block
   int max_blocks;
   int n_tiles;
   int64_t tokens;
@@ -44,11 +57,216 @@ struct ExpertGemmParams {
   float clamp_limit;
   const float* route_w;  // stage 2: [T*k]
   uint16_t* h_out;       // stage 1: [rows][I]
-  float* hsum_out;       // stage 1: [rows][I/128]
+  float* hsum_out;       // stage 1: [rows][I/64]
   float* contrib;        // stage 2: [rows][H]
   int out_cols;          // stage 2: H
 };
 
+struct BlockInfo {
+  int expert;
+  int64_t slot_base;
+  bool shared;
+  bool active;
+};
+
+__device__ __forceinline__ BlockInfo block_info(const ExpertGemmParams& p, int blk) {
+  BlockInfo b;
+  b.shared = blk >= p.max_blocks;
+  b.active = true;
+  if (!b.shared) {
+    const int total = p.ntpp[0];
+    b.active = total > 0 && (int64_t)blk * p.block_size < total;
+    b.expert = b.active ? p.expert_ids[blk] : 0;
+    b.slot_base = (int64_t)blk * p.block_size;
+  } else {
+    b.expert = p.shared_expert;
+    b.slot_base = (int64_t)(blk - p.max_blocks) * p.shared_block_size;
+  }
+  return b;
+}
+
+// Row id (index into h / contrib) of token column `col` of a block, -1 if padded.
+__device__ __forceinline__ int64_t slot_rowid(const ExpertGemmParams& p, const BlockInfo& b, int col,
+                                              int64_t tk) {
+  if (col >= (b.shared ? p.shared_block_size : p.block_size)) return -1;
+  if (!b.shared) {
+    const int32_t f = p.sorted[b.slot_base + col];
+    return (f >= 0 && f < tk) ? (int64_t)f : -1;
+  }
+  const int64_t t = b.slot_base + col;
+  return t < p.tokens ? tk + t : -1;
+}
+
+template <int STAGE>
+__device__ __forceinline__ int64_t act_row_of(int64_t rowid, int64_t tk, int topk) {
+  if (rowid < 0) return -1;
+  if (STAGE == 1) return rowid < tk ? rowid / topk : rowid - tk;
+  return rowid;
+}
+
+__device__ __forceinline__ void scale4(u32x2 sv, float (&sc)[4]) {
+  sc[0] = __uint_as_float(sv[0] << 16);
+  sc[1] = __uint_as_float(sv[0] & 0xFFFF0000u);
+  sc[2] = __uint_as_float(sv[1] << 16);
+  sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
+}
+
+// ------------------------------------------------------------------ decode
+// STAGE 1: wave w owns gate strip n0/16 + w and up strip (inter + n0)/16 + w,
+//          n0 = tile * 64 (one 64-row chunk of h per workgroup).
+// STAGE 2: wave w owns strips (n0 + 32 w)/16 + {0, 1}, n0 = tile * 128.
+// The 16 token slots x 128 K of the current group live in LDS (double
+// buffered, one barrier per group): every thread loads 16 bytes per group,
+// every wavefront reads its four MFMA B fragments with ds_read_b128.
+constexpr int kXsRowBytes = 272;  // 256 B of bf16 + 16 B pad (conflict-free b128 reads)
+
+template <int STAGE>
+__global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) {
+  constexpr int R = 2;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * kXsRowBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tile = blockIdx.x % p.n_tiles;
+  const int blk = blockIdx.x / p.n_tiles;
+  const int64_t tk = p.tokens * p.topk;
+  const BlockInfo b = block_info(p, blk);
+  if (!b.active) return;
+
+  const int64_t rowid = slot_rowid(p, b, lane & 15, tk);
+  const int64_t arow = act_row_of<STAGE>(rowid, tk, p.topk);
+  const int groups = p.k_dim / kGroup;
+  const int sums_per_row = p.k_dim / kSumChunk;
+
+  int n0, strip[R];
+  if (STAGE == 1) {
+    n0 = tile * 64;
+    strip[0] = n0 / 16 + wave;
+    strip[1] = (p.inter + n0) / 16 + wave;
+  } else {
+    n0 = tile * 128;
+    strip[0] = (n0 + 32 * wave) / 16;
+    strip[1] = strip[0] + 1;
+  }
+  const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + lane * 16;
+  const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + 4 * (lane >> 4);
+
+  // Activations and their sums through buffer loads; padded slots read 0.
+  const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act, (short)0, (int)(p.act_rows * p.k_dim * 2), kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act_sum, (short)0, (int)(p.act_rows * sums_per_row * 4), kRsrcFlags);
+  const int ld_slot = threadIdx.x >> 4;  // cooperative group load: slot, 16-byte part
+  const int ld_part = threadIdx.x & 15;
+  const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
+  const uint32_t ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + ld_part * 16) : kOobOffset;
+  const uint32_t sum_base = arow >= 0 ? (uint32_t)(arow * sums_per_row * 4) : kOobOffset;
+  const int ld_lds = ld_slot * kXsRowBytes + ld_part * 16;
+  const int rd_lds = (lane & 15) * kXsRowBytes + 16 * (lane >> 4);
+
+  u32x4 W[3][R];
+  u32x2 S[3][R];
+  float CS[2][2];
+  u32x4 xr;
+
+  auto issue_w = [&](int g, u32x4 (&w)[R], u32x2 (&s)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t t_idx = (int64_t)strip[r] * groups + g;
+      w[r] = load16_nt(wq + (t_idx << 10));
+      s[r] = *reinterpret_cast<const u32x2*>(ws + t_idx * 16);
+    }
+  };
+  auto issue_x = [&](int g, float (&cs)[2]) {
+    xr = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, ld_base + (uint32_t)(g * 256), 0, 0);
+    cs[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 8), 0, 0));
+    cs[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 8 + 4), 0, 0));
+  };
+
+  f32x4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  issue_x(0, CS[0]);
+  issue_w(0, W[0], S[0]);
+  if (groups > 1) issue_w(1, W[1], S[1]);
+  *reinterpret_cast<u32x4*>(&xs[0][ld_lds]) = xr;
+  __syncthreads();
+
+  for (int g0 = 0; g0 < groups; g0 += 6) {
+#pragma unroll
+    for (int u = 0; u < 6; ++u) {
+      const int g = g0 + u;
+      if (g < groups) {
+        if (g + 1 < groups) issue_x(g + 1, CS[(u + 1) & 1]);
+        if (g + 2 < groups) issue_w(g + 2, W[(u + 2) % 3], S[(u + 2) % 3]);
+        const uint8_t* xb = &xs[u & 1][rd_lds];
+        const float corr = kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
+        f32x4 tmp[R];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xb + 64 * d));
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            tmp[r] = mfma_bf16(dequant_biased(W[u % 3][r][d]), bfr,
+                               d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float sc[4];
+          scale4(S[u % 3][r], sc);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * (tmp[r][i] - corr);
+        }
+        if (g + 1 < groups) *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
+        __syncthreads();
+      }
+    }
+  }
+
+  if constexpr (STAGE == 1) {
+    __shared__ float red[4][16];
+    const float lim = p.clamp_limit;
+    uint32_t bits[4];
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float gt = acc[0][i];
+      float up = acc[1][i];
+      if (lim > 0.0f) {
+        gt = fminf(gt, lim);
+        up = fminf(fmaxf(up, -lim), lim);
+      }
+      bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+      part += __uint_as_float(bits[i] << 16);
+    }
+    if (rowid >= 0) {
+      const int n = n0 + 16 * wave + 4 * (lane >> 4);
+      u32x2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+      *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) = packed;
+    }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    if (lane < 16) red[wave][lane] = part;
+    __syncthreads();
+    if (threadIdx.x < 16 && rowid >= 0) {
+      const float total = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+      p.hsum_out[rowid * (p.inter / kSumChunk) + n0 / kSumChunk] = total;
+    }
+  } else {
+    if (rowid >= 0) {
+      const float wr = rowid < tk ? p.route_w[rowid] : 1.0f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int n = n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
+        f32x4 v = acc[r];
+        v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
+        *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ generic
 template <int C, int R, int STAGE>
 __global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
   const int lane = threadIdx.x & 63;
@@ -56,43 +274,19 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
   const int tile = blockIdx.x % p.n_tiles;
   const int blk = blockIdx.x / p.n_tiles;
   const int64_t tk = p.tokens * p.topk;
+  const BlockInfo b = block_info(p, blk);
+  if (!b.active) return;
 
-  int expert;
-  int64_t slot_base;
-  bool shared_blk = blk >= p.max_blocks;
-  if (!shared_blk) {
-    const int total = p.ntpp[0];
-    if (total <= 0 || (int64_t)blk * p.block_size >= total) return;
-    expert = p.expert_ids[blk];
-    slot_base = (int64_t)blk * p.block_size;
-  } else {
-    expert = p.shared_expert;
-    slot_base = (int64_t)(blk - p.max_blocks) * p.block_size;
-  }
-
-  // Token slot of this lane for each column tile.
   int64_t rowid[C];
   int64_t in_row[C];
 #pragma unroll
   for (int ct = 0; ct < C; ++ct) {
-    const int col = ct * 16 + (lane & 15);
-    rowid[ct] = -1;
-    if (col < p.block_size) {
-      if (!shared_blk) {
-        const int32_t f = p.sorted[slot_base + col];
-        if (f >= 0 && f < tk) rowid[ct] = f;
-      } else {
-        const int64_t t = slot_base + col;
-        if (t < p.tokens) rowid[ct] = tk + t;
-      }
-    }
-    if (STAGE == 1)
-      in_row[ct] = rowid[ct] < 0 ? -1 : (rowid[ct] < tk ? rowid[ct] / p.topk : rowid[ct] - tk);
-    else
-      in_row[ct] = rowid[ct];
+    rowid[ct] = slot_rowid(p, b, ct * 16 + (lane & 15), tk);
+    in_row[ct] = act_row_of<STAGE>(rowid[ct], tk, p.topk);
   }
 
   const int groups = p.k_dim / kGroup;
+  const int sums_per_row = p.k_dim / kSumChunk;
   const int n0 = tile * 128;
   int strip[R];
 #pragma unroll
@@ -102,8 +296,8 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
     else
       strip[s] = (n0 + 32 * wave) / 16 + s;
   }
-  const uint8_t* wq = p.wq + (int64_t)expert * p.wq_stride + lane * 16;
-  const uint16_t* ws = p.ws + (int64_t)expert * p.ws_stride + 4 * (lane >> 4);
+  const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + lane * 16;
+  const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + 4 * (lane >> 4);
   const int koff = 8 * (lane >> 4);
 
   f32x4 acc[R][C];
@@ -123,8 +317,13 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
     }
     float corr[C];
 #pragma unroll
-    for (int ct = 0; ct < C; ++ct)
-      corr[ct] = in_row[ct] >= 0 ? kDequantBias * p.act_gsum[in_row[ct] * groups + g] : 0.0f;
+    for (int ct = 0; ct < C; ++ct) {
+      corr[ct] = 0.0f;
+      if (in_row[ct] >= 0) {
+        const float* cs = p.act_sum + in_row[ct] * sums_per_row + 2 * g;
+        corr[ct] = kDequantBias * (cs[0] + cs[1]);
+      }
+    }
 
     f32x4 tmp[R][C];
 #pragma unroll
@@ -147,22 +346,18 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
     }
 #pragma unroll
     for (int s = 0; s < R; ++s) {
-      const float sc0 = __uint_as_float(sv[s][0] << 16);
-      const float sc1 = __uint_as_float(sv[s][0] & 0xFFFF0000u);
-      const float sc2 = __uint_as_float(sv[s][1] << 16);
-      const float sc3 = __uint_as_float(sv[s][1] & 0xFFFF0000u);
+      float sc[4];
+      scale4(sv[s], sc);
 #pragma unroll
-      for (int ct = 0; ct < C; ++ct) {
-        acc[s][ct][0] += sc0 * (tmp[s][ct][0] - corr[ct]);
-        acc[s][ct][1] += sc1 * (tmp[s][ct][1] - corr[ct]);
-        acc[s][ct][2] += sc2 * (tmp[s][ct][2] - corr[ct]);
-        acc[s][ct][3] += sc3 * (tmp[s][ct][3] - corr[ct]);
-      }
+      for (int ct = 0; ct < C; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[s][ct][i] += sc[i] * (tmp[s][ct][i] - corr[ct]);
     }
   }
 
   if constexpr (STAGE == 1) {
-    // SwiGLU epilogue: strips [0, R/2) are gate rows, [R/2, R) the matching up rows.
+    // SwiGLU epilogue: strips [0, R/2) are gate rows, [R/2, R) the matching up
+    // rows; waves 0-1 and 2-3 each cover one 64-row chunk of h.
     __shared__ float red[4][C * 16];
     const float lim = p.clamp_limit;
 #pragma unroll
@@ -194,22 +389,13 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
     }
     __syncthreads();
     if (threadIdx.x < C * 16) {
-      const int ct = threadIdx.x >> 4;
-      const int col = threadIdx.x;  // == ct*16 + lane for lane < 16
-      int64_t rid = -1;
-      if (col < p.block_size) {
-        if (!shared_blk) {
-          const int32_t f = p.sorted[slot_base + col];
-          if (f >= 0 && f < tk) rid = f;
-        } else if (slot_base + col < p.tokens) {
-          rid = tk + slot_base + col;
-        }
-      }
+      const int col = threadIdx.x;
+      const int64_t rid = slot_rowid(p, b, col, tk);
       if (rid >= 0) {
-        const float total = ((red[0][col] + red[1][col]) + red[2][col]) + red[3][col];
-        p.hsum_out[rid * (p.inter / kGroup) + n0 / kGroup] = total;
+        float* dst = p.hsum_out + rid * (p.inter / kSumChunk) + n0 / kSumChunk;
+        dst[0] = red[0][col] + red[1][col];
+        dst[1] = red[2][col] + red[3][col];
       }
-      (void)ct;
     }
   } else {
 #pragma unroll
@@ -227,21 +413,21 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
   }
 }
 
-// Per-row fp32 sums of bf16 activations over each 128-wide K group, summed in
+// Per-row fp32 sums of bf16 activations over each 64-wide K chunk, summed in
 // ascending k order.
-__global__ __launch_bounds__(256) void row_group_sum_kernel(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(256) void row_chunk_sum_kernel(const uint16_t* __restrict__ x,
                                                             int64_t rows, int k_dim,
                                                             float* __restrict__ out) {
-  const int groups = k_dim / kGroup;
+  const int chunks = k_dim / kSumChunk;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= rows * groups) return;
-  const int64_t r = idx / groups;
-  const int g = (int)(idx % groups);
-  const uint16_t* src = x + r * k_dim + g * kGroup;
+  if (idx >= rows * chunks) return;
+  const int64_t r = idx / chunks;
+  const int c = (int)(idx % chunks);
+  const uint16_t* src = x + r * k_dim + c * kSumChunk;
   float s = 0.0f;
-#pragma unroll 4
-  for (int c = 0; c < kGroup; c += 8) {
-    const u32x4 v = load16(src + c);
+#pragma unroll
+  for (int e = 0; e < kSumChunk; e += 8) {
+    const u32x4 v = load16(src + e);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       s += __uint_as_float(v[q] << 16);
@@ -295,11 +481,11 @@ static ExpertWorkspace carve_workspace(void* base, int64_t tokens, int topk, int
   ExpertWorkspace w;
   char* b = static_cast<char*>(base);
   w.xsum = reinterpret_cast<float*>(b + off);
-  off += align256(sizeof(float) * (size_t)tokens * (hidden / kGroup));
+  off += align256(sizeof(float) * (size_t)tokens * (hidden / kSumChunk));
   w.h = reinterpret_cast<uint16_t*>(b + off);
   off += align256(sizeof(uint16_t) * (size_t)rows * inter);
   w.hsum = reinterpret_cast<float*>(b + off);
-  off += align256(sizeof(float) * (size_t)rows * (inter / kGroup));
+  off += align256(sizeof(float) * (size_t)rows * (inter / kSumChunk));
   w.contrib = reinterpret_cast<float*>(b + off);
   off += align256(sizeof(float) * (size_t)rows * hidden);
   w.bytes = off;
@@ -332,14 +518,18 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   if (tokens == 0) return DSV4MOE_OK;
   ExpertWorkspace ws = carve_workspace(workspace, tokens, topk, hidden, inter, has_shared);
   const int max_blocks = (int)((capacity + block_size - 1) / block_size);
-  const int shared_blocks = has_shared ? (int)((tokens + block_size - 1) / block_size) : 0;
+  const bool decode = block_size <= 16;
+  const int shared_bs = decode ? 16 : block_size;
+  const int shared_blocks = has_shared ? (int)((tokens + shared_bs - 1) / shared_bs) : 0;
+  const int blocks = max_blocks + shared_blocks;
   const int C = (block_size + 15) / 16;
+  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
 
   {
-    const int64_t n = tokens * (hidden / kGroup);
-    hipLaunchKernelGGL(row_group_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+    const int64_t n = tokens * (hidden / kSumChunk);
+    hipLaunchKernelGGL(row_chunk_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                        stream, x, tokens, hidden, ws.xsum);
-    DSV4_CHECK_LAUNCH("row_group_sum_kernel");
+    DSV4_CHECK_LAUNCH("row_chunk_sum_kernel");
   }
   dsv4host::prof_stamp(dsv4host::kStampRowSum, stream);
   ExpertGemmParams p{};
@@ -347,6 +537,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.expert_ids = expert_ids;
   p.ntpp = ntpp;
   p.block_size = block_size;
+  p.shared_block_size = shared_bs;
   p.max_blocks = max_blocks;
   p.tokens = tokens;
   p.topk = topk;
@@ -361,12 +552,19 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.ws_stride = (int64_t)2 * inter * (hidden / kGroup);
   p.k_dim = hidden;
   p.act = x;
-  p.act_gsum = ws.xsum;
+  p.act_rows = tokens;
+  p.act_sum = ws.xsum;
   p.h_out = ws.h;
   p.hsum_out = ws.hsum;
-  p.n_tiles = inter / 128;
-  launch_stage<1>(C, p, (unsigned)(p.n_tiles * (max_blocks + shared_blocks)), stream);
-  DSV4_CHECK_LAUNCH("expert_gemm_kernel<stage1>");
+  if (decode) {
+    p.n_tiles = inter / 64;
+    hipLaunchKernelGGL(expert_decode_kernel<1>, dim3((unsigned)(p.n_tiles * blocks)), dim3(256),
+                       0, stream, p);
+  } else {
+    p.n_tiles = inter / 128;
+    launch_stage<1>(C, p, (unsigned)(p.n_tiles * blocks), stream);
+  }
+  DSV4_CHECK_LAUNCH("expert stage 1");
   dsv4host::prof_stamp(dsv4host::kStampStage1, stream);
 
   // stage 2: W2 [H, I]
@@ -376,13 +574,19 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.ws_stride = (int64_t)hidden * (inter / kGroup);
   p.k_dim = inter;
   p.act = ws.h;
-  p.act_gsum = ws.hsum;
+  p.act_rows = rows;
+  p.act_sum = ws.hsum;
   p.route_w = weights;
   p.contrib = ws.contrib;
   p.out_cols = hidden;
   p.n_tiles = hidden / 128;
-  launch_stage<2>(C, p, (unsigned)(p.n_tiles * (max_blocks + shared_blocks)), stream);
-  DSV4_CHECK_LAUNCH("expert_gemm_kernel<stage2>");
+  if (decode) {
+    hipLaunchKernelGGL(expert_decode_kernel<2>, dim3((unsigned)(p.n_tiles * blocks)), dim3(256),
+                       0, stream, p);
+  } else {
+    launch_stage<2>(C, p, (unsigned)(p.n_tiles * blocks), stream);
+  }
+  DSV4_CHECK_LAUNCH("expert stage 2");
   dsv4host::prof_stamp(dsv4host::kStampStage2, stream);
 
   {

@@ -71,14 +71,14 @@ def test_validation_rejects_before_launch():
 
 
 def test_workspace_formula():
-    # x row sums + h + h row sums + fp32 contributions, each 256-byte aligned
+    # x row sums (per 64 columns) + h + h row sums + fp32 contributions, each 256-byte aligned
     t, k, h, i = 64, 6, 4096, 2048
     rows = t * k + t
 
     def a(v):
         return (v + 255) // 256 * 256
 
-    expect = a(4 * t * (h // 128)) + a(2 * rows * i) + a(4 * rows * (i // 128)) + a(4 * rows * h)
+    expect = a(4 * t * (h // 64)) + a(2 * rows * i) + a(4 * rows * (i // 64)) + a(4 * rows * h)
     assert ops.experts_workspace_bytes(t, k, h, i, True) == expect
 
 
