@@ -271,6 +271,8 @@ static int validate_experts(const uint16_t* x, int64_t tokens, int32_t hidden, i
   DSV4_REQUIRE(experts >= 1 && experts <= 1024, "%s: experts must be in [1, 1024]", who);
   DSV4_REQUIRE(topk >= 1 && topk <= experts, "%s: topk must be in [1, experts]", who);
   DSV4_REQUIRE(valid_block_size(block_size), "%s: block_size %d not in {8,16,32,48,64}", who, block_size);
+  DSV4_REQUIRE(block_size <= 16 || hidden % 256 == 0,
+               "%s: block sizes above 16 need hidden %% 256 == 0", who);
   if (tokens == 0) return DSV4MOE_OK;
   const int64_t cap = max_padded(tokens * topk, experts, block_size);
   DSV4_REQUIRE(capacity == cap, "%s: capacity %lld != max_padded_tokens %lld", who,

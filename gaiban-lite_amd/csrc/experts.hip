@@ -24,7 +24,8 @@
 //    an order that never makes the in-order vmcnt wait on a prefetch;  padded
 //    token slots read zeros through out-of-range buffer loads (no branches in
 //    the K loop).  Shared-expert blocks carry 16 tokens.
-//  * expert_gemm_kernel (larger blocks): C column tiles of 16 tokens, R strips.
+//  * expert_prefill_kernel (blocks of 32-64 slots): 64 token slots x 256
+//    weight rows per workgroup, token tiles staged in LDS, XCD-aware order.
 #include "common.h"
 #include "../../include/dsv4moe.h"
 
@@ -266,110 +267,167 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
   }
 }
 
-// ------------------------------------------------------------------ generic
-template <int C, int R, int STAGE>
-__global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
+// ----------------------------------------------------------------- prefill
+// Alignment blocks of up to 64 token slots (block sizes 32/48/64).  Workgroup
+// tile: 64 token slots x 256 weight rows; wavefront w owns 64 rows:
+//   STAGE 1: gate strips (n0 + 32w)/16 + {0,1} and the matching up strips,
+//            n0 = tile * 128 (the workgroup covers h columns [n0, n0+128));
+//   STAGE 2: strips (n0 + 64w)/16 + {0..3}, n0 = tile * 256.
+// Per group the 64 x 128 token tile and its 64 group sums are staged in LDS
+// (double buffered); each wavefront reads 4 B fragments per K step and issues
+// 16 MFMAs.  Work items are dealt out XCD by XCD: item = (block, tile) with
+// blocks assigned round-robin to the 8 XCDs and all tiles of a block run on
+// the XCD that fetched its token rows into L2.
+constexpr int kPfSlots = 64;
+constexpr int kXcds = 8;
+
+template <int STAGE>
+__global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams p, int total_blocks) {
+  constexpr int R = 4;
+  constexpr int C = 4;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kPfSlots * kXsRowBytes];
+  __shared__ float xsum[2][kPfSlots];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int tile = blockIdx.x % p.n_tiles;
-  const int blk = blockIdx.x / p.n_tiles;
+
+  // XCD-aware item assignment (the dispatcher sends workgroup id i to XCD i % 8).
+  const int xcd = blockIdx.x % kXcds;
+  const int j = blockIdx.x / kXcds;
+  const int blk = (j / p.n_tiles) * kXcds + xcd;
+  const int tile = j % p.n_tiles;
+  if (blk >= total_blocks) return;
   const int64_t tk = p.tokens * p.topk;
   const BlockInfo b = block_info(p, blk);
   if (!b.active) return;
 
   int64_t rowid[C];
-  int64_t in_row[C];
 #pragma unroll
-  for (int ct = 0; ct < C; ++ct) {
-    rowid[ct] = slot_rowid(p, b, ct * 16 + (lane & 15), tk);
-    in_row[ct] = act_row_of<STAGE>(rowid[ct], tk, p.topk);
-  }
-
+  for (int ct = 0; ct < C; ++ct) rowid[ct] = slot_rowid(p, b, ct * 16 + (lane & 15), tk);
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
-  const int n0 = tile * 128;
-  int strip[R];
+
+  int n0, strip[R];
+  if (STAGE == 1) {
+    n0 = tile * 128;
+    strip[0] = (n0 + 32 * wave) / 16;
+    strip[1] = strip[0] + 1;
+    strip[2] = (p.inter + n0 + 32 * wave) / 16;
+    strip[3] = strip[2] + 1;
+  } else {
+    n0 = tile * 256;
 #pragma unroll
-  for (int s = 0; s < R; ++s) {
-    if (STAGE == 1)
-      strip[s] = (s < R / 2) ? (n0 + 32 * wave) / 16 + s : (p.inter + n0 + 32 * wave) / 16 + (s - R / 2);
-    else
-      strip[s] = (n0 + 32 * wave) / 16 + s;
+    for (int r = 0; r < R; ++r) strip[r] = (n0 + 64 * wave) / 16 + r;
   }
   const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + lane * 16;
   const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + 4 * (lane >> 4);
-  const int koff = 8 * (lane >> 4);
+
+  // cooperative staging: thread t loads slot t/4, 16-byte parts 4*(t%4)..+3
+  const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act, (short)0, (int)(p.act_rows * p.k_dim * 2), kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act_sum, (short)0, (int)(p.act_rows * sums_per_row * 4), kRsrcFlags);
+  const int ld_slot = threadIdx.x >> 2;
+  const int ld_part = (threadIdx.x & 3) * 4;
+  const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
+  const uint32_t ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + ld_part * 16) : kOobOffset;
+  const uint32_t sum_base = ld_row >= 0 ? (uint32_t)(ld_row * sums_per_row * 4) : kOobOffset;
+  const int ld_lds = ld_slot * kXsRowBytes + ld_part * 16;
+  const bool sum_loader = (threadIdx.x & 3) == 0;
+
+  u32x4 xr[4];
+  float sr[2];
+  auto issue_x = [&](int g) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      xr[q] = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, ld_base + (uint32_t)(g * 256 + q * 16), 0, 0);
+    sr[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 8), 0, 0));
+    sr[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 8 + 4), 0, 0));
+  };
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(&xs[buf][ld_lds + q * 16]) = xr[q];
+    if (sum_loader) xsum[buf][ld_slot] = sr[0] + sr[1];
+  };
+
+  u32x4 W[2][R];
+  u32x2 S[2][R];
+  auto issue_w = [&](int g, u32x4 (&w)[R], u32x2 (&s)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t t_idx = (int64_t)strip[r] * groups + g;
+      w[r] = load16(wq + (t_idx << 10));
+      s[r] = *reinterpret_cast<const u32x2*>(ws + t_idx * 16);
+    }
+  };
 
   f32x4 acc[R][C];
 #pragma unroll
-  for (int s = 0; s < R; ++s)
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int ct = 0; ct < C; ++ct) acc[s][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ct = 0; ct < C; ++ct) acc[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int g = 0; g < groups; ++g) {
-    u32x4 wv[R];
-    u32x2 sv[R];
-#pragma unroll
-    for (int s = 0; s < R; ++s) {
-      const int64_t t_idx = (int64_t)strip[s] * groups + g;
-      wv[s] = load16_nt(wq + (t_idx << 10));
-      sv[s] = *reinterpret_cast<const u32x2*>(ws + t_idx * 16);
-    }
-    float corr[C];
-#pragma unroll
-    for (int ct = 0; ct < C; ++ct) {
-      corr[ct] = 0.0f;
-      if (in_row[ct] >= 0) {
-        const float* cs = p.act_sum + in_row[ct] * sums_per_row + 2 * g;
-        corr[ct] = kDequantBias * (cs[0] + cs[1]);
-      }
-    }
+  issue_x(0);
+  issue_w(0, W[0], S[0]);
+  store_x(0);
+  __syncthreads();
 
-    f32x4 tmp[R][C];
+  const int rd_lds = (lane & 15) * kXsRowBytes + 16 * (lane >> 4);
+  for (int g0 = 0; g0 < groups; g0 += 2) {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      bf16x8 bfr[C];
+    for (int u = 0; u < 2; ++u) {
+      const int g = g0 + u;
+      if (g < groups) {
+        if (g + 1 < groups) {
+          issue_x(g + 1);
+          issue_w(g + 1, W[(u + 1) & 1], S[(u + 1) & 1]);
+        }
+        float corr[C];
 #pragma unroll
-      for (int ct = 0; ct < C; ++ct) {
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (in_row[ct] >= 0)
-          v = load16(p.act + in_row[ct] * p.k_dim + g * kGroup + d * 32 + koff);
-        bfr[ct] = __builtin_bit_cast(bf16x8, v);
+        for (int ct = 0; ct < C; ++ct) corr[ct] = kDequantBias * xsum[u][ct * 16 + (lane & 15)];
+        f32x4 tmp[R][C];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          bf16x8 bfr[C];
+#pragma unroll
+          for (int ct = 0; ct < C; ++ct)
+            bfr[ct] = __builtin_bit_cast(
+                bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][rd_lds + ct * 16 * kXsRowBytes + 64 * d]));
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const bf16x8 a = dequant_biased(W[u][r][d]);
+#pragma unroll
+            for (int ct = 0; ct < C; ++ct)
+              tmp[r][ct] = mfma_bf16(a, bfr[ct], d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[r][ct]);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float sc[4];
+          scale4(S[u][r], sc);
+#pragma unroll
+          for (int ct = 0; ct < C; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * (tmp[r][ct][i] - corr[ct]);
+        }
+        if (g + 1 < groups) store_x((u + 1) & 1);
+        __syncthreads();
       }
-#pragma unroll
-      for (int s = 0; s < R; ++s) {
-        const bf16x8 a = dequant_biased(wv[s][d]);
-#pragma unroll
-        for (int ct = 0; ct < C; ++ct)
-          tmp[s][ct] = mfma_bf16(a, bfr[ct], d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[s][ct]);
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < R; ++s) {
-      float sc[4];
-      scale4(sv[s], sc);
-#pragma unroll
-      for (int ct = 0; ct < C; ++ct)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[s][ct][i] += sc[i] * (tmp[s][ct][i] - corr[ct]);
     }
   }
 
   if constexpr (STAGE == 1) {
-    // SwiGLU epilogue: strips [0, R/2) are gate rows, [R/2, R) the matching up
-    // rows; waves 0-1 and 2-3 each cover one 64-row chunk of h.
     __shared__ float red[4][C * 16];
     const float lim = p.clamp_limit;
 #pragma unroll
     for (int ct = 0; ct < C; ++ct) {
       float part = 0.0f;
 #pragma unroll
-      for (int s = 0; s < R / 2; ++s) {
+      for (int s = 0; s < 2; ++s) {
         uint32_t bits[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float gt = acc[s][ct][i];
-          float up = acc[s + R / 2][ct][i];
+          float up = acc[s + 2][ct][i];
           if (lim > 0.0f) {
             gt = fminf(gt, lim);
             up = fminf(fmaxf(up, -lim), lim);
@@ -403,9 +461,9 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(ExpertGemmParams p) {
       if (rowid[ct] < 0) continue;
       const float wr = rowid[ct] < tk ? p.route_w[rowid[ct]] : 1.0f;
 #pragma unroll
-      for (int s = 0; s < R; ++s) {
-        const int n = n0 + 32 * wave + 16 * s + 4 * (lane >> 4);
-        f32x4 v = acc[s][ct];
+      for (int r = 0; r < R; ++r) {
+        const int n = n0 + 64 * wave + 16 * r + 4 * (lane >> 4);
+        f32x4 v = acc[r][ct];
         v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
         *reinterpret_cast<f32x4*>(p.contrib + rowid[ct] * p.out_cols + n) = v;
       }
@@ -497,17 +555,6 @@ size_t dsv4_experts_workspace_bytes(int64_t tokens, int topk, int hidden, int in
   return carve_workspace(nullptr, tokens, topk, hidden, inter, has_shared).bytes;
 }
 
-template <int STAGE>
-static void launch_stage(int C, const ExpertGemmParams& p, unsigned grid, hipStream_t stream) {
-  constexpr int R = STAGE == 1 ? 4 : 2;
-  switch (C) {
-    case 1: hipLaunchKernelGGL((expert_gemm_kernel<1, R, STAGE>), dim3(grid), dim3(256), 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((expert_gemm_kernel<2, R, STAGE>), dim3(grid), dim3(256), 0, stream, p); break;
-    case 3: hipLaunchKernelGGL((expert_gemm_kernel<3, R, STAGE>), dim3(grid), dim3(256), 0, stream, p); break;
-    default: hipLaunchKernelGGL((expert_gemm_kernel<4, R, STAGE>), dim3(grid), dim3(256), 0, stream, p); break;
-  }
-}
-
 int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int inter,
                               int experts, int topk, const uint8_t* w13q, const uint16_t* w13s,
                               const uint8_t* w2q, const uint16_t* w2s, int has_shared,
@@ -522,7 +569,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   const int shared_bs = decode ? 16 : block_size;
   const int shared_blocks = has_shared ? (int)((tokens + shared_bs - 1) / shared_bs) : 0;
   const int blocks = max_blocks + shared_blocks;
-  const int C = (block_size + 15) / 16;
+  const int xcd_blocks = (blocks + kXcds - 1) / kXcds * kXcds;
   const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
 
   {
@@ -562,7 +609,8 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
                        0, stream, p);
   } else {
     p.n_tiles = inter / 128;
-    launch_stage<1>(C, p, (unsigned)(p.n_tiles * blocks), stream);
+    hipLaunchKernelGGL(expert_prefill_kernel<1>, dim3((unsigned)(p.n_tiles * xcd_blocks)),
+                       dim3(256), 0, stream, p, blocks);
   }
   DSV4_CHECK_LAUNCH("expert stage 1");
   dsv4host::prof_stamp(dsv4host::kStampStage1, stream);
@@ -579,12 +627,14 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.route_w = weights;
   p.contrib = ws.contrib;
   p.out_cols = hidden;
-  p.n_tiles = hidden / 128;
   if (decode) {
+    p.n_tiles = hidden / 128;
     hipLaunchKernelGGL(expert_decode_kernel<2>, dim3((unsigned)(p.n_tiles * blocks)), dim3(256),
                        0, stream, p);
   } else {
-    launch_stage<2>(C, p, (unsigned)(p.n_tiles * blocks), stream);
+    p.n_tiles = hidden / 256;
+    hipLaunchKernelGGL(expert_prefill_kernel<2>, dim3((unsigned)(p.n_tiles * xcd_blocks)),
+                       dim3(256), 0, stream, p, blocks);
   }
   DSV4_CHECK_LAUNCH("expert stage 2");
   dsv4host::prof_stamp(dsv4host::kStampStage2, stream);
