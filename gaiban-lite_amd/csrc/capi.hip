@@ -266,13 +266,11 @@ static int validate_experts(const uint16_t* x, int64_t tokens, int32_t hidden, i
                             int64_t capacity, int32_t block_size, uint16_t* out, void* workspace,
                             size_t workspace_bytes, int32_t has_shared, const char* who) {
   DSV4_REQUIRE(tokens >= 0, "%s: tokens must be >= 0", who);
-  DSV4_REQUIRE(hidden > 0 && hidden % 128 == 0, "%s: hidden=%d must be a positive multiple of 128", who, hidden);
-  DSV4_REQUIRE(inter > 0 && inter % 128 == 0, "%s: inter=%d must be a positive multiple of 128", who, inter);
+  DSV4_REQUIRE(hidden > 0 && hidden % 256 == 0, "%s: hidden=%d must be a positive multiple of 256", who, hidden);
+  DSV4_REQUIRE(inter > 0 && inter % 256 == 0, "%s: inter=%d must be a positive multiple of 256", who, inter);
   DSV4_REQUIRE(experts >= 1 && experts <= 1024, "%s: experts must be in [1, 1024]", who);
   DSV4_REQUIRE(topk >= 1 && topk <= experts, "%s: topk must be in [1, experts]", who);
   DSV4_REQUIRE(valid_block_size(block_size), "%s: block_size %d not in {8,16,32,48,64}", who, block_size);
-  DSV4_REQUIRE(block_size <= 16 || hidden % 256 == 0,
-               "%s: block sizes above 16 need hidden %% 256 == 0", who);
   if (tokens == 0) return DSV4MOE_OK;
   const int64_t cap = max_padded(tokens * topk, experts, block_size);
   DSV4_REQUIRE(capacity == cap, "%s: capacity %lld != max_padded_tokens %lld", who,

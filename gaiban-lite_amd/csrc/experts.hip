@@ -26,6 +26,8 @@
 //    the K loop).  Shared-expert blocks carry 16 tokens.
 //  * expert_prefill_kernel (blocks of 32-64 slots): 64 token slots x 256
 //    weight rows per workgroup, token tiles staged in LDS, XCD-aware order.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/dsv4moe.h"
 
@@ -101,7 +103,7 @@ __device__ __forceinline__ int64_t slot_rowid(const ExpertGemmParams& p, const B
 template <int STAGE>
 __device__ __forceinline__ int64_t act_row_of(int64_t rowid, int64_t tk, int topk) {
   if (rowid < 0) return -1;
-  if (STAGE == 1) return rowid < tk ? rowid / topk : rowid - tk;
+  if (STAGE == 1) return rowid < tk ? (int64_t)((uint32_t)rowid / (uint32_t)topk) : rowid - tk;
   return rowid;
 }
 
@@ -164,8 +166,11 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
   const int ld_lds = ld_slot * kXsRowBytes + ld_part * 16;
   const int rd_lds = (lane & 15) * kXsRowBytes + 16 * (lane >> 4);
 
-  u32x4 W[3][R];
-  u32x2 S[3][R];
+  // Steady state: activations + sums one group ahead (ring 2), weights two
+  // groups ahead (ring 4); prefetch indices are clamped to the last group so
+  // every load is unconditional and the compiler's vmcnt waits stay exact.
+  u32x4 W[4][R];
+  u32x2 S[4][R];
   float CS[2][2];
   u32x4 xr;
 
@@ -189,38 +194,37 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
 
   issue_x(0, CS[0]);
   issue_w(0, W[0], S[0]);
-  if (groups > 1) issue_w(1, W[1], S[1]);
+  issue_w(groups > 1 ? 1 : 0, W[1], S[1]);
   *reinterpret_cast<u32x4*>(&xs[0][ld_lds]) = xr;
   __syncthreads();
 
-  for (int g0 = 0; g0 < groups; g0 += 6) {
+  const int last = groups - 1;
+  for (int g0 = 0; g0 < groups; g0 += 4) {  // groups % 4 == 0 (checked on the host)
 #pragma unroll
-    for (int u = 0; u < 6; ++u) {
+    for (int u = 0; u < 4; ++u) {
       const int g = g0 + u;
-      if (g < groups) {
-        if (g + 1 < groups) issue_x(g + 1, CS[(u + 1) & 1]);
-        if (g + 2 < groups) issue_w(g + 2, W[(u + 2) % 3], S[(u + 2) % 3]);
-        const uint8_t* xb = &xs[u & 1][rd_lds];
-        const float corr = kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
-        f32x4 tmp[R];
+      issue_x(g + 1 < last ? g + 1 : last, CS[(u + 1) & 1]);
+      issue_w(g + 2 < last ? g + 2 : last, W[(u + 2) & 3], S[(u + 2) & 3]);
+      const uint8_t* xb = &xs[u & 1][rd_lds];
+      const float corr = kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
+      f32x4 tmp[R];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xb + 64 * d));
+      for (int d = 0; d < 4; ++d) {
+        const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xb + 64 * d));
 #pragma unroll
-          for (int r = 0; r < R; ++r)
-            tmp[r] = mfma_bf16(dequant_biased(W[u % 3][r][d]), bfr,
-                               d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          float sc[4];
-          scale4(S[u % 3][r], sc);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * (tmp[r][i] - corr);
-        }
-        if (g + 1 < groups) *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
-        __syncthreads();
+        for (int r = 0; r < R; ++r)
+          tmp[r] = mfma_bf16(dequant_biased(W[u][r][d]), bfr,
+                             d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[r]);
       }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float sc[4];
+        scale4(S[u][r], sc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * (tmp[r][i] - corr);
+      }
+      *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
+      __syncthreads();
     }
   }
 
@@ -273,9 +277,9 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
 //   STAGE 1: gate strips (n0 + 32w)/16 + {0,1} and the matching up strips,
 //            n0 = tile * 128 (the workgroup covers h columns [n0, n0+128));
 //   STAGE 2: strips (n0 + 64w)/16 + {0..3}, n0 = tile * 256.
-// Per group the 64 x 128 token tile and its 64 group sums are staged in LDS
-// (double buffered); each wavefront reads 4 B fragments per K step and issues
-// 16 MFMAs.  Work items are dealt out XCD by XCD: item = (block, tile) with
+// Per group the 64 x 128 token tile and its 64 group sums are copied into LDS
+// by buffer_load ... lds (double buffered, one group ahead); each wavefront
+// reads 4 B fragments per K step and issues 16 MFMAs.  Work items are dealt out XCD by XCD: item = (block, tile) with
 // blocks assigned round-robin to the 8 XCDs and all tiles of a block run on
 // the XCD that fetched its token rows into L2.
 constexpr int kPfSlots = 64;
@@ -285,8 +289,18 @@ template <int STAGE>
 __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams p, int total_blocks) {
   constexpr int R = 4;
   constexpr int C = 4;
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kPfSlots * kXsRowBytes];
-  __shared__ float xsum[2][kPfSlots];
+  // Per group, copied into LDS by buffer_load ... lds (double buffered):
+  //  * token tile: 64 slots x 256 B, 16-byte part p of slot s stored at part
+  //    p ^ (s & 15) (conflict-free ds_read_b128 of the B fragments);
+  //  * the 64 slots' two 64-wide activation sums;
+  //  * each wavefront's 4 weight tiles (4 KiB) and their 16-row scales (128 B).
+  // Padded slots read zeros (out-of-range buffer offsets).
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kPfSlots * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * kTileBytes];
+  // 64 lanes x 4 B per scale DMA: lanes 0..31 carry the 4 strips' 32-byte
+  // rows, lanes 32..63 write zeros into the upper half of the 256-byte slot.
+  __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];
+  __shared__ float xsum[2][2][kPfSlots];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
@@ -300,63 +314,70 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   const BlockInfo b = block_info(p, blk);
   if (!b.active) return;
 
-  int64_t rowid[C];
-#pragma unroll
-  for (int ct = 0; ct < C; ++ct) rowid[ct] = slot_rowid(p, b, ct * 16 + (lane & 15), tk);
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
 
-  int n0, strip[R];
+  int n0, strip0, strip2;
   if (STAGE == 1) {
     n0 = tile * 128;
-    strip[0] = (n0 + 32 * wave) / 16;
-    strip[1] = strip[0] + 1;
-    strip[2] = (p.inter + n0 + 32 * wave) / 16;
-    strip[3] = strip[2] + 1;
+    strip0 = (n0 + 32 * wave) / 16;
+    strip2 = (p.inter + n0 + 32 * wave) / 16;
   } else {
     n0 = tile * 256;
-#pragma unroll
-    for (int r = 0; r < R; ++r) strip[r] = (n0 + 64 * wave) / 16 + r;
+    strip0 = (n0 + 64 * wave) / 16;
+    strip2 = strip0 + 2;
   }
-  const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + lane * 16;
-  const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + 4 * (lane >> 4);
+  // wavefront strips r = 0..3: strip0, strip0 + 1, strip2, strip2 + 1
 
-  // cooperative staging: thread t loads slot t/4, 16-byte parts 4*(t%4)..+3
   const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.act, (short)0, (int)(p.act_rows * p.k_dim * 2), kRsrcFlags);
   const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.act_sum, (short)0, (int)(p.act_rows * sums_per_row * 4), kRsrcFlags);
-  const int ld_slot = threadIdx.x >> 2;
-  const int ld_part = (threadIdx.x & 3) * 4;
-  const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
-  const uint32_t ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + ld_part * 16) : kOobOffset;
-  const uint32_t sum_base = ld_row >= 0 ? (uint32_t)(ld_row * sums_per_row * 4) : kOobOffset;
-  const int ld_lds = ld_slot * kXsRowBytes + ld_part * 16;
-  const bool sum_loader = (threadIdx.x & 3) == 0;
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.wq + (int64_t)b.expert * p.wq_stride), (short)0, (int)p.wq_stride, kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.ws + (int64_t)b.expert * p.ws_stride), (short)0, (int)(p.ws_stride * 2), kRsrcFlags);
 
-  u32x4 xr[4];
-  float sr[2];
-  auto issue_x = [&](int g) {
+  // token tile: DMA q (0..3) of wave w fills LDS rows 16w + 4q + lane/16
+  uint32_t dma_off[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = 16 * wave + 4 * q + (lane >> 4);
+    const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, row, tk), tk, p.topk);
+    const int part = (lane & 15) ^ (row & 15);
+    dma_off[q] = ar >= 0 ? (uint32_t)(ar * p.k_dim * 2 + part * 16) : kOobOffset;
+  }
+  uint32_t sum_off = kOobOffset;
+  if (wave == 0) {
+    const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, lane, tk), tk, p.topk);
+    if (ar >= 0) sum_off = (uint32_t)(ar * sums_per_row * 4);
+  }
+  // weight tiles: (strip r, group g) at byte (strip * groups + g) * 1 KiB
+  const uint32_t w_off0 = (uint32_t)(strip0 * groups) * kTileBytes + lane * 16;
+  const uint32_t w_off2 = (uint32_t)(strip2 * groups) * kTileBytes + lane * 16;
+  const uint32_t w_next = (uint32_t)groups * kTileBytes;
+  // scales: lanes 0..31 copy 4 bytes each of the 4 strips' 32-byte rows
+  const int s_strip = (lane >> 3) & 3;
+  const int s_base_strip = (s_strip < 2 ? strip0 : strip2) + (s_strip & 1);
+  const uint32_t s_off = lane < 32 ? (uint32_t)(s_base_strip * groups) * 32 + (lane & 7) * 4 : kOobOffset;
+
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  auto issue = [&](int g, int buf) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      xr[q] = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, ld_base + (uint32_t)(g * 256 + q * 16), 0, 0);
-    sr[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 8), 0, 0));
-    sr[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 8 + 4), 0, 0));
-  };
-  auto store_x = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4*>(&xs[buf][ld_lds + q * 16]) = xr[q];
-    if (sum_loader) xsum[buf][ld_slot] = sr[0] + sr[1];
-  };
-
-  u32x4 W[2][R];
-  u32x2 S[2][R];
-  auto issue_w = [&](int g, u32x4 (&w)[R], u32x2 (&s)[R]) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t t_idx = (int64_t)strip[r] * groups + g;
-      w[r] = load16(wq + (t_idx << 10));
-      s[r] = *reinterpret_cast<const u32x2*>(ws + t_idx * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(act_rsrc, (lds_ptr)&xs[buf][(16 * wave + 4 * q) * 256], 16,
+                                               dma_off[q], g * 256, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][0], 16, w_off0, g * kTileBytes, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][kTileBytes], 16, w_off0 + w_next,
+                                             g * kTileBytes, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][2 * kTileBytes], 16, w_off2,
+                                             g * kTileBytes, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][3 * kTileBytes], 16, w_off2 + w_next,
+                                             g * kTileBytes, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_ptr)&scl[buf][wave][0], 4, s_off, g * 32, 0, 0);
+    if (wave == 0) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sum_rsrc, (lds_ptr)&xsum[buf][0][0], 4, sum_off, g * 8, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sum_rsrc, (lds_ptr)&xsum[buf][1][0], 4, sum_off, g * 8 + 4, 0, 0);
     }
   };
 
@@ -366,60 +387,71 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
 #pragma unroll
     for (int ct = 0; ct < C; ++ct) acc[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  issue_x(0);
-  issue_w(0, W[0], S[0]);
-  store_x(0);
-  __syncthreads();
-
-  const int rd_lds = (lane & 15) * kXsRowBytes + 16 * (lane >> 4);
-  for (int g0 = 0; g0 < groups; g0 += 2) {
+  const int sw = lane & 15;  // swizzle key of this lane's slots (ct*16 + sw)
+  // One group: optionally prefetch group g+1 into the other buffers, then
+  // 64 MFMAs and the fp32 group scaling.
+  auto step = [&](int g, auto u_c, auto prefetch_c) {
+    constexpr int u = decltype(u_c)::value;
+    if constexpr (decltype(prefetch_c)::value) issue(g + 1, (u + 1) & 1);
+    u32x4 wv[R];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int g = g0 + u;
-      if (g < groups) {
-        if (g + 1 < groups) {
-          issue_x(g + 1);
-          issue_w(g + 1, W[(u + 1) & 1], S[(u + 1) & 1]);
-        }
-        float corr[C];
+    for (int r = 0; r < R; ++r)
+      wv[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]);
+    f32x4 tmp[R][C];
 #pragma unroll
-        for (int ct = 0; ct < C; ++ct) corr[ct] = kDequantBias * xsum[u][ct * 16 + (lane & 15)];
-        f32x4 tmp[R][C];
+    for (int d = 0; d < 4; ++d) {
+      const int part = ((4 * d + (lane >> 4)) ^ sw) * 16;
+      bf16x8 bfr[C];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          bf16x8 bfr[C];
+      for (int ct = 0; ct < C; ++ct)
+        bfr[ct] = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][(ct * 16 + sw) * 256 + part]));
 #pragma unroll
-          for (int ct = 0; ct < C; ++ct)
-            bfr[ct] = __builtin_bit_cast(
-                bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][rd_lds + ct * 16 * kXsRowBytes + 64 * d]));
+      for (int r = 0; r < R; ++r) {
+        const bf16x8 a = dequant_biased(wv[r][d]);
 #pragma unroll
-          for (int r = 0; r < R; ++r) {
-            const bf16x8 a = dequant_biased(W[u][r][d]);
-#pragma unroll
-            for (int ct = 0; ct < C; ++ct)
-              tmp[r][ct] = mfma_bf16(a, bfr[ct], d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[r][ct]);
-          }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          float sc[4];
-          scale4(S[u][r], sc);
-#pragma unroll
-          for (int ct = 0; ct < C; ++ct)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * (tmp[r][ct][i] - corr[ct]);
-        }
-        if (g + 1 < groups) store_x((u + 1) & 1);
-        __syncthreads();
+        for (int ct = 0; ct < C; ++ct)
+          tmp[r][ct] = mfma_bf16(a, bfr[ct], d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[r][ct]);
       }
     }
+    float corr[C];
+#pragma unroll
+    for (int ct = 0; ct < C; ++ct)
+      corr[ct] = kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const u32x2 sv = *reinterpret_cast<const u32x2*>(&scl[u][wave][r * 32 + 8 * (lane >> 4)]);
+      float sc[4];
+      scale4(sv, sc);
+#pragma unroll
+      for (int ct = 0; ct < C; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * (tmp[r][ct][i] - corr[ct]);
+    }
+    __syncthreads();
+  };
+  using U0 = std::integral_constant<int, 0>;
+  using U1 = std::integral_constant<int, 1>;
+  using PF = std::true_type;
+  using NOPF = std::false_type;
+
+  issue(0, 0);
+  __syncthreads();
+  // groups is even (checked on the host); the last group issues no prefetch,
+  // so no LDS DMA is in flight when the workgroup leaves the loop.
+  for (int g0 = 0; g0 + 2 < groups; g0 += 2) {
+    step(g0, U0{}, PF{});
+    step(g0 + 1, U1{}, PF{});
   }
+  step(groups - 2, U0{}, PF{});
+  step(groups - 1, U1{}, NOPF{});
 
   if constexpr (STAGE == 1) {
     __shared__ float red[4][C * 16];
     const float lim = p.clamp_limit;
 #pragma unroll
     for (int ct = 0; ct < C; ++ct) {
+      const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
       float part = 0.0f;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
@@ -435,10 +467,10 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
           bits[i] = float_to_bf16_bits(silu_f(gt) * up);
           part += __uint_as_float(bits[i] << 16);
         }
-        if (rowid[ct] >= 0) {
+        if (rowid >= 0) {
           const int n = n0 + 32 * wave + 16 * s + 4 * (lane >> 4);
           u32x2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
-          *reinterpret_cast<u32x2*>(p.h_out + rowid[ct] * p.inter + n) = packed;
+          *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) = packed;
         }
       }
       part += __shfl_xor(part, 16, 64);
@@ -458,14 +490,15 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   } else {
 #pragma unroll
     for (int ct = 0; ct < C; ++ct) {
-      if (rowid[ct] < 0) continue;
-      const float wr = rowid[ct] < tk ? p.route_w[rowid[ct]] : 1.0f;
+      const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
+      if (rowid < 0) continue;
+      const float wr = rowid < tk ? p.route_w[rowid] : 1.0f;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int n = n0 + 64 * wave + 16 * r + 4 * (lane >> 4);
         f32x4 v = acc[r][ct];
         v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
-        *reinterpret_cast<f32x4*>(p.contrib + rowid[ct] * p.out_cols + n) = v;
+        *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
       }
     }
   }
@@ -565,7 +598,8 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   if (tokens == 0) return DSV4MOE_OK;
   ExpertWorkspace ws = carve_workspace(workspace, tokens, topk, hidden, inter, has_shared);
   const int max_blocks = (int)((capacity + block_size - 1) / block_size);
-  const bool decode = block_size <= 16;
+  // decode kernel: blocks of <= 16 slots and K groups in multiples of 4
+  const bool decode = block_size <= 16 && hidden % 512 == 0 && inter % 512 == 0;
   const int shared_bs = decode ? 16 : block_size;
   const int shared_blocks = has_shared ? (int)((tokens + shared_bs - 1) / shared_bs) : 0;
   const int blocks = max_blocks + shared_blocks;

@@ -67,8 +67,8 @@ class TP4MoEConfig:
             )
         for name in ("hidden_size", "intermediate_size"):
             value = getattr(self, name)
-            if not isinstance(value, int) or value <= 0 or value % 128:
-                raise ValueError(f"{name} must be a positive multiple of 128")
+            if not isinstance(value, int) or value <= 0 or value % 256:
+                raise ValueError(f"{name} must be a positive multiple of 256")
         if not isinstance(self.experts, int) or not 1 <= self.experts <= 1024:
             raise ValueError("experts must be in [1, 1024]")
         if not isinstance(self.topk, int) or not 1 <= self.topk < self.experts or self.topk > 16:

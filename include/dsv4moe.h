@@ -162,7 +162,7 @@ size_t dsv4moe_experts_workspace_bytes(int64_t tokens, int32_t topk, int32_t hid
  *   sorted_token_ids / expert_ids / num_tokens_post_padded: dsv4moe_align output
  *   clamp_limit > 0: gate = min(gate, L), up = clamp(up, -L, L) before SiLU(gate)*up
  *   out      bf16 [tokens, hidden] = bf16( sum_j routed_j + shared ), fp32 accumulation
- * hidden % 128 == 0, inter % 128 == 0, block_size in {8,16,32,48,64}.
+ * hidden % 256 == 0, inter % 256 == 0, block_size in {8,16,32,48,64}.
  */
 int dsv4moe_experts_w4a16(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
                           int32_t experts, int32_t topk, const uint8_t* w13q,
