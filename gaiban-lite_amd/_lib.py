@@ -18,6 +18,8 @@ DSV4MOE_EINVAL = 1
 DSV4MOE_EHIP = 2
 
 SCORE_FUNCS = {"sigmoid": 0, "softmax": 1, "sqrtsoftplus": 2}
+PAIR_PLAIN = 0
+PAIR_GATED = 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -40,7 +42,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_route_hash": (ctypes.c_int, [_p, _p, _i64, _p, _i64, _i32, _i32, _f32, _p, _p, _p, _p]),
     "dsv4moe_gate_logits": (ctypes.c_int, [_p, _p, _i64, _i32, _i32, _p, _p]),
     "dsv4moe_align": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p]),
-    "dsv4moe_pack_int4_g128": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
+    "dsv4moe_pack_int4_g128": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p]),
     "dsv4moe_experts_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "dsv4moe_experts_w4a16": (
         ctypes.c_int,

@@ -68,7 +68,7 @@ int dsv4_launch_gate_logits(const uint16_t*, const uint16_t*, int64_t, int, int,
                             hipStream_t);
 int dsv4_launch_align(const int32_t*, int64_t, int32_t, int32_t, int32_t*, int64_t, int32_t*,
                       int64_t, int32_t*, hipStream_t);
-int dsv4_launch_pack(const uint8_t*, const uint16_t*, int64_t, int64_t, int64_t, uint8_t*,
+int dsv4_launch_pack(const uint8_t*, const uint16_t*, int64_t, int64_t, int64_t, int, uint8_t*,
                      uint16_t*, hipStream_t);
 size_t dsv4_experts_workspace_bytes(int64_t, int, int, int, int);
 int dsv4_launch_experts_w4a16(const uint16_t*, int64_t, int, int, int, int, const uint8_t*,
@@ -241,16 +241,18 @@ int dsv4moe_align(const int32_t* ids, int64_t tokens, int32_t topk, int32_t expe
 }
 
 int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, int64_t batch,
-                           int64_t n, int64_t k, uint8_t* packed, uint16_t* packed_scales,
-                           void* stream) {
+                           int64_t n, int64_t k, int32_t pairing, uint8_t* packed,
+                           uint16_t* packed_scales, void* stream) {
   clear_error();
   DSV4_REQUIRE(batch >= 0 && n >= 0 && k >= 0, "pack: negative size");
-  DSV4_REQUIRE(n % 16 == 0, "pack: n=%lld must be a multiple of 16", (long long)n);
+  DSV4_REQUIRE(n % 32 == 0, "pack: n=%lld must be a multiple of 32", (long long)n);
+  DSV4_REQUIRE(pairing == DSV4MOE_PAIR_PLAIN || pairing == DSV4MOE_PAIR_GATED,
+               "pack: unknown pairing %d", pairing);
   DSV4_REQUIRE(k % DSV4MOE_GROUP == 0, "pack: k=%lld must be a multiple of 128", (long long)k);
   if (batch == 0 || n == 0 || k == 0) return DSV4MOE_OK;
   DSV4_REQUIRE(canon && canon_scales && packed && packed_scales, "pack: null pointer");
   DSV4_REQUIRE(aligned(canon, 4) && aligned(packed, 16), "pack: canon 4-byte / packed 16-byte alignment required");
-  return dsv4_launch_pack(canon, canon_scales, batch, n, k, packed, packed_scales,
+  return dsv4_launch_pack(canon, canon_scales, batch, n, k, pairing, packed, packed_scales,
                           static_cast<hipStream_t>(stream));
 }
 

@@ -140,18 +140,12 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
 
-  int n0, strip[R];
-  if (STAGE == 1) {
-    n0 = tile * 64;
-    strip[0] = n0 / 16 + wave;
-    strip[1] = (p.inter + n0) / 16 + wave;
-  } else {
-    n0 = tile * 128;
-    strip[0] = (n0 + 32 * wave) / 16;
-    strip[1] = strip[0] + 1;
-  }
-  const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + lane * 16;
-  const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + 4 * (lane >> 4);
+  // wavefront w streams strip pair tile*4 + w: stage 1 gate + up strip
+  // (h columns n0 + 16w ..), stage 2 strips (n0 + 32w)/16 + {0, 1}
+  const int n0 = STAGE == 1 ? tile * 64 : tile * 128;
+  const int pair = tile * 4 + wave;
+  const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
+  const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
 
   // Activations and their sums through buffer loads; padded slots read 0.
   const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -170,17 +164,14 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
   // groups ahead (ring 4); prefetch indices are clamped to the last group so
   // every load is unconditional and the compiler's vmcnt waits stay exact.
   u32x4 W[4][R];
-  u32x2 S[4][R];
+  u32x4 S[4];
   float CS[2][2];
   u32x4 xr;
 
-  auto issue_w = [&](int g, u32x4 (&w)[R], u32x2 (&s)[R]) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t t_idx = (int64_t)strip[r] * groups + g;
-      w[r] = load16_nt(wq + (t_idx << 10));
-      s[r] = *reinterpret_cast<const u32x2*>(ws + t_idx * 16);
-    }
+  auto issue_w = [&](int g, u32x4 (&w)[R], u32x4& s) {
+    w[0] = load16_nt(wq + g * 2048);
+    w[1] = load16_nt(wq + g * 2048 + 1024);
+    s = load16(ws + g * 32);  // 4 rows of both members
   };
   auto issue_x = [&](int g, float (&cs)[2]) {
     xr = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, ld_base + (uint32_t)(g * 256), 0, 0);
@@ -219,7 +210,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float sc[4];
-        scale4(S[u][r], sc);
+        scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * (tmp[r][i] - corr);
       }
@@ -297,8 +288,8 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   // Padded slots read zeros (out-of-range buffer offsets).
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kPfSlots * 256];
   __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * kTileBytes];
-  // 64 lanes x 4 B per scale DMA: lanes 0..31 carry the 4 strips' 32-byte
-  // rows, lanes 32..63 write zeros into the upper half of the 256-byte slot.
+  // 64 lanes x 4 B per scale DMA: lanes 0..31 carry the two pairs' 64-byte
+  // blocks, lanes 32..63 write zeros into the upper half of the 256-byte slot.
   __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];
   __shared__ float xsum[2][2][kPfSlots];
   const int lane = threadIdx.x & 63;
@@ -317,17 +308,11 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
 
-  int n0, strip0, strip2;
-  if (STAGE == 1) {
-    n0 = tile * 128;
-    strip0 = (n0 + 32 * wave) / 16;
-    strip2 = (p.inter + n0 + 32 * wave) / 16;
-  } else {
-    n0 = tile * 256;
-    strip0 = (n0 + 64 * wave) / 16;
-    strip2 = strip0 + 2;
-  }
-  // wavefront strips r = 0..3: strip0, strip0 + 1, strip2, strip2 + 1
+  // wavefront w streams strip pairs p0 = tile*8 + 2w and p0 + 1; its strips
+  // r = 2j + m are member m of pair p0 + j.  Stage 1: gate (m = 0) and up
+  // (m = 1) rows of h columns n0 + 32w + 16j ..; stage 2: rows n0 + 64w + 16r.
+  const int n0 = STAGE == 1 ? tile * 128 : tile * 256;
+  const int p0 = tile * 8 + 2 * wave;
 
   const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.act, (short)0, (int)(p.act_rows * p.k_dim * 2), kRsrcFlags);
@@ -352,14 +337,11 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
     const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, lane, tk), tk, p.topk);
     if (ar >= 0) sum_off = (uint32_t)(ar * sums_per_row * 4);
   }
-  // weight tiles: (strip r, group g) at byte (strip * groups + g) * 1 KiB
-  const uint32_t w_off0 = (uint32_t)(strip0 * groups) * kTileBytes + lane * 16;
-  const uint32_t w_off2 = (uint32_t)(strip2 * groups) * kTileBytes + lane * 16;
-  const uint32_t w_next = (uint32_t)groups * kTileBytes;
-  // scales: lanes 0..31 copy 4 bytes each of the 4 strips' 32-byte rows
-  const int s_strip = (lane >> 3) & 3;
-  const int s_base_strip = (s_strip < 2 ? strip0 : strip2) + (s_strip & 1);
-  const uint32_t s_off = lane < 32 ? (uint32_t)(s_base_strip * groups) * 32 + (lane & 7) * 4 : kOobOffset;
+  // weight tiles: pair p, group g, member m at byte ((p*groups + g)*2 + m) * 1 KiB
+  const uint32_t w_off0 = (uint32_t)(p0 * groups) * 2048 + lane * 16;
+  const uint32_t w_off1 = (uint32_t)((p0 + 1) * groups) * 2048 + lane * 16;
+  // scales: 64 bytes per (pair, group); lanes 0..31 copy 4 bytes each of both pairs
+  const uint32_t s_off = lane < 32 ? (uint32_t)((p0 + (lane >> 4)) * groups) * 64 + (lane & 15) * 4 : kOobOffset;
 
   typedef __attribute__((address_space(3))) void* lds_ptr;
   auto issue = [&](int g, int buf) {
@@ -367,14 +349,14 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
     for (int q = 0; q < 4; ++q)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(act_rsrc, (lds_ptr)&xs[buf][(16 * wave + 4 * q) * 256], 16,
                                                dma_off[q], g * 256, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][0], 16, w_off0, g * kTileBytes, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][kTileBytes], 16, w_off0 + w_next,
-                                             g * kTileBytes, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][2 * kTileBytes], 16, w_off2,
-                                             g * kTileBytes, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][3 * kTileBytes], 16, w_off2 + w_next,
-                                             g * kTileBytes, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_ptr)&scl[buf][wave][0], 4, s_off, g * 32, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][0], 16, w_off0, g * 2048, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][kTileBytes], 16, w_off0 + kTileBytes,
+                                             g * 2048, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][2 * kTileBytes], 16, w_off1,
+                                             g * 2048, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][3 * kTileBytes], 16, w_off1 + kTileBytes,
+                                             g * 2048, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_ptr)&scl[buf][wave][0], 4, s_off, g * 64, 0, 0);
     if (wave == 0) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(sum_rsrc, (lds_ptr)&xsum[buf][0][0], 4, sum_off, g * 8, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(sum_rsrc, (lds_ptr)&xsum[buf][1][0], 4, sum_off, g * 8 + 4, 0, 0);
@@ -420,7 +402,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
       corr[ct] = kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const u32x2 sv = *reinterpret_cast<const u32x2*>(&scl[u][wave][r * 32 + 8 * (lane >> 4)]);
+      const u32x2 sv = *reinterpret_cast<const u32x2*>(&scl[u][wave][(r >> 1) * 64 + 16 * (lane >> 4) + 8 * (r & 1)]);
       float sc[4];
       scale4(sv, sc);
 #pragma unroll
@@ -458,8 +440,8 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
         uint32_t bits[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float gt = acc[s][ct][i];
-          float up = acc[s + 2][ct][i];
+          float gt = acc[2 * s][ct][i];
+          float up = acc[2 * s + 1][ct][i];
           if (lim > 0.0f) {
             gt = fminf(gt, lim);
             up = fminf(fmaxf(up, -lim), lim);

@@ -164,9 +164,11 @@ def align_into(
     )
 
 
-def pack_int4_g128(canon: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def pack_int4_g128(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = False
+                   ) -> tuple[torch.Tensor, torch.Tensor]:
     """Checkpoint-layout int4 [.., n, k/2] u8 + bf16 scales [.., n, k/128] ->
-    tiled (packed u8 [.., n*k/2], scales bf16 [.., n/16, k/128, 16])."""
+    pair-interleaved tiles (packed u8 [.., n*k/2], scales bf16 [.., n*k/128]).
+    ``gated`` pairs row strip p with strip p of the second half (w13 gate/up)."""
 
     if canon.ndim == 2:
         canon = canon.unsqueeze(0)
@@ -180,9 +182,10 @@ def pack_int4_g128(canon: torch.Tensor, scales: torch.Tensor) -> tuple[torch.Ten
     _check("canon", canon, dtype=torch.uint8, device=dev)
     _check("scales", scales, dtype=torch.bfloat16, shape=(batch, n, k // GROUP), device=dev)
     packed = torch.empty((batch, n * half_k), dtype=torch.uint8, device=dev)
-    packed_scales = torch.empty((batch, n // 16, k // GROUP, 16), dtype=torch.bfloat16, device=dev)
-    call("dsv4moe_pack_int4_g128", ptr(canon), ptr(scales), batch, n, k, ptr(packed),
-         ptr(packed_scales), _lib.current_stream(dev))
+    packed_scales = torch.empty((batch, n * (k // GROUP)), dtype=torch.bfloat16, device=dev)
+    call("dsv4moe_pack_int4_g128", ptr(canon), ptr(scales), batch, n, k,
+         _lib.PAIR_GATED if gated else _lib.PAIR_PLAIN, ptr(packed), ptr(packed_scales),
+         _lib.current_stream(dev))
     if squeeze:
         return packed[0], packed_scales[0]
     return packed, packed_scales

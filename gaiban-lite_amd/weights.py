@@ -7,11 +7,13 @@ stacked over the expert axis, repacked once at load time by the HIP packer
 expert, when present, is stored as expert index ``experts`` in the same arrays
 and runs inside the same grouped kernels with route weight 1.
 
-Layout per expert (H = hidden, I = intermediate):
-  w13_q  uint8 [E', I*H]        tiles of W13 [2I, H] (rows [0,I) gate w1, [I,2I) up w3)
-  w13_s  bf16  [E', 2I/16, H/128, 16]
-  w2_q   uint8 [E', H*I/2]      tiles of W2 [H, I]
-  w2_s   bf16  [E', H/16, I/128, 16]
+Layout per expert (H = hidden, I = intermediate), pair-interleaved tiles of
+16 rows x 128 K (see ``include/dsv4moe.h``, ``dsv4moe_pack_int4_g128``):
+  w13_q  uint8 [E', I*H]        W13 [2I, H] (rows [0,I) gate w1, [I,2I) up w3),
+                                gate strip p paired with up strip p
+  w13_s  bf16  [E', 2I*H/128]
+  w2_q   uint8 [E', H*I/2]      W2 [H, I], strips 2p and 2p+1 paired
+  w2_s   bf16  [E', H*I/128]
 with E' = experts + (1 if shared).
 """
 
@@ -65,9 +67,9 @@ class ResidentInt4MoEWeights:
             raise ValueError("hidden and intermediate sizes must be multiples of 128")
         expected = {
             "w13_q": ((e_tot, i * h), torch.uint8),
-            "w13_s": ((e_tot, 2 * i // 16, h // GROUP, 16), torch.bfloat16),
+            "w13_s": ((e_tot, 2 * i * (h // GROUP)), torch.bfloat16),
             "w2_q": ((e_tot, h * i // 2), torch.uint8),
-            "w2_s": ((e_tot, h // 16, i // GROUP, 16), torch.bfloat16),
+            "w2_s": ((e_tot, h * (i // GROUP)), torch.bfloat16),
         }
         for name, (shape, dtype) in expected.items():
             t = getattr(self, name)
@@ -103,8 +105,8 @@ class ResidentInt4MoEWeights:
             raise ValueError("w2_packed must be [E', H, I/2] matching w13_packed")
         if e_tot != experts + (1 if has_shared else 0):
             raise ValueError("expert count does not match the stacked tensors")
-        q13, s13 = ops.pack_int4_g128(w13_packed.contiguous(), w13_scale.contiguous())
-        q2, s2 = ops.pack_int4_g128(w2_packed.contiguous(), w2_scale.contiguous())
+        q13, s13 = ops.pack_int4_g128(w13_packed.contiguous(), w13_scale.contiguous(), gated=True)
+        q2, s2 = ops.pack_int4_g128(w2_packed.contiguous(), w2_scale.contiguous(), gated=False)
         out = cls(q13, s13, q2, s2, experts, hidden, inter, has_shared, layer_id, checkpoint_id,
                   marlin_input_dtype)
         out.validate()

@@ -130,18 +130,24 @@ int dsv4moe_align(const int32_t* ids, int64_t tokens, int32_t topk, int32_t expe
                   void* stream);
 
 /*
- * Repack int4 group-128 weights from the checkpoint layout into the tiled
- * layout the expert kernels stream.  Replaces the load-time Marlin repack
- * (runtime/dsv4_direct/ops/marlin_moe.py:173-223).
+ * Repack int4 group-128 weights from the checkpoint layout into the
+ * pair-interleaved tiled layout the expert kernels stream.  Replaces the
+ * load-time Marlin repack (runtime/dsv4_direct/ops/marlin_moe.py:173-223).
  *   canon        uint8 [batch, n, k/2]   (low nibble = even k, two's complement)
  *   canon_scales bf16  [batch, n, k/128]
- *   packed       uint8 [batch, n*k/2]     out (tiles of 16 rows x 128 k, 1 KiB each)
- *   packed_scales bf16 [batch, n/16, k/128, 16]  out
- * n % 16 == 0, k % 128 == 0.
+ *   pairing      DSV4MOE_PAIR_PLAIN: strip pair p = rows 32p..32p+31 (w2);
+ *                DSV4MOE_PAIR_GATED: pair p = rows 16p.. and n/2+16p.. (w13:
+ *                the gate row strip and its up row strip)
+ *   packed       uint8 [batch, n*k/2]  out: tile (p, g, m) of 16 rows x 128 k
+ *                at byte ((p*(k/128) + g)*2 + m)*1024
+ *   packed_scales bf16 [batch, n*k/128] out: [p][g][quad][m][4 rows]
+ * n % 32 == 0, k % 128 == 0.
  */
+#define DSV4MOE_PAIR_PLAIN 0
+#define DSV4MOE_PAIR_GATED 1
 int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, int64_t batch,
-                           int64_t n, int64_t k, uint8_t* packed, uint16_t* packed_scales,
-                           void* stream);
+                           int64_t n, int64_t k, int32_t pairing, uint8_t* packed,
+                           uint16_t* packed_scales, void* stream);
 
 /*
  * Workspace needed by dsv4moe_experts_w4a16 / _w4a8 (bytes).
@@ -154,9 +160,9 @@ size_t dsv4moe_experts_workspace_bytes(int64_t tokens, int32_t topk, int32_t hid
  * Replaces the vLLM _fused_marlin_moe call (runtime/dsv4_direct/moe_runtime.py:1829-1856),
  * the top-k sum (:1857), shared_bf16_partial (:246-263) and the combine add (:1873).
  *   x        bf16 [tokens, hidden]
- *   w13q/w13s  tiled int4 + scales, experts(+1 shared) x [2*inter, hidden]
- *              (rows [0,inter) = gate w1, [inter,2*inter) = up w3)
- *   w2q/w2s    tiled int4 + scales, experts(+1 shared) x [hidden, inter]
+ *   w13q/w13s  tiled int4 + scales (DSV4MOE_PAIR_GATED), experts(+1 shared) x
+ *              [2*inter, hidden] (rows [0,inter) = gate w1, [inter,2*inter) = up w3)
+ *   w2q/w2s    tiled int4 + scales (DSV4MOE_PAIR_PLAIN), experts(+1 shared) x [hidden, inter]
  *   has_shared 1: expert index `experts` is the always-on shared expert
  *   weights  fp32 [tokens, topk]  (route weights, applied to the w2 output)
  *   sorted_token_ids / expert_ids / num_tokens_post_padded: dsv4moe_align output

@@ -67,26 +67,35 @@ def assert_moe_close(out, ref, tol: float = MOE_TOL, what: str = "") -> dict:
     return err
 
 
-def np_tile_pack(canon: np.ndarray, scales_bits: np.ndarray):
-    """Independent numpy statement of the tiled int4 layout (see
-    gaiban-lite_amd/csrc/pack.hip): returns (packed bytes [n*k/2], scales [n/16, k/128, 16])."""
+def np_tile_pack(canon: np.ndarray, scales_bits: np.ndarray, gated: bool = False):
+    """Independent numpy statement of the pair-interleaved tiled int4 layout
+    (see gaiban-lite_amd/csrc/pack.hip): returns (packed bytes [n*k/2],
+    scales [n*k/128] as uint16)."""
 
     q = O.unpack_int4_rows(canon).astype(np.int32)  # [n, k]
     n, k = q.shape
     u = (q + 8).astype(np.uint32)
     groups = k // 128
-    out = np.zeros((n // 16, groups, 64, 4), dtype=np.uint32)
+    pairs = n // 32
     lane = np.arange(64)
-    rows_in_strip = lane % 16
-    for s in range(n // 16):
-        for g in range(groups):
-            for d in range(4):
-                k0 = g * 128 + 32 * d + 8 * (lane // 16)
-                word = np.zeros(64, dtype=np.uint32)
-                for j in range(4):
-                    word |= u[s * 16 + rows_in_strip, k0 + 2 * j] << np.uint32(4 * j)
-                    word |= u[s * 16 + rows_in_strip, k0 + 2 * j + 1] << np.uint32(16 + 4 * j)
-                out[s, g, :, d] = word
-    packed = out.reshape(-1).view(np.uint8)
-    sc = scales_bits.reshape(n // 16, 16, groups).transpose(0, 2, 1).copy()
-    return packed, sc
+
+    def row0(p, m):
+        return (p * 16 + m * (n // 2)) if gated else ((2 * p + m) * 16)
+
+    out = np.zeros((pairs, groups, 2, 64, 4), dtype=np.uint32)
+    sc = np.zeros((pairs, groups, 4, 2, 4), dtype=np.uint16)
+    sb = scales_bits.reshape(n, groups)
+    for p in range(pairs):
+        for m in range(2):
+            rows = row0(p, m) + lane % 16
+            for g in range(groups):
+                for d in range(4):
+                    k0 = g * 128 + 32 * d + 8 * (lane // 16)
+                    word = np.zeros(64, dtype=np.uint32)
+                    for j in range(4):
+                        word |= u[rows, k0 + 2 * j] << np.uint32(4 * j)
+                        word |= u[rows, k0 + 2 * j + 1] << np.uint32(16 + 4 * j)
+                    out[p, g, m, :, d] = word
+                for quad in range(4):
+                    sc[p, g, quad, m, :] = sb[row0(p, m) + 4 * quad + np.arange(4), g]
+    return out.reshape(-1).view(np.uint8), sc.reshape(-1)

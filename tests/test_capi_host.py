@@ -59,7 +59,8 @@ def test_validation_rejects_before_launch():
     assert "topk" in _einval("dsv4moe_route_topk", fake, None, 4, 8, 9, 0, 1.0, fake, fake, None, None, None, None)
     assert "score_func" in _einval("dsv4moe_route_topk", fake, None, 4, 8, 2, 7, 1.0, fake, fake, None, None, None, None)
     assert "capacity" in _einval("dsv4moe_align", fake, 4, 6, 256, 8, fake, 191, fake, 24, fake, None)
-    assert "multiple of 16" in _einval("dsv4moe_pack_int4_g128", fake, fake, 1, 24, 128, fake, fake, None)
+    assert "multiple of 32" in _einval("dsv4moe_pack_int4_g128", fake, fake, 1, 48, 128, 0, fake, fake, None)
+    assert "pairing" in _einval("dsv4moe_pack_int4_g128", fake, fake, 1, 64, 128, 2, fake, fake, None)
     assert "block_size" in _einval("dsv4moe_experts_w4a16", fake, 4, 4096, 2048, 256, 6, fake, fake, fake, fake,
                                    1, fake, fake, 192, fake, fake, 12, 0.0, fake, fake, 1 << 30, None)
     assert "hidden" in _einval("dsv4moe_experts_w4a16", fake, 4, 4000, 2048, 256, 6, fake, fake, fake, fake,
