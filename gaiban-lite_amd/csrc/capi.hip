@@ -76,6 +76,12 @@ int dsv4_launch_experts_w4a16(const uint16_t*, int64_t, int, int, int, int, cons
                               const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
                               uint16_t*, void*, hipStream_t);
 
+int32_t dsv4_w8a16_split_k(int64_t, int64_t, int64_t);
+size_t dsv4_w8a16_workspace_bytes(int64_t, int64_t, int32_t);
+int dsv4_launch_pack_int8(const int8_t*, int64_t, int64_t, uint8_t*, hipStream_t);
+int dsv4_launch_w8a16(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, const uint16_t*,
+                      int32_t, float*, uint16_t*, hipStream_t);
+
 using dsv4host::clear_error;
 using dsv4host::set_error;
 
@@ -357,6 +363,48 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                                    has_shared ? 1 : 0, weights, sorted_token_ids, capacity,
                                    expert_ids, num_tokens_post_padded, block_size, clamp_limit,
                                    out, workspace, s);
+}
+
+int dsv4moe_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(n > 0 && n % 16 == 0, "pack_int8: n must be a positive multiple of 16, got %lld", (long long)n);
+  DSV4_REQUIRE(k > 0 && k % 128 == 0, "pack_int8: k must be a positive multiple of 128, got %lld", (long long)k);
+  DSV4_REQUIRE(n * k < (int64_t)1 << 31, "pack_int8: n*k must be below 2^31");
+  DSV4_REQUIRE(w && packed, "pack_int8: null pointer");
+  DSV4_REQUIRE(aligned(w, 16) && aligned(packed, 16), "pack_int8: buffers must be 16-byte aligned");
+  return dsv4_launch_pack_int8(w, n, k, packed, static_cast<hipStream_t>(stream));
+}
+
+int32_t dsv4moe_w8a16_split_k(int64_t m, int64_t n, int64_t k) { return dsv4_w8a16_split_k(m, n, k); }
+
+size_t dsv4moe_w8a16_workspace_bytes(int64_t m, int64_t n, int32_t split_k) {
+  if (m < 0 || n <= 0 || split_k < 1) return 0;
+  return dsv4_w8a16_workspace_bytes(m, n, split_k);
+}
+
+int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
+                         const uint16_t* ws, int32_t split_k, float* workspace,
+                         size_t workspace_bytes, uint16_t* out, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(m >= 0, "w8a16_linear: m must be >= 0");
+  DSV4_REQUIRE(n > 0 && n % 16 == 0, "w8a16_linear: n must be a positive multiple of 16, got %lld", (long long)n);
+  DSV4_REQUIRE(k > 0 && k % 128 == 0, "w8a16_linear: k must be a positive multiple of 128, got %lld", (long long)k);
+  DSV4_REQUIRE(split_k == 1 || split_k == 2 || split_k == 4 || split_k == 8 || split_k == 16,
+               "w8a16_linear: split_k must be one of 1, 2, 4, 8, 16, got %d", split_k);
+  DSV4_REQUIRE(split_k <= k / 128, "w8a16_linear: split_k=%d exceeds the K-block count %lld", split_k,
+               (long long)(k / 128));
+  DSV4_REQUIRE(m * k * 2 < (int64_t)1 << 31 && n * k < (int64_t)1 << 31,
+               "w8a16_linear: m*k*2 and n*k must be below 2^31");
+  if (m == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(a && wq && ws && out, "w8a16_linear: null pointer");
+  DSV4_REQUIRE(aligned(a, 16) && aligned(wq, 16) && aligned(ws, 8) && aligned(out, 8),
+               "w8a16_linear: a and wq must be 16-byte aligned, ws and out 8-byte aligned");
+  const size_t need = dsv4_w8a16_workspace_bytes(m, n, split_k);
+  DSV4_REQUIRE(workspace_bytes >= need, "w8a16_linear: workspace of %zu bytes is below the %zu needed",
+               workspace_bytes, need);
+  DSV4_REQUIRE(need == 0 || (workspace && aligned(workspace, 16)),
+               "w8a16_linear: split_k > 1 needs a 16-byte aligned workspace");
+  return dsv4_launch_w8a16(a, m, n, k, wq, ws, split_k, workspace, out, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

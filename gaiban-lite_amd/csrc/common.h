@@ -59,6 +59,16 @@ __device__ __forceinline__ u32x4 load16_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// buffer_load ... lds of `size` bytes per lane (M0 = lds base, lane i writes
+// base + i*size).  Wrapped in a plain function so that template kernels whose
+// LDS arrays have template-dependent types still get their host-side launch
+// stubs (a target builtin with dependent arguments fails host instantiation).
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, lds_void_ptr lds, uint32_t voffset,
+                                          uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 16, voffset, soffset, 0, 0);
+}
+
 __device__ __forceinline__ float silu_f(float g) {
   return g / (1.0f + __expf(-g));
 }

@@ -1,0 +1,314 @@
+// W8A16 dense linear for gfx950: C[M,N] = bf16( A[M,K] . (Q[N,K] * s[N])^T ),
+// A bf16, Q int8 symmetric per output channel, s bf16, fp32 accumulation.
+//
+// Restates the weight-only linear of experiments/C1F-integrated-block/
+// weight_only_linear.py:537-702 (bf16 MMA over a weight reconstructed in
+// registers, fp32 accumulate, optional split-K into an fp32 [split, M, N]
+// workspace reduced in split order, one bf16 rounding) for the int8
+// per-channel format: the scale factors out of the K sum and is applied once
+// in the epilogue.
+//
+// Weight layout (dsv4moe_pack_int8): 1 KiB tiles of 16 rows x 64 K, tile
+// (strip, window) at byte (strip * K/64 + window) * 1024; lane l's 16 bytes are
+// row 16*strip + l%16, K 64*window + 16*(l/16) .. +15.  A wavefront therefore
+// streams one contiguous KiB per strip and window.  Each lane's 16 bytes feed
+// two MFMA 16x16x32 steps (bytes 0-7: K 16j..16j+7, bytes 8-15: K 16j+8..+15,
+// j = l/16); the activation fragments use the same K assignment, so the
+// product is the plain dot product over a permuted K order.
+#include <type_traits>
+
+#include "common.h"
+#include "../../include/dsv4moe.h"
+
+namespace dsv4 {
+
+constexpr int kWin = 64;               // K per window
+constexpr int kLinXcds = 8;
+constexpr uint32_t kLinOob = 0x80000000u;
+constexpr int kLinRsrcFlags = 0x00020000;
+
+struct LinearParams {
+  const uint16_t* a;
+  int64_t m;
+  int n;
+  int k;
+  const uint8_t* wq;
+  const uint16_t* ws;
+  int split;
+  int win_per_split;
+  int tiles_n;
+  int tiles_m;
+  uint16_t* out;
+  float* partial;  // [split][M][N] when split > 1
+};
+
+// 8 int8 weights (two dwords, K order) -> 8 bf16.  Every int8 is exact in
+// bf16; the signed byte converts through v_cvt_f32_i32 (SDWA byte select) and
+// the bf16 is the upper half of the float (exact, no rounding).
+__device__ __forceinline__ bf16x8 dequant_i8x8(uint32_t lo, uint32_t hi) {
+  const uint32_t f0 = __float_as_uint((float)(int8_t)(lo));
+  const uint32_t f1 = __float_as_uint((float)(int8_t)(lo >> 8));
+  const uint32_t f2 = __float_as_uint((float)(int8_t)(lo >> 16));
+  const uint32_t f3 = __float_as_uint((float)(int8_t)(lo >> 24));
+  const uint32_t f4 = __float_as_uint((float)(int8_t)(hi));
+  const uint32_t f5 = __float_as_uint((float)(int8_t)(hi >> 8));
+  const uint32_t f6 = __float_as_uint((float)(int8_t)(hi >> 16));
+  const uint32_t f7 = __float_as_uint((float)(int8_t)(hi >> 24));
+  u32x4 p;
+  p[0] = __builtin_amdgcn_perm(f1, f0, 0x07060302u);
+  p[1] = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
+  p[2] = __builtin_amdgcn_perm(f5, f4, 0x07060302u);
+  p[3] = __builtin_amdgcn_perm(f7, f6, 0x07060302u);
+  return __builtin_bit_cast(bf16x8, p);
+}
+
+// Workgroup tile: 64*R output channels (wavefront w owns strips 4R*tn + R*w + r)
+// x 16*C tokens, over one K split.  Per window, buffer_load ... lds copies the
+// token tile (16C rows x 128 B, 16-byte part q of row t stored at q ^ (t & 7))
+// and each wavefront's R weight tiles into LDS, double buffered.
+template <int R, int C>
+__global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * C * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * 1024];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  // XCD-aware item order: workgroup id i runs on XCD i % 8; each XCD takes a
+  // contiguous range of items, and items are split-major, then token tile,
+  // then channel tile, so one XCD's L2 keeps sharing an activation tile.
+  const int items = p.split * p.tiles_m * p.tiles_n;
+  const int per_xcd = (items + kLinXcds - 1) / kLinXcds;
+  const int item = (blockIdx.x % kLinXcds) * per_xcd + blockIdx.x / kLinXcds;
+  if (item >= items) return;
+  const int tn = item % p.tiles_n;
+  const int tm = (item / p.tiles_n) % p.tiles_m;
+  const int sp = item / (p.tiles_n * p.tiles_m);
+
+  const int wins = p.k / kWin;
+  const int w_begin = sp * p.win_per_split;
+  const int w_end = min(wins, w_begin + p.win_per_split);
+  const int nw = w_end - w_begin;  // may be 0 for a trailing split: it writes zeros
+
+  const int strips = p.n >> 4;
+  const int strip0 = tn * 4 * R + wave * R;
+
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.a, (short)0, (int)(p.m * p.k * 2), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wq, (short)0, (int)((int64_t)p.n * p.k), kLinRsrcFlags);
+
+  // token tile: 2C DMAs of 1 KiB (8 rows of 128 B); wavefront w issues DMA q = w + 4i
+  constexpr int kActDma = 2 * C;
+  constexpr int kActPerWave = (kActDma + 3) / 4;
+  uint32_t a_off[kActPerWave];
+#pragma unroll
+  for (int i = 0; i < kActPerWave; ++i) {
+    const int q = wave + 4 * i;
+    const int row = q * 8 + (lane >> 3);
+    const int64_t tok = (int64_t)tm * 16 * C + row;
+    const int part = (lane & 7) ^ (row & 7);
+    a_off[i] = (q < kActDma && tok < p.m) ? (uint32_t)(tok * p.k * 2 + part * 16) : kLinOob;
+  }
+  uint32_t w_off[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+
+  auto issue = [&](int win, int buf) {
+#pragma unroll
+    for (int i = 0; i < kActPerWave; ++i) {
+      const int q = wave + 4 * i;
+      if (q < kActDma) lds_dma16(a_rsrc, (lds_void_ptr)&xs[buf][q * 1024], a_off[i], win * 128);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 1024], w_off[r], win * 1024);
+  };
+
+  f32x4 acc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+  auto step = [&](int win, auto u_c, auto pf_c) {
+    constexpr int u = decltype(u_c)::value;
+    if constexpr (decltype(pf_c)::value) issue(win + 1, u ^ 1);
+    u32x4 raw[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      raw[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * 1024 + lane * 16]);
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      bf16x8 a[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) a[r] = dequant_i8x8(raw[r][2 * d], raw[r][2 * d + 1]);
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int row = c * 16 + n16;
+        const int part = (2 * j + d) ^ (row & 7);
+        const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + part * 16]));
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][c] = mfma_bf16(a[r], b, acc[r][c]);
+      }
+    }
+    __syncthreads();
+  };
+  using U0 = std::integral_constant<int, 0>;
+  using U1 = std::integral_constant<int, 1>;
+  using PF = std::true_type;
+  using NOPF = std::false_type;
+
+  if (nw > 0) {
+    issue(w_begin, 0);
+    __syncthreads();
+    int i = 0;
+    for (; i + 2 < nw; i += 2) {
+      step(w_begin + i, U0{}, PF{});
+      step(w_begin + i + 1, U1{}, PF{});
+    }
+    // the last window issues no prefetch, so no LDS DMA is in flight at exit
+    if (nw - i == 2) {
+      step(w_begin + i, U0{}, PF{});
+      step(w_begin + i + 1, U1{}, NOPF{});
+    } else {
+      step(w_begin + i, U0{}, NOPF{});
+    }
+  }
+
+  // epilogue: lane holds channels 16*strip + 4*j + (0..3) of token c*16 + n16
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int strip = strip0 + r;
+    if (strip >= strips) continue;
+    const int n = strip * 16 + 4 * j;
+    const u32x2 sv = *reinterpret_cast<const u32x2*>(p.ws + n);
+    float sc[4];
+    sc[0] = __uint_as_float(sv[0] << 16);
+    sc[1] = __uint_as_float(sv[0] & 0xFFFF0000u);
+    sc[2] = __uint_as_float(sv[1] << 16);
+    sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t tok = (int64_t)tm * 16 * C + c * 16 + n16;
+      if (tok >= p.m) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[r][c][e] * sc[e];
+      if (p.split == 1) {
+        const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        *reinterpret_cast<u32x2*>(p.out + tok * p.n + n) = o;
+      } else {
+        float* dst = p.partial + ((int64_t)sp * p.m + tok) * p.n + n;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+      }
+    }
+  }
+}
+
+// out[m][n] = bf16(sum over splits, in split order, of partial[s][m][n]).
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float* partial, int split, int64_t mn,
+                                                           uint16_t* out) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 4 elements each
+  if (q * 4 >= mn) return;
+  f32x4 s = *reinterpret_cast<const f32x4*>(partial + q * 4);
+  for (int i = 1; i < split; ++i) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(partial + (int64_t)i * mn + q * 4);
+    s[0] += v[0];
+    s[1] += v[1];
+    s[2] += v[2];
+    s[3] += v[3];
+  }
+  *reinterpret_cast<u32x2*>(out + q * 4) = u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
+}
+
+// Row-major int8 [N][K] -> 1 KiB tiles (16 rows x 64 K); one thread per 16 bytes.
+__global__ __launch_bounds__(256) void pack_int8_kernel(const uint8_t* src, int64_t n, int64_t k, uint8_t* dst) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c * 16 >= n * k) return;
+  const int64_t wins = k / kWin;
+  const int64_t tile = c >> 6;
+  const int lane = (int)(c & 63);
+  const int64_t strip = tile / wins;
+  const int64_t win = tile % wins;
+  const int64_t row = strip * 16 + (lane & 15);
+  const int64_t col = win * kWin + 16 * (lane >> 4);
+  *reinterpret_cast<u32x4*>(dst + c * 16) = *reinterpret_cast<const u32x4*>(src + row * k + col);
+}
+
+static void launch_w8a16_kernel(const LinearParams& p, int r, int c, hipStream_t stream) {
+  const int items = p.split * p.tiles_m * p.tiles_n;
+  const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
+  if (r == 4) hipLaunchKernelGGL((w8a16_kernel<4, 8>), grid, dim3(256), 0, stream, p);
+  else if (c == 1) hipLaunchKernelGGL((w8a16_kernel<2, 1>), grid, dim3(256), 0, stream, p);
+  else if (c == 2) hipLaunchKernelGGL((w8a16_kernel<2, 2>), grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL((w8a16_kernel<2, 4>), grid, dim3(256), 0, stream, p);
+}
+
+}  // namespace dsv4
+
+using namespace dsv4;
+
+// Geometry of the instance chosen for M: (R strips per wavefront, C token tiles).
+static void w8a16_geometry(int64_t m, int* r, int* c) {
+  if (m <= 16) { *r = 2; *c = 1; }
+  else if (m <= 32) { *r = 2; *c = 2; }
+  else if (m <= 64) { *r = 2; *c = 4; }
+  else { *r = 4; *c = 8; }
+}
+
+int32_t dsv4_w8a16_split_k(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return -1;
+  int r, c;
+  w8a16_geometry(m, &r, &c);
+  const int64_t tiles = ((n + 64 * r - 1) / (64 * r)) * ((m + 16 * c - 1) / (16 * c));
+  const int64_t wins = k / kWin;
+  int split = 1;
+  // widen over K until about two workgroups per CU, keeping >= 4 windows per split
+  while (split < 16 && tiles * split < 512 && wins / (split * 2) >= 4) split *= 2;
+  return split;
+}
+
+size_t dsv4_w8a16_workspace_bytes(int64_t m, int64_t n, int32_t split) {
+  return split > 1 ? (size_t)split * (size_t)m * (size_t)n * sizeof(float) : 0;
+}
+
+int dsv4_launch_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed, hipStream_t stream) {
+  const int64_t chunks = n * k / 16;
+  const int64_t blocks = (chunks + 255) / 256;
+  hipLaunchKernelGGL(pack_int8_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     reinterpret_cast<const uint8_t*>(w), n, k, packed);
+  DSV4_CHECK_LAUNCH("pack_int8_kernel");
+  return DSV4MOE_OK;
+}
+
+int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
+                      const uint16_t* ws, int32_t split, float* workspace, uint16_t* out,
+                      hipStream_t stream) {
+  int r, c;
+  w8a16_geometry(m, &r, &c);
+  LinearParams p;
+  p.a = a;
+  p.m = m;
+  p.n = (int)n;
+  p.k = (int)k;
+  p.wq = wq;
+  p.ws = ws;
+  p.split = split;
+  const int wins = (int)(k / kWin);
+  p.win_per_split = (wins + split - 1) / split;
+  p.tiles_n = (int)((n + 64 * r - 1) / (64 * r));
+  p.tiles_m = (int)((m + 16 * c - 1) / (16 * c));
+  p.out = out;
+  p.partial = workspace;
+  launch_w8a16_kernel(p, r, c, stream);
+  DSV4_CHECK_LAUNCH("w8a16_kernel");
+  if (split > 1) {
+    const int64_t quads = m * n / 4;
+    hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
+                       workspace, split, m * n, out);
+    DSV4_CHECK_LAUNCH("split_reduce_kernel");
+  }
+  return DSV4MOE_OK;
+}

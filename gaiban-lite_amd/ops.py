@@ -268,3 +268,44 @@ def layer_w4a16_into(
         ptr(num_tokens_post_padded), ptr(out), ptr(workspace), workspace.numel(),
         _lib.current_stream(dev),
     )
+
+
+def pack_int8(weight: torch.Tensor) -> torch.Tensor:
+    """Row-major int8 [n, k] -> tiled uint8 [n*k] (16 rows x 64 K per KiB tile)."""
+
+    if weight.ndim != 2:
+        raise ValueError("weight must be [n, k]")
+    n, k = weight.shape
+    _check("weight", weight, dtype=torch.int8, device=weight.device)
+    packed = torch.empty((n * k,), dtype=torch.uint8, device=weight.device)
+    call("dsv4moe_pack_int8", ptr(weight), n, k, ptr(packed), _lib.current_stream(weight.device))
+    return packed
+
+
+def w8a16_split_k(m: int, n: int, k: int) -> int:
+    split = int(_lib.load().dsv4moe_w8a16_split_k(m, n, k))
+    if split < 1:
+        raise ValueError("m, n and k must be positive")
+    return split
+
+
+def w8a16_workspace_bytes(m: int, n: int, split_k: int) -> int:
+    return int(_lib.load().dsv4moe_w8a16_workspace_bytes(m, n, split_k))
+
+
+def w8a16_linear_into(a: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, out: torch.Tensor,
+                      workspace: torch.Tensor | None, *, n: int, split_k: int) -> None:
+    if a.ndim != 2:
+        raise ValueError("activation must be [m, k]")
+    m, k = a.shape
+    dev = a.device
+    _check("activation", a, dtype=torch.bfloat16, device=dev)
+    _check("weight", wq, dtype=torch.uint8, shape=(n * k,), device=dev)
+    _check("weight_scale", ws, dtype=torch.bfloat16, shape=(n,), device=dev)
+    _check("out", out, dtype=torch.bfloat16, shape=(m, n), device=dev)
+    ws_bytes = 0
+    if workspace is not None:
+        _check("workspace", workspace, dtype=torch.float32, device=dev)
+        ws_bytes = workspace.numel() * 4
+    call("dsv4moe_w8a16_linear", ptr(a), m, n, k, ptr(wq), ptr(ws), int(split_k), ptr(workspace),
+         ws_bytes, ptr(out), _lib.current_stream(dev))

@@ -86,12 +86,23 @@ def zipf_ids(tokens: int, experts: int, topk: int, *, alpha: float = 1.1, seed: 
     return logits.topk(topk, dim=-1)[1].to(torch.int32)
 
 
+def make_int8_linear(n: int, k: int, *, seed: int = 3, device="cuda"):
+    """W8A16 weights: int8 uniform in [-127, 127] [n, k] and bf16 per-channel
+    scales ~ U(0.005, 0.02) [n]."""
+
+    g = _gen(seed * 1_000_003 + 77, device)
+    q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=device, generator=g)
+    s = (torch.rand((n,), device=device, generator=g) * 0.015 + 0.005).to(torch.bfloat16)
+    return q, s
+
+
 __all__ = [
     "FLASH",
     "TINY",
     "LayerShape",
     "make_checkpoint_experts",
     "make_hidden",
+    "make_int8_linear",
     "make_logits",
     "zipf_ids",
 ]

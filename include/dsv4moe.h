@@ -195,6 +195,33 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                         int32_t* num_tokens_post_padded, uint16_t* out, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/*
+ * W8A16 dense linear: out[M,N] = bf16( a[M,K] . (q[N,K] * s[N])^T ), int8
+ * symmetric per-output-channel weights, bf16 scales, fp32 accumulation.
+ * Replaces w8a16_gemm_into / make_gemm_plan / _automatic_split_k
+ * (experiments/C1F-integrated-block/weight_only_linear.py:794-823, :181-221,
+ * :168-179) and its kernels (:537-702) for the int8 per-channel format.
+ *
+ * dsv4moe_pack_int8: row-major int8 [n, k] -> 1 KiB tiles of 16 rows x 64 k,
+ *   tile (strip, window) at byte (strip*(k/64) + window)*1024, lane l's 16 bytes
+ *   = row 16*strip + l%16, k 64*window + 16*(l/16) ..+15.  n % 16 == 0, k % 128 == 0.
+ * dsv4moe_w8a16_split_k: this library's split-K policy for (m, n, k), 1..16.
+ * dsv4moe_w8a16_workspace_bytes: split*m*n*4 when split > 1, else 0.
+ * dsv4moe_w8a16_linear:
+ *   a       bf16 [m, k]
+ *   wq      packed int8 (dsv4moe_pack_int8), ws bf16 [n]
+ *   split_k 1, 2, 4, 8 or 16 (<= k/128); > 1 uses workspace fp32 [split, m, n],
+ *           partials reduced in split order before the single bf16 rounding
+ *   out     bf16 [m, n]
+ * m >= 0, n % 16 == 0, k % 128 == 0, m*k*2 and n*k below 2^31.
+ */
+int dsv4moe_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed, void* stream);
+int32_t dsv4moe_w8a16_split_k(int64_t m, int64_t n, int64_t k);
+size_t dsv4moe_w8a16_workspace_bytes(int64_t m, int64_t n, int32_t split_k);
+int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
+                         const uint16_t* ws, int32_t split_k, float* workspace,
+                         size_t workspace_bytes, uint16_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

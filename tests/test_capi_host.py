@@ -71,6 +71,31 @@ def test_validation_rejects_before_launch():
                                   ws - 1, None)
 
 
+def test_w8a16_validation_and_split_policy():
+    fake = ctypes.c_void_p(0x1000)
+    lib = _lib.load()
+    args = lambda m, n, k, split, ws_bytes: (fake, m, n, k, fake, fake, split, fake, ws_bytes, fake, None)
+    assert "multiple of 16" in _einval("dsv4moe_w8a16_linear", *args(4, 40, 4096, 1, 0))
+    assert "multiple of 128" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 4000, 1, 0))
+    assert "split_k" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 4096, 3, 1 << 30))
+    assert "K-block" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 256, 4, 1 << 30))
+    need = lib.dsv4moe_w8a16_workspace_bytes(4, 64, 2)
+    assert need == 2 * 4 * 64 * 4 and lib.dsv4moe_w8a16_workspace_bytes(4, 64, 1) == 0
+    assert "workspace" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 4096, 2, need - 1))
+    assert "multiple of 16" in _einval("dsv4moe_pack_int8", fake, 24, 128, fake, None)
+    assert lib.dsv4moe_w8a16_linear(fake, 0, 64, 4096, fake, fake, 1, None, 0, fake, None) == _lib.DSV4MOE_OK
+    # this library's policy: a power of two in [1, 16] leaving >= 4 windows of 64 K per split,
+    # raised only while the grid is below 512 workgroups
+    for m in (1, 16, 17, 64, 65, 8192):
+        for n in (1024, 4096, 16384):
+            split = lib.dsv4moe_w8a16_split_k(m, n, 4096)
+            assert split in (1, 2, 4, 8, 16)
+            assert 4096 // 64 // split >= 4
+    assert lib.dsv4moe_w8a16_split_k(8192, 4096, 4096) == 1
+    assert lib.dsv4moe_w8a16_split_k(1, 4096, 4096) > 1
+    assert lib.dsv4moe_w8a16_split_k(0, 4096, 4096) == -1
+
+
 def test_workspace_formula():
     # x row sums (per 64 columns) + h + h row sums + fp32 contributions, each 256-byte aligned
     t, k, h, i = 64, 6, 4096, 2048

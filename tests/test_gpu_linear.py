@@ -1,0 +1,98 @@
+"""W8A16 dense linear: bf16 output against the fp32 closed form
+C = A . (Q * s)^T (oracle ``w8a16_linear_f32``) on seeded inputs, to max_rel
+and rel_fro <= 1e-2, at the benchmark shapes (K=4096, N in {4096, 1024,
+16384}, M in {1, 64, 8192}), every split-K width, ragged M and N, and the
+tiled packer against an independent numpy statement of its layout.
+
+Rows of C depend only on the same row of A, so M=8192 is checked on a seeded
+subset of rows (the kernel still computes all of them).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gaiban_lite_amd import ops, synthetic as S
+from gaiban_lite_amd import weight_only_linear as L
+from helpers import assert_moe_close, bf16_bits, to_np_f32
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def np_pack_int8(q: np.ndarray) -> np.ndarray:
+    n, k = q.shape
+    t = q.reshape(n // 16, 16, k // 64, 4, 16)          # strip, row, window, j, byte
+    t = t.transpose(0, 2, 3, 1, 4)                       # strip, window, j, row, byte -> lane = 16j + row
+    return np.ascontiguousarray(t).reshape(-1).view(np.uint8)
+
+
+def run(m, n, k, *, split=None, seed=3, rows=None):
+    print(f"[w8a16] M={m} N={n} K={k} split={split}", flush=True)
+    q, s = S.make_int8_linear(n, k, seed=seed, device=DEV)
+    a = torch.randn((m, k), device=DEV, generator=torch.Generator(DEV).manual_seed(seed + 100)).to(torch.bfloat16)
+    prep = L.prepare_int8_weight(q, s)
+    out = L.w8a16_linear(a, prep, split_k=split)
+    torch.cuda.synchronize()
+    rows = np.arange(m) if rows is None else rows
+    ref = O.w8a16_linear_f32(to_np_f32(a)[rows], q.cpu().numpy(), bf16_bits(s))
+    err = assert_moe_close(to_np_f32(out)[rows], ref, what=f"M={m} N={n} split={split}")
+    print(f"    {err}", flush=True)
+    return out
+
+
+def test_pack_int8_layout():
+    q, _ = S.make_int8_linear(64, 256, seed=5, device=DEV)
+    packed = ops.pack_int8(q)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(packed.cpu().numpy(), np_pack_int8(q.cpu().numpy()))
+
+
+@pytest.mark.parametrize("n", [4096, 1024, 16384])
+@pytest.mark.parametrize("m", [1, 64])
+def test_decode_shapes(m, n):
+    run(m, n, 4096)
+
+
+@pytest.mark.parametrize("n", [4096, 1024, 16384])
+def test_prefill_shapes_row_subset(n):
+    rows = np.sort(np.random.default_rng(n).choice(8192, 96, replace=False))
+    run(8192, n, 4096, rows=rows)
+
+
+@pytest.mark.parametrize("split", [1, 2, 4, 8, 16])
+def test_every_split_width(split):
+    out = run(64, 1024, 4096, split=split)
+    base = run(64, 1024, 4096, split=1) if split != 1 else out
+    # a different split only changes the fp32 summation order
+    d = (out.float() - base.float()).abs().max().item()
+    assert d <= 2e-2 * base.float().abs().max().item()
+
+
+@pytest.mark.parametrize("m", [2, 3, 17, 33, 65, 100, 129])
+@pytest.mark.parametrize("n,k", [(48, 256), (208, 384)])
+def test_ragged_shapes(m, n, k):
+    run(m, n, k)
+    run(m, n, k, split=2)
+
+
+def test_zero_rows_and_contract_errors():
+    q, s = S.make_int8_linear(64, 256, device=DEV)
+    prep = L.prepare_int8_weight(q, s)
+    a = torch.empty((0, 256), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((0, 64), dtype=torch.bfloat16, device=DEV)
+    ops.w8a16_linear_into(a, prep.packed, prep.scale, out, None, n=64, split_k=1)
+    plan = L.make_gemm_plan(4, 64, 256, split_k=2)
+    a = torch.zeros((4, 256), dtype=torch.bfloat16, device=DEV)
+    out = torch.empty((4, 64), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError):
+        L.w8a16_gemm_into(a, prep.packed, prep.scale, out,
+                          torch.empty((1, 4, 64), dtype=torch.float32, device=DEV), plan=plan)
+    with pytest.raises(TypeError):
+        L.w8a16_gemm_into(a.float(), prep.packed, prep.scale, out, L.allocate_workspace(plan, DEV), plan=plan)
+    with pytest.raises(ValueError):
+        L.make_gemm_plan(4, 64, 200)
+    with pytest.raises(ValueError):
+        L.make_gemm_plan(4, 64, 256, split_k=4)  # 2 K-blocks
