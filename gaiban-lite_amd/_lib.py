@@ -55,6 +55,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _sz, _p],
     ),
     "dsv4moe_pack_int8": (ctypes.c_int, [_p, _i64, _i64, _p, _p]),
+    "dsv4moe_experts_w4a8_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
+    "dsv4moe_experts_w4a8": (
+        ctypes.c_int,
+        [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _p, _p, _i64, _p, _p, _i32,
+         _f32, _p, _p, _sz, _p],
+    ),
+    "dsv4moe_act_quant_fp8": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p]),
     "dsv4moe_w8a16_split_k": (_i32, [_i64, _i64, _i64]),
     "dsv4moe_w8a16_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "dsv4moe_w8a16_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),

@@ -76,6 +76,12 @@ int dsv4_launch_experts_w4a16(const uint16_t*, int64_t, int, int, int, int, cons
                               const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
                               uint16_t*, void*, hipStream_t);
 
+size_t dsv4_experts_w4a8_workspace_bytes(int64_t, int, int, int, int);
+int dsv4_launch_act_quant_fp8(const uint16_t*, int64_t, int, uint8_t*, float*, float*, hipStream_t);
+int dsv4_launch_experts_w4a8(const uint16_t*, int64_t, int, int, int, int, const uint8_t*,
+                             const uint16_t*, const uint8_t*, const uint16_t*, int, const float*,
+                             const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
+                             uint16_t*, void*, hipStream_t);
 int32_t dsv4_w8a16_split_k(int64_t, int64_t, int64_t);
 size_t dsv4_w8a16_workspace_bytes(int64_t, int64_t, int32_t);
 int dsv4_launch_pack_int8(const int8_t*, int64_t, int64_t, uint8_t*, hipStream_t);
@@ -272,8 +278,11 @@ static int validate_experts(const uint16_t* x, int64_t tokens, int32_t hidden, i
                             int32_t experts, int32_t topk, const uint8_t* w13q,
                             const uint16_t* w13s, const uint8_t* w2q, const uint16_t* w2s,
                             int64_t capacity, int32_t block_size, uint16_t* out, void* workspace,
-                            size_t workspace_bytes, int32_t has_shared, const char* who) {
+                            size_t workspace_bytes, int32_t has_shared, const char* who,
+                            bool a8 = false) {
   DSV4_REQUIRE(tokens >= 0, "%s: tokens must be >= 0", who);
+  DSV4_REQUIRE(!a8 || (hidden % 512 == 0 && inter % 512 == 0),
+               "%s: W4A8 needs hidden and inter to be multiples of 512 (got %d, %d)", who, hidden, inter);
   DSV4_REQUIRE(hidden > 0 && hidden % 256 == 0, "%s: hidden=%d must be a positive multiple of 256", who, hidden);
   DSV4_REQUIRE(inter > 0 && inter % 256 == 0, "%s: inter=%d must be a positive multiple of 256", who, inter);
   DSV4_REQUIRE(experts >= 1 && experts <= 1024, "%s: experts must be in [1, 1024]", who);
@@ -287,7 +296,8 @@ static int validate_experts(const uint16_t* x, int64_t tokens, int32_t hidden, i
   DSV4_REQUIRE(aligned(x, 16) && aligned(w13q, 16) && aligned(w2q, 16) && aligned(w13s, 8) &&
                    aligned(w2s, 8) && aligned(out, 8) && aligned(workspace, 256),
                "%s: alignment (x/w*q 16 B, scales/out 8 B, workspace 256 B)", who);
-  const size_t need = dsv4_experts_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0);
+  const size_t need = a8 ? dsv4_experts_w4a8_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0)
+                        : dsv4_experts_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0);
   DSV4_REQUIRE(workspace_bytes >= need, "%s: workspace %zu bytes < required %zu", who,
                workspace_bytes, need);
   const int64_t act_rows = tokens * topk + (has_shared ? tokens : 0);
@@ -405,6 +415,48 @@ int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, con
   DSV4_REQUIRE(need == 0 || (workspace && aligned(workspace, 16)),
                "w8a16_linear: split_k > 1 needs a 16-byte aligned workspace");
   return dsv4_launch_w8a16(a, m, n, k, wq, ws, split_k, workspace, out, static_cast<hipStream_t>(stream));
+}
+
+size_t dsv4moe_experts_w4a8_workspace_bytes(int64_t tokens, int32_t topk, int32_t hidden, int32_t inter,
+                                            int32_t has_shared) {
+  if (tokens < 0 || topk < 1 || hidden <= 0 || inter <= 0) return 0;
+  return dsv4_experts_w4a8_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0);
+}
+
+int dsv4moe_act_quant_fp8(const uint16_t* x, int64_t rows, int32_t k, uint8_t* q, float* scale,
+                          float* group_sums, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(rows >= 0, "act_quant_fp8: rows must be >= 0");
+  DSV4_REQUIRE(k > 0 && k % 512 == 0, "act_quant_fp8: k=%d must be a positive multiple of 512", k);
+  DSV4_REQUIRE(rows * (int64_t)k * 2 < 0x7FFFFFFFLL, "act_quant_fp8: input exceeds 2 GiB");
+  if (rows == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(x && q && scale && group_sums, "act_quant_fp8: null pointer");
+  DSV4_REQUIRE(aligned(x, 16) && aligned(q, 8) && aligned(scale, 4) && aligned(group_sums, 4),
+               "act_quant_fp8: alignment (x 16 B, q 8 B)");
+  return dsv4_launch_act_quant_fp8(x, rows, k, q, scale, group_sums, static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_experts_w4a8(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
+                         int32_t experts, int32_t topk, const uint8_t* w13q, const uint16_t* w13s,
+                         const uint8_t* w2q, const uint16_t* w2s, int32_t has_shared,
+                         const float* weights, const int32_t* sorted_token_ids, int64_t capacity,
+                         const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                         int32_t block_size, float clamp_limit, uint16_t* out, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = validate_experts(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s, capacity,
+                            block_size, out, workspace, workspace_bytes, has_shared, "experts_w4a8", true);
+  if (rc != DSV4MOE_OK || tokens == 0) return rc;
+  DSV4_REQUIRE(weights && sorted_token_ids && expert_ids && num_tokens_post_padded,
+               "experts_w4a8: null route/alignment pointer");
+  DSV4_REQUIRE(!(clamp_limit < 0.0f) && clamp_limit < 3.0e38f, "experts_w4a8: clamp_limit must be >= 0 and finite");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dsv4host::prof_stamp(dsv4host::kStampBegin, s);
+  dsv4host::prof_stamp(dsv4host::kStampRoute, s);
+  dsv4host::prof_stamp(dsv4host::kStampAlign, s);
+  return dsv4_launch_experts_w4a8(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+                                  has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
+                                  num_tokens_post_padded, block_size, clamp_limit, out, workspace, s);
 }
 
 }  // extern "C"

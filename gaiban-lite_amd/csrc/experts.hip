@@ -28,91 +28,10 @@
 //    weight rows per workgroup, token tiles staged in LDS, XCD-aware order.
 #include <type_traits>
 
-#include "common.h"
+#include "experts_common.h"
 #include "../../include/dsv4moe.h"
 
 namespace dsv4 {
-
-constexpr int kSumChunk = 64;            // granularity of the activation row sums
-constexpr uint32_t kOobOffset = 0x80000000u;  // buffer offset past every resource
-constexpr int kRsrcFlags = 0x00020000;    // raw buffer, gfx950 dword3
-
-struct ExpertGemmParams {
-  const uint8_t* wq;     // tiled int4, expert-major
-  const uint16_t* ws;    // tiled scales
-  int64_t wq_stride;     // bytes per expert
-  int64_t ws_stride;     // scale elements per expert
-  int k_dim;             // K of the weight matrix
-  int inter;             // stage 1: first up-projection row
-  const uint16_t* act;   // stage 1: x [T][H]; stage 2: h [rows][I]
-  int64_t act_rows;      // rows of `act`
-  const float* act_sum;  // [act_rows][k_dim/64] row sums of `act`
-  const int32_t* sorted;
-  const int32_t* expert_ids;
-  const int32_t* ntpp;
-  int block_size;
-  int shared_block_size; // token slots per shared-expert block
-  int max_blocks;
-  int n_tiles;
-  int64_t tokens;
-  int topk;
-  int shared_expert;     // expert index of the shared expert, -1 if none
-  float clamp_limit;
-  const float* route_w;  // stage 2: [T*k]
-  uint16_t* h_out;       // stage 1: [rows][I]
-  float* hsum_out;       // stage 1: [rows][I/64]
-  float* contrib;        // stage 2: [rows][H]
-  int out_cols;          // stage 2: H
-};
-
-struct BlockInfo {
-  int expert;
-  int64_t slot_base;
-  bool shared;
-  bool active;
-};
-
-__device__ __forceinline__ BlockInfo block_info(const ExpertGemmParams& p, int blk) {
-  BlockInfo b;
-  b.shared = blk >= p.max_blocks;
-  b.active = true;
-  if (!b.shared) {
-    const int total = p.ntpp[0];
-    b.active = total > 0 && (int64_t)blk * p.block_size < total;
-    b.expert = b.active ? p.expert_ids[blk] : 0;
-    b.slot_base = (int64_t)blk * p.block_size;
-  } else {
-    b.expert = p.shared_expert;
-    b.slot_base = (int64_t)(blk - p.max_blocks) * p.shared_block_size;
-  }
-  return b;
-}
-
-// Row id (index into h / contrib) of token column `col` of a block, -1 if padded.
-__device__ __forceinline__ int64_t slot_rowid(const ExpertGemmParams& p, const BlockInfo& b, int col,
-                                              int64_t tk) {
-  if (col >= (b.shared ? p.shared_block_size : p.block_size)) return -1;
-  if (!b.shared) {
-    const int32_t f = p.sorted[b.slot_base + col];
-    return (f >= 0 && f < tk) ? (int64_t)f : -1;
-  }
-  const int64_t t = b.slot_base + col;
-  return t < p.tokens ? tk + t : -1;
-}
-
-template <int STAGE>
-__device__ __forceinline__ int64_t act_row_of(int64_t rowid, int64_t tk, int topk) {
-  if (rowid < 0) return -1;
-  if (STAGE == 1) return rowid < tk ? (int64_t)((uint32_t)rowid / (uint32_t)topk) : rowid - tk;
-  return rowid;
-}
-
-__device__ __forceinline__ void scale4(u32x2 sv, float (&sc)[4]) {
-  sc[0] = __uint_as_float(sv[0] << 16);
-  sc[1] = __uint_as_float(sv[0] & 0xFFFF0000u);
-  sc[2] = __uint_as_float(sv[1] << 16);
-  sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
-}
 
 // ------------------------------------------------------------------ decode
 // STAGE 1: wave w owns gate strip n0/16 + w and up strip (inter + n0)/16 + w,
@@ -274,7 +193,6 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
 // blocks assigned round-robin to the 8 XCDs and all tiles of a block run on
 // the XCD that fetched its token rows into L2.
 constexpr int kPfSlots = 64;
-constexpr int kXcds = 8;
 
 template <int STAGE>
 __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams p, int total_blocks) {
@@ -655,12 +573,17 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   DSV4_CHECK_LAUNCH("expert stage 2");
   dsv4host::prof_stamp(dsv4host::kStampStage2, stream);
 
-  {
-    const int64_t n = tokens * (hidden / 4);
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                       ws.contrib, tokens, topk, hidden, has_shared, out);
-    DSV4_CHECK_LAUNCH("combine_kernel");
-  }
+  const int rc = dsv4_launch_combine(ws.contrib, tokens, topk, hidden, has_shared, out, stream);
+  if (rc != DSV4MOE_OK) return rc;
   dsv4host::prof_stamp(dsv4host::kStampCombine, stream);
+  return DSV4MOE_OK;
+}
+
+int dsv4_launch_combine(const float* contrib, int64_t tokens, int topk, int hidden, int has_shared,
+                        uint16_t* out, hipStream_t stream) {
+  const int64_t n = tokens * (hidden / 4);
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     contrib, tokens, topk, hidden, has_shared, out);
+  DSV4_CHECK_LAUNCH("combine_kernel");
   return DSV4MOE_OK;
 }

@@ -1,0 +1,96 @@
+// Helpers shared by the bf16 (W4A16) and fp8 (W4A8) grouped expert kernels:
+// kernel parameters, alignment-block decoding and slot -> row mapping.
+#pragma once
+
+#include "common.h"
+
+namespace dsv4 {
+
+constexpr int kSumChunk = 64;            // granularity of the activation row sums
+constexpr uint32_t kOobOffset = 0x80000000u;  // buffer offset past every resource
+constexpr int kRsrcFlags = 0x00020000;    // raw buffer, gfx950 dword3
+constexpr int kXcds = 8;                  // XCDs; workgroup id i runs on XCD i % 8
+
+struct ExpertGemmParams {
+  const uint8_t* wq;     // tiled int4, expert-major
+  const uint16_t* ws;    // tiled scales
+  int64_t wq_stride;     // bytes per expert
+  int64_t ws_stride;     // scale elements per expert
+  int k_dim;             // K of the weight matrix
+  int inter;             // stage 1: first up-projection row
+  const uint16_t* act;   // stage 1: x [T][H]; stage 2: h [rows][I]
+  int64_t act_rows;      // rows of `act`
+  const float* act_sum;  // [act_rows][k_dim/64] row sums of `act`
+  const int32_t* sorted;
+  const int32_t* expert_ids;
+  const int32_t* ntpp;
+  int block_size;
+  int shared_block_size; // token slots per shared-expert block
+  int max_blocks;
+  int n_tiles;
+  int64_t tokens;
+  int topk;
+  int shared_expert;     // expert index of the shared expert, -1 if none
+  float clamp_limit;
+  const float* route_w;  // stage 2: [T*k]
+  uint16_t* h_out;       // stage 1: [rows][I]
+  float* hsum_out;       // stage 1: [rows][I/64]
+  float* contrib;        // stage 2: [rows][H]
+  int out_cols;          // stage 2: H
+  const float* act_scale;  // fp8 kernels: per-row activation scale [act_rows]
+};
+
+struct BlockInfo {
+  int expert;
+  int64_t slot_base;
+  bool shared;
+  bool active;
+};
+
+__device__ __forceinline__ BlockInfo block_info(const ExpertGemmParams& p, int blk) {
+  BlockInfo b;
+  b.shared = blk >= p.max_blocks;
+  b.active = true;
+  if (!b.shared) {
+    const int total = p.ntpp[0];
+    b.active = total > 0 && (int64_t)blk * p.block_size < total;
+    b.expert = b.active ? p.expert_ids[blk] : 0;
+    b.slot_base = (int64_t)blk * p.block_size;
+  } else {
+    b.expert = p.shared_expert;
+    b.slot_base = (int64_t)(blk - p.max_blocks) * p.shared_block_size;
+  }
+  return b;
+}
+
+// Row id (index into h / contrib) of token column `col` of a block, -1 if padded.
+__device__ __forceinline__ int64_t slot_rowid(const ExpertGemmParams& p, const BlockInfo& b, int col,
+                                              int64_t tk) {
+  if (col >= (b.shared ? p.shared_block_size : p.block_size)) return -1;
+  if (!b.shared) {
+    const int32_t f = p.sorted[b.slot_base + col];
+    return (f >= 0 && f < tk) ? (int64_t)f : -1;
+  }
+  const int64_t t = b.slot_base + col;
+  return t < p.tokens ? tk + t : -1;
+}
+
+template <int STAGE>
+__device__ __forceinline__ int64_t act_row_of(int64_t rowid, int64_t tk, int topk) {
+  if (rowid < 0) return -1;
+  if (STAGE == 1) return rowid < tk ? (int64_t)((uint32_t)rowid / (uint32_t)topk) : rowid - tk;
+  return rowid;
+}
+
+__device__ __forceinline__ void scale4(u32x2 sv, float (&sc)[4]) {
+  sc[0] = __uint_as_float(sv[0] << 16);
+  sc[1] = __uint_as_float(sv[0] & 0xFFFF0000u);
+  sc[2] = __uint_as_float(sv[1] << 16);
+  sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
+}
+
+}  // namespace dsv4
+
+// Host launchers shared by both expert paths (experts.hip).
+int dsv4_launch_combine(const float* contrib, int64_t tokens, int topk, int hidden, int has_shared,
+                        uint16_t* out, hipStream_t stream);

@@ -1,0 +1,552 @@
+// W4A8: grouped int4 expert GEMMs on the gfx950 fp8 MFMA (16x16x128 f8f6f4).
+//
+// Restates vLLM's _fused_marlin_moe with input_dtype = float8_e4m3fn as
+// configured at runtime/dsv4_direct/moe_runtime.py:207-235,1829-1856: the
+// expert inputs (x for stage 1, the bf16 SwiGLU output h for stage 2) are
+// quantised per row to OCP e4m3 with s = max(amax, 1e-12) / 448 and
+// q = e4m3(clamp(v / s, -448, 448)); the products accumulate in fp32 and the
+// row scale multiplies the result.
+//
+// int4 weights enter the fp8 MFMA without a lookup: the offset-binary nibble
+// u = q + 8 (0..15) placed in a byte is the e4m3 encoding of u * 2^-9 (bytes
+// 0..7 are subnormals m * 2^-9, bytes 8..15 are (8 + m) * 2^-9).  Per
+// quantisation group g of weight row n and activation row t the MFMA gives
+// 2^-9 * sum(u * xq); the kernels add s[n, g] * (that - sum_g(xq) / 64) and
+// the epilogue multiplies by 512 * s_row, which equals
+// s_row * sum_g s[n, g] * sum(q * xq).
+//
+// Operand layout: a lane of the 16x16x128 MFMA holds 32 K values of one row
+// (A) or column (B) in 8 dwords; both operands assign K values to (lane group,
+// byte) the same way, so any fixed assignment gives the dot product.  The
+// tiled int4 weights expand, per 16-byte lane chunk, dword d (8 nibbles, K
+// k0 = 32d + 8j .. +7, slots as in the bf16 path) into the byte dwords
+// (w & 0x0F0F0F0F, (w >> 4) & 0x0F0F0F0F) = K k0 + {0,4,1,5}, k0 + {2,6,3,7}.
+// The activation quantiser writes each 128-K group in exactly that order: 32
+// bytes per lane group j, dword pair d holding K 32d + 8j + {0,4,1,5,2,6,3,7}.
+#include <type_traits>
+
+#include "experts_common.h"
+#include "../../include/dsv4moe.h"
+
+namespace dsv4 {
+
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+
+__device__ __forceinline__ f32x4 mfma_fp8(i32x8 a, i32x8 b) {
+  // unit E8M0 block scales (127 = 2^0)
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127,
+                                                           0, 127);
+}
+
+// 16 bytes of tiled int4 (32 nibbles) -> 32 e4m3 bytes of u * 2^-9.
+__device__ __forceinline__ i32x8 spread_nibbles(u32x4 w) {
+  i32x8 a;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    a[2 * d] = (int)(w[d] & 0x0F0F0F0Fu);
+    a[2 * d + 1] = (int)((w[d] >> 4) & 0x0F0F0F0Fu);
+  }
+  return a;
+}
+
+constexpr float kInvSum = 1.0f / 64.0f;  // 8 * 2^-9
+constexpr float kUnScale = 512.0f;       // 2^9
+
+// ------------------------------------------------------------ activation quant
+// One wavefront per row (K % 512 == 0).  Writes q (e4m3, MFMA order), the
+// row scale and, per 128-K group, the fp32 sum of the 128 e4m3 values (each
+// lane adds its 8 values in K order, then a fixed xor tree over 16 lanes).
+__global__ __launch_bounds__(256) void act_quant_fp8_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                            int k, uint8_t* __restrict__ q,
+                                                            float* __restrict__ scale,
+                                                            float* __restrict__ gsum) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* src = x + row * k;
+  const int iters = k / 512;
+  float amax = 0.0f;
+  for (int i = 0; i < iters; ++i) {
+    const u32x4 v = load16(src + (lane + 64 * i) * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[e] << 16)));
+      amax = fmaxf(amax, fabsf(__uint_as_float(v[e] & 0xFFFF0000u)));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  const float s = fmaxf(amax, 1e-12f) / 448.0f;
+  if (lane == 0) scale[row] = s;
+
+  const int groups = k / 128;
+  for (int i = 0; i < iters; ++i) {
+    const int o = lane + 64 * i;  // octet: K 8o .. 8o+7
+    const u32x4 v = load16(src + o * 8);
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = __uint_as_float(v[e] << 16);
+      f[2 * e + 1] = __uint_as_float(v[e] & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / s, -448.0f), 448.0f);
+    // output byte b holds K offset {0,4,1,5,2,6,3,7}[b]
+    int lo = 0, hi = 0;
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[4], lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[1], f[5], lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[6], hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[3], f[7], hi, true);
+    // decoded values in K order for the group sum
+    float dq[8];
+    dq[0] = __builtin_amdgcn_cvt_f32_fp8(lo, 0);
+    dq[4] = __builtin_amdgcn_cvt_f32_fp8(lo, 1);
+    dq[1] = __builtin_amdgcn_cvt_f32_fp8(lo, 2);
+    dq[5] = __builtin_amdgcn_cvt_f32_fp8(lo, 3);
+    dq[2] = __builtin_amdgcn_cvt_f32_fp8(hi, 0);
+    dq[6] = __builtin_amdgcn_cvt_f32_fp8(hi, 1);
+    dq[3] = __builtin_amdgcn_cvt_f32_fp8(hi, 2);
+    dq[7] = __builtin_amdgcn_cvt_f32_fp8(hi, 3);
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum += dq[e];
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    sum += __shfl_xor(sum, 4, 64);
+    sum += __shfl_xor(sum, 8, 64);
+    const int g = o >> 4;
+    const int lo16 = o & 15;
+    const int d = lo16 >> 2;
+    const int j = lo16 & 3;
+    *reinterpret_cast<u32x2*>(q + row * k + g * 128 + j * 32 + d * 8) = u32x2{(uint32_t)lo, (uint32_t)hi};
+    if ((lane & 15) == 0) gsum[row * groups + g] = sum;
+  }
+}
+
+// ------------------------------------------------------------------ decode
+// Alignment blocks of <= 16 token slots; workgroup = 4 wavefronts, wavefront w
+// streams strip pair tile*4 + w (stage 1: gate + up strip, h columns
+// n0 + 16w ..; stage 2: strips (n0 + 32w)/16 + {0, 1}).  The 16 slots x 128 B
+// of the current group are staged in LDS (rows of 144 B), one group ahead.
+constexpr int kF8Row = 144;
+
+template <int STAGE>
+__global__ __launch_bounds__(256) void expert_fp8_decode_kernel(ExpertGemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][32 * kF8Row];  // rows 16..31: unused landing rows
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int tile = blockIdx.x % p.n_tiles;
+  const int blk = blockIdx.x / p.n_tiles;
+  const int64_t tk = p.tokens * p.topk;
+  const BlockInfo b = block_info(p, blk);
+  if (!b.active) return;
+
+  const int64_t rowid = slot_rowid(p, b, lane & 15, tk);
+  const int64_t arow = act_row_of<STAGE>(rowid, tk, p.topk);
+  const int groups = p.k_dim / kGroup;
+
+  const int n0 = STAGE == 1 ? tile * 64 : tile * 128;
+  const int pair = tile * 4 + wave;
+  const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
+  const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
+
+  const uint8_t* act = reinterpret_cast<const uint8_t*>(p.act);
+  const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)act, (short)0, (int)(p.act_rows * p.k_dim), kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act_sum, (short)0, (int)(p.act_rows * groups * 4), kRsrcFlags);
+  const int ld_slot = threadIdx.x >> 3;  // 0..31; slots >= 16 load zeros into the landing rows
+  const int ld_part = threadIdx.x & 7;
+  const int64_t ld_row =
+      ld_slot < 16 ? act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk) : (int64_t)-1;
+  const uint32_t ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim + ld_part * 16) : kOobOffset;
+  const uint32_t sum_base = arow >= 0 ? (uint32_t)(arow * groups * 4) : kOobOffset;
+  const int ld_lds = ld_slot * kF8Row + ld_part * 16;
+  const int rd_lds = (lane & 15) * kF8Row + 32 * (lane >> 4);
+
+  u32x4 W[4][2];
+  u32x4 S[4];
+  float CS[2];
+  u32x4 xr;
+  auto issue_w = [&](int g, u32x4 (&w)[2], u32x4& s) {
+    w[0] = load16_nt(wq + g * 2048);
+    w[1] = load16_nt(wq + g * 2048 + 1024);
+    s = load16(ws + g * 32);
+  };
+  auto issue_x = [&](int g, float& cs) {
+    xr = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, ld_base + (uint32_t)(g * 128), 0, 0);
+    cs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 4), 0, 0));
+  };
+
+  f32x4 acc[2];
+  acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  issue_x(0, CS[0]);
+  issue_w(0, W[0], S[0]);
+  issue_w(groups > 1 ? 1 : 0, W[1], S[1]);
+  *reinterpret_cast<u32x4*>(&xs[0][ld_lds]) = xr;
+  __syncthreads();
+
+  const int last = groups - 1;
+  for (int g0 = 0; g0 < groups; g0 += 4) {  // groups % 4 == 0 (checked on the host)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + u;
+      issue_x(g + 1 < last ? g + 1 : last, CS[(u + 1) & 1]);
+      issue_w(g + 2 < last ? g + 2 : last, W[(u + 2) & 3], S[(u + 2) & 3]);
+      const uint8_t* xb = &xs[u & 1][rd_lds];
+      const u32x4 b0 = *reinterpret_cast<const u32x4*>(xb);
+      const u32x4 b1 = *reinterpret_cast<const u32x4*>(xb + 16);
+      const i32x8 bf = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                        (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+      const float corr = CS[u & 1] * kInvSum;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const f32x4 tmp = mfma_fp8(spread_nibbles(W[u][r]), bf);
+        float sc[4];
+        scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * (tmp[i] - corr);
+      }
+      *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
+      __syncthreads();
+    }
+  }
+
+  if (rowid < 0) return;
+  const float mult = kUnScale * p.act_scale[arow];
+  if constexpr (STAGE == 1) {
+    const float lim = p.clamp_limit;
+    uint32_t bits[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float gt = acc[0][i] * mult;
+      float up = acc[1][i] * mult;
+      if (lim > 0.0f) {
+        gt = fminf(gt, lim);
+        up = fminf(fmaxf(up, -lim), lim);
+      }
+      bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+    }
+    const int n = n0 + 16 * wave + 4 * (lane >> 4);
+    *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) =
+        u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+  } else {
+    const float wm = (rowid < tk ? p.route_w[rowid] : 1.0f) * mult;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int n = n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
+      const f32x4 v = {acc[r][0] * wm, acc[r][1] * wm, acc[r][2] * wm, acc[r][3] * wm};
+      *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+    }
+  }
+}
+
+// ----------------------------------------------------------------- prefill
+// Blocks of up to 64 slots: workgroup tile 64 slots x 256 weight rows, the
+// same strip assignment and XCD-aware order as the bf16 prefill kernel.  Per
+// group the 64 x 128 B token tile (16-byte part q of slot s at q ^ (s & 7)),
+// the slots' group sums and each wavefront's 4 weight tiles and scales are
+// copied into LDS by buffer_load ... lds, double buffered.
+constexpr int kF8Slots = 64;
+
+template <int STAGE>
+__global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmParams p, int total_blocks) {
+  constexpr int R = 4;
+  constexpr int C = 4;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kF8Slots * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];
+  __shared__ float xsum[2][kF8Slots];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  const int xcd = blockIdx.x % kXcds;
+  const int jj = blockIdx.x / kXcds;
+  const int blk = (jj / p.n_tiles) * kXcds + xcd;
+  const int tile = jj % p.n_tiles;
+  if (blk >= total_blocks) return;
+  const int64_t tk = p.tokens * p.topk;
+  const BlockInfo b = block_info(p, blk);
+  if (!b.active) return;
+
+  const int groups = p.k_dim / kGroup;
+  const int n0 = STAGE == 1 ? tile * 128 : tile * 256;
+  const int p0 = tile * 8 + 2 * wave;
+
+  const uint8_t* act = reinterpret_cast<const uint8_t*>(p.act);
+  const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)act, (short)0, (int)(p.act_rows * p.k_dim), kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act_sum, (short)0, (int)(p.act_rows * groups * 4), kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.wq + (int64_t)b.expert * p.wq_stride), (short)0, (int)p.wq_stride, kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.ws + (int64_t)b.expert * p.ws_stride), (short)0, (int)(p.ws_stride * 2), kRsrcFlags);
+
+  // token tile: DMA q (0..1) of wave w fills slots 16w + 8q + lane/8
+  uint32_t dma_off[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = 16 * wave + 8 * q + (lane >> 3);
+    const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, row, tk), tk, p.topk);
+    const int part = (lane & 7) ^ (row & 7);
+    dma_off[q] = ar >= 0 ? (uint32_t)(ar * p.k_dim + part * 16) : kOobOffset;
+  }
+  uint32_t sum_off = kOobOffset;
+  if (wave == 0) {
+    const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, lane, tk), tk, p.topk);
+    if (ar >= 0) sum_off = (uint32_t)(ar * groups * 4);
+  }
+  const uint32_t w_off0 = (uint32_t)(p0 * groups) * 2048 + lane * 16;
+  const uint32_t w_off1 = (uint32_t)((p0 + 1) * groups) * 2048 + lane * 16;
+  const uint32_t s_off = lane < 32 ? (uint32_t)((p0 + (lane >> 4)) * groups) * 64 + (lane & 15) * 4 : kOobOffset;
+
+  auto issue = [&](int g, int buf) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      lds_dma16(act_rsrc, (lds_void_ptr)&xs[buf][(16 * wave + 8 * q) * 128], dma_off[q], g * 128);
+    lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][0], w_off0, g * 2048);
+    lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][kTileBytes], w_off0 + kTileBytes, g * 2048);
+    lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][2 * kTileBytes], w_off1, g * 2048);
+    lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][3 * kTileBytes], w_off1 + kTileBytes, g * 2048);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_void_ptr)&scl[buf][wave][0], 4, s_off, g * 64, 0, 0);
+    if (wave == 0)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sum_rsrc, (lds_void_ptr)&xsum[buf][0], 4, sum_off, g * 4, 0, 0);
+  };
+
+  f32x4 acc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int ct = 0; ct < C; ++ct) acc[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int sw = lane & 15;
+  const int jg = lane >> 4;
+  auto step = [&](int g, auto u_c, auto prefetch_c) {
+    constexpr int u = decltype(u_c)::value;
+    if constexpr (decltype(prefetch_c)::value) issue(g + 1, (u + 1) & 1);
+    i32x8 bfr[C];
+#pragma unroll
+    for (int ct = 0; ct < C; ++ct) {
+      const int row = ct * 16 + sw;
+      const u32x4 b0 = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((2 * jg) ^ (row & 7)) * 16]);
+      const u32x4 b1 = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((2 * jg + 1) ^ (row & 7)) * 16]);
+      bfr[ct] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+    }
+    float corr[C];
+#pragma unroll
+    for (int ct = 0; ct < C; ++ct) corr[ct] = xsum[u][ct * 16 + sw] * kInvSum;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const i32x8 a = spread_nibbles(*reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]));
+      const u32x2 sv = *reinterpret_cast<const u32x2*>(&scl[u][wave][(r >> 1) * 64 + 16 * jg + 8 * (r & 1)]);
+      float sc[4];
+      scale4(sv, sc);
+      f32x4 tmp[C];
+#pragma unroll
+      for (int ct = 0; ct < C; ++ct) tmp[ct] = mfma_fp8(a, bfr[ct]);
+#pragma unroll
+      for (int ct = 0; ct < C; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * (tmp[ct][i] - corr[ct]);
+    }
+    __syncthreads();
+  };
+  using U0 = std::integral_constant<int, 0>;
+  using U1 = std::integral_constant<int, 1>;
+  using PF = std::true_type;
+  using NOPF = std::false_type;
+
+  issue(0, 0);
+  __syncthreads();
+  for (int g0 = 0; g0 + 2 < groups; g0 += 2) {
+    step(g0, U0{}, PF{});
+    step(g0 + 1, U1{}, PF{});
+  }
+  step(groups - 2, U0{}, PF{});
+  step(groups - 1, U1{}, NOPF{});
+
+#pragma unroll
+  for (int ct = 0; ct < C; ++ct) {
+    const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
+    if (rowid < 0) continue;
+    const int64_t arow = act_row_of<STAGE>(rowid, tk, p.topk);
+    const float mult = kUnScale * p.act_scale[arow];
+    if constexpr (STAGE == 1) {
+      const float lim = p.clamp_limit;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        uint32_t bits[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float gt = acc[2 * s][ct][i] * mult;
+          float up = acc[2 * s + 1][ct][i] * mult;
+          if (lim > 0.0f) {
+            gt = fminf(gt, lim);
+            up = fminf(fmaxf(up, -lim), lim);
+          }
+          bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+        }
+        const int n = n0 + 32 * wave + 16 * s + 4 * jg;
+        *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) =
+            u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+      }
+    } else {
+      const float wm = (rowid < tk ? p.route_w[rowid] : 1.0f) * mult;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int n = n0 + 64 * wave + 16 * r + 4 * jg;
+        const f32x4 v = {acc[r][ct][0] * wm, acc[r][ct][1] * wm, acc[r][ct][2] * wm, acc[r][ct][3] * wm};
+        *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+      }
+    }
+  }
+}
+
+static void launch_act_quant(const uint16_t* x, int64_t rows, int k, uint8_t* q, float* scale, float* gsum,
+                             hipStream_t stream) {
+  hipLaunchKernelGGL(act_quant_fp8_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, x, rows, k,
+                     q, scale, gsum);
+}
+
+static void launch_fp8_stage(const ExpertGemmParams& p, bool decode, int stage, int blocks, hipStream_t stream) {
+  if (decode) {
+    const dim3 grid((unsigned)(p.n_tiles * blocks));
+    if (stage == 1) hipLaunchKernelGGL(expert_fp8_decode_kernel<1>, grid, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL(expert_fp8_decode_kernel<2>, grid, dim3(256), 0, stream, p);
+  } else {
+    const int xcd_blocks = (blocks + kXcds - 1) / kXcds * kXcds;
+    const dim3 grid((unsigned)(p.n_tiles * xcd_blocks));
+    if (stage == 1) hipLaunchKernelGGL(expert_fp8_prefill_kernel<1>, grid, dim3(256), 0, stream, p, blocks);
+    else hipLaunchKernelGGL(expert_fp8_prefill_kernel<2>, grid, dim3(256), 0, stream, p, blocks);
+  }
+}
+
+}  // namespace dsv4
+
+using namespace dsv4;
+
+struct Fp8Workspace {
+  uint8_t* xq;
+  float* xscale;
+  float* xsum;
+  uint16_t* h;
+  uint8_t* hq;
+  float* hscale;
+  float* hsum;
+  float* contrib;
+  size_t bytes;
+};
+
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static Fp8Workspace carve_fp8(void* base, int64_t tokens, int topk, int hidden, int inter, int has_shared) {
+  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
+  char* b = static_cast<char*>(base);
+  size_t off = 0;
+  Fp8Workspace w;
+  w.xq = reinterpret_cast<uint8_t*>(b + off);
+  off += al256((size_t)tokens * hidden);
+  w.xscale = reinterpret_cast<float*>(b + off);
+  off += al256(sizeof(float) * (size_t)tokens);
+  w.xsum = reinterpret_cast<float*>(b + off);
+  off += al256(sizeof(float) * (size_t)tokens * (hidden / kGroup));
+  w.h = reinterpret_cast<uint16_t*>(b + off);
+  off += al256(sizeof(uint16_t) * (size_t)rows * inter);
+  w.hq = reinterpret_cast<uint8_t*>(b + off);
+  off += al256((size_t)rows * inter);
+  w.hscale = reinterpret_cast<float*>(b + off);
+  off += al256(sizeof(float) * (size_t)rows);
+  w.hsum = reinterpret_cast<float*>(b + off);
+  off += al256(sizeof(float) * (size_t)rows * (inter / kGroup));
+  w.contrib = reinterpret_cast<float*>(b + off);
+  off += al256(sizeof(float) * (size_t)rows * hidden);
+  w.bytes = off;
+  return w;
+}
+
+size_t dsv4_experts_w4a8_workspace_bytes(int64_t tokens, int topk, int hidden, int inter, int has_shared) {
+  return carve_fp8(nullptr, tokens, topk, hidden, inter, has_shared).bytes;
+}
+
+int dsv4_launch_act_quant_fp8(const uint16_t* x, int64_t rows, int k, uint8_t* q, float* scale, float* gsum,
+                              hipStream_t stream) {
+  if (rows == 0) return DSV4MOE_OK;
+  launch_act_quant(x, rows, k, q, scale, gsum, stream);
+  DSV4_CHECK_LAUNCH("act_quant_fp8_kernel");
+  return DSV4MOE_OK;
+}
+
+int dsv4_launch_experts_w4a8(const uint16_t* x, int64_t tokens, int hidden, int inter, int experts, int topk,
+                             const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
+                             const uint16_t* w2s, int has_shared, const float* weights, const int32_t* sorted,
+                             int64_t capacity, const int32_t* expert_ids, const int32_t* ntpp, int block_size,
+                             float clamp_limit, uint16_t* out, void* workspace, hipStream_t stream) {
+  if (tokens == 0) return DSV4MOE_OK;
+  Fp8Workspace ws = carve_fp8(workspace, tokens, topk, hidden, inter, has_shared);
+  const int max_blocks = (int)((capacity + block_size - 1) / block_size);
+  const bool decode = block_size <= 16 && hidden % 512 == 0 && inter % 512 == 0;
+  const int shared_bs = decode ? 16 : block_size;
+  const int shared_blocks = has_shared ? (int)((tokens + shared_bs - 1) / shared_bs) : 0;
+  const int blocks = max_blocks + shared_blocks;
+  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
+
+  launch_act_quant(x, tokens, hidden, ws.xq, ws.xscale, ws.xsum, stream);
+  DSV4_CHECK_LAUNCH("act_quant_fp8_kernel (x)");
+  dsv4host::prof_stamp(dsv4host::kStampRowSum, stream);
+
+  ExpertGemmParams p{};
+  p.sorted = sorted;
+  p.expert_ids = expert_ids;
+  p.ntpp = ntpp;
+  p.block_size = block_size;
+  p.shared_block_size = shared_bs;
+  p.max_blocks = max_blocks;
+  p.tokens = tokens;
+  p.topk = topk;
+  p.shared_expert = has_shared ? experts : -1;
+  p.clamp_limit = clamp_limit;
+  p.inter = inter;
+
+  p.wq = w13q;
+  p.ws = w13s;
+  p.wq_stride = (int64_t)2 * inter * hidden / 2;
+  p.ws_stride = (int64_t)2 * inter * (hidden / kGroup);
+  p.k_dim = hidden;
+  p.act = reinterpret_cast<const uint16_t*>(ws.xq);
+  p.act_rows = tokens;
+  p.act_sum = ws.xsum;
+  p.act_scale = ws.xscale;
+  p.h_out = ws.h;
+  p.n_tiles = decode ? inter / 64 : inter / 128;
+  launch_fp8_stage(p, decode, 1, blocks, stream);
+  DSV4_CHECK_LAUNCH("expert fp8 stage 1");
+
+  launch_act_quant(ws.h, rows, inter, ws.hq, ws.hscale, ws.hsum, stream);
+  DSV4_CHECK_LAUNCH("act_quant_fp8_kernel (h)");
+  dsv4host::prof_stamp(dsv4host::kStampStage1, stream);
+
+  p.wq = w2q;
+  p.ws = w2s;
+  p.wq_stride = (int64_t)hidden * inter / 2;
+  p.ws_stride = (int64_t)hidden * (inter / kGroup);
+  p.k_dim = inter;
+  p.act = reinterpret_cast<const uint16_t*>(ws.hq);
+  p.act_rows = rows;
+  p.act_sum = ws.hsum;
+  p.act_scale = ws.hscale;
+  p.route_w = weights;
+  p.contrib = ws.contrib;
+  p.out_cols = hidden;
+  p.n_tiles = decode ? hidden / 128 : hidden / 256;
+  launch_fp8_stage(p, decode, 2, blocks, stream);
+  DSV4_CHECK_LAUNCH("expert fp8 stage 2");
+  dsv4host::prof_stamp(dsv4host::kStampStage2, stream);
+
+  const int rc = dsv4_launch_combine(ws.contrib, tokens, topk, hidden, has_shared, out, stream);
+  if (rc != DSV4MOE_OK) return rc;
+  dsv4host::prof_stamp(dsv4host::kStampCombine, stream);
+  return DSV4MOE_OK;
+}

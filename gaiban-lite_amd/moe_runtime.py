@@ -258,8 +258,8 @@ class TP4MoE:
                 f"resident input dtype {getattr(resident, 'marlin_input_dtype', None)!r} "
                 f"does not match requested {marlin_input_dtype!r}"
             )
-        if marlin_input_dtype is not None:
-            raise NotImplementedError("the W4A8 layer path is provided by experts_w4a8 (not yet wired)")
+        if marlin_input_dtype is not None and (config.hidden_size % 512 or config.intermediate_size % 512):
+            raise ValueError("W4A8 needs hidden and intermediate sizes that are multiples of 512")
         if not isinstance(resident, ResidentInt4MoEWeights):
             raise TypeError("resident must be ResidentInt4MoEWeights")
         resident.validate()
@@ -350,9 +350,8 @@ class TP4MoE:
             return
         bs = ops.block_size_m(rows, cfg.topk, cfg.experts, 1 if self._marlin_input_dtype else 2)
         template = torch.empty(rows, cfg.topk, dtype=torch.int32, device=self.device)
-        ws_bytes = ops.experts_workspace_bytes(
-            rows, cfg.topk, cfg.hidden_size, cfg.intermediate_size, bool(cfg.shared_experts)
-        )
+        ws_fn = ops.experts_w4a8_workspace_bytes if self._marlin_input_dtype else ops.experts_workspace_bytes
+        ws_bytes = ws_fn(rows, cfg.topk, cfg.hidden_size, cfg.intermediate_size, bool(cfg.shared_experts))
         self._buffers[key] = _LayerBuffers(
             workspace=torch.empty(ws_bytes, dtype=torch.uint8, device=self.device),
             logits=torch.empty(rows, cfg.experts, dtype=torch.float32, device=self.device),
@@ -581,6 +580,7 @@ class TP4MoE:
                 a = buffers.alignment
                 fused = (
                     self.route_kind == "learned"
+                    and self._marlin_input_dtype is None
                     and override is None
                     and self._owned_alignment_provider is None
                     and self._route_tensor_observer is None
@@ -657,7 +657,8 @@ class TP4MoE:
                     if aligned is not a:
                         self._poison_alignment_runtime()
                         raise RuntimeError("alignment provider must return the caller-owned output")
-                ops.experts_w4a16_into(
+                experts_into = ops.experts_w4a8_into if self._marlin_input_dtype else ops.experts_w4a16_into
+                experts_into(
                     flat, w13q=self.resident.w13_q, w13s=self.resident.w13_s,
                     w2q=self.resident.w2_q, w2s=self.resident.w2_s, experts=cfg.experts,
                     inter=cfg.intermediate_size, has_shared=bool(cfg.shared_experts),

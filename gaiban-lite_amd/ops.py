@@ -195,7 +195,37 @@ def experts_workspace_bytes(tokens: int, topk: int, hidden: int, inter: int, has
     return int(_lib.load().dsv4moe_experts_workspace_bytes(tokens, topk, hidden, inter, int(bool(has_shared))))
 
 
-def experts_w4a16_into(
+def experts_w4a8_workspace_bytes(tokens: int, topk: int, hidden: int, inter: int, has_shared: bool) -> int:
+    return int(_lib.load().dsv4moe_experts_w4a8_workspace_bytes(tokens, topk, hidden, inter,
+                                                                  int(bool(has_shared))))
+
+
+def act_quant_fp8_into(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor, group_sums: torch.Tensor) -> None:
+    """Per-row e4m3 quantisation (q in the fp8 MFMA byte order, see
+    ``dsv4moe_act_quant_fp8``)."""
+
+    rows, k = x.shape
+    dev = x.device
+    _check("x", x, dtype=torch.bfloat16, device=dev)
+    _check("q", q, dtype=torch.uint8, shape=(rows, k), device=dev)
+    _check("scale", scale, dtype=torch.float32, shape=(rows,), device=dev)
+    _check("group_sums", group_sums, dtype=torch.float32, shape=(rows, k // GROUP), device=dev)
+    call("dsv4moe_act_quant_fp8", ptr(x), rows, k, ptr(q), ptr(scale), ptr(group_sums),
+         _lib.current_stream(dev))
+
+
+def experts_w4a8_into(x: torch.Tensor, **kw) -> None:
+    """W4A8 counterpart of ``experts_w4a16_into`` (same keywords)."""
+
+    _experts_into("dsv4moe_experts_w4a8", x, **kw)
+
+
+def experts_w4a16_into(x: torch.Tensor, **kw) -> None:
+    _experts_into("dsv4moe_experts_w4a16", x, **kw)
+
+
+def _experts_into(
+    entry: str,
     x: torch.Tensor,
     *,
     w13q, w13s, w2q, w2s,
@@ -219,7 +249,7 @@ def experts_w4a16_into(
     _check("route_weights", route_weights, dtype=torch.float32, shape=(tokens, topk), device=dev)
     _check("workspace", workspace, dtype=torch.uint8, device=dev)
     call(
-        "dsv4moe_experts_w4a16", ptr(x), tokens, hidden, inter, experts, topk, ptr(w13q),
+        entry, ptr(x), tokens, hidden, inter, experts, topk, ptr(w13q),
         ptr(w13s), ptr(w2q), ptr(w2s), int(bool(has_shared)), ptr(route_weights),
         ptr(sorted_token_ids), sorted_token_ids.numel(), ptr(expert_ids),
         ptr(num_tokens_post_padded), block_size, float(clamp_limit), ptr(out), ptr(workspace),

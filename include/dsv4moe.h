@@ -222,6 +222,43 @@ int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, con
                          const uint16_t* ws, int32_t split_k, float* workspace,
                          size_t workspace_bytes, uint16_t* out, void* stream);
 
+/*
+ * W4A8 variant of dsv4moe_experts_w4a16 on the gfx950 fp8 MFMA
+ * (v_mfma_scale_f32_16x16x128_f8f6f4, unit block scales).  Replaces the vLLM
+ * _fused_marlin_moe call with input_dtype = float8_e4m3fn
+ * (runtime/dsv4_direct/moe_runtime.py:1829-1856) and its per-token activation
+ * quantiser (_preset_w4a8_activation_quant, :207-235): x and the bf16 SwiGLU
+ * output h are each quantised per row to OCP e4m3 (s = max(amax, 1e-12)/448,
+ * q = e4m3(clamp(v/s, -448, 448)), round to nearest even) before their GEMM.
+ * Same arguments, weights (the tiled int4 layout) and output as the W4A16
+ * entry point; workspace from dsv4moe_experts_w4a8_workspace_bytes.
+ * hidden % 512 == 0, inter % 512 == 0.
+ */
+size_t dsv4moe_experts_w4a8_workspace_bytes(int64_t tokens, int32_t topk, int32_t hidden,
+                                            int32_t inter, int32_t has_shared);
+int dsv4moe_experts_w4a8(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
+                         int32_t experts, int32_t topk, const uint8_t* w13q, const uint16_t* w13s,
+                         const uint8_t* w2q, const uint16_t* w2s, int32_t has_shared,
+                         const float* weights, const int32_t* sorted_token_ids, int64_t capacity,
+                         const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                         int32_t block_size, float clamp_limit, uint16_t* out, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/*
+ * Per-row fp8 activation quantiser used by dsv4moe_experts_w4a8
+ * (moe_runtime.py:229-232):
+ *   x           bf16 [rows, k]
+ *   q           e4m3 [rows, k] out, each 128-column group stored in the fp8
+ *               MFMA order: byte j*32 + d*8 + b holds column 32d + 8j + P[b],
+ *               P = {0,4,1,5,2,6,3,7}, j, d in 0..3
+ *   scale       fp32 [rows] out: max(amax, 1e-12) / 448
+ *   group_sums  fp32 [rows, k/128] out: sum of the decoded e4m3 values of
+ *               each group (the kernels' offset correction)
+ * k % 512 == 0.
+ */
+int dsv4moe_act_quant_fp8(const uint16_t* x, int64_t rows, int32_t k, uint8_t* q, float* scale,
+                          float* group_sums, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
