@@ -35,6 +35,13 @@ What pins each function (checked in ``tests/test_oracle_*.py``):
   of ``runtime/c2f_moe_combine_gate.py:54-84`` on a large sample.
 * ``w8a16_linear_f32`` / ``automatic_split_k`` -- scalar loop on tiny shapes;
   split-K policy known answers from ``weight_only_linear.py:168-179``.
+* ``act_quant_per_token_fp8`` -- torch's ``float8_e4m3fn`` cast of the same
+  scaled, clamped values; ``moe_w4a8_f32`` -- a float64 pipeline built on that
+  torch cast (quantised x, bf16 SwiGLU, quantised h, weight on the w2 output,
+  shared expert) on tiny shapes.
+* ``hash_route`` -- its closed form (table gather, renormalised sqrt-softplus).
+* ``moe_bf16_mirror`` -- the CPU baseline, not a checker: within 1e-2 of
+  ``moe_fp32`` and outputs on the bf16 grid (parity unpinned beyond that).
 """
 
 from __future__ import annotations

@@ -135,3 +135,39 @@ def test_w8a16_oracle_and_split_k_policy():
     assert O.automatic_split_k(1, 1024, 1024) == 1      # 8 K blocks
     assert O.automatic_split_k(64, 16384, 4096) == 1
     assert O.automatic_split_k(8192, 4096, 4096) == 1
+
+
+def test_moe_w4a8_oracle_against_torch_fp8_pipeline():
+    """W4A8 oracle vs an independent float64 pipeline whose fp8 rounding is
+    torch's float8_e4m3fn cast: per-token quant of x, fp32->bf16 SwiGLU,
+    per-row quant of h, route weight on the w2 output, shared expert weight 1."""
+
+    import torch
+
+    rng = np.random.default_rng(9)
+    e, h, i, t, k = 3, 128, 128, 5, 2
+    src = _tiny_source(rng, e + 1, h, i)
+    x = O.bf16_round((rng.standard_normal((t, h)) * 3).astype(np.float32))
+    ids = np.array([[0, 2], [1, 0], [2, 1], [0, 1], [2, 0]])
+    w = rng.uniform(0.1, 1.0, size=(t, k)).astype(np.float32)
+    got = O.moe_w4a8_f32(x, ids, w, src, shared_index=e, clamp_limit=0.4)
+
+    def quant(v):
+        v = torch.from_numpy(np.asarray(v, dtype=np.float32))
+        s = v.abs().amax(-1, keepdim=True).clamp_min(1e-12) / 448.0
+        q = (v / s).clamp(-448, 448).to(torch.float8_e4m3fn).to(torch.float64)
+        return (q * s.double()).numpy()
+
+    xd = quant(x)
+    ref = np.zeros((t, h))
+    for tok in range(t):
+        pairs = [(ids[tok, j], float(w[tok, j])) for j in range(k)] + [(e, 1.0)]
+        for ex, weight in pairs:
+            w13 = src.w13(ex).astype(np.float64)
+            g = np.minimum(xd[tok] @ w13[:i].T, 0.4)
+            u = np.clip(xd[tok] @ w13[i:].T, -0.4, 0.4)
+            act = torch.from_numpy((g / (1 + np.exp(-g)) * u).astype(np.float32)).to(torch.bfloat16).float().numpy()
+            ref[tok] += (quant(act[None])[0] @ src.w2(ex).astype(np.float64).T) * weight
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    # the quantisation is not the identity: the W4A8 result differs from the W4A16 one
+    assert O.rel_fro(got, O.moe_fp32(x, ids, w, src, shared_index=e, clamp_limit=0.4)) > 1e-3
