@@ -10,11 +10,18 @@ activations ~ N(0,1), router logits ~ N(0,1), T = 64 tokens per step.
 A step is one ``TP4MoE.forward_tensor`` call (router from the logits ->
 alignment -> grouped w13 + SwiGLU -> grouped w2 x route weight -> combine with
 the shared expert -> owning output clone) with inputs resident in HBM.  Inputs
-rotate through a pool of seeded batches so every step routes differently.
+rotate through a pool of seeded batches so every step routes differently (a
+fixed-routing figure is reported beside it).
 
-Also reported (secondary, same line): the 8192-token prefill of the same
-layer, and the CPU baseline (the oracle's restatement of the reference torch
-path timed on this host's cores on a bounded sample).
+Also reported on the same line (secondary): decode at T in {1, 8, 256},
+prefill at T in {2048, 4096, 8192}, the W4A8 layer (uniform and Zipf routing,
+T = 64 and 8192), the W8A16 dense linear at K = 4096, and the CPU baseline
+(the oracle's restatement of the reference torch path timed on this host's
+cores on a bounded sample).
+
+``--copy-calibration`` instead runs a plain 512 MiB device copy (torch
+``copy_``) 5 times: the reference kernel for scaling the FETCH_SIZE /
+WRITE_SIZE counters of a ``rocprofv3 --pmc`` run to bytes.
 """
 
 from __future__ import annotations
@@ -23,6 +30,7 @@ import argparse
 import importlib
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -34,6 +42,8 @@ if str(ROOT) not in sys.path:
 METRIC = "MoE layer tokens/s; decode HBM GB/s and prefill MFMA TFLOP/s as % of peak"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+TRAFFIC_PROFILE = ROOT / "profiles" / "expert_decode_w13_T64_hbm_traffic.md"
 
 
 def log(*a):
@@ -47,12 +57,56 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--pool", type=int, default=16)
-    ap.add_argument("--prefill-tokens", type=int, default=8192, help="0 skips the prefill line")
+    ap.add_argument("--prefill-tokens", type=int, default=8192, help="0 skips the prefill lines")
     ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--secondary", type=int, default=1, help="0 skips the extra decode/prefill/W4A8/W8A16 lines")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline")
     ap.add_argument("--cpu-tokens", type=int, default=64)
+    ap.add_argument("--cpu-batches", type=int, default=6)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-calibration", action="store_true")
     return ap.parse_args()
+
+
+def copy_calibration() -> int:
+    import torch
+
+    n = 512 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": n, "launches": 5}), flush=True)
+    return 0
+
+
+def traffic_from_profile():
+    """HBM bytes per stage-1 decode launch measured by the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch\s*=\s*([0-9]+)", text)
+    return int(m.group(1)) if m else None
+
+
+def cuda_timer(fn, n):
+    import torch
+
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(n):
+        fn(i)
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / n
 
 
 def main() -> int:
@@ -64,6 +118,8 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if args.copy_calibration:
+        return copy_calibration()
     import numpy as np
     import torch
 
@@ -83,82 +139,100 @@ def main() -> int:
                            route_scale=1.0, clamp_limit=0.0, score_func="sigmoid", shared_experts=1)
     gate_w = (torch.randn(E, H, device=dev) * 0.02).to(torch.bfloat16)
     gate = pkg.ResidentGateWeights(weight=gate_w)
-    rows = [T] + ([args.prefill_tokens] if args.prefill_tokens else [])
+    decode_ts = [T] + ([1, 8, 256] if args.secondary else [])
+    prefill_ts = []
+    if args.prefill_tokens:
+        prefill_ts = [args.prefill_tokens] + ([2048, 4096] if args.secondary else [])
+    rows = sorted(set(decode_ts + prefill_ts))
     layer = pkg.TP4MoE(config=cfg, resident=resident, gate=gate, device=dev, global_row_shapes=rows)
     b_e = pkg.int4_g128_expert_bytes(H, I)
     b13 = 2 * I * H // 2 + 2 * I * (H // 128) * 2
 
+    def layer_bytes(t, d):
+        return (d + 1) * b_e + 2 * t * H * 2 + t * E * 4 + t * K * 8
+
+    def pools(t, n, base):
+        xs = [S.make_hidden(t, H, seed=base + i, device=dev).view(1, t, H) for i in range(n)]
+        lgs = [S.make_logits(t, E, seed=base + 500 + i, device=dev) for i in range(n)]
+        d = [int(torch.unique(pkg.route_from_logits(lg, topk=K, score_func="sigmoid").routing_ids).numel())
+             for lg in lgs]
+        return xs, lgs, d
+
     # ------------------------------------------------------------- decode
-    xs = [S.make_hidden(T, H, seed=1000 + i, device=dev).view(1, T, H) for i in range(args.pool)]
-    lgs = [S.make_logits(T, E, seed=2000 + i, device=dev) for i in range(args.pool)]
-    distinct = []
-    for lg in lgs:
-        ids = pkg.route_from_logits(lg, topk=K, score_func="sigmoid").routing_ids
-        distinct.append(int(torch.unique(ids).numel()))
+    xs, lgs, distinct = pools(T, args.pool, 1000)
     for i in range(args.warmup):
         layer.forward_tensor(xs[i % args.pool], router_logits=lgs[i % args.pool])
     torch.cuda.synchronize()
 
-    def timed(nsteps, profile):
-        if profile:
-            ops.profile_begin(nsteps)
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0.record()
-        for i in range(nsteps):
-            layer.forward_tensor(xs[i % args.pool], router_logits=lgs[i % args.pool])
-        t1.record()
-        torch.cuda.synchronize()
-        prof = ops.profile_end() if profile else (None, 0)
-        return t0.elapsed_time(t1) / nsteps, prof
+    def step(i):
+        layer.forward_tensor(xs[i % args.pool], router_logits=lgs[i % args.pool])
 
-    ms, (kern, ncalls) = timed(args.steps, True)
-    ms_plain, _ = timed(args.steps, False)
+    ops.profile_begin(args.steps)
+    ms = cuda_timer(step, args.steps)
+    kern, ncalls = ops.profile_end()
+    ms_plain = cuda_timer(step, args.steps)
+    ms_fixed = cuda_timer(lambda i: layer.forward_tensor(xs[0], router_logits=lgs[0]), args.steps)
     d_mean = float(np.mean([distinct[i % args.pool] for i in range(args.steps)]))
-    layer_bytes = (d_mean + 1) * b_e + 2 * T * H * 2 + T * E * 4 + T * K * 8
     stage1_bytes = (d_mean + 1) * b13 + T * H * 2 + (T * K + T) * I * 2
     st1_ms = kern["stage1_w13"]
     achieved = stage1_bytes / (st1_ms * 1e-3) / 1e9
-    log(f"[bench] decode T={T}: {ms:.4f} ms/step profiled, {ms_plain:.4f} ms/step plain; kernels {kern}")
+    log(f"[bench] decode T={T}: {ms:.4f} ms/step profiled, {ms_plain:.4f} plain, {ms_fixed:.4f} fixed routing; "
+        f"kernels {kern}")
+
+    secondary = {}
+    if args.secondary:
+        dec = {}
+        for t in decode_ts[1:]:
+            xt, lt, dt_ = pools(t, 8, 4000 + t)
+            for i in range(5):
+                layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8])
+            n = 100
+            ms_t = cuda_timer(lambda i: layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8]), n)
+            dm = float(np.mean(dt_))
+            gbs = layer_bytes(t, dm) / (ms_t * 1e-3) / 1e9
+            dec[str(t)] = {"ms_per_step": round(ms_t, 4), "tokens_per_s": round(t / (ms_t * 1e-3), 1),
+                           "distinct_experts_mean": round(dm, 1), "layer_hbm_gbs": round(gbs, 1),
+                           "layer_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            log(f"[bench] decode T={t}: {dec[str(t)]}")
+        secondary["decode_other_T"] = dec
 
     # ------------------------------------------------------------- prefill
     prefill = None
-    if args.prefill_tokens:
-        TP = args.prefill_tokens
-        xp = S.make_hidden(TP, H, seed=3000, device=dev).view(1, TP, H)
-        lp = S.make_logits(TP, E, seed=3001, device=dev)
-        for _ in range(2):
-            layer.forward_tensor(xp, router_logits=lp)
-        torch.cuda.synchronize()
-        ops.profile_begin(args.prefill_steps)
-        p0 = torch.cuda.Event(enable_timing=True)
-        p1 = torch.cuda.Event(enable_timing=True)
-        p0.record()
-        for _ in range(args.prefill_steps):
-            layer.forward_tensor(xp, router_logits=lp)
-        p1.record()
-        torch.cuda.synchronize()
-        pk, _ = ops.profile_end()
-        pms = p0.elapsed_time(p1) / args.prefill_steps
-        flops = 6.0 * TP * (K + 1) * H * I
-        mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
-        prefill = {
-            "tokens": TP,
-            "ms_per_step": round(pms, 4),
-            "tokens_per_s": round(TP / (pms * 1e-3), 1),
-            "layer_tflops": round(flops / (pms * 1e-3) / 1e12, 2),
-            "layer_frac_of_bf16_peak": round(flops / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-            "grouped_gemm_tflops": round(flops / (mm_ms * 1e-3) / 1e12, 2),
-            "kernel_ms": {k: round(v, 4) for k, v in pk.items()},
-        }
-        log(f"[bench] prefill T={TP}: {prefill}")
+    if prefill_ts:
+        prefill = {}
+        for tp in prefill_ts:
+            xp = S.make_hidden(tp, H, seed=3000, device=dev).view(1, tp, H)
+            lp = S.make_logits(tp, E, seed=3001, device=dev)
+            for _ in range(2):
+                layer.forward_tensor(xp, router_logits=lp)
+            ops.profile_begin(args.prefill_steps)
+            pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps)
+            pk, _ = ops.profile_end()
+            flops = 6.0 * tp * (K + 1) * H * I
+            mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
+            entry = {
+                "ms_per_step": round(pms, 4),
+                "tokens_per_s": round(tp / (pms * 1e-3), 1),
+                "layer_tflops": round(flops / (pms * 1e-3) / 1e12, 2),
+                "layer_frac_of_bf16_peak": round(flops / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                "grouped_gemm_tflops": round(flops / (mm_ms * 1e-3) / 1e12, 2),
+                "kernel_ms": {k: round(v, 4) for k, v in pk.items()},
+            }
+            prefill[str(tp)] = entry
+            log(f"[bench] prefill T={tp}: {entry}")
+            del xp, lp
+
+    # -------------------------------------------------------- W4A8 and W8A16
+    if args.secondary:
+        secondary["w4a8"] = bench_w4a8(pkg, resident, gate, cfg, dev, T, args)
+        secondary["w8a16_linear"] = bench_w8a16(pkg, dev)
 
     # ------------------------------------------------------------ CPU baseline
     cpu = None
     if args.cpu_baseline:
-        cpu = cpu_baseline(pkg, w13, s13, w2, s2, lgs[0], xs[0].view(T, H), args.cpu_tokens, E, K)
+        cpu = cpu_baseline(pkg, w13, s13, w2, s2, lgs, xs, args.cpu_tokens, args.cpu_batches, E, K)
 
+    traffic = traffic_from_profile()
     line = {
         "metric": METRIC,
         "value": round(T / (ms * 1e-3), 1),
@@ -183,34 +257,132 @@ def main() -> int:
             "distinct_experts_mean": round(d_mean, 2),
             "parallelism": "single GPU, whole layer resident",
         },
-        "layer_hbm_gbs": round(layer_bytes / (ms * 1e-3) / 1e9, 1),
-        "layer_frac_of_hbm_peak": round(layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "layer_hbm_gbs": round(layer_bytes(T, d_mean) / (ms * 1e-3) / 1e9, 1),
+        "layer_frac_of_hbm_peak": round(layer_bytes(T, d_mean) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "ms_per_step_unprofiled": round(ms_plain, 5),
+        "ms_per_step_fixed_routing": round(ms_fixed, 5),
         "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
         "roofline": {
-            "kernel": "expert_gemm_kernel stage 1 (w13 + SwiGLU), decode",
+            "kernel": "expert_decode_kernel<1> (w13 + SwiGLU), decode T=64",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "algorithmic_bytes_per_launch": int(stage1_bytes),
             "launch_ms": round(st1_ms, 5),
             "launches_timed": ncalls,
         },
         "prefill": prefill,
+        **secondary,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
 
 
-def cpu_baseline(pkg, w13, s13, w2, s2, logits, x, tokens, E, K):
+def bench_w4a8(pkg, resident, gate, cfg, dev, T, args):
+    """W4A8 experts (fp8 activations, the same resident int4 weights) at the
+    decode T and the prefill size, uniform routing (router from logits) and
+    Zipf(1.1) routing (fixed ids); a step is route (uniform only) + alignment +
+    experts + combine, all stream-ordered launches."""
+
+    import torch
+
+    S, ops = pkg.synthetic, pkg.ops
+    E, H, I, K = cfg.experts, cfg.hidden_size, cfg.intermediate_size, cfg.topk
+    ts = [T] + ([args.prefill_tokens] if args.prefill_tokens else [])
+    out = {}
+    for t in ts:
+        x = S.make_hidden(t, H, seed=5000 + t, device=dev)
+        lg = S.make_logits(t, E, seed=5500 + t, device=dev)
+        bs = ops.block_size_m(t, K, E, 1)
+        cap = pkg.max_padded_tokens(t * K, E, bs)
+        sorted_ids = torch.empty(cap, dtype=torch.int32, device=dev)
+        expert_ids = torch.empty((cap + bs - 1) // bs, dtype=torch.int32, device=dev)
+        ntpp = torch.empty(1, dtype=torch.int32, device=dev)
+        ids = torch.empty((t, K), dtype=torch.int32, device=dev)
+        w = torch.empty((t, K), dtype=torch.float32, device=dev)
+        o = torch.empty((t, H), dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(ops.experts_w4a8_workspace_bytes(t, K, H, I, True), dtype=torch.uint8, device=dev)
+        zipf_ids = S.zipf_ids(t, E, K, seed=4, device=dev)
+        counts = torch.bincount(zipf_ids.view(-1).long(), minlength=E).float()
+        for routing in ("uniform", "zipf"):
+            def step(i):
+                if routing == "uniform":
+                    ops.route_topk_into(lg, None, topk=K, score_func="sigmoid", route_scale=1.0, ids=ids, weights=w)
+                else:
+                    ids.copy_(zipf_ids)
+                ops.align_into(ids, block_size=bs, num_experts=E, sorted_token_ids=sorted_ids,
+                               expert_ids=expert_ids, num_tokens_post_padded=ntpp)
+                ops.experts_w4a8_into(x, w13q=resident.w13_q, w13s=resident.w13_s, w2q=resident.w2_q,
+                                      w2s=resident.w2_s, experts=E, inter=I, has_shared=True, route_weights=w,
+                                      sorted_token_ids=sorted_ids, expert_ids=expert_ids,
+                                      num_tokens_post_padded=ntpp, block_size=bs, clamp_limit=0.0, out=o,
+                                      workspace=ws)
+            ops.route_topk_into(lg, None, topk=K, score_func="sigmoid", route_scale=1.0, ids=ids, weights=w)
+            for i in range(3):
+                step(i)
+            n = 50 if t <= 256 else 5
+            ops.profile_begin(n)
+            ms = cuda_timer(step, n)
+            pk, _ = ops.profile_end()
+            flops = 6.0 * t * (K + 1) * H * I
+            entry = {"ms_per_step": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1), "block_size": bs,
+                     "kernel_ms": {k: round(v, 4) for k, v in pk.items() if k not in ("route", "align")}}
+            if t > 256:
+                entry["layer_tflops"] = round(flops / (ms * 1e-3) / 1e12, 2)
+                entry["layer_frac_of_fp8_peak"] = round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)
+            if routing == "zipf":
+                entry["hottest_over_mean_load"] = round(float(counts.max() / counts.mean()), 1)
+            out[f"T{t}_{routing}"] = entry
+            log(f"[bench] w4a8 T={t} {routing}: {entry}")
+        del x, lg, o, ws
+    return out
+
+
+def bench_w8a16(pkg, dev):
+    """W8A16 dense linear, K = 4096, N in {4096, 1024, 16384}, M in {1, 64, 8192}."""
+
+    import torch
+
+    L = pkg.weight_only_linear
+    S = pkg.synthetic
+    out = {}
+    k = 4096
+    for n in (4096, 1024, 16384):
+        q, s = S.make_int8_linear(n, k, device=dev)
+        prep = L.prepare_int8_weight(q, s)
+        del q
+        for m in (1, 64, 8192):
+            a = S.make_hidden(m, k, seed=6000 + m, device=dev)
+            plan = L.make_gemm_plan(m, n, k)
+            o = torch.empty(plan.output_shape, dtype=torch.bfloat16, device=dev)
+            ws = L.allocate_workspace(plan, dev)
+            for _ in range(3):
+                L.w8a16_gemm_into(a, prep.packed, prep.scale, o, ws, plan=plan)
+            it = 50 if m < 8192 else 10
+            ms = cuda_timer(lambda i: L.w8a16_gemm_into(a, prep.packed, prep.scale, o, ws, plan=plan), it)
+            byts = n * k + 2 * n + 2 * m * k + 2 * m * n
+            fl = 2.0 * m * n * k
+            entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2),
+                     "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+            entry["frac_of_peak"] = (round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if m <= 64
+                                     else round(fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
+            entry["bound"] = "hbm" if m <= 64 else "mfma"
+            out[f"M{m}_N{n}"] = entry
+            log(f"[bench] w8a16 M={m} N={n}: {entry}")
+            del a, o, ws
+        del prep
+    return out
+
+
+def cpu_baseline(pkg, w13, s13, w2, s2, lgs, xs, tokens, batches, E, K):
     """The oracle's restatement of the reference torch MoE path
     (dense_moe.py:289-354 op order, bf16 dequant-then-matmul, plus the shared
-    expert and add), timed on the host over the first `tokens` rows of one
-    decode batch: router, alignment and all touched experts."""
+    expert and add), timed on the host over `batches` decode batches of
+    `tokens` rows each: router, alignment and all touched experts."""
 
     import numpy as np
     import torch
@@ -223,12 +395,17 @@ def cpu_baseline(pkg, w13, s13, w2, s2, logits, x, tokens, E, K):
     from threadpoolctl import threadpool_limits
 
     cores = min(os.cpu_count() or 1, 16)
-    lg = logits[:tokens].cpu().numpy()
-    xn = x[:tokens].float().cpu().numpy()
-    r = O.route_topk(lg, K, score_func=O.SCORE_SIGMOID)
-    touched = sorted(set(np.unique(r.ids).tolist()) | {E})
+    batches = min(batches, len(xs))
+    data = []
+    touched = set()
+    for b in range(batches):
+        lg = lgs[b][:tokens].cpu().numpy()
+        xn = xs[b].view(-1, xs[b].shape[-1])[:tokens].float().cpu().numpy()
+        data.append((lg, xn))
+        touched |= set(np.unique(O.route_topk(lg, K, score_func=O.SCORE_SIGMOID).ids).tolist())
+    touched |= {E}
     host = {}
-    for e in touched:  # resident weights: copied before the timed region
+    for e in sorted(touched):  # resident weights: copied before the timed region
         host[e] = (w13[e].cpu().numpy(), s13[e].contiguous().view(torch.int16).cpu().numpy().view(np.uint16),
                    w2[e].cpu().numpy(), s2[e].contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
 
@@ -245,18 +422,20 @@ def cpu_baseline(pkg, w13, s13, w2, s2, logits, x, tokens, E, K):
     src = HostSource()
     with threadpool_limits(limits=1):
         t0 = time.perf_counter()
-        rr = O.route_topk(lg, K, score_func=O.SCORE_SIGMOID)
-        O.moe_align(rr.ids, 8, E)
-        O.moe_bf16_mirror(xn, rr.ids, rr.weights, src, shared_index=E, workers=cores)
+        for lg, xn in data:
+            rr = O.route_topk(lg, K, score_func=O.SCORE_SIGMOID)
+            O.moe_align(rr.ids, 8, E)
+            O.moe_bf16_mirror(xn, rr.ids, rr.weights, src, shared_index=E, workers=cores)
         dt = time.perf_counter() - t0
-    log(f"[bench] cpu baseline: {tokens} tokens, {len(touched)} experts in {dt:.2f} s on {cores} threads")
+    total = tokens * len(data)
+    log(f"[bench] cpu baseline: {len(data)} batches x {tokens} tokens in {dt:.2f} s on {cores} threads")
     return {
-        "value": round(tokens / dt, 2),
+        "value": round(total / dt, 2),
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"one decode batch of {tokens} tokens of the same layer ({len(touched)} experts incl. shared), "
-                  "router + alignment + bf16 dequant-then-matmul experts + combine, numpy, "
+        "sample": f"{len(data)} decode batches of {tokens} tokens of the same layer (router + alignment + "
+                  "bf16 dequant-then-matmul over every touched expert incl. shared + combine), numpy, "
                   f"{dt:.2f} s wall",
     }
 
