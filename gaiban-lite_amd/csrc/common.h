@@ -38,12 +38,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // 2j+1, j = 0..3.  OR-ing a nibble into the mantissa of bf16 128.0 (0x4300)
 // gives exactly 128 + u = q + 136; the kernels remove the 136*sum(x) term with
 // the per-group activation sums.
-__device__ __forceinline__ bf16x8 dequant_biased(uint32_t w) {
+//
+// `magic` is 0x43004300 held in a VGPR (dequant_magic()): with the mask as an
+// SGPR constant each pair is then one v_and_or_b32 (gfx9 VOP3 encodings take
+// no literals and one SGPR), instead of a v_and_b32 + v_or_b32 pair.
+__device__ __forceinline__ uint32_t dequant_magic() {
+  uint32_t m;
+  asm("v_mov_b32 %0, 0x43004300" : "=v"(m));
+  return m;
+}
+__device__ __forceinline__ bf16x8 dequant_biased(uint32_t w, uint32_t magic) {
   u32x4 p;
-  p[0] = (w & 0x000F000Fu) | 0x43004300u;
-  p[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  p[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  p[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  p[0] = (w & 0x000F000Fu) | magic;
+  p[1] = ((w >> 4) & 0x000F000Fu) | magic;
+  p[2] = ((w >> 8) & 0x000F000Fu) | magic;
+  p[3] = ((w >> 12) & 0x000F000Fu) | magic;
   return __builtin_bit_cast(bf16x8, p);
 }
 constexpr float kDequantBias = 136.0f;
@@ -58,6 +67,15 @@ __device__ __forceinline__ u32x4 load16(const void* p) {
 __device__ __forceinline__ u32x4 load16_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
+
+// LDS tiles of 16-row groups read with ds_read_b128 by lanes (row = lane % 16,
+// part = f(lane / 16)) are swizzled so that every 8-lane and every 16-lane
+// group of one read touches distinct 16-byte bank slots (measured with
+// SQ_LDS_BANK_CONFLICT on gfx950; padding rows to 144 or 272 bytes does not
+// achieve this):
+//   256-byte rows: 16-byte part q of row r at q ^ (r & 15);
+//   128-byte rows: part q of row r at q ^ swz128(r).
+__device__ __forceinline__ int swz128(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // buffer_load ... lds of `size` bytes per lane (M0 = lds base, lane i writes
 // base + i*size).  Wrapped in a plain function so that template kernels whose

@@ -12,9 +12,10 @@
 //            (moe_runtime.py:1857,1873 with a single fp32 accumulation).
 //
 // Arithmetic per quantisation group g (128 K values) of weight row n and
-// token column t:  the MFMA sums (q + 136) * x (dequant_biased), the kernel
-// subtracts 136 * sum_g(x) (from the precomputed 64-wide row sums, added in a
-// fixed order) and accumulates s[n, g] * partial in fp32.
+// token column t:  the MFMA chain starts from -136 * sum_g(x) (from the
+// precomputed 64-wide row sums, added in a fixed order) and sums
+// (q + 136) * x (dequant_biased), which leaves sum_g(q * x); the kernel
+// accumulates s[n, g] times it in fp32.
 //
 // Two kernels share this arithmetic:
 //  * expert_decode_kernel (alignment blocks of <= 16 token slots): one
@@ -40,12 +41,11 @@ namespace dsv4 {
 // The 16 token slots x 128 K of the current group live in LDS (double
 // buffered, one barrier per group): every thread loads 16 bytes per group,
 // every wavefront reads its four MFMA B fragments with ds_read_b128.
-constexpr int kXsRowBytes = 272;  // 256 B of bf16 + 16 B pad (conflict-free b128 reads)
 
 template <int STAGE>
 __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) {
   constexpr int R = 2;
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * kXsRowBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * 256];  // part q of slot s at q ^ s
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int tile = blockIdx.x % p.n_tiles;
@@ -76,8 +76,10 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
   const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
   const uint32_t ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + ld_part * 16) : kOobOffset;
   const uint32_t sum_base = arow >= 0 ? (uint32_t)(arow * sums_per_row * 4) : kOobOffset;
-  const int ld_lds = ld_slot * kXsRowBytes + ld_part * 16;
-  const int rd_lds = (lane & 15) * kXsRowBytes + 16 * (lane >> 4);
+  const int ld_lds = ld_slot * 256 + ((ld_part ^ ld_slot) * 16);
+  int rd_lds[4];  // K step d: part 4d + lane/16 of slot lane % 16
+#pragma unroll
+  for (int d = 0; d < 4; ++d) rd_lds[d] = (lane & 15) * 256 + (((4 * d + (lane >> 4)) ^ (lane & 15)) * 16);
 
   // Steady state: activations + sums one group ahead (ring 2), weights two
   // groups ahead (ring 4); prefetch indices are clamped to the last group so
@@ -101,6 +103,7 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
   f32x4 acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t magic = dequant_magic();
 
   issue_x(0, CS[0]);
   issue_w(0, W[0], S[0]);
@@ -115,23 +118,22 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
       const int g = g0 + u;
       issue_x(g + 1 < last ? g + 1 : last, CS[(u + 1) & 1]);
       issue_w(g + 2 < last ? g + 2 : last, W[(u + 2) & 3], S[(u + 2) & 3]);
-      const uint8_t* xb = &xs[u & 1][rd_lds];
-      const float corr = kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
+      // the MFMA chain starts from -136 * sum_g(x): it yields sum_g(q * x) directly
+      const float nc = -kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
+      const f32x4 init = {nc, nc, nc, nc};
       f32x4 tmp[R];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(xb + 64 * d));
+        const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds[d]]));
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-          tmp[r] = mfma_bf16(dequant_biased(W[u][r][d]), bfr,
-                             d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[r]);
+        for (int r = 0; r < R; ++r) tmp[r] = mfma_bf16(dequant_biased(W[u][r][d], magic), bfr, d == 0 ? init : tmp[r]);
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float sc[4];
         scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * (tmp[r][i] - corr);
+        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * tmp[r][i];
       }
       *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
       __syncthreads();
@@ -189,9 +191,10 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
 //   STAGE 2: strips (n0 + 64w)/16 + {0..3}, n0 = tile * 256.
 // Per group the 64 x 128 token tile and its 64 group sums are copied into LDS
 // by buffer_load ... lds (double buffered, one group ahead); each wavefront
-// reads 4 B fragments per K step and issues 16 MFMAs.  Work items are dealt out XCD by XCD: item = (block, tile) with
-// blocks assigned round-robin to the 8 XCDs and all tiles of a block run on
-// the XCD that fetched its token rows into L2.
+// reads 4 B fragments per K step and issues 16 MFMAs.  Work items (block,
+// tile) follow prefill_item: groups of consecutive blocks run tile by tile on
+// one XCD, so a weight tile is fetched once for the group and a block's token
+// rows stay in that XCD's L2 across its tiles.
 constexpr int kPfSlots = 64;
 
 template <int STAGE>
@@ -213,12 +216,8 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
-  // XCD-aware item assignment (the dispatcher sends workgroup id i to XCD i % 8).
-  const int xcd = blockIdx.x % kXcds;
-  const int j = blockIdx.x / kXcds;
-  const int blk = (j / p.n_tiles) * kXcds + xcd;
-  const int tile = j % p.n_tiles;
-  if (blk >= total_blocks) return;
+  int blk, tile;
+  if (!prefill_item(p.n_tiles, total_blocks, blk, tile)) return;
   const int64_t tk = p.tokens * p.topk;
   const BlockInfo b = block_info(p, blk);
   if (!b.active) return;
@@ -288,6 +287,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
     for (int ct = 0; ct < C; ++ct) acc[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int sw = lane & 15;  // swizzle key of this lane's slots (ct*16 + sw)
+  const uint32_t magic = dequant_magic();
   // One group: optionally prefetch group g+1 into the other buffers, then
   // 64 MFMAs and the fp32 group scaling.
   auto step = [&](int g, auto u_c, auto prefetch_c) {
@@ -297,6 +297,13 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
 #pragma unroll
     for (int r = 0; r < R; ++r)
       wv[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]);
+    // each MFMA chain starts from -136 * sum_g(x) of its token column
+    f32x4 init[C];
+#pragma unroll
+    for (int ct = 0; ct < C; ++ct) {
+      const float nc = -kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
+      init[ct] = f32x4{nc, nc, nc, nc};
+    }
     f32x4 tmp[R][C];
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -308,16 +315,12 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
             bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][(ct * 16 + sw) * 256 + part]));
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const bf16x8 a = dequant_biased(wv[r][d]);
+        const bf16x8 a = dequant_biased(wv[r][d], magic);
 #pragma unroll
         for (int ct = 0; ct < C; ++ct)
-          tmp[r][ct] = mfma_bf16(a, bfr[ct], d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[r][ct]);
+          tmp[r][ct] = mfma_bf16(a, bfr[ct], d == 0 ? init[ct] : tmp[r][ct]);
       }
     }
-    float corr[C];
-#pragma unroll
-    for (int ct = 0; ct < C; ++ct)
-      corr[ct] = kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const u32x2 sv = *reinterpret_cast<const u32x2*>(&scl[u][wave][(r >> 1) * 64 + 16 * (lane >> 4) + 8 * (r & 1)]);
@@ -326,7 +329,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
 #pragma unroll
       for (int ct = 0; ct < C; ++ct)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * (tmp[r][ct][i] - corr[ct]);
+        for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * tmp[r][ct][i];
     }
     __syncthreads();
   };
@@ -503,7 +506,6 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   const int shared_bs = decode ? 16 : block_size;
   const int shared_blocks = has_shared ? (int)((tokens + shared_bs - 1) / shared_bs) : 0;
   const int blocks = max_blocks + shared_blocks;
-  const int xcd_blocks = (blocks + kXcds - 1) / kXcds * kXcds;
   const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
 
   {
@@ -543,7 +545,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
                        0, stream, p);
   } else {
     p.n_tiles = inter / 128;
-    hipLaunchKernelGGL(expert_prefill_kernel<1>, dim3((unsigned)(p.n_tiles * xcd_blocks)),
+    hipLaunchKernelGGL(expert_prefill_kernel<1>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)),
                        dim3(256), 0, stream, p, blocks);
   }
   DSV4_CHECK_LAUNCH("expert stage 1");
@@ -567,7 +569,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
                        0, stream, p);
   } else {
     p.n_tiles = hidden / 256;
-    hipLaunchKernelGGL(expert_prefill_kernel<2>, dim3((unsigned)(p.n_tiles * xcd_blocks)),
+    hipLaunchKernelGGL(expert_prefill_kernel<2>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)),
                        dim3(256), 0, stream, p, blocks);
   }
   DSV4_CHECK_LAUNCH("expert stage 2");

@@ -89,6 +89,32 @@ __device__ __forceinline__ void scale4(u32x2 sv, float (&sc)[4]) {
   sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
 }
 
+// Prefill work order.  Items are (alignment block, N tile).  Consecutive
+// blocks, which mostly belong to the same expert, form groups of kBlkGroup;
+// a group's items run tile by tile, so its workgroups stream the same weight
+// tile together and its token rows stay in one L2.  The dispatcher sends
+// workgroup id i to XCD i % 8; groups are dealt to the XCDs round-robin
+// (group g on XCD g % 8), which keeps the XCDs balanced when the active
+// blocks, the padding blocks and the shared-expert blocks sit in different
+// parts of the block list.
+constexpr int kBlkGroup = 4;
+
+__host__ __device__ __forceinline__ int prefill_grid(int total_blocks, int n_tiles) {
+  const int groups = (total_blocks + kBlkGroup - 1) / kBlkGroup;
+  return (groups + kXcds - 1) / kXcds * kBlkGroup * n_tiles * kXcds;
+}
+
+__device__ __forceinline__ bool prefill_item(int n_tiles, int total_blocks, int& blk, int& tile) {
+  const int xcd = (int)(blockIdx.x % kXcds);
+  const int j = (int)(blockIdx.x / kXcds);
+  const int span = kBlkGroup * n_tiles;
+  const int g = (j / span) * kXcds + xcd;
+  const int rem = j % span;
+  tile = rem / kBlkGroup;
+  blk = g * kBlkGroup + rem % kBlkGroup;
+  return blk < total_blocks;
+}
+
 }  // namespace dsv4
 
 // Host launchers shared by both expert paths (experts.hip).

@@ -11,8 +11,10 @@
 // u = q + 8 (0..15) placed in a byte is the e4m3 encoding of u * 2^-9 (bytes
 // 0..7 are subnormals m * 2^-9, bytes 8..15 are (8 + m) * 2^-9).  Per
 // quantisation group g of weight row n and activation row t the MFMA gives
-// 2^-9 * sum(u * xq); the kernels add s[n, g] * (that - sum_g(xq) / 64) and
-// the epilogue multiplies by 512 * s_row, which equals
+// 2^-9 * sum(u * xq); minus sum_g(xq) / 64 that is 2^-9 * sum(q * xq) (the
+// decode kernel starts the MFMA from -sum_g(xq) / 64, the prefill kernel
+// subtracts it afterwards); the kernels add s[n, g] times that and the
+// epilogue multiplies by 512 * s_row, which equals
 // s_row * sum_g s[n, g] * sum(q * xq).
 //
 // Operand layout: a lane of the 16x16x128 MFMA holds 32 K values of one row
@@ -32,10 +34,9 @@ namespace dsv4 {
 
 typedef __attribute__((ext_vector_type(8))) int i32x8;
 
-__device__ __forceinline__ f32x4 mfma_fp8(i32x8 a, i32x8 b) {
+__device__ __forceinline__ f32x4 mfma_fp8(i32x8 a, i32x8 b, f32x4 c) {
   // unit E8M0 block scales (127 = 2^0)
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127,
-                                                           0, 127);
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
 // 16 bytes of tiled int4 (32 nibbles) -> 32 e4m3 bytes of u * 2^-9.
@@ -127,12 +128,11 @@ __global__ __launch_bounds__(256) void act_quant_fp8_kernel(const uint16_t* __re
 // Alignment blocks of <= 16 token slots; workgroup = 4 wavefronts, wavefront w
 // streams strip pair tile*4 + w (stage 1: gate + up strip, h columns
 // n0 + 16w ..; stage 2: strips (n0 + 32w)/16 + {0, 1}).  The 16 slots x 128 B
-// of the current group are staged in LDS (rows of 144 B), one group ahead.
-constexpr int kF8Row = 144;
-
+// of the current group are staged in LDS (part q of slot s at q ^ swz128(s)),
+// one group ahead.
 template <int STAGE>
 __global__ __launch_bounds__(256) void expert_fp8_decode_kernel(ExpertGemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][32 * kF8Row];  // rows 16..31: unused landing rows
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][32 * 128];  // rows 16..31: unused landing rows
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int tile = blockIdx.x % p.n_tiles;
@@ -161,8 +161,9 @@ __global__ __launch_bounds__(256) void expert_fp8_decode_kernel(ExpertGemmParams
       ld_slot < 16 ? act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk) : (int64_t)-1;
   const uint32_t ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim + ld_part * 16) : kOobOffset;
   const uint32_t sum_base = arow >= 0 ? (uint32_t)(arow * groups * 4) : kOobOffset;
-  const int ld_lds = ld_slot * kF8Row + ld_part * 16;
-  const int rd_lds = (lane & 15) * kF8Row + 32 * (lane >> 4);
+  const int ld_lds = ld_slot * 128 + ((ld_part ^ swz128(ld_slot)) * 16);
+  const int rd_lds0 = (lane & 15) * 128 + (((2 * (lane >> 4)) ^ swz128(lane & 15)) * 16);
+  const int rd_lds1 = (lane & 15) * 128 + (((2 * (lane >> 4) + 1) ^ swz128(lane & 15)) * 16);
 
   u32x4 W[4][2];
   u32x4 S[4];
@@ -195,19 +196,19 @@ __global__ __launch_bounds__(256) void expert_fp8_decode_kernel(ExpertGemmParams
       const int g = g0 + u;
       issue_x(g + 1 < last ? g + 1 : last, CS[(u + 1) & 1]);
       issue_w(g + 2 < last ? g + 2 : last, W[(u + 2) & 3], S[(u + 2) & 3]);
-      const uint8_t* xb = &xs[u & 1][rd_lds];
-      const u32x4 b0 = *reinterpret_cast<const u32x4*>(xb);
-      const u32x4 b1 = *reinterpret_cast<const u32x4*>(xb + 16);
+      const u32x4 b0 = *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds0]);
+      const u32x4 b1 = *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds1]);
       const i32x8 bf = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
                         (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-      const float corr = CS[u & 1] * kInvSum;
+      const float nc = -CS[u & 1] * kInvSum;
+      const f32x4 init = {nc, nc, nc, nc};
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const f32x4 tmp = mfma_fp8(spread_nibbles(W[u][r]), bf);
+        const f32x4 tmp = mfma_fp8(spread_nibbles(W[u][r]), bf, init);
         float sc[4];
         scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * (tmp[i] - corr);
+        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * tmp[i];
       }
       *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
       __syncthreads();
@@ -245,8 +246,8 @@ __global__ __launch_bounds__(256) void expert_fp8_decode_kernel(ExpertGemmParams
 
 // ----------------------------------------------------------------- prefill
 // Blocks of up to 64 slots: workgroup tile 64 slots x 256 weight rows, the
-// same strip assignment and XCD-aware order as the bf16 prefill kernel.  Per
-// group the 64 x 128 B token tile (16-byte part q of slot s at q ^ (s & 7)),
+// same strip assignment and work order as the bf16 prefill kernel.  Per
+// group the 64 x 128 B token tile (16-byte part q of slot s at q ^ swz128(s)),
 // the slots' group sums and each wavefront's 4 weight tiles and scales are
 // copied into LDS by buffer_load ... lds, double buffered.
 constexpr int kF8Slots = 64;
@@ -262,11 +263,8 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
-  const int xcd = blockIdx.x % kXcds;
-  const int jj = blockIdx.x / kXcds;
-  const int blk = (jj / p.n_tiles) * kXcds + xcd;
-  const int tile = jj % p.n_tiles;
-  if (blk >= total_blocks) return;
+  int blk, tile;
+  if (!prefill_item(p.n_tiles, total_blocks, blk, tile)) return;
   const int64_t tk = p.tokens * p.topk;
   const BlockInfo b = block_info(p, blk);
   if (!b.active) return;
@@ -291,7 +289,7 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
   for (int q = 0; q < 2; ++q) {
     const int row = 16 * wave + 8 * q + (lane >> 3);
     const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, row, tk), tk, p.topk);
-    const int part = (lane & 7) ^ (row & 7);
+    const int part = (lane & 7) ^ swz128(row);
     dma_off[q] = ar >= 0 ? (uint32_t)(ar * p.k_dim + part * 16) : kOobOffset;
   }
   uint32_t sum_off = kOobOffset;
@@ -331,8 +329,8 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
 #pragma unroll
     for (int ct = 0; ct < C; ++ct) {
       const int row = ct * 16 + sw;
-      const u32x4 b0 = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((2 * jg) ^ (row & 7)) * 16]);
-      const u32x4 b1 = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((2 * jg + 1) ^ (row & 7)) * 16]);
+      const u32x4 b0 = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((2 * jg) ^ swz128(row)) * 16]);
+      const u32x4 b1 = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((2 * jg + 1) ^ swz128(row)) * 16]);
       bfr[ct] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
     }
     float corr[C];
@@ -346,7 +344,7 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
       scale4(sv, sc);
       f32x4 tmp[C];
 #pragma unroll
-      for (int ct = 0; ct < C; ++ct) tmp[ct] = mfma_fp8(a, bfr[ct]);
+      for (int ct = 0; ct < C; ++ct) tmp[ct] = mfma_fp8(a, bfr[ct], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
       for (int ct = 0; ct < C; ++ct)
 #pragma unroll
@@ -417,8 +415,7 @@ static void launch_fp8_stage(const ExpertGemmParams& p, bool decode, int stage, 
     if (stage == 1) hipLaunchKernelGGL(expert_fp8_decode_kernel<1>, grid, dim3(256), 0, stream, p);
     else hipLaunchKernelGGL(expert_fp8_decode_kernel<2>, grid, dim3(256), 0, stream, p);
   } else {
-    const int xcd_blocks = (blocks + kXcds - 1) / kXcds * kXcds;
-    const dim3 grid((unsigned)(p.n_tiles * xcd_blocks));
+    const dim3 grid((unsigned)prefill_grid(blocks, p.n_tiles));
     if (stage == 1) hipLaunchKernelGGL(expert_fp8_prefill_kernel<1>, grid, dim3(256), 0, stream, p, blocks);
     else hipLaunchKernelGGL(expert_fp8_prefill_kernel<2>, grid, dim3(256), 0, stream, p, blocks);
   }

@@ -64,7 +64,8 @@ __device__ __forceinline__ bf16x8 dequant_i8x8(uint32_t lo, uint32_t hi) {
 
 // Workgroup tile: 64*R output channels (wavefront w owns strips 4R*tn + R*w + r)
 // x 16*C tokens, over one K split.  Per window, buffer_load ... lds copies the
-// token tile (16C rows x 128 B, 16-byte part q of row t stored at q ^ (t & 7))
+// token tile (16C rows x 128 B, 16-byte part q of row t stored at
+// q ^ swz128(t))
 // and each wavefront's R weight tiles into LDS, double buffered.
 template <int R, int C>
 __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
     const int q = wave + 4 * i;
     const int row = q * 8 + (lane >> 3);
     const int64_t tok = (int64_t)tm * 16 * C + row;
-    const int part = (lane & 7) ^ (row & 7);
+    const int part = (lane & 7) ^ swz128(row);
     a_off[i] = (q < kActDma && tok < p.m) ? (uint32_t)(tok * p.k * 2 + part * 16) : kLinOob;
   }
   uint32_t w_off[R];
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const int row = c * 16 + n16;
-        const int part = (2 * j + d) ^ (row & 7);
+        const int part = (2 * j + d) ^ swz128(row);
         const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + part * 16]));
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r][c] = mfma_bf16(a[r], b, acc[r][c]);
