@@ -2,16 +2,18 @@
 
 The library is required: every device entry point of this package calls
 through it, and there is no fallback implementation.  A missing library raises
-``RuntimeError`` at the first call.
+``RuntimeError`` at the first call.  ``DSV4MOE_LIBRARY`` may name another build
+of the same library (for example one built for a different target).
 """
 
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().with_name("libdsv4moe.so")
+LIB_PATH = Path(os.environ.get("DSV4MOE_LIBRARY") or Path(__file__).resolve().with_name("libdsv4moe.so"))
 
 DSV4MOE_OK = 0
 DSV4MOE_EINVAL = 1

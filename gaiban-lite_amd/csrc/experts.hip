@@ -27,6 +27,7 @@
 //    the K loop).  Shared-expert blocks carry 16 tokens.
 //  * expert_prefill_kernel (blocks of 32-64 slots): 64 token slots x 256
 //    weight rows per workgroup, token tiles staged in LDS, XCD-aware order.
+#include <algorithm>
 #include <type_traits>
 
 #include "experts_common.h"
@@ -35,36 +36,68 @@
 namespace dsv4 {
 
 // ------------------------------------------------------------------ decode
+// Persistent: the grid is sized to the resident workgroups; workgroup w takes
+// items w, w + stride, ... of the active items (block, tile) -- routed
+// blocks below ceil(ntpp / block_size), then the shared-expert blocks -- so no
+// workgroup is launched for a padding block.  The K stream runs on across
+// item boundaries: the next item's activation group and first two weight
+// groups are fetched during the current item's last groups, and its metadata
+// (expert, row ids) is loaded when the current item starts.
 // STAGE 1: wave w owns gate strip n0/16 + w and up strip (inter + n0)/16 + w,
-//          n0 = tile * 64 (one 64-row chunk of h per workgroup).
+//          n0 = tile * 64 (one 64-row chunk of h per item).
 // STAGE 2: wave w owns strips (n0 + 32 w)/16 + {0, 1}, n0 = tile * 128.
 // The 16 token slots x 128 K of the current group live in LDS (double
 // buffered, one barrier per group): every thread loads 16 bytes per group,
 // every wavefront reads its four MFMA B fragments with ds_read_b128.
 
+struct DecodeItem {
+  const uint8_t* wq;   // this lane's 16 bytes of the pair's first tile
+  const uint16_t* ws;  // this lane's 4 scales of the pair's first group
+  uint32_t ld_base;    // loader thread: activation row offset of its slot (or out of range)
+  uint32_t sum_base;   // lane: row-sum offset of its slot (or out of range)
+  int64_t rowid;       // lane: row id of its slot, -1 if padded
+  int n0;
+};
+
 template <int STAGE>
-__global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) {
-  constexpr int R = 2;
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * 256];  // part q of slot s at q ^ s
+__device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int item, int routed, int64_t tk) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int tile = blockIdx.x % p.n_tiles;
-  const int blk = blockIdx.x / p.n_tiles;
-  const int64_t tk = p.tokens * p.topk;
+  const int bi = item / p.n_tiles;
+  const int tile = item - bi * p.n_tiles;
+  const int blk = bi < routed ? bi : p.max_blocks + (bi - routed);
   const BlockInfo b = block_info(p, blk);
-  if (!b.active) return;
-
-  const int64_t rowid = slot_rowid(p, b, lane & 15, tk);
-  const int64_t arow = act_row_of<STAGE>(rowid, tk, p.topk);
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
-
-  // wavefront w streams strip pair tile*4 + w: stage 1 gate + up strip
-  // (h columns n0 + 16w ..), stage 2 strips (n0 + 32w)/16 + {0, 1}
-  const int n0 = STAGE == 1 ? tile * 64 : tile * 128;
+  DecodeItem it;
+  it.n0 = STAGE == 1 ? tile * 64 : tile * 128;
   const int pair = tile * 4 + wave;
-  const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
-  const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
+  it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
+  it.ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
+  it.rowid = slot_rowid(p, b, lane & 15, tk);
+  const int64_t arow = act_row_of<STAGE>(it.rowid, tk, p.topk);
+  it.sum_base = arow >= 0 ? (uint32_t)(arow * sums_per_row * 4) : kOobOffset;
+  const int ld_slot = threadIdx.x >> 4;
+  const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
+  it.ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + (threadIdx.x & 15) * 16) : kOobOffset;
+  return it;
+}
+
+template <int STAGE>
+__global__ __launch_bounds__(256, 4) void expert_decode_kernel(ExpertGemmParams p) {
+  constexpr int R = 2;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * 256];  // part q of slot s at q ^ s
+  __shared__ float red[4][16];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t tk = p.tokens * p.topk;
+  const int routed = decode_routed_blocks(p);
+  const int n_items = decode_items(p, routed);
+  const int stride = decode_stride(n_items);
+  int item = blockIdx.x;
+  if (item >= stride || item >= n_items) return;  // uniform per workgroup
+  const int groups = p.k_dim / kGroup;
+  const int sums_per_row = p.k_dim / kSumChunk;
 
   // Activations and their sums through buffer loads; padded slots read 0.
   const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -72,114 +105,122 @@ __global__ __launch_bounds__(256) void expert_decode_kernel(ExpertGemmParams p) 
   const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.act_sum, (short)0, (int)(p.act_rows * sums_per_row * 4), kRsrcFlags);
   const int ld_slot = threadIdx.x >> 4;  // cooperative group load: slot, 16-byte part
-  const int ld_part = threadIdx.x & 15;
-  const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
-  const uint32_t ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + ld_part * 16) : kOobOffset;
-  const uint32_t sum_base = arow >= 0 ? (uint32_t)(arow * sums_per_row * 4) : kOobOffset;
-  const int ld_lds = ld_slot * 256 + ((ld_part ^ ld_slot) * 16);
+  const int ld_lds = ld_slot * 256 + (((threadIdx.x & 15) ^ ld_slot) * 16);
   int rd_lds[4];  // K step d: part 4d + lane/16 of slot lane % 16
 #pragma unroll
   for (int d = 0; d < 4; ++d) rd_lds[d] = (lane & 15) * 256 + (((4 * d + (lane >> 4)) ^ (lane & 15)) * 16);
 
-  // Steady state: activations + sums one group ahead (ring 2), weights two
-  // groups ahead (ring 4); prefetch indices are clamped to the last group so
-  // every load is unconditional and the compiler's vmcnt waits stay exact.
+  DecodeItem cur = decode_item<STAGE>(p, item, routed, tk);
+  int next = item + stride;
+  DecodeItem nxt = next < n_items ? decode_item<STAGE>(p, next, routed, tk) : cur;
+
+  // Weights two groups ahead (ring 4), activations + sums one group ahead
+  // (ring 2).  At the end of an item the prefetches continue with the next
+  // item (or re-read the current one when there is none), so every load is
+  // unconditional and the compiler's vmcnt waits stay exact.
   u32x4 W[4][R];
   u32x4 S[4];
   float CS[2][2];
   u32x4 xr;
 
-  auto issue_w = [&](int g, u32x4 (&w)[R], u32x4& s) {
-    w[0] = load16_nt(wq + g * 2048);
-    w[1] = load16_nt(wq + g * 2048 + 1024);
-    s = load16(ws + g * 32);  // 4 rows of both members
+  auto issue_w = [&](const DecodeItem& it, int g, u32x4 (&w)[R], u32x4& s) {
+    w[0] = load16_nt(it.wq + g * 2048);
+    w[1] = load16_nt(it.wq + g * 2048 + 1024);
+    s = load16(it.ws + g * 32);  // 4 rows of both members
   };
-  auto issue_x = [&](int g, float (&cs)[2]) {
-    xr = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, ld_base + (uint32_t)(g * 256), 0, 0);
-    cs[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 8), 0, 0));
-    cs[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 8 + 4), 0, 0));
+  auto issue_x = [&](const DecodeItem& it, int g, float (&cs)[2]) {
+    xr = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, it.ld_base + (uint32_t)(g * 256), 0, 0);
+    cs[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, it.sum_base + (uint32_t)(g * 8), 0, 0));
+    cs[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, it.sum_base + (uint32_t)(g * 8 + 4), 0, 0));
   };
 
-  f32x4 acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint32_t magic = dequant_magic();
-
-  issue_x(0, CS[0]);
-  issue_w(0, W[0], S[0]);
-  issue_w(groups > 1 ? 1 : 0, W[1], S[1]);
+  issue_x(cur, 0, CS[0]);
+  issue_w(cur, 0, W[0], S[0]);
+  issue_w(cur, 1, W[1], S[1]);
   *reinterpret_cast<u32x4*>(&xs[0][ld_lds]) = xr;
   __syncthreads();
 
-  const int last = groups - 1;
-  for (int g0 = 0; g0 < groups; g0 += 4) {  // groups % 4 == 0 (checked on the host)
+  for (;;) {
+    f32x4 acc[R];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int g = g0 + u;
-      issue_x(g + 1 < last ? g + 1 : last, CS[(u + 1) & 1]);
-      issue_w(g + 2 < last ? g + 2 : last, W[(u + 2) & 3], S[(u + 2) & 3]);
-      // the MFMA chain starts from -136 * sum_g(x): it yields sum_g(q * x) directly
-      const float nc = -kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
-      const f32x4 init = {nc, nc, nc, nc};
-      f32x4 tmp[R];
+    for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g0 = 0; g0 < groups; g0 += 4) {  // groups % 4 == 0 (checked on the host)
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds[d]]));
+      for (int u = 0; u < 4; ++u) {
+        const int g = g0 + u;
+        const bool xn = g + 1 >= groups;  // the activation prefetch crosses into the next item
+        issue_x(xn ? nxt : cur, xn ? 0 : g + 1, CS[(u + 1) & 1]);
+        const bool wn = g + 2 >= groups;
+        issue_w(wn ? nxt : cur, wn ? g + 2 - groups : g + 2, W[(u + 2) & 3], S[(u + 2) & 3]);
+        // the MFMA chain starts from -136 * sum_g(x): it yields sum_g(q * x) directly
+        const float nc = -kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
+        const f32x4 init = {nc, nc, nc, nc};
+        f32x4 tmp[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) tmp[r] = mfma_bf16(dequant_biased(W[u][r][d], magic), bfr, d == 0 ? init : tmp[r]);
+        for (int d = 0; d < 4; ++d) {
+          const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds[d]]));
+#pragma unroll
+          for (int r = 0; r < R; ++r) tmp[r] = mfma_bf16(dequant_biased(W[u][r][d], magic), bfr, d == 0 ? init : tmp[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float sc[4];
+          scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * tmp[r][i];
+        }
+        *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
+        __syncthreads();
       }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float sc[4];
-        scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * tmp[r][i];
-      }
-      *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
-      __syncthreads();
     }
-  }
 
-  if constexpr (STAGE == 1) {
-    __shared__ float red[4][16];
-    const float lim = p.clamp_limit;
-    uint32_t bits[4];
-    float part = 0.0f;
+    const int64_t rowid = cur.rowid;
+    if constexpr (STAGE == 1) {
+      const float lim = p.clamp_limit;
+      uint32_t bits[4];
+      float part = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float gt = acc[0][i];
-      float up = acc[1][i];
-      if (lim > 0.0f) {
-        gt = fminf(gt, lim);
-        up = fminf(fmaxf(up, -lim), lim);
+      for (int i = 0; i < 4; ++i) {
+        float gt = acc[0][i];
+        float up = acc[1][i];
+        if (lim > 0.0f) {
+          gt = fminf(gt, lim);
+          up = fminf(fmaxf(up, -lim), lim);
+        }
+        bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+        part += __uint_as_float(bits[i] << 16);
       }
-      bits[i] = float_to_bf16_bits(silu_f(gt) * up);
-      part += __uint_as_float(bits[i] << 16);
-    }
-    if (rowid >= 0) {
-      const int n = n0 + 16 * wave + 4 * (lane >> 4);
-      u32x2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
-      *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) = packed;
-    }
-    part += __shfl_xor(part, 16, 64);
-    part += __shfl_xor(part, 32, 64);
-    if (lane < 16) red[wave][lane] = part;
-    __syncthreads();
-    if (threadIdx.x < 16 && rowid >= 0) {
-      const float total = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-      p.hsum_out[rowid * (p.inter / kSumChunk) + n0 / kSumChunk] = total;
-    }
-  } else {
-    if (rowid >= 0) {
-      const float wr = rowid < tk ? p.route_w[rowid] : 1.0f;
+      if (rowid >= 0) {
+        const int n = cur.n0 + 16 * wave + 4 * (lane >> 4);
+        u32x2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+        *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) = packed;
+      }
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      if (lane < 16) red[wave][lane] = part;
+      __syncthreads();
+      if (threadIdx.x < 16 && rowid >= 0) {
+        const float total = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+        p.hsum_out[rowid * (p.inter / kSumChunk) + cur.n0 / kSumChunk] = total;
+      }
+    } else {
+      if (rowid >= 0) {
+        const float wr = rowid < tk ? p.route_w[rowid] : 1.0f;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int n = n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
-        f32x4 v = acc[r];
-        v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
-        *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+        for (int r = 0; r < R; ++r) {
+          const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
+          f32x4 v = acc[r];
+          v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
+          *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+        }
       }
     }
+    if (next >= n_items) break;  // uniform per workgroup; the last prefetches re-read cur
+    item = next;
+    cur = nxt;
+    next = item + stride;
+    nxt = next < n_items ? decode_item<STAGE>(p, next, routed, tk) : cur;
   }
 }
 
@@ -468,6 +509,24 @@ struct ExpertWorkspace {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Resident workgroups of a decode kernel on the current device (CUs x
+// occupancy), cached per device: the persistent grid size.
+template <int STAGE>
+static int decode_resident_grid() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, expert_decode_kernel<STAGE>, 256, 0) != hipSuccess ||
+        per_cu <= 0)
+      per_cu = 1;
+    cache[dev] = cus * per_cu;
+  }
+  return cache[dev];
+}
+
 static ExpertWorkspace carve_workspace(void* base, int64_t tokens, int topk, int hidden, int inter,
                                        int has_shared) {
   const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
@@ -541,8 +600,8 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.hsum_out = ws.hsum;
   if (decode) {
     p.n_tiles = inter / 64;
-    hipLaunchKernelGGL(expert_decode_kernel<1>, dim3((unsigned)(p.n_tiles * blocks)), dim3(256),
-                       0, stream, p);
+    const int grid = std::min(p.n_tiles * blocks, decode_resident_grid<1>());
+    hipLaunchKernelGGL(expert_decode_kernel<1>, dim3((unsigned)grid), dim3(256), 0, stream, p);
   } else {
     p.n_tiles = inter / 128;
     hipLaunchKernelGGL(expert_prefill_kernel<1>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)),
@@ -565,8 +624,8 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.out_cols = hidden;
   if (decode) {
     p.n_tiles = hidden / 128;
-    hipLaunchKernelGGL(expert_decode_kernel<2>, dim3((unsigned)(p.n_tiles * blocks)), dim3(256),
-                       0, stream, p);
+    const int grid = std::min(p.n_tiles * blocks, decode_resident_grid<2>());
+    hipLaunchKernelGGL(expert_decode_kernel<2>, dim3((unsigned)grid), dim3(256), 0, stream, p);
   } else {
     p.n_tiles = hidden / 256;
     hipLaunchKernelGGL(expert_prefill_kernel<2>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)),

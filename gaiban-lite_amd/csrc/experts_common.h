@@ -89,6 +89,24 @@ __device__ __forceinline__ void scale4(u32x2 sv, float (&sc)[4]) {
   sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
 }
 
+// Persistent decode kernels: active items (block, tile) are the routed blocks
+// below ceil(ntpp / block_size) followed by the shared-expert blocks, times the
+// N tiles.
+__device__ __forceinline__ int decode_routed_blocks(const ExpertGemmParams& p) {
+  const int total = p.ntpp[0];
+  return total > 0 ? (total + p.block_size - 1) / p.block_size : 0;
+}
+
+__device__ __forceinline__ int decode_items(const ExpertGemmParams& p, int routed) {
+  const int shared = p.shared_expert >= 0 ? (int)((p.tokens + p.shared_block_size - 1) / p.shared_block_size) : 0;
+  return (routed + shared) * p.n_tiles;
+}
+
+// Workgroup stride over the items: the whole grid.  (Shrinking the grid so
+// that the last round is full was measured slower: fewer workgroups keep
+// fewer bytes in flight, which costs more than the partial last round.)
+__device__ __forceinline__ int decode_stride(int) { return (int)gridDim.x; }
+
 // Prefill work order.  Items are (alignment block, N tile).  Consecutive
 // blocks, which mostly belong to the same expert, form groups of kBlkGroup;
 // a group's items run tile by tile, so its workgroups stream the same weight

@@ -25,6 +25,7 @@
 // (w & 0x0F0F0F0F, (w >> 4) & 0x0F0F0F0F) = K k0 + {0,4,1,5}, k0 + {2,6,3,7}.
 // The activation quantiser writes each 128-K group in exactly that order: 32
 // bytes per lane group j, dword pair d holding K 32d + 8j + {0,4,1,5,2,6,3,7}.
+#include <algorithm>
 #include <type_traits>
 
 #include "experts_common.h"
@@ -125,122 +126,161 @@ __global__ __launch_bounds__(256) void act_quant_fp8_kernel(const uint16_t* __re
 }
 
 // ------------------------------------------------------------------ decode
-// Alignment blocks of <= 16 token slots; workgroup = 4 wavefronts, wavefront w
-// streams strip pair tile*4 + w (stage 1: gate + up strip, h columns
-// n0 + 16w ..; stage 2: strips (n0 + 32w)/16 + {0, 1}).  The 16 slots x 128 B
-// of the current group are staged in LDS (part q of slot s at q ^ swz128(s)),
-// one group ahead.
+// Persistent, like the bf16 decode kernel: workgroup w takes items w, w +
+// stride, ... of the active (block, tile) items, and the K stream (weights two
+// groups ahead, activations one group ahead) runs on across item boundaries.
+// Wavefront w streams strip pair tile*4 + w (stage 1: gate + up strip, h
+// columns n0 + 16w ..; stage 2: strips (n0 + 32w)/16 + {0, 1}).  The 16 slots
+// x 128 B of the current group are staged in LDS (part q of slot s at
+// q ^ swz128(s)); the loader threads of slots 16..31 fill unused landing rows.
+
+struct Fp8DecodeItem {
+  const uint8_t* wq;
+  const uint16_t* ws;
+  uint32_t ld_base;   // loader thread: activation byte offset of its slot (or out of range)
+  uint32_t sum_base;  // lane: group-sum offset of its slot (or out of range)
+  int64_t rowid;      // lane: row id of its slot, -1 if padded
+  int64_t arow;       // lane: activation row of its slot, -1 if padded
+  int n0;
+};
+
 template <int STAGE>
-__global__ __launch_bounds__(256) void expert_fp8_decode_kernel(ExpertGemmParams p) {
+__device__ __forceinline__ Fp8DecodeItem fp8_decode_item(const ExpertGemmParams& p, int item, int routed,
+                                                         int64_t tk) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int bi = item / p.n_tiles;
+  const int tile = item - bi * p.n_tiles;
+  const int blk = bi < routed ? bi : p.max_blocks + (bi - routed);
+  const BlockInfo b = block_info(p, blk);
+  const int groups = p.k_dim / kGroup;
+  Fp8DecodeItem it;
+  it.n0 = STAGE == 1 ? tile * 64 : tile * 128;
+  const int pair = tile * 4 + wave;
+  it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
+  it.ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
+  it.rowid = slot_rowid(p, b, lane & 15, tk);
+  it.arow = act_row_of<STAGE>(it.rowid, tk, p.topk);
+  it.sum_base = it.arow >= 0 ? (uint32_t)(it.arow * groups * 4) : kOobOffset;
+  const int ld_slot = threadIdx.x >> 3;
+  const int64_t ld_row =
+      ld_slot < 16 ? act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk) : (int64_t)-1;
+  it.ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim + (threadIdx.x & 7) * 16) : kOobOffset;
+  return it;
+}
+
+template <int STAGE>
+__global__ __launch_bounds__(256, 4) void expert_fp8_decode_kernel(ExpertGemmParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][32 * 128];  // rows 16..31: unused landing rows
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int tile = blockIdx.x % p.n_tiles;
-  const int blk = blockIdx.x / p.n_tiles;
   const int64_t tk = p.tokens * p.topk;
-  const BlockInfo b = block_info(p, blk);
-  if (!b.active) return;
-
-  const int64_t rowid = slot_rowid(p, b, lane & 15, tk);
-  const int64_t arow = act_row_of<STAGE>(rowid, tk, p.topk);
+  const int routed = decode_routed_blocks(p);
+  const int n_items = decode_items(p, routed);
+  const int stride = decode_stride(n_items);
+  int item = blockIdx.x;
+  if (item >= stride || item >= n_items) return;  // uniform per workgroup
   const int groups = p.k_dim / kGroup;
-
-  const int n0 = STAGE == 1 ? tile * 64 : tile * 128;
-  const int pair = tile * 4 + wave;
-  const uint8_t* wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
-  const uint16_t* ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
 
   const uint8_t* act = reinterpret_cast<const uint8_t*>(p.act);
   const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)act, (short)0, (int)(p.act_rows * p.k_dim), kRsrcFlags);
   const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.act_sum, (short)0, (int)(p.act_rows * groups * 4), kRsrcFlags);
-  const int ld_slot = threadIdx.x >> 3;  // 0..31; slots >= 16 load zeros into the landing rows
-  const int ld_part = threadIdx.x & 7;
-  const int64_t ld_row =
-      ld_slot < 16 ? act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk) : (int64_t)-1;
-  const uint32_t ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim + ld_part * 16) : kOobOffset;
-  const uint32_t sum_base = arow >= 0 ? (uint32_t)(arow * groups * 4) : kOobOffset;
-  const int ld_lds = ld_slot * 128 + ((ld_part ^ swz128(ld_slot)) * 16);
+  const int ld_slot = threadIdx.x >> 3;
+  const int ld_lds = ld_slot * 128 + (((threadIdx.x & 7) ^ swz128(ld_slot)) * 16);
   const int rd_lds0 = (lane & 15) * 128 + (((2 * (lane >> 4)) ^ swz128(lane & 15)) * 16);
   const int rd_lds1 = (lane & 15) * 128 + (((2 * (lane >> 4) + 1) ^ swz128(lane & 15)) * 16);
+
+  Fp8DecodeItem cur = fp8_decode_item<STAGE>(p, item, routed, tk);
+  int next = item + stride;
+  Fp8DecodeItem nxt = next < n_items ? fp8_decode_item<STAGE>(p, next, routed, tk) : cur;
 
   u32x4 W[4][2];
   u32x4 S[4];
   float CS[2];
   u32x4 xr;
-  auto issue_w = [&](int g, u32x4 (&w)[2], u32x4& s) {
-    w[0] = load16_nt(wq + g * 2048);
-    w[1] = load16_nt(wq + g * 2048 + 1024);
-    s = load16(ws + g * 32);
+  auto issue_w = [&](const Fp8DecodeItem& it, int g, u32x4 (&w)[2], u32x4& s) {
+    w[0] = load16_nt(it.wq + g * 2048);
+    w[1] = load16_nt(it.wq + g * 2048 + 1024);
+    s = load16(it.ws + g * 32);
   };
-  auto issue_x = [&](int g, float& cs) {
-    xr = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, ld_base + (uint32_t)(g * 128), 0, 0);
-    cs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, sum_base + (uint32_t)(g * 4), 0, 0));
+  auto issue_x = [&](const Fp8DecodeItem& it, int g, float& cs) {
+    xr = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, it.ld_base + (uint32_t)(g * 128), 0, 0);
+    cs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, it.sum_base + (uint32_t)(g * 4), 0, 0));
   };
 
-  f32x4 acc[2];
-  acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
-  acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  issue_x(0, CS[0]);
-  issue_w(0, W[0], S[0]);
-  issue_w(groups > 1 ? 1 : 0, W[1], S[1]);
+  issue_x(cur, 0, CS[0]);
+  issue_w(cur, 0, W[0], S[0]);
+  issue_w(cur, 1, W[1], S[1]);
   *reinterpret_cast<u32x4*>(&xs[0][ld_lds]) = xr;
   __syncthreads();
 
-  const int last = groups - 1;
-  for (int g0 = 0; g0 < groups; g0 += 4) {  // groups % 4 == 0 (checked on the host)
+  for (;;) {
+    f32x4 acc[2];
+    acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g0 = 0; g0 < groups; g0 += 4) {  // groups % 4 == 0 (checked on the host)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int g = g0 + u;
-      issue_x(g + 1 < last ? g + 1 : last, CS[(u + 1) & 1]);
-      issue_w(g + 2 < last ? g + 2 : last, W[(u + 2) & 3], S[(u + 2) & 3]);
-      const u32x4 b0 = *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds0]);
-      const u32x4 b1 = *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds1]);
-      const i32x8 bf = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
-                        (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
-      const float nc = -CS[u & 1] * kInvSum;
-      const f32x4 init = {nc, nc, nc, nc};
+      for (int u = 0; u < 4; ++u) {
+        const int g = g0 + u;
+        const bool xn = g + 1 >= groups;
+        issue_x(xn ? nxt : cur, xn ? 0 : g + 1, CS[(u + 1) & 1]);
+        const bool wn = g + 2 >= groups;
+        issue_w(wn ? nxt : cur, wn ? g + 2 - groups : g + 2, W[(u + 2) & 3], S[(u + 2) & 3]);
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds0]);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(&xs[u & 1][rd_lds1]);
+        const i32x8 bf = {(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3],
+                          (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+        const float nc = -CS[u & 1] * kInvSum;
+        const f32x4 init = {nc, nc, nc, nc};
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const f32x4 tmp = mfma_fp8(spread_nibbles(W[u][r]), bf, init);
-        float sc[4];
-        scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
+        for (int r = 0; r < 2; ++r) {
+          const f32x4 tmp = mfma_fp8(spread_nibbles(W[u][r]), bf, init);
+          float sc[4];
+          scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * tmp[i];
+          for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * tmp[i];
+        }
+        *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
+        __syncthreads();
       }
-      *reinterpret_cast<u32x4*>(&xs[(u + 1) & 1][ld_lds]) = xr;
-      __syncthreads();
     }
-  }
 
-  if (rowid < 0) return;
-  const float mult = kUnScale * p.act_scale[arow];
-  if constexpr (STAGE == 1) {
-    const float lim = p.clamp_limit;
-    uint32_t bits[4];
+    const int64_t rowid = cur.rowid;
+    if (rowid >= 0) {
+      const float mult = kUnScale * p.act_scale[cur.arow];
+      if constexpr (STAGE == 1) {
+        const float lim = p.clamp_limit;
+        uint32_t bits[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float gt = acc[0][i] * mult;
-      float up = acc[1][i] * mult;
-      if (lim > 0.0f) {
-        gt = fminf(gt, lim);
-        up = fminf(fmaxf(up, -lim), lim);
+        for (int i = 0; i < 4; ++i) {
+          float gt = acc[0][i] * mult;
+          float up = acc[1][i] * mult;
+          if (lim > 0.0f) {
+            gt = fminf(gt, lim);
+            up = fminf(fmaxf(up, -lim), lim);
+          }
+          bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+        }
+        const int n = cur.n0 + 16 * wave + 4 * (lane >> 4);
+        *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) =
+            u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+      } else {
+        const float wm = (rowid < tk ? p.route_w[rowid] : 1.0f) * mult;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
+          const f32x4 v = {acc[r][0] * wm, acc[r][1] * wm, acc[r][2] * wm, acc[r][3] * wm};
+          *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+        }
       }
-      bits[i] = float_to_bf16_bits(silu_f(gt) * up);
     }
-    const int n = n0 + 16 * wave + 4 * (lane >> 4);
-    *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) =
-        u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
-  } else {
-    const float wm = (rowid < tk ? p.route_w[rowid] : 1.0f) * mult;
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int n = n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
-      const f32x4 v = {acc[r][0] * wm, acc[r][1] * wm, acc[r][2] * wm, acc[r][3] * wm};
-      *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
-    }
+    if (next >= n_items) break;  // uniform per workgroup; the last prefetches re-read cur
+    item = next;
+    cur = nxt;
+    next = item + stride;
+    nxt = next < n_items ? fp8_decode_item<STAGE>(p, next, routed, tk) : cur;
   }
 }
 
@@ -409,11 +449,31 @@ static void launch_act_quant(const uint16_t* x, int64_t rows, int k, uint8_t* q,
                      q, scale, gsum);
 }
 
+template <int STAGE>
+static int fp8_decode_resident_grid() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, expert_fp8_decode_kernel<STAGE>, 256, 0) != hipSuccess ||
+        per_cu <= 0)
+      per_cu = 1;
+    cache[dev] = cus * per_cu;
+  }
+  return cache[dev];
+}
+
 static void launch_fp8_stage(const ExpertGemmParams& p, bool decode, int stage, int blocks, hipStream_t stream) {
   if (decode) {
-    const dim3 grid((unsigned)(p.n_tiles * blocks));
-    if (stage == 1) hipLaunchKernelGGL(expert_fp8_decode_kernel<1>, grid, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL(expert_fp8_decode_kernel<2>, grid, dim3(256), 0, stream, p);
+    if (stage == 1) {
+      const dim3 grid((unsigned)std::min(p.n_tiles * blocks, fp8_decode_resident_grid<1>()));
+      hipLaunchKernelGGL(expert_fp8_decode_kernel<1>, grid, dim3(256), 0, stream, p);
+    } else {
+      const dim3 grid((unsigned)std::min(p.n_tiles * blocks, fp8_decode_resident_grid<2>()));
+      hipLaunchKernelGGL(expert_fp8_decode_kernel<2>, grid, dim3(256), 0, stream, p);
+    }
   } else {
     const dim3 grid((unsigned)prefill_grid(blocks, p.n_tiles));
     if (stage == 1) hipLaunchKernelGGL(expert_fp8_prefill_kernel<1>, grid, dim3(256), 0, stream, p, blocks);
