@@ -32,6 +32,10 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # IEEE division and square root in the router's fixed operation sequence.
     "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # MFMA accumulators in ordinary VGPRs: the kernels rescale them with VALU
+    # FMAs once per K group, which AGPR accumulators would turn into extra
+    # v_accvgpr moves per element.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
 ]

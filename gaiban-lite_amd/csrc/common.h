@@ -87,6 +87,55 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, lds_void_
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds, 16, voffset, soffset, 0, 0);
 }
 
+// The same copies issued as inline assembly.  The compiler does not see these
+// as LDS writes, so it adds no vmcnt wait before ds_reads of *other* LDS
+// buffers (it cannot tell the DMA destinations apart and would otherwise make
+// every ds_read wait for the in-flight prefetch).  The caller must wait with
+// lds_dma_wait_all() before the barrier that publishes the copied data.
+// `lds` is the LDS byte address of lane 0's destination (M0); lane i writes
+// lds + i*16 (dwordx4) or lds + i*4 (dword).
+// (The asm bodies exist only in the device pass; the host pass of these
+// device functions has no AMDGPU register constraints.)
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds, uint32_t voffset,
+                                           uint32_t soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // lds and soffset are wavefront-uniform; readfirstlane makes them scalar
+  // for the compiler when it cannot prove it
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soffset))
+               : "memory", "m0");
+#endif
+}
+__device__ __forceinline__ void lds_copy4(__amdgpu_buffer_rsrc_t rsrc, uint32_t lds, uint32_t voffset,
+                                          uint32_t soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soffset))
+               : "memory", "m0");
+#endif
+}
+// Wait until at most N of this wavefront's vector-memory operations are
+// outstanding (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void lds_dma_wait_keep() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+#endif
+}
+__device__ __forceinline__ void lds_dma_wait_all() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
+}
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)p;
+}
+
 __device__ __forceinline__ float silu_f(float g) {
   return g / (1.0f + __expf(-g));
 }

@@ -301,23 +301,18 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   // scales: 64 bytes per (pair, group); lanes 0..31 copy 4 bytes each of both pairs
   const uint32_t s_off = lane < 32 ? (uint32_t)((p0 + (lane >> 4)) * groups) * 64 + (lane & 15) * 4 : kOobOffset;
 
-  typedef __attribute__((address_space(3))) void* lds_ptr;
   auto issue = [&](int g, int buf) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(act_rsrc, (lds_ptr)&xs[buf][(16 * wave + 4 * q) * 256], 16,
-                                               dma_off[q], g * 256, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][0], 16, w_off0, g * 2048, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][kTileBytes], 16, w_off0 + kTileBytes,
-                                             g * 2048, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][2 * kTileBytes], 16, w_off1,
-                                             g * 2048, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr)&wts[buf][wave][3 * kTileBytes], 16, w_off1 + kTileBytes,
-                                             g * 2048, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_ptr)&scl[buf][wave][0], 4, s_off, g * 64, 0, 0);
+      lds_copy16(act_rsrc, lds_addr(&xs[buf][(16 * wave + 4 * q) * 256]), dma_off[q], g * 256);
+    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][0]), w_off0, g * 2048);
+    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][kTileBytes]), w_off0 + kTileBytes, g * 2048);
+    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][2 * kTileBytes]), w_off1, g * 2048);
+    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][3 * kTileBytes]), w_off1 + kTileBytes, g * 2048);
+    lds_copy4(s_rsrc, lds_addr(&scl[buf][wave][0]), s_off, g * 64);
     if (wave == 0) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sum_rsrc, (lds_ptr)&xsum[buf][0][0], 4, sum_off, g * 8, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sum_rsrc, (lds_ptr)&xsum[buf][1][0], 4, sum_off, g * 8 + 4, 0, 0);
+      lds_copy4(sum_rsrc, lds_addr(&xsum[buf][0][0]), sum_off, g * 8);
+      lds_copy4(sum_rsrc, lds_addr(&xsum[buf][1][0]), sum_off, g * 8 + 4);
     }
   };
 
@@ -372,6 +367,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * tmp[r][ct][i];
     }
+    lds_dma_wait_all();
     __syncthreads();
   };
   using U0 = std::integral_constant<int, 0>;
@@ -380,6 +376,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   using NOPF = std::false_type;
 
   issue(0, 0);
+  lds_dma_wait_all();
   __syncthreads();
   // groups is even (checked on the host); the last group issues no prefetch,
   // so no LDS DMA is in flight when the workgroup leaves the loop.

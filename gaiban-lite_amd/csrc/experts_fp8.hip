@@ -341,17 +341,18 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
   const uint32_t w_off1 = (uint32_t)((p0 + 1) * groups) * 2048 + lane * 16;
   const uint32_t s_off = lane < 32 ? (uint32_t)((p0 + (lane >> 4)) * groups) * 64 + (lane & 15) * 4 : kOobOffset;
 
+  // LDS copies of group g into buffer `buf` (inline-asm DMA, waited for
+  // explicitly before the barrier that ends each step)
   auto issue = [&](int g, int buf) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
-      lds_dma16(act_rsrc, (lds_void_ptr)&xs[buf][(16 * wave + 8 * q) * 128], dma_off[q], g * 128);
-    lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][0], w_off0, g * 2048);
-    lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][kTileBytes], w_off0 + kTileBytes, g * 2048);
-    lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][2 * kTileBytes], w_off1, g * 2048);
-    lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][3 * kTileBytes], w_off1 + kTileBytes, g * 2048);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_void_ptr)&scl[buf][wave][0], 4, s_off, g * 64, 0, 0);
-    if (wave == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sum_rsrc, (lds_void_ptr)&xsum[buf][0], 4, sum_off, g * 4, 0, 0);
+      lds_copy16(act_rsrc, lds_addr(&xs[buf][(16 * wave + 8 * q) * 128]), dma_off[q], g * 128);
+    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][0]), w_off0, g * 2048);
+    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][kTileBytes]), w_off0 + kTileBytes, g * 2048);
+    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][2 * kTileBytes]), w_off1, g * 2048);
+    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][3 * kTileBytes]), w_off1 + kTileBytes, g * 2048);
+    lds_copy4(s_rsrc, lds_addr(&scl[buf][wave][0]), s_off, g * 64);
+    if (wave == 0) lds_copy4(sum_rsrc, lds_addr(&xsum[buf][0]), sum_off, g * 4);
   };
 
   f32x4 acc[R][C];
@@ -390,7 +391,8 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * (tmp[ct][i] - corr[ct]);
     }
-    __syncthreads();
+    lds_dma_wait_all();  // this wavefront's copies of group g + 1 have landed
+    __syncthreads();     // ... and everyone's; buffer u is free again
   };
   using U0 = std::integral_constant<int, 0>;
   using U1 = std::integral_constant<int, 1>;
@@ -398,6 +400,7 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
   using NOPF = std::false_type;
 
   issue(0, 0);
+  lds_dma_wait_all();
   __syncthreads();
   for (int g0 = 0; g0 + 2 < groups; g0 += 2) {
     step(g0, U0{}, PF{});

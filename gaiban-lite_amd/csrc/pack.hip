@@ -20,6 +20,14 @@
 // (bits 16+4j..) = k0+2j+1, offset-binary (q + 8).
 // Scales: element (((p*G + g)*4 + quad)*2 + m)*4 + i holds the scale of row
 // 4*quad + i of member m, so one 16-byte load returns 4 rows of both members.
+//
+// Zero scales.  A group whose scale is +-0 contributes exactly zero; the
+// packer stores its codes as q = 0 and gives it the nearest nonzero scale of
+// the same row (the previous group's, else the next one's, else 1.0).  The
+// product q * s is unchanged for every weight, and every packed scale is
+// nonzero, which the prefill kernels rely on: they keep each row's running
+// sum divided by the current group's scale and multiply it by the ratio of
+// consecutive scales.
 #include "common.h"
 #include "../../include/dsv4moe.h"
 
@@ -29,7 +37,10 @@ __device__ __forceinline__ int64_t member_row0(int64_t p, int m, int64_t n, int 
   return pairing == 0 ? (2 * p + m) * 16 : p * 16 + m * (n / 2);
 }
 
+__device__ __forceinline__ bool scale_is_zero(uint16_t bits) { return (bits & 0x7FFFu) == 0; }
+
 __global__ __launch_bounds__(256) void pack_int4_kernel(const uint8_t* __restrict__ canon,
+                                                        const uint16_t* __restrict__ canon_s,
                                                         uint8_t* __restrict__ packed,
                                                         int64_t n, int64_t k, int64_t batch,
                                                         int pairing) {
@@ -47,6 +58,7 @@ __global__ __launch_bounds__(256) void pack_int4_kernel(const uint8_t* __restric
     const int64_t p = (tin >> 1) / groups;
     const int64_t row = member_row0(p, m, n, pairing) + (lane & 15);
     const uint8_t* src_row = canon + mat * n * (k / 2) + row * (k / 2);
+    const bool zero_group = scale_is_zero(canon_s[mat * n * groups + row * groups + g]);
     u32x4 out;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -59,7 +71,7 @@ __global__ __launch_bounds__(256) void pack_int4_kernel(const uint8_t* __restric
         w |= ((byte & 0xFu) ^ 0x8u) << (4 * b);
         w |= ((byte >> 4) ^ 0x8u) << (16 + 4 * b);
       }
-      out[d] = w;
+      out[d] = zero_group ? 0x88888888u : w;  // q = 0 in every slot
     }
     *reinterpret_cast<u32x4*>(packed + mat * n * (k / 2) + tin * kTileBytes + lane * 16) = out;
   }
@@ -83,7 +95,17 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const uint16_t* __rest
     const int64_t mat = pm / (n / 32);
     const int64_t p = pm % (n / 32);
     const int64_t row = member_row0(p, m, n, pairing) + 4 * quad + i;
-    packed_s[idx] = canon_s[mat * n * groups + row * groups + g];
+    const uint16_t* srow = canon_s + mat * n * groups + row * groups;
+    uint16_t v = srow[g];
+    if (scale_is_zero(v)) {  // nearest nonzero scale of the row: earlier groups first
+      v = 0x3F80u;           // 1.0 when the whole row is zero
+      bool found = false;
+      for (int64_t h = g - 1; h >= 0 && !found; --h)
+        if (!scale_is_zero(srow[h])) { v = srow[h]; found = true; }
+      for (int64_t h = g + 1; h < groups && !found; ++h)
+        if (!scale_is_zero(srow[h])) { v = srow[h]; found = true; }
+    }
+    packed_s[idx] = v;
   }
 }
 
@@ -98,8 +120,8 @@ int dsv4_launch_pack(const uint8_t* canon, const uint16_t* canon_scales, int64_t
   const int64_t blocks = (work + 255) / 256;
   const unsigned grid = (unsigned)(blocks < 65535 * 16 ? blocks : 65535 * 16);
   if (work > 0) {
-    hipLaunchKernelGGL(pack_int4_kernel, dim3(grid), dim3(256), 0, stream, canon, packed, n, k,
-                       batch, pairing);
+    hipLaunchKernelGGL(pack_int4_kernel, dim3(grid), dim3(256), 0, stream, canon, canon_scales, packed,
+                       n, k, batch, pairing);
     DSV4_CHECK_LAUNCH("pack_int4_kernel");
   }
   const int64_t swork = batch * n * (k / kGroup);

@@ -141,6 +141,9 @@ int dsv4moe_align(const int32_t* ids, int64_t tokens, int32_t topk, int32_t expe
  *   packed       uint8 [batch, n*k/2]  out: tile (p, g, m) of 16 rows x 128 k
  *                at byte ((p*(k/128) + g)*2 + m)*1024
  *   packed_scales bf16 [batch, n*k/128] out: [p][g][quad][m][4 rows]
+ * A group whose scale is +-0 is stored with all codes q = 0 and the nearest
+ * nonzero scale of its row (previous group first, else next, else 1.0), which
+ * leaves every product q * s unchanged and every packed scale nonzero.
  * n % 32 == 0, k % 128 == 0.
  */
 #define DSV4MOE_PAIR_PLAIN 0

@@ -74,17 +74,26 @@ def np_tile_pack(canon: np.ndarray, scales_bits: np.ndarray, gated: bool = False
 
     q = O.unpack_int4_rows(canon).astype(np.int32)  # [n, k]
     n, k = q.shape
-    u = (q + 8).astype(np.uint32)
     groups = k // 128
     pairs = n // 32
     lane = np.arange(64)
+    # zero-scale groups: codes 0, scale = nearest nonzero of the row
+    # (previous group first, else next, else bf16 1.0)
+    sb = scales_bits.reshape(n, groups).copy()
+    zero = (sb & 0x7FFF) == 0
+    orig = sb.copy()
+    for r, g in zip(*np.nonzero(zero)):
+        q[r, g * 128:(g + 1) * 128] = 0
+        prev = [h for h in range(g - 1, -1, -1) if not zero[r, h]]
+        nxt = [h for h in range(g + 1, groups) if not zero[r, h]]
+        sb[r, g] = orig[r, prev[0]] if prev else (orig[r, nxt[0]] if nxt else 0x3F80)
+    u = (q + 8).astype(np.uint32)
 
     def row0(p, m):
         return (p * 16 + m * (n // 2)) if gated else ((2 * p + m) * 16)
 
     out = np.zeros((pairs, groups, 2, 64, 4), dtype=np.uint32)
     sc = np.zeros((pairs, groups, 4, 2, 4), dtype=np.uint16)
-    sb = scales_bits.reshape(n, groups)
     for p in range(pairs):
         for m in range(2):
             rows = row0(p, m) + lane % 16

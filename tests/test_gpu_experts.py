@@ -116,3 +116,68 @@ def test_flash_prefill_2048_subset():
 def test_flash_zipf_routing_subset():
     ids = S.zipf_ids(512, 256, 6, device=DEV)
     check_layer(S.FLASH, 512, rows=[0, 5, 511], seed=15, ids=ids)
+
+
+def test_flash_prefill_8192_zipf_subset():
+    """Zipf(1.1) routing at T=8192: the hottest experts span dozens of
+    alignment blocks (many 128-slot chunks), cold experts a partial block."""
+    ids = S.zipf_ids(8192, 256, 6, device=DEV)
+    counts = torch.bincount(ids.flatten(), minlength=256)
+    hot = int(torch.argmax(counts))
+    hot_rows = torch.nonzero((ids == hot).any(dim=1)).flatten()[[0, -1]].cpu().numpy()
+    check_layer(S.FLASH, 8192, rows=np.r_[0, 4097, 8191, hot_rows], seed=17, ids=ids)
+
+
+def _custom_layer_check(shape, s13_fn, s2_fn, ts, seed):
+    w13, s13, w2, s2 = S.make_checkpoint_experts(shape, seed=seed, device=DEV)
+    g = torch.Generator(DEV).manual_seed(seed)
+    s13 = s13_fn(s13, g)
+    s2 = s2_fn(s2, g)
+    res = ResidentInt4MoEWeights.from_checkpoint_layout(w13, s13, w2, s2, experts=shape.experts,
+                                                        has_shared=shape.has_shared)
+    src = DeviceExpertSource(w13, s13, w2, s2)
+    for t in ts:
+        x = S.make_hidden(t, shape.hidden, seed=seed + t, device=DEV)
+        r = route_from_logits(S.make_logits(t, shape.experts, seed=seed + t + 1, device=DEV), topk=shape.topk)
+        bs = ops.block_size_m(t, shape.topk, shape.experts)
+        align = deterministic_moe_align_block_size(r.routing_ids, block_size=bs, num_experts=shape.experts)
+        out = torch.empty((t, shape.hidden), dtype=torch.bfloat16, device=DEV)
+        ws = torch.empty(ops.experts_workspace_bytes(t, shape.topk, shape.hidden, shape.inter, shape.has_shared),
+                         dtype=torch.uint8, device=DEV)
+        ops.experts_w4a16_into(
+            x, w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, experts=shape.experts,
+            inter=shape.inter, has_shared=shape.has_shared, route_weights=r.routing_weights,
+            sorted_token_ids=align.sorted_token_ids, expert_ids=align.expert_ids,
+            num_tokens_post_padded=align.num_tokens_post_padded, block_size=bs, clamp_limit=0.0,
+            out=out, workspace=ws)
+        torch.cuda.synchronize()
+        ref = O.moe_fp32(to_np_f32(x), r.routing_ids.cpu().numpy(), r.routing_weights.cpu().numpy(), src,
+                         shared_index=shape.experts if shape.has_shared else None)
+        err = assert_moe_close(to_np_f32(out), ref, what=f"T={t} bs={bs}")
+        print(f"    T={t} bs={bs} {err}", flush=True)
+
+
+def test_zero_scale_groups_decode_and_prefill():
+    """Groups with zero scales (and whole zero rows) contribute nothing; the
+    packer's canonical form keeps the prefill scale ratios finite."""
+    shape = S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True)
+
+    def zero_some(s, g):
+        mask = torch.rand(s.shape, device=DEV, generator=g) < 0.25
+        s = torch.where(mask, torch.zeros_like(s), s)
+        s[:, 3, :] = 0.0
+        return s
+
+    _custom_layer_check(shape, zero_some, zero_some, ts=(8, 64, 200), seed=21)
+
+
+def test_wide_scale_range_prefill():
+    """Scales spanning 2^-14 .. 2^6 within a row: the running sum is kept
+    divided by the current group's scale, so consecutive ratios reach 2^20."""
+    shape = S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True)
+
+    def wide(s, g):
+        e = torch.randint(-14, 7, s.shape, device=DEV, generator=g).float()
+        return (torch.exp2(e) * (1.0 + torch.rand(s.shape, device=DEV, generator=g))).to(torch.bfloat16)
+
+    _custom_layer_check(shape, wide, wide, ts=(64, 200), seed=23)

@@ -26,6 +26,27 @@ def test_pack_matches_numpy_layout(n, k, batch, gated):
         np.testing.assert_array_equal(bf16_bits(ps[b]), ref_sc)
 
 
+@pytest.mark.parametrize("gated", [False, True])
+def test_pack_zero_scale_groups(gated):
+    """Groups with a +-0 scale are stored as q = 0 with the nearest nonzero
+    scale of the row (previous group first, else next, else 1.0)."""
+    n, k, batch = 64, 1024, 2
+    g = torch.Generator(DEV).manual_seed(7)
+    canon = torch.randint(0, 256, (batch, n, k // 2), dtype=torch.uint8, device=DEV, generator=g)
+    scales = (torch.rand((batch, n, k // 128), device=DEV, generator=g) + 0.5).to(torch.bfloat16)
+    mask = torch.rand((batch, n, k // 128), device=DEV, generator=g) < 0.3
+    scales = torch.where(mask, torch.zeros_like(scales), scales)
+    scales[0, 5, :] = 0.0           # a whole row of zero scales -> 1.0
+    scales[1, 7, :3] = -0.0         # leading zeros take the next nonzero scale
+    packed, ps = ops.pack_int4_g128(canon, scales, gated=gated)
+    torch.cuda.synchronize()
+    for b in range(batch):
+        ref_bytes, ref_sc = np_tile_pack(canon[b].cpu().numpy(), bf16_bits(scales[b]), gated=gated)
+        np.testing.assert_array_equal(packed[b].cpu().numpy(), ref_bytes)
+        np.testing.assert_array_equal(bf16_bits(ps[b]), ref_sc)
+    assert ((bf16_bits(ps) & 0x7FFF) != 0).all()
+
+
 def test_pack_rejects_bad_shapes():
     canon = torch.zeros((1, 48, 64), dtype=torch.uint8, device=DEV)  # n % 32 != 0
     scales = torch.zeros((1, 48, 1), dtype=torch.bfloat16, device=DEV)
