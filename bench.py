@@ -15,7 +15,9 @@ fixed-routing figure is reported beside it).
 
 Also reported on the same line (secondary): decode at T in {1, 8, 256},
 prefill at T in {2048, 4096, 8192}, the W4A8 layer (uniform and Zipf routing,
-T = 64 and 8192), the W8A16 dense linear at K = 4096, and the CPU baseline
+T = 64 and 8192), the same layer with MXFP4 experts (the reference
+checkpoint's E2M1 + E8M0 format, T = 64 and 8192), the W8A16 dense linear at
+K = 4096, and the CPU baseline
 (the oracle's restatement of the reference torch path timed on this host's
 cores on a bounded sample).
 
@@ -225,6 +227,7 @@ def main() -> int:
     # -------------------------------------------------------- W4A8 and W8A16
     if args.secondary:
         secondary["w4a8"] = bench_w4a8(pkg, resident, gate, cfg, dev, T, args)
+        secondary["mxfp4"] = bench_mxfp4(pkg, gate, cfg, dev, T, args)
         secondary["w8a16_linear"] = bench_w8a16(pkg, dev)
 
     # ------------------------------------------------------------ CPU baseline
@@ -339,6 +342,69 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args):
             out[f"T{t}_{routing}"] = entry
             log(f"[bench] w4a8 T={t} {routing}: {entry}")
         del x, lg, o, ws
+    return out
+
+
+def bench_mxfp4(pkg, gate, cfg, dev, T, args):
+    """The same layer with MXFP4 routed + shared experts (E2M1 codes, E8M0
+    scale per 32 K: the reference checkpoint's routed-expert format) through
+    the TP4MoE drop-in: decode at T (routing rotated over 8 batches) and
+    prefill at the prefill size; stage-1 decode HBM rate and prefill TFLOP/s."""
+
+    import numpy as np
+    import torch
+
+    S, ops = pkg.synthetic, pkg.ops
+    E, H, I, K = cfg.experts, cfg.hidden_size, cfg.intermediate_size, cfg.topk
+    w13, s13, w2, s2 = S.make_checkpoint_experts_mxfp4(S.FLASH, seed=args.seed, device=dev)
+    res = pkg.ResidentMXFP4MoEWeights.from_checkpoint_layout(w13, s13, w2, s2, experts=E, has_shared=True)
+    del w13, s13, w2, s2
+    rows = [T] + ([args.prefill_tokens] if args.prefill_tokens else [])
+    layer = pkg.TP4MoE(config=cfg, resident=res, gate=gate, device=dev, global_row_shapes=sorted(set(rows)))
+    b13 = 2 * I * H // 2 + 2 * I * H // 32
+    out = {"expert_bytes": pkg.mxfp4_g32_expert_bytes(H, I)}
+    xs = [S.make_hidden(T, H, seed=7000 + i, device=dev).view(1, T, H) for i in range(8)]
+    lgs = [S.make_logits(T, E, seed=7500 + i, device=dev) for i in range(8)]
+    distinct = [int(torch.unique(pkg.route_from_logits(lg, topk=K, score_func="sigmoid").routing_ids).numel())
+                for lg in lgs]
+    for i in range(5):
+        layer.forward_tensor(xs[i % 8], router_logits=lgs[i % 8])
+    n = 100
+    ops.profile_begin(n)
+    ms = cuda_timer(lambda i: layer.forward_tensor(xs[i % 8], router_logits=lgs[i % 8]), n)
+    pk, _ = ops.profile_end()
+    d_mean = float(np.mean([distinct[i % 8] for i in range(n)]))
+    st1 = (d_mean + 1) * b13 + T * H * 2 + (T * K + T) * I * 2
+    layer_b = (d_mean + 1) * out["expert_bytes"] + 2 * T * H * 2 + T * E * 4 + T * K * 8
+    out[f"decode_T{T}"] = {
+        "ms_per_step": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "layer_hbm_gbs": round(layer_b / (ms * 1e-3) / 1e9, 1),
+        "stage1_hbm_gbs": round(st1 / (pk["stage1_w13"] * 1e-3) / 1e9, 1),
+        "stage1_frac_of_hbm_peak": round(st1 / (pk["stage1_w13"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "kernel_ms": {k: round(v, 4) for k, v in pk.items()},
+    }
+    log(f"[bench] mxfp4 decode T={T}: {out[f'decode_T{T}']}")
+    if args.prefill_tokens:
+        tp = args.prefill_tokens
+        xp = S.make_hidden(tp, H, seed=3000, device=dev).view(1, tp, H)
+        lp = S.make_logits(tp, E, seed=3001, device=dev)
+        for _ in range(2):
+            layer.forward_tensor(xp, router_logits=lp)
+        ops.profile_begin(args.prefill_steps)
+        pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps)
+        pk, _ = ops.profile_end()
+        flops = 6.0 * tp * (K + 1) * H * I
+        mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
+        out[f"prefill_T{tp}"] = {
+            "ms_per_step": round(pms, 4), "tokens_per_s": round(tp / (pms * 1e-3), 1),
+            "layer_tflops": round(flops / (pms * 1e-3) / 1e12, 2),
+            "layer_frac_of_bf16_peak": round(flops / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "grouped_gemm_tflops": round(flops / (mm_ms * 1e-3) / 1e12, 2),
+            "kernel_ms": {k: round(v, 4) for k, v in pk.items()},
+        }
+        log(f"[bench] mxfp4 prefill T={tp}: {out[f'prefill_T{tp}']}")
+    del layer, res
+    torch.cuda.empty_cache()
     return out
 
 

@@ -42,7 +42,12 @@ from .moe_runtime import (  # noqa: F401
     TP4MoE,
     TP4MoEConfig,
 )
-from .weights import ResidentInt4MoEWeights, int4_g128_expert_bytes  # noqa: F401
+from .weights import (  # noqa: F401
+    ResidentInt4MoEWeights,
+    ResidentMXFP4MoEWeights,
+    int4_g128_expert_bytes,
+    mxfp4_g32_expert_bytes,
+)
 
 ALIAS = "gaiban_lite_amd"
 

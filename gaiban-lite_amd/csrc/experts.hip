@@ -496,15 +496,6 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 using namespace dsv4;
 
-struct ExpertWorkspace {
-  float* xsum;
-  uint16_t* h;
-  float* hsum;
-  float* contrib;
-  size_t bytes;
-};
-
-static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Resident workgroups of a decode kernel on the current device (CUs x
 // occupancy), cached per device: the persistent grid size.
@@ -522,24 +513,6 @@ static int decode_resident_grid() {
     cache[dev] = cus * per_cu;
   }
   return cache[dev];
-}
-
-static ExpertWorkspace carve_workspace(void* base, int64_t tokens, int topk, int hidden, int inter,
-                                       int has_shared) {
-  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
-  size_t off = 0;
-  ExpertWorkspace w;
-  char* b = static_cast<char*>(base);
-  w.xsum = reinterpret_cast<float*>(b + off);
-  off += align256(sizeof(float) * (size_t)tokens * (hidden / kSumChunk));
-  w.h = reinterpret_cast<uint16_t*>(b + off);
-  off += align256(sizeof(uint16_t) * (size_t)rows * inter);
-  w.hsum = reinterpret_cast<float*>(b + off);
-  off += align256(sizeof(float) * (size_t)rows * (inter / kSumChunk));
-  w.contrib = reinterpret_cast<float*>(b + off);
-  off += align256(sizeof(float) * (size_t)rows * hidden);
-  w.bytes = off;
-  return w;
 }
 
 size_t dsv4_experts_workspace_bytes(int64_t tokens, int topk, int hidden, int inter,

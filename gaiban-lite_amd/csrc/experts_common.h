@@ -38,6 +38,7 @@ struct ExpertGemmParams {
   float* contrib;        // stage 2: [rows][H]
   int out_cols;          // stage 2: H
   const float* act_scale;  // fp8 kernels: per-row activation scale [act_rows]
+  const uint8_t* ws8;      // MXFP4 kernels: tiled E8M0 scales (ws_stride bytes per expert)
 };
 
 struct BlockInfo {
@@ -135,6 +136,37 @@ __device__ __forceinline__ bool prefill_item(int n_tiles, int total_blocks, int&
 
 }  // namespace dsv4
 
-// Host launchers shared by both expert paths (experts.hip).
+// Workspace of the expert launchers (caller-owned, 256-byte aligned pieces):
+// x row sums per 64 columns, h bf16 [rows][I], h row sums, fp32
+// contributions [rows][H]; rows = T*k (+ T with the shared expert).
+struct ExpertWorkspace {
+  float* xsum;
+  uint16_t* h;
+  float* hsum;
+  float* contrib;
+  size_t bytes;
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+inline ExpertWorkspace carve_workspace(void* base, int64_t tokens, int topk, int hidden, int inter,
+                                       int has_shared) {
+  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
+  size_t off = 0;
+  ExpertWorkspace w;
+  char* b = static_cast<char*>(base);
+  w.xsum = reinterpret_cast<float*>(b + off);
+  off += align256(sizeof(float) * (size_t)tokens * (hidden / dsv4::kSumChunk));
+  w.h = reinterpret_cast<uint16_t*>(b + off);
+  off += align256(sizeof(uint16_t) * (size_t)rows * inter);
+  w.hsum = reinterpret_cast<float*>(b + off);
+  off += align256(sizeof(float) * (size_t)rows * (inter / dsv4::kSumChunk));
+  w.contrib = reinterpret_cast<float*>(b + off);
+  off += align256(sizeof(float) * (size_t)rows * hidden);
+  w.bytes = off;
+  return w;
+}
+
+// Host launchers shared by the expert paths (experts.hip).
 int dsv4_launch_combine(const float* contrib, int64_t tokens, int topk, int hidden, int has_shared,
                         uint16_t* out, hipStream_t stream);

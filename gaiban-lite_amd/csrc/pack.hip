@@ -109,9 +109,84 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const uint16_t* __rest
   }
 }
 
+// MXFP4 (E2M1 codes, one E8M0 scale per 32 K; the reference checkpoint
+// format, runtime/dsv4_direct/moe_forward.py:126-155).  Same tile geometry
+// and pair interleave as the int4 layout; inside a tile lane L's dword d is
+// the 4 checkpoint bytes of row L%16, k0 = 128g + 32d + 8*(L/16) .. k0+7
+// (low nibble = even k), which is the byte order v_cvt_scalef32_pk_bf16_fp4
+// consumes.  Scales: 128 bytes per (pair, group), byte (r16*2 + m)*4 + d
+// holds the E8M0 scale of row r16 of member m for k in [128g + 32d, +32), so
+// one 8-byte load gives a lane both members' four scales.
+__global__ __launch_bounds__(256) void pack_mxfp4_kernel(const uint8_t* __restrict__ canon,
+                                                         uint8_t* __restrict__ packed, int64_t n,
+                                                         int64_t k, int64_t batch, int pairing) {
+  const int64_t groups = k / kGroup;
+  const int64_t tiles_per_mat = (n / 16) * groups;
+  const int64_t total = batch * tiles_per_mat * 64;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(idx & 63);
+    const int64_t tile = idx >> 6;  // destination tile order: (mat, p, g, m)
+    const int64_t mat = tile / tiles_per_mat;
+    const int64_t tin = tile % tiles_per_mat;
+    const int m = (int)(tin & 1);
+    const int64_t g = (tin >> 1) % groups;
+    const int64_t p = (tin >> 1) / groups;
+    const int64_t row = member_row0(p, m, n, pairing) + (lane & 15);
+    const uint8_t* src_row = canon + mat * n * (k / 2) + row * (k / 2);
+    u32x4 out;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      out[d] = *reinterpret_cast<const uint32_t*>(src_row + (g * kGroup + 32 * d + 8 * (lane >> 4)) / 2);
+    *reinterpret_cast<u32x4*>(packed + mat * n * (k / 2) + tin * kTileBytes + lane * 16) = out;
+  }
+}
+
+__global__ __launch_bounds__(256) void pack_e8m0_kernel(const uint8_t* __restrict__ canon_s,
+                                                        uint8_t* __restrict__ packed_s, int64_t n,
+                                                        int64_t k, int64_t batch, int pairing) {
+  const int64_t groups = k / kGroup;
+  const int64_t total = batch * n * (k / 32);
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    // destination order (mat, p, g, r16, m, d)
+    const int d = (int)(idx & 3);
+    const int m = (int)((idx >> 2) & 1);
+    const int r16 = (int)((idx >> 3) & 15);
+    const int64_t rest = idx >> 7;  // (mat, p, g)
+    const int64_t g = rest % groups;
+    const int64_t pm = rest / groups;
+    const int64_t mat = pm / (n / 32);
+    const int64_t p = pm % (n / 32);
+    const int64_t row = member_row0(p, m, n, pairing) + r16;
+    packed_s[idx] = canon_s[mat * n * (k / 32) + row * (k / 32) + 4 * g + d];
+  }
+}
+
 }  // namespace dsv4
 
 using namespace dsv4;
+
+int dsv4_launch_pack_mxfp4(const uint8_t* canon, const uint8_t* canon_scales, int64_t batch, int64_t n,
+                           int64_t k, int pairing, uint8_t* packed, uint8_t* packed_scales,
+                           hipStream_t stream) {
+  const int64_t work = batch * (n / 16) * (k / kGroup) * 64;
+  const int64_t blocks = (work + 255) / 256;
+  const unsigned grid = (unsigned)(blocks < 65535 * 16 ? blocks : 65535 * 16);
+  if (work > 0) {
+    hipLaunchKernelGGL(pack_mxfp4_kernel, dim3(grid), dim3(256), 0, stream, canon, packed, n, k, batch, pairing);
+    DSV4_CHECK_LAUNCH("pack_mxfp4_kernel");
+  }
+  const int64_t swork = batch * n * (k / 32);
+  const int64_t sblocks = (swork + 255) / 256;
+  const unsigned sgrid = (unsigned)(sblocks < 65535 * 16 ? sblocks : 65535 * 16);
+  if (swork > 0) {
+    hipLaunchKernelGGL(pack_e8m0_kernel, dim3(sgrid), dim3(256), 0, stream, canon_scales, packed_scales, n, k,
+                       batch, pairing);
+    DSV4_CHECK_LAUNCH("pack_e8m0_kernel");
+  }
+  return DSV4MOE_OK;
+}
 
 int dsv4_launch_pack(const uint8_t* canon, const uint16_t* canon_scales, int64_t batch, int64_t n,
                      int64_t k, int pairing, uint8_t* packed, uint16_t* packed_scales,

@@ -31,7 +31,7 @@ from .deterministic_moe_align import (
     DeterministicMoEAlignment,
     allocate_deterministic_moe_alignment,
 )
-from .weights import ResidentInt4MoEWeights
+from .weights import ResidentInt4MoEWeights, ResidentMXFP4MoEWeights
 
 SCORE_FUNCS = ("sigmoid", "softmax", "sqrtsoftplus")
 
@@ -229,7 +229,7 @@ class TP4MoE:
         self,
         *,
         config: TP4MoEConfig,
-        resident: ResidentInt4MoEWeights,
+        resident: ResidentInt4MoEWeights | ResidentMXFP4MoEWeights,
         gate: ResidentGateWeights,
         rank: int = 0,
         device: torch.device,
@@ -260,8 +260,8 @@ class TP4MoE:
             )
         if marlin_input_dtype is not None and (config.hidden_size % 512 or config.intermediate_size % 512):
             raise ValueError("W4A8 needs hidden and intermediate sizes that are multiples of 512")
-        if not isinstance(resident, ResidentInt4MoEWeights):
-            raise TypeError("resident must be ResidentInt4MoEWeights")
+        if not isinstance(resident, (ResidentInt4MoEWeights, ResidentMXFP4MoEWeights)):
+            raise TypeError("resident must be ResidentInt4MoEWeights or ResidentMXFP4MoEWeights")
         resident.validate()
         if (resident.experts, resident.hidden_size, resident.intermediate_size) != (
             config.experts, config.hidden_size, config.intermediate_size
@@ -301,6 +301,7 @@ class TP4MoE:
         self.device = device
         self.group = group
         self._marlin_input_dtype = marlin_input_dtype
+        self._mxfp4 = isinstance(resident, ResidentMXFP4MoEWeights)
         self._gate_weight = gate.weight.to(torch.bfloat16).contiguous()
         self._gate_bias = None if gate.bias is None else gate.bias.float().contiguous()
         self.overlap_stats: dict[str, int] = {
@@ -581,6 +582,7 @@ class TP4MoE:
                 fused = (
                     self.route_kind == "learned"
                     and self._marlin_input_dtype is None
+                    and not self._mxfp4
                     and override is None
                     and self._owned_alignment_provider is None
                     and self._route_tensor_observer is None
@@ -657,7 +659,12 @@ class TP4MoE:
                     if aligned is not a:
                         self._poison_alignment_runtime()
                         raise RuntimeError("alignment provider must return the caller-owned output")
-                experts_into = ops.experts_w4a8_into if self._marlin_input_dtype else ops.experts_w4a16_into
+                if self._mxfp4:
+                    experts_into = ops.experts_mxfp4_into
+                elif self._marlin_input_dtype:
+                    experts_into = ops.experts_w4a8_into
+                else:
+                    experts_into = ops.experts_w4a16_into
                 experts_into(
                     flat, w13q=self.resident.w13_q, w13s=self.resident.w13_s,
                     w2q=self.resident.w2_q, w2s=self.resident.w2_s, experts=cfg.experts,

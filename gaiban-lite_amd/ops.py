@@ -191,6 +191,33 @@ def pack_int4_g128(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = F
     return packed, packed_scales
 
 
+def pack_mxfp4_g32(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = False
+                   ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Checkpoint-layout MXFP4 [.., n, k/2] u8 (E2M1, low nibble = even k) +
+    E8M0 scales [.., n, k/32] u8 -> tiles (packed u8 [.., n*k/2], scales u8
+    [.., n*k/32]) in the tile geometry and pairing of ``pack_int4_g128``."""
+
+    if canon.ndim == 2:
+        canon = canon.unsqueeze(0)
+        scales = scales.unsqueeze(0)
+        squeeze = True
+    else:
+        squeeze = False
+    batch, n, half_k = canon.shape
+    k = half_k * 2
+    dev = canon.device
+    _check("canon", canon, dtype=torch.uint8, device=dev)
+    _check("scales", scales, dtype=torch.uint8, shape=(batch, n, k // 32), device=dev)
+    packed = torch.empty((batch, n * half_k), dtype=torch.uint8, device=dev)
+    packed_scales = torch.empty((batch, n * (k // 32)), dtype=torch.uint8, device=dev)
+    call("dsv4moe_pack_mxfp4_g32", ptr(canon), ptr(scales), batch, n, k,
+         _lib.PAIR_GATED if gated else _lib.PAIR_PLAIN, ptr(packed), ptr(packed_scales),
+         _lib.current_stream(dev))
+    if squeeze:
+        return packed[0], packed_scales[0]
+    return packed, packed_scales
+
+
 def experts_workspace_bytes(tokens: int, topk: int, hidden: int, inter: int, has_shared: bool) -> int:
     return int(_lib.load().dsv4moe_experts_workspace_bytes(tokens, topk, hidden, inter, int(bool(has_shared))))
 
@@ -222,6 +249,13 @@ def experts_w4a8_into(x: torch.Tensor, **kw) -> None:
 
 def experts_w4a16_into(x: torch.Tensor, **kw) -> None:
     _experts_into("dsv4moe_experts_w4a16", x, **kw)
+
+
+def experts_mxfp4_into(x: torch.Tensor, **kw) -> None:
+    """MXFP4 experts (``dsv4moe_experts_mxfp4``); same keywords as
+    ``experts_w4a16_into`` with ``pack_mxfp4_g32`` weights and E8M0 scales."""
+
+    _experts_into("dsv4moe_experts_mxfp4", x, **kw)
 
 
 def _experts_into(

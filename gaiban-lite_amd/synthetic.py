@@ -66,6 +66,35 @@ def make_checkpoint_experts(shape: LayerShape, *, seed: int = 0, device="cuda",
     return w13, s13, w2, s2
 
 
+def make_checkpoint_experts_mxfp4(shape: LayerShape, *, seed: int = 0, device="cuda",
+                                  experts: range | None = None):
+    """Checkpoint-layout MXFP4 weights (the reference's routed-expert format,
+    ``moe_forward.py:126-155``) for all (or a range of) experts.
+
+    Returns (w13_packed [n, 2I, H/2] u8, w13_scale [n, 2I, H/32] u8 E8M0,
+             w2_packed [n, H, I/2] u8, w2_scale [n, H, I/32] u8 E8M0).
+    Codes are uniform bytes (two E2M1 codes each); E8M0 scale bytes are
+    uniform in [119, 122], i.e. 2^-8 .. 2^-5, which gives weights of the same
+    magnitude as the int4-g128 generator.  Seeded per expert as
+    ``make_checkpoint_experts``.
+    """
+
+    ids = range(shape.total_experts) if experts is None else experts
+    n = len(ids)
+    h, i = shape.hidden, shape.inter
+    w13 = torch.empty((n, 2 * i, h // 2), dtype=torch.uint8, device=device)
+    s13 = torch.empty((n, 2 * i, h // 32), dtype=torch.uint8, device=device)
+    w2 = torch.empty((n, h, i // 2), dtype=torch.uint8, device=device)
+    s2 = torch.empty((n, h, i // 32), dtype=torch.uint8, device=device)
+    for slot, e in enumerate(ids):
+        g = _gen(seed * 1_000_003 + e + 500_000, device)
+        w13[slot] = torch.randint(0, 256, (2 * i, h // 2), dtype=torch.uint8, device=device, generator=g)
+        s13[slot] = torch.randint(119, 123, (2 * i, h // 32), dtype=torch.uint8, device=device, generator=g)
+        w2[slot] = torch.randint(0, 256, (h, i // 2), dtype=torch.uint8, device=device, generator=g)
+        s2[slot] = torch.randint(119, 123, (h, i // 32), dtype=torch.uint8, device=device, generator=g)
+    return w13, s13, w2, s2
+
+
 def make_hidden(tokens: int, hidden: int, *, seed: int = 1, device="cuda") -> torch.Tensor:
     return torch.randn((tokens, hidden), device=device, generator=_gen(seed, device)).to(torch.bfloat16)
 
@@ -101,6 +130,7 @@ __all__ = [
     "TINY",
     "LayerShape",
     "make_checkpoint_experts",
+    "make_checkpoint_experts_mxfp4",
     "make_hidden",
     "make_int8_linear",
     "make_logits",

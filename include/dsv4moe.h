@@ -199,6 +199,38 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                         size_t workspace_bytes, void* stream);
 
 /*
+ * MXFP4 experts: E2M1 codes with one E8M0 scale per 32 K, the checkpoint
+ * format of the reference's routed experts (runtime/dsv4_direct/moe_forward.py:
+ * 23-40,115-155; the MXFP4 Marlin path of ops/marlin_moe.py:173-223 and
+ * moe_runtime.py:1829-1856; dense restatement ops/dense_moe.py:41-68,336-354).
+ *
+ * dsv4moe_pack_mxfp4_g32 repacks checkpoint-layout weights:
+ *   canon        uint8 [batch, n, k/2]  (E2M1, low nibble = even k)
+ *   canon_scales uint8 [batch, n, k/32] (E8M0: 2^(e-127); 255 is reserved)
+ *   packed       uint8 [batch, n*k/2]   out: the tile geometry and pairing of
+ *                dsv4moe_pack_int4_g128; lane L's dword d of a tile holds the 4
+ *                checkpoint bytes of row L%16 for k = 128g + 32d + 8*(L/16) ..
+ *   packed_scales uint8 [batch, n*k/32] out: 128 bytes per (pair, group),
+ *                byte (r16*2 + m)*4 + d = scale of row r16 of member m for
+ *                k in [128g + 32d, +32)
+ *   n % 32 == 0, k % 128 == 0.
+ * dsv4moe_experts_mxfp4: as dsv4moe_experts_w4a16 (same routing, alignment,
+ * workspace from dsv4moe_experts_workspace_bytes, combine and output) with
+ * MXFP4-packed weights: W = code * 2^(e-127) exactly, bf16 MFMA with fp32
+ * accumulation.  hidden % 512 == 0, inter % 512 == 0.
+ */
+int dsv4moe_pack_mxfp4_g32(const uint8_t* canon, const uint8_t* canon_scales, int64_t batch,
+                           int64_t n, int64_t k, int32_t pairing, uint8_t* packed,
+                           uint8_t* packed_scales, void* stream);
+int dsv4moe_experts_mxfp4(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
+                          int32_t experts, int32_t topk, const uint8_t* w13q, const uint8_t* w13s,
+                          const uint8_t* w2q, const uint8_t* w2s, int32_t has_shared,
+                          const float* weights, const int32_t* sorted_token_ids, int64_t capacity,
+                          const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                          int32_t block_size, float clamp_limit, uint16_t* out, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
  * W8A16 dense linear: out[M,N] = bf16( a[M,K] . (q[N,K] * s[N])^T ), int8
  * symmetric per-output-channel weights, bf16 scales, fp32 accumulation.
  * Replaces w8a16_gemm_into / make_gemm_plan / _automatic_split_k

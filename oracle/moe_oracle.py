@@ -60,6 +60,7 @@ __all__ = [
     "SCORE_SQRTSOFTPLUS",
     "AlignResult",
     "ExpertSource",
+    "MXFP4ExpertSource",
     "RouteResult",
     "act_quant_per_token_fp8",
     "automatic_split_k",
@@ -594,6 +595,23 @@ class ExpertSource:
 
     def w2(self, e: int) -> np.ndarray:
         return dequant_int4_g128(np.asarray(self.w2_packed[e]), np.asarray(self.w2_scale[e]), self.group)
+
+
+class MXFP4ExpertSource(ExpertSource):
+    """Accessor for MXFP4 experts in the checkpoint layout (the reference's
+    routed-expert format, ``moe_forward.py:126-155``): ``w13_packed``
+    [E', 2I, H/2] u8 E2M1 codes (low nibble = even k), ``w13_scale``
+    [E', 2I, H/32] u8 E8M0, ``w2_packed`` [E', H, I/2], ``w2_scale`` [E', H, I/32].
+    Dequantisation is ``dequant_mxfp4`` (pinned by the FP4 table and E8M0 KATs)."""
+
+    def __init__(self, w13_packed, w13_scale, w2_packed, w2_scale):
+        super().__init__(w13_packed, w13_scale, w2_packed, w2_scale, group=32)
+
+    def w13(self, e: int) -> np.ndarray:
+        return dequant_mxfp4(np.asarray(self.w13_packed[e]), np.asarray(self.w13_scale[e]))
+
+    def w2(self, e: int) -> np.ndarray:
+        return dequant_mxfp4(np.asarray(self.w2_packed[e]), np.asarray(self.w2_scale[e]))
 
 
 def moe_fp32(

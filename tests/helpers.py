@@ -108,3 +108,32 @@ def np_tile_pack(canon: np.ndarray, scales_bits: np.ndarray, gated: bool = False
                 for quad in range(4):
                     sc[p, g, quad, m, :] = sb[row0(p, m) + 4 * quad + np.arange(4), g]
     return out.reshape(-1).view(np.uint8), sc.reshape(-1)
+
+
+def np_tile_pack_mxfp4(canon: np.ndarray, scale_codes: np.ndarray, gated: bool = False):
+    """Independent numpy statement of the MXFP4 tile layout (see
+    gaiban-lite_amd/csrc/pack.hip): returns (packed bytes [n*k/2], scale bytes
+    [n*k/32])."""
+
+    n, half_k = canon.shape
+    k = half_k * 2
+    groups = k // 128
+    pairs = n // 32
+    lane = np.arange(64)
+
+    def row0(p, m):
+        return (p * 16 + m * (n // 2)) if gated else ((2 * p + m) * 16)
+
+    out = np.zeros((pairs, groups, 2, 64, 16), dtype=np.uint8)
+    sc = np.zeros((pairs, groups, 16, 2, 4), dtype=np.uint8)
+    for p in range(pairs):
+        for m in range(2):
+            rows = row0(p, m) + lane % 16
+            for g in range(groups):
+                for d in range(4):
+                    b0 = (g * 128 + 32 * d + 8 * (lane // 16)) // 2
+                    for j in range(4):
+                        out[p, g, m, :, 4 * d + j] = canon[rows, b0 + j]
+                for r16 in range(16):
+                    sc[p, g, r16, m, :] = scale_codes[row0(p, m) + r16, 4 * g:4 * g + 4]
+    return out.reshape(-1), sc.reshape(-1)

@@ -171,3 +171,35 @@ def test_moe_w4a8_oracle_against_torch_fp8_pipeline():
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
     # the quantisation is not the identity: the W4A8 result differs from the W4A16 one
     assert O.rel_fro(got, O.moe_fp32(x, ids, w, src, shared_index=e, clamp_limit=0.4)) > 1e-3
+
+
+def test_e8m0_decode_matches_torch_float8_e8m0fnu():
+    """The reference decodes scales with scale.view(torch.float8_e8m0fnu).float()
+    (moe_forward.py:115-123); the oracle's decode equals it for every byte but
+    the reserved 255 (NaN there, rejected here)."""
+
+    import torch
+
+    codes = np.arange(255, dtype=np.uint8)
+    ref = torch.from_numpy(codes.copy()).view(torch.float8_e8m0fnu).float().numpy()
+    np.testing.assert_array_equal(O.decode_e8m0(codes), ref)
+    assert np.isnan(torch.tensor([255], dtype=torch.uint8).view(torch.float8_e8m0fnu).float().item())
+
+
+def test_mxfp4_source_is_dequant_then_matmul():
+    """MXFP4ExpertSource dequantises with dequant_mxfp4 (w13 rows = gate, up)."""
+
+    rng = np.random.default_rng(5)
+    e, h, i = 2, 256, 128
+    w13 = rng.integers(0, 256, size=(e, 2 * i, h // 2), dtype=np.uint8)
+    s13 = rng.integers(118, 124, size=(e, 2 * i, h // 32), dtype=np.uint8)
+    w2 = rng.integers(0, 256, size=(e, h, i // 2), dtype=np.uint8)
+    s2 = rng.integers(118, 124, size=(e, h, i // 32), dtype=np.uint8)
+    src = O.MXFP4ExpertSource(w13, s13, w2, s2)
+    table = np.asarray(O.FP4_VALUES, dtype=np.float32)
+    for ex in range(e):
+        w = src.w13(ex)
+        for n, k in ((0, 0), (5, 33), (2 * i - 1, h - 1)):
+            code = (w13[ex, n, k // 2] >> (4 * (k % 2))) & 0xF
+            assert w[n, k] == table[code] * np.float32(2.0 ** (int(s13[ex, n, k // 32]) - 127))
+        assert src.w2(ex).shape == (h, i)
