@@ -169,17 +169,23 @@ def main() -> int:
     def step(i):
         layer.forward_tensor(xs[i % args.pool], router_logits=lgs[i % args.pool])
 
-    ops.profile_begin(args.steps)
+    # timed region: K steps with two HIP events per step around the roofline
+    # kernel (stage 1), recorded by the library on the launch stream
+    ops.profile_begin(args.steps, intervals=["stage1_w13"])
     ms = cuda_timer(step, args.steps)
-    kern, ncalls = ops.profile_end()
+    roof, ncalls = ops.profile_end()
+    # the same steps with all seven stamps (per-kernel breakdown), and with none
+    ops.profile_begin(args.steps)
+    ms_all = cuda_timer(step, args.steps)
+    kern, _ = ops.profile_end()
     ms_plain = cuda_timer(step, args.steps)
     ms_fixed = cuda_timer(lambda i: layer.forward_tensor(xs[0], router_logits=lgs[0]), args.steps)
     d_mean = float(np.mean([distinct[i % args.pool] for i in range(args.steps)]))
     stage1_bytes = (d_mean + 1) * b13 + T * H * 2 + (T * K + T) * I * 2
-    st1_ms = kern["stage1_w13"]
+    st1_ms = roof["stage1_w13"]
     achieved = stage1_bytes / (st1_ms * 1e-3) / 1e9
-    log(f"[bench] decode T={T}: {ms:.4f} ms/step profiled, {ms_plain:.4f} plain, {ms_fixed:.4f} fixed routing; "
-        f"kernels {kern}")
+    log(f"[bench] decode T={T}: {ms:.4f} ms/step (stage-1 events), {ms_all:.4f} with all kernel events, "
+        f"{ms_plain:.4f} without events, {ms_fixed:.4f} fixed routing; kernels {kern}")
 
     secondary = {}
     if args.secondary:
@@ -190,11 +196,15 @@ def main() -> int:
                 layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8])
             n = 100
             ms_t = cuda_timer(lambda i: layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8]), n)
+            ops.profile_begin(n)
+            cuda_timer(lambda i: layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8]), n)
+            kt, _ = ops.profile_end()
             dm = float(np.mean(dt_))
             gbs = layer_bytes(t, dm) / (ms_t * 1e-3) / 1e9
             dec[str(t)] = {"ms_per_step": round(ms_t, 4), "tokens_per_s": round(t / (ms_t * 1e-3), 1),
                            "distinct_experts_mean": round(dm, 1), "layer_hbm_gbs": round(gbs, 1),
-                           "layer_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+                           "layer_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                           "kernel_ms": {k: round(v, 4) for k, v in kt.items()}}
             log(f"[bench] decode T={t}: {dec[str(t)]}")
         secondary["decode_other_T"] = dec
 
@@ -262,6 +272,7 @@ def main() -> int:
         },
         "layer_hbm_gbs": round(layer_bytes(T, d_mean) / (ms * 1e-3) / 1e9, 1),
         "layer_frac_of_hbm_peak": round(layer_bytes(T, d_mean) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "ms_per_step_all_kernel_events": round(ms_all, 5),
         "ms_per_step_unprofiled": round(ms_plain, 5),
         "ms_per_step_fixed_routing": round(ms_fixed, 5),
         "kernel_ms": {k: round(v, 5) for k, v in kern.items()},

@@ -34,6 +34,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_last_error": (ctypes.c_char_p, []),
     "dsv4moe_abi_version": (_i32, []),
     "dsv4moe_profile_begin": (ctypes.c_int, [_i32]),
+    "dsv4moe_profile_begin_stamps": (ctypes.c_int, [_i32, ctypes.c_uint32]),
     "dsv4moe_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_float), _i32, ctypes.POINTER(_i32)]),
     "dsv4moe_block_size_m": (_i32, [_i64, _i32, _i32, _i32]),
     "dsv4moe_max_padded_tokens": (_i64, [_i64, _i32, _i32]),

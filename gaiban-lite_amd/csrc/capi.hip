@@ -38,13 +38,15 @@ struct ProfileState {
   std::vector<hipEvent_t> events;
   int max_calls = 0;
   int call = 0;
+  uint32_t mask = 0;  // stamps recorded (bit i = stamp i)
   bool active = false;
 };
 static ProfileState g_prof;
 
 void prof_stamp(int stamp, hipStream_t stream) {
   if (!g_prof.active || g_prof.call >= g_prof.max_calls) return;
-  (void)hipEventRecord(g_prof.events[(size_t)g_prof.call * kNumStamps + stamp], stream);
+  if (g_prof.mask & (1u << stamp))
+    (void)hipEventRecord(g_prof.events[(size_t)g_prof.call * kNumStamps + stamp], stream);
   if (stamp == kNumStamps - 1) ++g_prof.call;
 }
 
@@ -55,6 +57,7 @@ static void prof_release() {
   g_prof.active = false;
   g_prof.call = 0;
   g_prof.max_calls = 0;
+  g_prof.mask = 0;
 }
 
 }  // namespace dsv4host
@@ -119,8 +122,14 @@ const char* dsv4moe_last_error(void) { return dsv4host::g_error; }
 int32_t dsv4moe_abi_version(void) { return 1; }
 
 int dsv4moe_profile_begin(int32_t max_calls) {
+  return dsv4moe_profile_begin_stamps(max_calls, (1u << dsv4host::kNumStamps) - 1u);
+}
+
+int dsv4moe_profile_begin_stamps(int32_t max_calls, uint32_t stamp_mask) {
   clear_error();
   DSV4_REQUIRE(max_calls > 0 && max_calls <= 100000, "profile_begin: max_calls must be in [1, 100000]");
+  DSV4_REQUIRE(stamp_mask != 0 && (stamp_mask >> dsv4host::kNumStamps) == 0,
+               "profile_begin: stamp_mask must select stamps 0..%d", dsv4host::kNumStamps - 1);
   dsv4host::prof_release();
   dsv4host::g_prof.events.resize((size_t)max_calls * dsv4host::kNumStamps);
   for (auto& e : dsv4host::g_prof.events) {
@@ -133,6 +142,7 @@ int dsv4moe_profile_begin(int32_t max_calls) {
   }
   dsv4host::g_prof.max_calls = max_calls;
   dsv4host::g_prof.call = 0;
+  dsv4host::g_prof.mask = stamp_mask;
   dsv4host::g_prof.active = true;
   return DSV4MOE_OK;
 }
@@ -145,14 +155,20 @@ int dsv4moe_profile_end(float* mean_ms, int32_t n_intervals, int32_t* calls_reco
   DSV4_REQUIRE(mean_ms && n_intervals == kNumStamps - 1, "profile_end: need %d output slots",
                kNumStamps - 1);
   const int calls = g_prof.call;
-  for (int i = 0; i < kNumStamps - 1; ++i) mean_ms[i] = 0.0f;
+  const uint32_t mask = g_prof.mask;
+  // intervals whose two stamps were not both recorded read -1
+  for (int i = 1; i < kNumStamps; ++i)
+    mean_ms[i - 1] = ((mask >> (i - 1)) & 3u) == 3u ? 0.0f : -1.0f;
+  int last = kNumStamps - 1;
+  while (!(mask & (1u << last))) --last;
   int rc = DSV4MOE_OK;
-  if (calls > 0 && hipEventSynchronize(g_prof.events[(size_t)calls * kNumStamps - 1]) != hipSuccess) {
+  if (calls > 0 && hipEventSynchronize(g_prof.events[(size_t)(calls - 1) * kNumStamps + last]) != hipSuccess) {
     set_error("profile_end: hipEventSynchronize failed");
     rc = DSV4MOE_EHIP;
   }
   for (int c = 0; c < calls && rc == DSV4MOE_OK; ++c) {
     for (int i = 1; i < kNumStamps; ++i) {
+      if (((mask >> (i - 1)) & 3u) != 3u) continue;
       float ms = 0.0f;
       if (hipEventElapsedTime(&ms, g_prof.events[(size_t)c * kNumStamps + i - 1],
                               g_prof.events[(size_t)c * kNumStamps + i]) != hipSuccess) {

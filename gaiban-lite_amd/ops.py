@@ -33,21 +33,32 @@ def _check(name, t, *, dtype, shape=None, device=None):
 PROFILE_INTERVALS = ("route", "align", "row_sums", "stage1_w13", "stage2_w2", "combine")
 
 
-def profile_begin(max_calls: int) -> None:
-    """Start per-kernel HIP-event timing of the next ``max_calls`` layer calls."""
+def profile_begin(max_calls: int, intervals=None) -> None:
+    """Start per-kernel HIP-event timing of the next ``max_calls`` layer calls.
 
-    call("dsv4moe_profile_begin", int(max_calls))
+    ``intervals`` (names from PROFILE_INTERVALS) limits the events recorded to
+    the stamps bounding those intervals (two events per call for one kernel);
+    None records all seven stamps."""
+
+    if intervals is None:
+        call("dsv4moe_profile_begin", int(max_calls))
+        return
+    mask = 0
+    for name in intervals:
+        i = PROFILE_INTERVALS.index(name)  # interval i lies between stamps i and i + 1
+        mask |= (1 << i) | (1 << (i + 1))
+    call("dsv4moe_profile_begin_stamps", int(max_calls), mask)
 
 
 def profile_end() -> tuple[dict[str, float], int]:
-    """Stop timing; returns (mean ms per kernel interval, calls recorded)."""
+    """Stop timing; returns (mean ms per timed kernel interval, calls recorded)."""
 
     import ctypes
 
     out = (ctypes.c_float * len(PROFILE_INTERVALS))()
     calls = ctypes.c_int32(0)
     call("dsv4moe_profile_end", out, len(PROFILE_INTERVALS), ctypes.byref(calls))
-    return {k: float(out[i]) for i, k in enumerate(PROFILE_INTERVALS)}, int(calls.value)
+    return {k: float(out[i]) for i, k in enumerate(PROFILE_INTERVALS) if out[i] >= 0.0}, int(calls.value)
 
 
 def score_func_id(score_func: str | int) -> int:

@@ -54,6 +54,13 @@ int32_t dsv4moe_abi_version(void);
  */
 int dsv4moe_profile_begin(int32_t max_calls);
 int dsv4moe_profile_end(float* mean_ms, int32_t n_intervals, int32_t* calls_recorded);
+/*
+ * As dsv4moe_profile_begin, recording only the stamps whose bit is set in
+ * stamp_mask (bit i = stamp i in the order above), so that a timed loop can
+ * measure one kernel with two events instead of seven.  Intervals whose two
+ * stamps are not both recorded read -1 in dsv4moe_profile_end.
+ */
+int dsv4moe_profile_begin_stamps(int32_t max_calls, uint32_t stamp_mask);
 
 /*
  * Block-size policy for the expert alignment.
