@@ -77,7 +77,14 @@ size_t dsv4_experts_workspace_bytes(int64_t, int, int, int, int);
 int dsv4_launch_experts_w4a16(const uint16_t*, int64_t, int, int, int, int, const uint8_t*,
                               const uint16_t*, const uint8_t*, const uint16_t*, int, const float*,
                               const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
-                              uint16_t*, void*, hipStream_t);
+                              uint16_t*, void*, hipStream_t, bool rowsums_ready = false);
+float* dsv4_experts_xsum(void*, int64_t, int, int, int, int);
+int dsv4_launch_prologue(int32_t, const float*, const float*, int64_t, int32_t, int32_t, int32_t, float, int32_t*,
+                         float*, float*, int32_t, int32_t*, int64_t, int32_t*, int64_t, int32_t*, const uint16_t*,
+                         int32_t, float*, hipStream_t);
+// Largest token count routed inside the one-workgroup prologue (one token per
+// wavefront); above it the wide route kernel runs first.
+constexpr int64_t kPrologueRouteMaxTokens = 16;
 
 int dsv4_launch_pack_mxfp4(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, int, uint8_t*, uint8_t*,
                            hipStream_t);
@@ -421,19 +428,28 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                "layer_w4a16: null route/alignment pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   dsv4host::prof_stamp(dsv4host::kStampBegin, s);
-  rc = dsv4_launch_route_topk(logits, bias, tokens, experts, topk, score_func, route_scale, ids,
-                              weights, margin, nullptr, nullptr, s);
-  if (rc != DSV4MOE_OK) return rc;
-  dsv4host::prof_stamp(dsv4host::kStampRoute, s);
   const int64_t nblocks = (capacity + block_size - 1) / block_size;
-  rc = dsv4_launch_align(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity,
-                         expert_ids, nblocks, num_tokens_post_padded, s);
+  // One prologue launch aligns the ids and computes the activation row sums;
+  // for small T it also routes (then the route interval of the profile covers
+  // the whole prologue, and the align interval is empty).
+  const bool route_in_prologue = tokens <= kPrologueRouteMaxTokens;
+  if (!route_in_prologue) {
+    rc = dsv4_launch_route_topk(logits, bias, tokens, experts, topk, score_func, route_scale, ids,
+                                weights, margin, nullptr, nullptr, s);
+    if (rc != DSV4MOE_OK) return rc;
+    dsv4host::prof_stamp(dsv4host::kStampRoute, s);
+  }
+  float* xsum = dsv4_experts_xsum(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0);
+  rc = dsv4_launch_prologue(route_in_prologue ? 1 : 0, logits, bias, tokens, experts, topk, score_func, route_scale,
+                            ids, weights, margin, block_size, sorted_token_ids, capacity, expert_ids, nblocks,
+                            num_tokens_post_padded, x, hidden, xsum, s);
   if (rc != DSV4MOE_OK) return rc;
+  if (route_in_prologue) dsv4host::prof_stamp(dsv4host::kStampRoute, s);
   dsv4host::prof_stamp(dsv4host::kStampAlign, s);
   return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
-                                   has_shared ? 1 : 0, weights, sorted_token_ids, capacity,
-                                   expert_ids, num_tokens_post_padded, block_size, clamp_limit,
-                                   out, workspace, s);
+                                   has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
+                                   num_tokens_post_padded, block_size, clamp_limit, out, workspace, s,
+                                   /*rowsums_ready=*/true);
 }
 
 int dsv4moe_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed, void* stream) {

@@ -520,13 +520,19 @@ size_t dsv4_experts_workspace_bytes(int64_t tokens, int topk, int hidden, int in
   return carve_workspace(nullptr, tokens, topk, hidden, inter, has_shared).bytes;
 }
 
+// The activation row sums inside an experts workspace (written by the
+// prologue launch when the caller fuses them there).
+float* dsv4_experts_xsum(void* workspace, int64_t tokens, int topk, int hidden, int inter, int has_shared) {
+  return carve_workspace(workspace, tokens, topk, hidden, inter, has_shared).xsum;
+}
+
 int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int inter,
                               int experts, int topk, const uint8_t* w13q, const uint16_t* w13s,
                               const uint8_t* w2q, const uint16_t* w2s, int has_shared,
                               const float* weights, const int32_t* sorted, int64_t capacity,
                               const int32_t* expert_ids, const int32_t* ntpp, int block_size,
                               float clamp_limit, uint16_t* out, void* workspace,
-                              hipStream_t stream) {
+                              hipStream_t stream, bool rowsums_ready) {
   if (tokens == 0) return DSV4MOE_OK;
   ExpertWorkspace ws = carve_workspace(workspace, tokens, topk, hidden, inter, has_shared);
   const int max_blocks = (int)((capacity + block_size - 1) / block_size);
@@ -537,7 +543,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   const int blocks = max_blocks + shared_blocks;
   const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
 
-  {
+  if (!rowsums_ready) {
     const int64_t n = tokens * (hidden / kSumChunk);
     hipLaunchKernelGGL(row_chunk_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                        stream, x, tokens, hidden, ws.xsum);

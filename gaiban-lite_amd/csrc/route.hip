@@ -12,7 +12,10 @@
 //   log   : m in [sqrt(1/2), sqrt(2)), log m = 2 atanh((m-1)/(m+1)) (odd
 //           series to s^9), plus e*ln2 split in two parts.
 //   log1p : Goldberg's compensation log(w) * (u / (w - 1)), w = 1 + u.
+#include <algorithm>
+
 #include "common.h"
+#include "align_impl.h"
 #include "../../include/dsv4moe.h"
 
 #pragma clang fp contract(off)
@@ -83,15 +86,29 @@ __device__ __forceinline__ float key_value(uint32_t key) {
   return __uint_as_float((key & 0x80000000u) ? (key & 0x7FFFFFFFu) : ~key);
 }
 
+// Maximum of a 64-bit key over the wavefront, returned to every lane.  DPP
+// steps (row_shr 1/2/4/8, then row_bcast 15/31) build an inclusive running
+// maximum whose lane 63 covers all lanes; a lane whose DPP source is outside
+// its row keeps its own value.  Plain VALU moves, no LDS round trips (the
+// keys are distinct, so the reduction order cannot change the result).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_step(uint64_t v) {
+  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp((int)lo, (int)lo, CTRL, ROW_MASK, 0xF, false);
+  const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp((int)hi, (int)hi, CTRL, ROW_MASK, 0xF, false);
+  const uint64_t o = ((uint64_t)ohi << 32) | olo;
+  return o > v ? o : v;
+}
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, off, 64);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
+  v = dpp_max_step<0x111, 0xF>(v);  // row_shr:1
+  v = dpp_max_step<0x112, 0xF>(v);  // row_shr:2
+  v = dpp_max_step<0x114, 0xF>(v);  // row_shr:4
+  v = dpp_max_step<0x118, 0xF>(v);  // row_shr:8
+  v = dpp_max_step<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_max_step<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
 }
 
 template <int SCORE>
@@ -105,121 +122,219 @@ __device__ __forceinline__ float score_of(float logit, float row_max, float row_
   }
 }
 
+// Route NT tokens t0, t0 + tstride, ... (those below `tokens`) with one
+// wavefront (every lane calls it).  The tokens are independent: their loads
+// are issued together and their selection rounds interleave, so one memory
+// latency and one dependency chain cover all of them.  Per token the
+// operations and their order are those of a single-token route.
+template <int SCORE, int EPL, int NT>
+__device__ __forceinline__ void route_tokens(const float* __restrict__ logits, const float* __restrict__ bias,
+                                             int64_t t0, int64_t tstride, int64_t tokens, int experts, int topk,
+                                             float route_scale, int32_t* __restrict__ ids,
+                                             float* __restrict__ weights, float* __restrict__ margin,
+                                             int32_t* __restrict__ sel_ids, float* __restrict__ sel_scores) {
+  const int lane = threadIdx.x & 63;
+  bool valid[NT];
+  const float* row[NT];
+  float lg[NT][EPL];
+  float sel[NT][EPL];
+  uint32_t live[NT];
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    const int64_t t = t0 + u * tstride;
+    valid[u] = t < tokens;
+    row[u] = logits + (valid[u] ? t : 0) * experts;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + 64 * j;
+      lg[u][j] = (valid[u] && e < experts) ? row[u][e] : 0.0f;
+    }
+  }
+  float bv[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    bv[j] = (bias != nullptr && e < experts) ? bias[e] : 0.0f;
+  }
+
+  float row_max[NT], row_sum[NT];
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    row_max[u] = 0.0f;
+    row_sum[u] = 1.0f;
+    if constexpr (SCORE == DSV4MOE_SCORE_SOFTMAX) {
+      float m = -__builtin_huge_valf();
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (lane + 64 * j < experts) m = fmaxf(m, lg[u][j]);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+      row_max[u] = m;
+      float part = 0.0f;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (lane + 64 * j < experts) part = part + exp_seq(lg[u][j] - row_max[u]);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off, 64);
+      row_sum[u] = part;
+    }
+    live[u] = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int e = lane + 64 * j;
+      if (e < experts) {
+        float sc = score_of<SCORE>(lg[u][j], row_max[u], row_sum[u]);
+        if (bias != nullptr) sc = sc + bv[j];
+        sel[u][j] = sc;
+        live[u] |= 1u << j;
+      } else {
+        sel[u][j] = 0.0f;
+      }
+    }
+  }
+
+  // Selection: round r takes the (score, -id)-largest live expert; lane r
+  // keeps the id of round r, and rounds k-1 and k give the margin.
+  const int depth = topk + 1 <= experts ? topk + 1 : experts;
+  int my_id[NT];
+  float kth[NT], nxt[NT];
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    my_id[u] = 0;
+    kth[u] = 0.0f;
+    nxt[u] = 0.0f;
+  }
+  for (int r = 0; r < depth; ++r) {
+    uint64_t win[NT];
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+      uint64_t best = 0;
+      int best_j = -1;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) {
+        if (live[u] & (1u << j)) {
+          const int e = lane + 64 * j;
+          const uint64_t c = ((uint64_t)order_key(sel[u][j]) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+          if (best_j < 0 || c > best) {
+            best = c;
+            best_j = j;
+          }
+        }
+      }
+      win[u] = wave_max_u64(best);
+    }
+#pragma unroll
+    for (int u = 0; u < NT; ++u) {
+      const int e_win = (int)(0xFFFFFFFFu - (uint32_t)(win[u] & 0xFFFFFFFFu));
+      const float s_win = key_value((uint32_t)(win[u] >> 32));
+      if ((e_win & 63) == lane) live[u] &= ~(1u << (e_win >> 6));
+      if (lane == r) my_id[u] = e_win;
+      if (r == topk - 1) kth[u] = s_win;
+      if (r == topk) nxt[u] = s_win;
+      if (valid[u] && lane == 0) {
+        const int64_t t = t0 + u * tstride;
+        if (sel_ids) sel_ids[t * depth + r] = e_win;
+        if (sel_scores) sel_scores[t * depth + r] = s_win;
+      }
+    }
+  }
+
+  // Unbiased score of selected expert r, recomputed by lane r from its logit.
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    float my_score = 0.0f;
+    if (valid[u] && lane < topk) my_score = score_of<SCORE>(row[u][my_id[u]], row_max[u], row_sum[u]);
+    float w = my_score;
+    if constexpr (SCORE != DSV4MOE_SCORE_SOFTMAX) {
+      // sequential sum in selection order (lane r holds selected expert r)
+      const int sbits = __float_as_int(my_score);
+      float total = __int_as_float(__builtin_amdgcn_readlane(sbits, 0));
+      for (int r = 1; r < topk; ++r) total = total + __int_as_float(__builtin_amdgcn_readlane(sbits, r));
+      w = w / total;
+    }
+    w = w * route_scale;
+    if (!valid[u]) continue;
+    const int64_t t = t0 + u * tstride;
+    if (lane < topk) {
+      ids[t * topk + lane] = my_id[u];
+      weights[t * topk + lane] = w;
+    }
+    if (lane == 0 && margin != nullptr) margin[t] = depth > topk ? kth[u] - nxt[u] : 0.0f;
+  }
+}
+
 template <int SCORE, int EPL>
 __global__ __launch_bounds__(256) void route_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ bias, int64_t tokens,
     int experts, int topk, float route_scale, int32_t* __restrict__ ids,
     float* __restrict__ weights, float* __restrict__ margin, int32_t* __restrict__ sel_ids,
     float* __restrict__ sel_scores) {
-  const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (t >= tokens) return;
-  const float* row = logits + t * experts;
+  route_tokens<SCORE, EPL, 1>(logits, bias, t, 0, tokens, experts, topk, route_scale, ids, weights, margin,
+                              sel_ids, sel_scores);
+}
 
-  float lg[EPL];
-  float sel[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    lg[j] = e < experts ? row[e] : 0.0f;
-  }
+// Layer prologue in one launch: workgroup 0 routes every token when `route`
+// is set (wavefront w takes tokens w, w + 16, ...; used for T <= 16, since
+// routing is VALU-bound and one workgroup runs on one CU) and then runs the
+// alignment over the ids; workgroups 1.. compute the per-64-column row sums
+// of the activations (summed in ascending k, as row_chunk_sum_kernel).
+// Replaces the route, align and row-sum launches (or the last two).
+struct PrologueArgs {
+  const float* logits;
+  const float* bias;
+  int64_t tokens;
+  int experts;
+  int topk;
+  float route_scale;
+  int32_t* ids;
+  float* weights;
+  float* margin;
+  int expert_bits;
+  int block_size;
+  int32_t* sorted_ids;
+  int64_t capacity;
+  int32_t* expert_ids;
+  int64_t num_blocks;
+  int32_t* ntpp;
+  const uint16_t* x;   // row sums: x [tokens][hidden] (null: none)
+  int hidden;
+  float* xsum;         // [tokens][hidden / 64]
+  int route;           // route in workgroup 0 (else ids are given)
+};
 
-  float row_max = 0.0f, row_sum = 1.0f;
-  if constexpr (SCORE == DSV4MOE_SCORE_SOFTMAX) {
-    float m = -__builtin_huge_valf();
-#pragma unroll
-    for (int j = 0; j < EPL; ++j)
-      if (lane + 64 * j < experts) m = fmaxf(m, lg[j]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    row_max = m;
-    float part = 0.0f;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j)
-      if (lane + 64 * j < experts) part = part + exp_seq(lg[j] - row_max);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off, 64);
-    row_sum = part;
-  }
-
-  uint32_t live = 0;
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    if (e < experts) {
-      float s = score_of<SCORE>(lg[j], row_max, row_sum);
-      if (bias != nullptr) s = s + bias[e];
-      sel[j] = s;
-      live |= 1u << j;
-    } else {
-      sel[j] = 0.0f;
+template <int SCORE, int EPL>
+__global__ __launch_bounds__(kAlignThreads) void prologue_kernel(PrologueArgs a) {
+  if (blockIdx.x == 0) {
+    if (a.route) {
+      for (int64_t t = threadIdx.x >> 6; t < a.tokens; t += kAlignWaves)
+        route_tokens<SCORE, EPL, 1>(a.logits, a.bias, t, 0, a.tokens, a.experts, a.topk, a.route_scale, a.ids,
+                                    a.weights, a.margin, nullptr, nullptr);
+      __syncthreads();  // every id is written (workgroup-scope visibility)
     }
+    align_block(a.ids, a.tokens * a.topk, a.experts, a.expert_bits, a.block_size, a.sorted_ids, a.capacity,
+                a.expert_ids, a.num_blocks, a.ntpp);
+    return;
   }
-
-  const int depth = topk + 1 <= experts ? topk + 1 : experts;
-  int chosen_id[kMaxTopk + 1];
-  float chosen_sel[kMaxTopk + 1];
+  const int chunks = a.hidden / 64;
+  const int64_t n = a.tokens * chunks;
+  for (int64_t idx = (int64_t)(blockIdx.x - 1) * kAlignThreads + threadIdx.x; idx < n;
+       idx += (int64_t)(gridDim.x - 1) * kAlignThreads) {
+    const int64_t r = idx / chunks;
+    const int c = (int)(idx % chunks);
+    const uint16_t* src = a.x + r * a.hidden + c * 64;
+    float sum = 0.0f;
 #pragma unroll
-  for (int r = 0; r < kMaxTopk + 1; ++r) {
-    chosen_id[r] = 0;
-    chosen_sel[r] = 0.0f;
-    if (r >= depth) continue;
-    uint64_t best = 0;
-    int best_j = -1;
+    for (int e = 0; e < 64; e += 8) {
+      const u32x4 v = load16(src + e);
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      if (live & (1u << j)) {
-        const int e = lane + 64 * j;
-        const uint64_t c = ((uint64_t)order_key(sel[j]) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
-        if (best_j < 0 || c > best) {
-          best = c;
-          best_j = j;
-        }
+      for (int q = 0; q < 4; ++q) {
+        sum += __uint_as_float(v[q] << 16);
+        sum += __uint_as_float(v[q] & 0xFFFF0000u);
       }
     }
-    const uint64_t win = wave_max_u64(best);
-    const int e_win = (int)(0xFFFFFFFFu - (uint32_t)(win & 0xFFFFFFFFu));
-    if ((e_win & 63) == lane) live &= ~(1u << (e_win >> 6));
-    chosen_id[r] = e_win;
-    chosen_sel[r] = key_value((uint32_t)(win >> 32));
-  }
-
-  // Unbiased score of selected expert r, recomputed by lane r from its logit.
-  float my_score = 0.0f;
-  int my_id = 0;
-#pragma unroll
-  for (int r = 0; r < kMaxTopk; ++r)
-    if (r < topk && lane == r) my_id = chosen_id[r];
-  if (lane < topk) my_score = score_of<SCORE>(row[my_id], row_max, row_sum);
-
-  float w = my_score;
-  if constexpr (SCORE != DSV4MOE_SCORE_SOFTMAX) {
-    float total = __shfl(my_score, 0, 64);
-    for (int r = 1; r < topk; ++r) total = total + __shfl(my_score, r, 64);
-    w = w / total;
-  }
-  w = w * route_scale;
-  if (lane < topk) {
-    ids[t * topk + lane] = my_id;
-    weights[t * topk + lane] = w;
-  }
-  if (lane == 0 && margin != nullptr) {
-    float kth = 0.0f, next = 0.0f;
-#pragma unroll
-    for (int r = 0; r < kMaxTopk + 1; ++r) {
-      if (r == topk - 1) kth = chosen_sel[r];
-      if (r == topk) next = chosen_sel[r];
-    }
-    margin[t] = depth > topk ? kth - next : 0.0f;
-  }
-  if (sel_ids != nullptr || sel_scores != nullptr) {
-#pragma unroll
-    for (int r = 0; r < kMaxTopk + 1; ++r) {
-      if (r < depth && lane == r) {
-        if (sel_ids) sel_ids[t * depth + r] = chosen_id[r];
-        if (sel_scores) sel_scores[t * depth + r] = chosen_sel[r];
-      }
-    }
+    a.xsum[idx] = sum;
   }
 }
 
@@ -325,5 +440,36 @@ int dsv4_launch_route_hash(const float* logits, const int64_t* tid2eid, int64_t 
                      logits, tid2eid, vocab, input_ids, tokens, experts, topk, route_scale, ids,
                      weights, selected_scores);
   DSV4_CHECK_LAUNCH("route_hash_kernel");
+  return DSV4MOE_OK;
+}
+
+// [Route +] align [+ row sums when x is given] as one launch.
+int dsv4_launch_prologue(int32_t route, const float* logits, const float* bias, int64_t tokens, int32_t experts,
+                         int32_t topk, int32_t score_func, float route_scale, int32_t* ids, float* weights,
+                         float* margin, int32_t block_size, int32_t* sorted_ids, int64_t capacity,
+                         int32_t* expert_ids, int64_t num_blocks, int32_t* ntpp, const uint16_t* x, int32_t hidden,
+                         float* xsum, hipStream_t stream) {
+  if (tokens == 0) return DSV4MOE_OK;
+  PrologueArgs a{logits, bias, tokens, experts, topk, route_scale, ids, weights, margin, 0, block_size,
+                 sorted_ids, capacity, expert_ids, num_blocks, ntpp, x, hidden, xsum, route};
+  while ((1 << a.expert_bits) < experts) ++a.expert_bits;
+  const int64_t sums = x != nullptr ? tokens * (hidden / 64) : 0;
+  const unsigned grid = 1u + (unsigned)std::min<int64_t>((sums + kAlignThreads - 1) / kAlignThreads, 64);
+  const int epl = (experts + 63) / 64;
+#define DSV4_PROLOGUE(S, N) hipLaunchKernelGGL((prologue_kernel<S, N>), dim3(grid), dim3(kAlignThreads), 0, stream, a)
+#define DSV4_PROLOGUE_EPL(S)          \
+  if (epl <= 1) DSV4_PROLOGUE(S, 1);  \
+  else if (epl <= 2) DSV4_PROLOGUE(S, 2); \
+  else if (epl <= 4) DSV4_PROLOGUE(S, 4); \
+  else if (epl <= 8) DSV4_PROLOGUE(S, 8); \
+  else DSV4_PROLOGUE(S, 16);
+  switch (score_func) {
+    case DSV4MOE_SCORE_SIGMOID: DSV4_PROLOGUE_EPL(DSV4MOE_SCORE_SIGMOID) break;
+    case DSV4MOE_SCORE_SOFTMAX: DSV4_PROLOGUE_EPL(DSV4MOE_SCORE_SOFTMAX) break;
+    default: DSV4_PROLOGUE_EPL(DSV4MOE_SCORE_SQRTSOFTPLUS) break;
+  }
+#undef DSV4_PROLOGUE_EPL
+#undef DSV4_PROLOGUE
+  DSV4_CHECK_LAUNCH("prologue_kernel");
   return DSV4MOE_OK;
 }
