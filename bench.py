@@ -236,6 +236,7 @@ def main() -> int:
 
     # -------------------------------------------------------- W4A8 and W8A16
     if args.secondary:
+        secondary["decode_graph"] = bench_graph(layer, S, dev, [1, 8, T], H, E)
         secondary["w4a8"] = bench_w4a8(pkg, resident, gate, cfg, dev, T, args)
         secondary["mxfp4"] = bench_mxfp4(pkg, gate, cfg, dev, T, args)
         secondary["w8a16_linear"] = bench_w8a16(pkg, dev)
@@ -294,6 +295,57 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_graph(layer, S, dev, ts, H, E):
+    """The decode layer call captured once as a HIP graph (torch.cuda.graph,
+    after resetting the slot's completion event, as the reference's stateful
+    graphs do) and replayed: per step the new activations and logits are
+    copied into the captured inputs, then the graph replays.  Eager = the same
+    steps as separate launches."""
+
+    import torch
+
+    out = {}
+    for t in ts:
+        xs = [S.make_hidden(t, H, seed=7000 + t + i, device=dev).view(1, t, H) for i in range(8)]
+        lgs = [S.make_logits(t, E, seed=7500 + t + i, device=dev) for i in range(8)]
+        x_s, lg_s = xs[0].clone(), lgs[0].clone()
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                layer.forward_tensor(x_s, router_logits=lg_s)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        layer.reset_free_slot_completion_event(t, 0)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            layer.forward_tensor(x_s, router_logits=lg_s)
+        torch.cuda.synchronize()
+
+        def replay(i):
+            x_s.copy_(xs[i % 8])
+            lg_s.copy_(lgs[i % 8])
+            graph.replay()
+
+        def eager(i):
+            x_s.copy_(xs[i % 8])
+            lg_s.copy_(lgs[i % 8])
+            layer.forward_tensor(x_s, router_logits=lg_s)
+
+        n = 200
+        for i in range(10):
+            replay(i)
+        ms_g = cuda_timer(replay, n)
+        ms_e = cuda_timer(eager, n)
+        out[str(t)] = {"ms_per_step_graph": round(ms_g, 4), "ms_per_step_eager": round(ms_e, 4),
+                       "tokens_per_s_graph": round(t / (ms_g * 1e-3), 1)}
+        log(f"[bench] decode graph T={t}: {out[str(t)]}")
+        del graph
+        torch.cuda.synchronize()
+        layer.reset_free_slot_completion_event(t, 0)
+    return out
 
 
 def bench_w4a8(pkg, resident, gate, cfg, dev, T, args):

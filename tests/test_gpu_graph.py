@@ -1,0 +1,84 @@
+"""Graph capture of the decode layer call (the reference captures whole decode
+stages, ``stateful_graph.py:398-470``, after resetting each MoE slot's
+completion event, ``moe_runtime.py:1285-1316``).
+
+``TP4MoE.forward_tensor`` is captured with ``torch.cuda.graph`` (a HIP graph)
+and replayed several times with new inputs copied into the captured input
+tensors, with eager work and synchronisations between the replays; every
+replay must equal an eager call on another slot bit for bit.  The path records
+no memset nodes: every launch in it is a kernel, plus the output copy.
+"""
+
+import pytest
+import torch
+
+from gaiban_lite_amd import ResidentGateWeights, ResidentInt4MoEWeights, TP4MoE, TP4MoEConfig, synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def build(shape, rows):
+    w13, s13, w2, s2 = S.make_checkpoint_experts(shape, seed=9, device=DEV)
+    res = ResidentInt4MoEWeights.from_checkpoint_layout(w13, s13, w2, s2, experts=shape.experts, has_shared=True)
+    g = torch.Generator(DEV).manual_seed(21)
+    wg = (torch.randn((shape.experts, shape.hidden), device=DEV, generator=g) * 0.03).to(torch.bfloat16)
+    bias = torch.randn((shape.experts,), device=DEV, generator=g) * 0.05
+    cfg = TP4MoEConfig(hidden_size=shape.hidden, intermediate_size=shape.inter, experts=shape.experts,
+                       topk=shape.topk, route_scale=2.5, clamp_limit=10.0, score_func="sqrtsoftplus",
+                       shared_experts=1)
+    return TP4MoE(config=cfg, resident=res, gate=ResidentGateWeights(weight=wg, bias=bias), device=DEV,
+                  global_row_shapes=rows, slots_per_shape=2)
+
+
+@pytest.mark.parametrize("use_logits", [False, True])
+@pytest.mark.parametrize("shape,rows", [
+    (S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True), 1),
+    (S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True), 64),
+    (S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True), 8),
+    (S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True), 64),
+])
+def test_capture_and_replay_matches_eager(shape, rows, use_logits):
+    print(f"[graph] E={shape.experts} T={rows} logits={use_logits}", flush=True)
+    layer = build(shape, [rows])
+    xs = [S.make_hidden(rows, shape.hidden, seed=40 + i, device=DEV).view(1, rows, shape.hidden) for i in range(5)]
+    lgs = [S.make_logits(rows, shape.experts, seed=60 + i, device=DEV) for i in range(5)]
+    x_s = xs[0].clone()
+    lg_s = lgs[0].clone()
+
+    def call(x, lg, slot):
+        return layer.forward_tensor(x, router_logits=lg if use_logits else None, slot=slot)
+
+    side = torch.cuda.Stream(DEV)
+    side.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            call(x_s, lg_s, 0)
+    torch.cuda.current_stream(DEV).wait_stream(side)
+    torch.cuda.synchronize()
+
+    layer.reset_free_slot_completion_event(rows, 0)
+    assert layer.slot_completion_status(rows, 0) == {"state": "free", "has_completion_event": False}
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_s = call(x_s, lg_s, 0)
+    torch.cuda.synchronize()
+
+    for i in range(1, 5):
+        x_s.copy_(xs[i])
+        lg_s.copy_(lgs[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = call(xs[i], lgs[i], 1)  # eager work between the replays, other slot
+        torch.cuda.synchronize()
+        assert torch.equal(out_s, eager), f"replay {i} differs from the eager call"
+    # the first input again, after the others
+    x_s.copy_(xs[0])
+    lg_s.copy_(lgs[0])
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out_s, call(xs[0], lgs[0], 1))
+    assert layer.slot_completion_status(rows, 0)["state"] == "free"
+    del graph
+    torch.cuda.synchronize()
