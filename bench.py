@@ -240,6 +240,7 @@ def main() -> int:
         secondary["w4a8"] = bench_w4a8(pkg, resident, gate, cfg, dev, T, args)
         secondary["mxfp4"] = bench_mxfp4(pkg, gate, cfg, dev, T, args)
         secondary["w8a16_linear"] = bench_w8a16(pkg, dev)
+        secondary["w8a16_fp8_block_linear"] = bench_w8a16(pkg, dev, fmt="fp8")
 
     # ------------------------------------------------------------ CPU baseline
     cpu = None
@@ -471,8 +472,10 @@ def bench_mxfp4(pkg, gate, cfg, dev, T, args):
     return out
 
 
-def bench_w8a16(pkg, dev):
-    """W8A16 dense linear, K = 4096, N in {4096, 1024, 16384}, M in {1, 64, 8192}."""
+def bench_w8a16(pkg, dev, fmt="int8"):
+    """W8A16 dense linear, K = 4096, N in {4096, 1024, 16384}, M in {1, 64, 8192};
+    fmt "int8" (per-channel bf16 scales) or "fp8" (E4M3 with E8M0 128x128
+    block scales, the reference checkpoint's format)."""
 
     import torch
 
@@ -481,8 +484,16 @@ def bench_w8a16(pkg, dev):
     out = {}
     k = 4096
     for n in (4096, 1024, 16384):
-        q, s = S.make_int8_linear(n, k, device=dev)
-        prep = L.prepare_int8_weight(q, s)
+        if fmt == "fp8":
+            q, s = S.make_fp8_block_linear(n, k, device=dev)
+            prep = L.prepare_fp8_block_weight(q, s)
+            gemm = L.w8a16_fp8_gemm_into
+            scale_bytes = s.numel()
+        else:
+            q, s = S.make_int8_linear(n, k, device=dev)
+            prep = L.prepare_int8_weight(q, s)
+            gemm = L.w8a16_gemm_into
+            scale_bytes = 2 * n
         del q
         for m in (1, 64, 8192):
             a = S.make_hidden(m, k, seed=6000 + m, device=dev)
@@ -490,10 +501,10 @@ def bench_w8a16(pkg, dev):
             o = torch.empty(plan.output_shape, dtype=torch.bfloat16, device=dev)
             ws = L.allocate_workspace(plan, dev)
             for _ in range(3):
-                L.w8a16_gemm_into(a, prep.packed, prep.scale, o, ws, plan=plan)
+                gemm(a, prep.packed, prep.scale, o, ws, plan=plan)
             it = 50 if m < 8192 else 10
-            ms = cuda_timer(lambda i: L.w8a16_gemm_into(a, prep.packed, prep.scale, o, ws, plan=plan), it)
-            byts = n * k + 2 * n + 2 * m * k + 2 * m * n
+            ms = cuda_timer(lambda i: gemm(a, prep.packed, prep.scale, o, ws, plan=plan), it)
+            byts = n * k + scale_bytes + 2 * m * k + 2 * m * n
             fl = 2.0 * m * n * k
             entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2),
                      "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
@@ -501,7 +512,7 @@ def bench_w8a16(pkg, dev):
                                      else round(fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
             entry["bound"] = "hbm" if m <= 64 else "mfma"
             out[f"M{m}_N{n}"] = entry
-            log(f"[bench] w8a16 M={m} N={n}: {entry}")
+            log(f"[bench] w8a16 {fmt} M={m} N={n}: {entry}")
             del a, o, ws
         del prep
     return out

@@ -74,6 +74,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_w8a16_split_k": (_i32, [_i64, _i64, _i64]),
     "dsv4moe_w8a16_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "dsv4moe_w8a16_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),
+    "dsv4moe_w8a16_fp8_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),
 }
 
 _lock = threading.Lock()

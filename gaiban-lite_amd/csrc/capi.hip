@@ -101,7 +101,7 @@ int32_t dsv4_w8a16_split_k(int64_t, int64_t, int64_t);
 size_t dsv4_w8a16_workspace_bytes(int64_t, int64_t, int32_t);
 int dsv4_launch_pack_int8(const int8_t*, int64_t, int64_t, uint8_t*, hipStream_t);
 int dsv4_launch_w8a16(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, const uint16_t*,
-                      int32_t, float*, uint16_t*, hipStream_t);
+                      const uint8_t*, int32_t, float*, uint16_t*, hipStream_t);
 
 using dsv4host::clear_error;
 using dsv4host::set_error;
@@ -469,29 +469,51 @@ size_t dsv4moe_w8a16_workspace_bytes(int64_t m, int64_t n, int32_t split_k) {
   return dsv4_w8a16_workspace_bytes(m, n, split_k);
 }
 
+// Shared checks of the two W8A16 entry points (who = entry name).
+static int validate_w8a16(const char* who, const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
+                          const void* scales, int32_t split_k, float* workspace, size_t workspace_bytes,
+                          uint16_t* out) {
+  DSV4_REQUIRE(m >= 0, "%s: m must be >= 0", who);
+  DSV4_REQUIRE(n > 0 && n % 16 == 0, "%s: n must be a positive multiple of 16, got %lld", who, (long long)n);
+  DSV4_REQUIRE(k > 0 && k % 128 == 0, "%s: k must be a positive multiple of 128, got %lld", who, (long long)k);
+  DSV4_REQUIRE(split_k == 1 || split_k == 2 || split_k == 4 || split_k == 8 || split_k == 16,
+               "%s: split_k must be one of 1, 2, 4, 8, 16, got %d", who, split_k);
+  DSV4_REQUIRE(split_k <= k / 128, "%s: split_k=%d exceeds the K-block count %lld", who, split_k,
+               (long long)(k / 128));
+  DSV4_REQUIRE(m * k * 2 < (int64_t)1 << 31 && n * k < (int64_t)1 << 31,
+               "%s: m*k*2 and n*k must be below 2^31", who);
+  if (m == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(a && wq && scales && out, "%s: null pointer", who);
+  DSV4_REQUIRE(aligned(a, 16) && aligned(wq, 16) && aligned(out, 8),
+               "%s: a and wq must be 16-byte aligned, out 8-byte aligned", who);
+  const size_t need = dsv4_w8a16_workspace_bytes(m, n, split_k);
+  DSV4_REQUIRE(workspace_bytes >= need, "%s: workspace of %zu bytes is below the %zu needed", who,
+               workspace_bytes, need);
+  DSV4_REQUIRE(need == 0 || (workspace && aligned(workspace, 16)),
+               "%s: split_k > 1 needs a 16-byte aligned workspace", who);
+  return DSV4MOE_OK;
+}
+
 int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
                          const uint16_t* ws, int32_t split_k, float* workspace,
                          size_t workspace_bytes, uint16_t* out, void* stream) {
   clear_error();
-  DSV4_REQUIRE(m >= 0, "w8a16_linear: m must be >= 0");
-  DSV4_REQUIRE(n > 0 && n % 16 == 0, "w8a16_linear: n must be a positive multiple of 16, got %lld", (long long)n);
-  DSV4_REQUIRE(k > 0 && k % 128 == 0, "w8a16_linear: k must be a positive multiple of 128, got %lld", (long long)k);
-  DSV4_REQUIRE(split_k == 1 || split_k == 2 || split_k == 4 || split_k == 8 || split_k == 16,
-               "w8a16_linear: split_k must be one of 1, 2, 4, 8, 16, got %d", split_k);
-  DSV4_REQUIRE(split_k <= k / 128, "w8a16_linear: split_k=%d exceeds the K-block count %lld", split_k,
-               (long long)(k / 128));
-  DSV4_REQUIRE(m * k * 2 < (int64_t)1 << 31 && n * k < (int64_t)1 << 31,
-               "w8a16_linear: m*k*2 and n*k must be below 2^31");
-  if (m == 0) return DSV4MOE_OK;
-  DSV4_REQUIRE(a && wq && ws && out, "w8a16_linear: null pointer");
-  DSV4_REQUIRE(aligned(a, 16) && aligned(wq, 16) && aligned(ws, 8) && aligned(out, 8),
-               "w8a16_linear: a and wq must be 16-byte aligned, ws and out 8-byte aligned");
-  const size_t need = dsv4_w8a16_workspace_bytes(m, n, split_k);
-  DSV4_REQUIRE(workspace_bytes >= need, "w8a16_linear: workspace of %zu bytes is below the %zu needed",
-               workspace_bytes, need);
-  DSV4_REQUIRE(need == 0 || (workspace && aligned(workspace, 16)),
-               "w8a16_linear: split_k > 1 needs a 16-byte aligned workspace");
-  return dsv4_launch_w8a16(a, m, n, k, wq, ws, split_k, workspace, out, static_cast<hipStream_t>(stream));
+  int rc = validate_w8a16("w8a16_linear", a, m, n, k, wq, ws, split_k, workspace, workspace_bytes, out);
+  if (rc != DSV4MOE_OK || m == 0) return rc;
+  DSV4_REQUIRE(aligned(ws, 8), "w8a16_linear: ws must be 8-byte aligned");
+  return dsv4_launch_w8a16(a, m, n, k, wq, ws, nullptr, split_k, workspace, out,
+                           static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
+                             const uint8_t* ws8, int32_t split_k, float* workspace, size_t workspace_bytes,
+                             uint16_t* out, void* stream) {
+  clear_error();
+  int rc = validate_w8a16("w8a16_fp8_linear", a, m, n, k, wq, ws8, split_k, workspace, workspace_bytes, out);
+  if (rc != DSV4MOE_OK || m == 0) return rc;
+  DSV4_REQUIRE(k <= 32768, "w8a16_fp8_linear: k must be <= 32768, got %lld", (long long)k);
+  return dsv4_launch_w8a16(a, m, n, k, wq, nullptr, ws8, split_k, workspace, out,
+                           static_cast<hipStream_t>(stream));
 }
 
 size_t dsv4moe_experts_w4a8_workspace_bytes(int64_t tokens, int32_t topk, int32_t hidden, int32_t inter,

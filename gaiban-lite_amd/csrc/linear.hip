@@ -1,12 +1,20 @@
-// W8A16 dense linear for gfx950: C[M,N] = bf16( A[M,K] . (Q[N,K] * s[N])^T ),
-// A bf16, Q int8 symmetric per output channel, s bf16, fp32 accumulation.
+// W8A16 dense linear for gfx950: C[M,N] = bf16( A[M,K] . W[N,K]^T ), A bf16,
+// fp32 accumulation, with W in one of two formats:
+//   * int8 symmetric per output channel, W = Q * s[n] (s bf16);
+//   * FP8 E4M3 with one E8M0 scale per 128 x 128 block, W = Q * 2^(e-127),
+//     the reference checkpoint's format (weight_only_linear.py:488-513,
+//     537-598; moe_forward.py:158-176).
 //
 // Restates the weight-only linear of experiments/C1F-integrated-block/
 // weight_only_linear.py:537-702 (bf16 MMA over a weight reconstructed in
 // registers, fp32 accumulate, optional split-K into an fp32 [split, M, N]
 // workspace reduced in split order, one bf16 rounding) for the int8
 // per-channel format: the scale factors out of the K sum and is applied once
-// in the epilogue.
+// in the epilogue.  The FP8 weights convert with v_cvt_scalef32_pk_bf16_fp8,
+// whose fp32 scale operand carries the E8M0 byte in its exponent field: the
+// product is exact in bf16 (3 mantissa bits times a power of two), so the
+// MFMA sees the reference's bf16(Q * scale) and no epilogue scale is needed.
+// A 16-row strip and a 64-K window lie inside one 128 x 128 scale block.
 //
 // Weight layout (dsv4moe_pack_int8): 1 KiB tiles of 16 rows x 64 K, tile
 // (strip, window) at byte (strip * K/64 + window) * 1024; lane l's 16 bytes are
@@ -33,7 +41,9 @@ struct LinearParams {
   int n;
   int k;
   const uint8_t* wq;
-  const uint16_t* ws;
+  const uint16_t* ws;    // int8 format: bf16 [N]
+  const uint8_t* ws8;    // FP8 format: E8M0 [ceil(N/128)][K/128]
+  int kblocks;           // K / 128
   int split;
   int win_per_split;
   int tiles_n;
@@ -62,12 +72,24 @@ __device__ __forceinline__ bf16x8 dequant_i8x8(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(bf16x8, p);
 }
 
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+// 8 FP8 E4M3 weights (two dwords, K order, low byte first) -> 8 bf16 times
+// the power of two whose exponent field `scale` carries.
+__device__ __forceinline__ bf16x8 dequant_fp8x8(uint32_t lo, uint32_t hi, float scale) {
+  const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, scale, false);
+  const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, scale, true);
+  const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, scale, false);
+  const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, scale, true);
+  return bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
 // Workgroup tile: 64*R output channels (wavefront w owns strips 4R*tn + R*w + r)
 // x 16*C tokens, over one K split.  Per window, buffer_load ... lds copies the
 // token tile (16C rows x 128 B, 16-byte part q of row t stored at
 // q ^ swz128(t))
 // and each wavefront's R weight tiles into LDS, double buffered.
-template <int R, int C>
+template <int R, int C, bool FP8>
 __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * C * 128];
   __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * 1024];
@@ -114,6 +136,16 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
 #pragma unroll
   for (int r = 0; r < R; ++r)
     w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+  // FP8: the wavefront's R strips lie in one 128-row scale block (R divides
+  // 8); lane i holds the E8M0 bytes of K blocks i, 64 + i, 128 + i, 192 + i,
+  // loaded before any copy is in flight (K <= 32768, checked on the host)
+  uint32_t srow[4] = {0, 0, 0, 0};
+  if constexpr (FP8) {
+    const uint8_t* row = p.ws8 + (int64_t)(min(strip0, strips - 1) >> 3) * p.kblocks;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (64 * q + lane < p.kblocks) srow[q] = row[64 * q + lane];
+  }
 
   auto issue = [&](int win, int buf) {
 #pragma unroll
@@ -140,11 +172,22 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
       raw[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * 1024 + lane * 16]);
+    float bscale = 0.0f;  // FP8: E8M0 byte of (this wavefront's row block, K block) as an fp32 exponent field
+    if constexpr (FP8) {
+      const int kb = win >> 1;
+      const uint32_t word = kb < 64 ? srow[0] : (kb < 128 ? srow[1] : (kb < 192 ? srow[2] : srow[3]));
+      bscale = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)word, kb & 63) << 23);
+    }
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
       bf16x8 a[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) a[r] = dequant_i8x8(raw[r][2 * d], raw[r][2 * d + 1]);
+      for (int r = 0; r < R; ++r) {
+        if constexpr (FP8)
+          a[r] = dequant_fp8x8(raw[r][2 * d], raw[r][2 * d + 1], bscale);
+        else
+          a[r] = dequant_i8x8(raw[r][2 * d], raw[r][2 * d + 1]);
+      }
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const int row = c * 16 + n16;
@@ -184,12 +227,14 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
     const int strip = strip0 + r;
     if (strip >= strips) continue;
     const int n = strip * 16 + 4 * j;
-    const u32x2 sv = *reinterpret_cast<const u32x2*>(p.ws + n);
-    float sc[4];
-    sc[0] = __uint_as_float(sv[0] << 16);
-    sc[1] = __uint_as_float(sv[0] & 0xFFFF0000u);
-    sc[2] = __uint_as_float(sv[1] << 16);
-    sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
+    float sc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if constexpr (!FP8) {
+      const u32x2 sv = *reinterpret_cast<const u32x2*>(p.ws + n);
+      sc[0] = __uint_as_float(sv[0] << 16);
+      sc[1] = __uint_as_float(sv[0] & 0xFFFF0000u);
+      sc[2] = __uint_as_float(sv[1] << 16);
+      sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
+    }
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const int64_t tok = (int64_t)tm * 16 * C + c * 16 + n16;
@@ -238,13 +283,14 @@ __global__ __launch_bounds__(256) void pack_int8_kernel(const uint8_t* src, int6
   *reinterpret_cast<u32x4*>(dst + c * 16) = *reinterpret_cast<const u32x4*>(src + row * k + col);
 }
 
+template <bool FP8>
 static void launch_w8a16_kernel(const LinearParams& p, int r, int c, hipStream_t stream) {
   const int items = p.split * p.tiles_m * p.tiles_n;
   const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
-  if (r == 4) hipLaunchKernelGGL((w8a16_kernel<4, 8>), grid, dim3(256), 0, stream, p);
-  else if (c == 1) hipLaunchKernelGGL((w8a16_kernel<2, 1>), grid, dim3(256), 0, stream, p);
-  else if (c == 2) hipLaunchKernelGGL((w8a16_kernel<2, 2>), grid, dim3(256), 0, stream, p);
-  else hipLaunchKernelGGL((w8a16_kernel<2, 4>), grid, dim3(256), 0, stream, p);
+  if (r == 4) hipLaunchKernelGGL((w8a16_kernel<4, 8, FP8>), grid, dim3(256), 0, stream, p);
+  else if (c == 1) hipLaunchKernelGGL((w8a16_kernel<2, 1, FP8>), grid, dim3(256), 0, stream, p);
+  else if (c == 2) hipLaunchKernelGGL((w8a16_kernel<2, 2, FP8>), grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL((w8a16_kernel<2, 4, FP8>), grid, dim3(256), 0, stream, p);
 }
 
 }  // namespace dsv4
@@ -284,8 +330,9 @@ int dsv4_launch_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed
   return DSV4MOE_OK;
 }
 
+// ws (int8 format, bf16 [N]) or ws8 (FP8 format, E8M0 [ceil(N/128)][K/128]): exactly one is set.
 int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
-                      const uint16_t* ws, int32_t split, float* workspace, uint16_t* out,
+                      const uint16_t* ws, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
                       hipStream_t stream) {
   int r, c;
   w8a16_geometry(m, &r, &c);
@@ -296,6 +343,8 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
   p.k = (int)k;
   p.wq = wq;
   p.ws = ws;
+  p.ws8 = ws8;
+  p.kblocks = (int)(k / 128);
   p.split = split;
   const int wins = (int)(k / kWin);
   p.win_per_split = (wins + split - 1) / split;
@@ -303,7 +352,10 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
   p.tiles_m = (int)((m + 16 * c - 1) / (16 * c));
   p.out = out;
   p.partial = workspace;
-  launch_w8a16_kernel(p, r, c, stream);
+  if (ws8 != nullptr)
+    launch_w8a16_kernel<true>(p, r, c, stream);
+  else
+    launch_w8a16_kernel<false>(p, r, c, stream);
   DSV4_CHECK_LAUNCH("w8a16_kernel");
   if (split > 1) {
     const int64_t quads = m * n / 4;

@@ -357,6 +357,18 @@ def pack_int8(weight: torch.Tensor) -> torch.Tensor:
     return packed
 
 
+def pack_fp8(weight: torch.Tensor) -> torch.Tensor:
+    """Row-major FP8 E4M3 codes [n, k] (uint8 or float8_e4m3fn) -> the same
+    tiled uint8 [n*k] layout as ``pack_int8`` (a byte permutation)."""
+
+    if weight.ndim != 2:
+        raise ValueError("weight must be [n, k]")
+    if weight.dtype == torch.float8_e4m3fn:
+        weight = weight.view(torch.uint8)
+    _check("weight", weight, dtype=torch.uint8, device=weight.device)
+    return pack_int8(weight.view(torch.int8))
+
+
 def w8a16_split_k(m: int, n: int, k: int) -> int:
     split = int(_lib.load().dsv4moe_w8a16_split_k(m, n, k))
     if split < 1:
@@ -383,4 +395,25 @@ def w8a16_linear_into(a: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, out: 
         _check("workspace", workspace, dtype=torch.float32, device=dev)
         ws_bytes = workspace.numel() * 4
     call("dsv4moe_w8a16_linear", ptr(a), m, n, k, ptr(wq), ptr(ws), int(split_k), ptr(workspace),
+         ws_bytes, ptr(out), _lib.current_stream(dev))
+
+
+def w8a16_fp8_linear_into(a: torch.Tensor, wq: torch.Tensor, ws8: torch.Tensor, out: torch.Tensor,
+                          workspace: torch.Tensor | None, *, n: int, split_k: int) -> None:
+    """FP8 E4M3 weights (packed by ``pack_fp8``) with E8M0 128 x 128 block
+    scales ``ws8`` uint8 [ceil(n/128), k/128] (``dsv4moe_w8a16_fp8_linear``)."""
+
+    if a.ndim != 2:
+        raise ValueError("activation must be [m, k]")
+    m, k = a.shape
+    dev = a.device
+    _check("activation", a, dtype=torch.bfloat16, device=dev)
+    _check("weight", wq, dtype=torch.uint8, shape=(n * k,), device=dev)
+    _check("weight_scale", ws8, dtype=torch.uint8, shape=((n + 127) // 128, k // 128), device=dev)
+    _check("out", out, dtype=torch.bfloat16, shape=(m, n), device=dev)
+    ws_bytes = 0
+    if workspace is not None:
+        _check("workspace", workspace, dtype=torch.float32, device=dev)
+        ws_bytes = workspace.numel() * 4
+    call("dsv4moe_w8a16_fp8_linear", ptr(a), m, n, k, ptr(wq), ptr(ws8), int(split_k), ptr(workspace),
          ws_bytes, ptr(out), _lib.current_stream(dev))

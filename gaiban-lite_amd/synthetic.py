@@ -125,6 +125,25 @@ def make_int8_linear(n: int, k: int, *, seed: int = 3, device="cuda"):
     return q, s
 
 
+def make_fp8_block_linear(n: int, k: int, *, seed: int = 3, device="cuda", std: float = 0.02):
+    """Checkpoint-style FP8 block weights: W ~ N(0, std^2) [n, k] quantised per
+    128 x 128 block to E4M3 with the power-of-two E8M0 scale 2^ceil(log2(amax/448))
+    (the block's largest magnitude maps into E4M3's range).  Returns
+    (codes uint8 [n, k], scale codes uint8 [ceil(n/128), k/128])."""
+
+    g = _gen(seed * 1_000_003 + 91, device)
+    w = torch.randn((n, k), device=device, generator=g) * std
+    nb, kb = (n + 127) // 128, k // 128
+    pad = torch.zeros((nb * 128, k), device=device)
+    pad[:n] = w
+    amax = pad.abs().view(nb, 128, kb, 128).amax(dim=(1, 3)).clamp_min(1e-30)
+    e = torch.ceil(torch.log2(amax / 448.0)).clamp(-127, 127)
+    scale = torch.exp2(e)
+    q = (pad.view(nb, 128, kb, 128) / scale[:, None, :, None]).view(nb * 128, k)[:n]
+    codes = q.to(torch.float8_e4m3fn).view(torch.uint8)
+    return codes.contiguous(), (e + 127).to(torch.uint8).contiguous()
+
+
 __all__ = [
     "FLASH",
     "TINY",
@@ -132,6 +151,7 @@ __all__ = [
     "make_checkpoint_experts",
     "make_checkpoint_experts_mxfp4",
     "make_hidden",
+    "make_fp8_block_linear",
     "make_int8_linear",
     "make_logits",
     "zipf_ids",

@@ -9,10 +9,14 @@ geometry with its caller-owned fp32 split-K workspace ``[split_k, M, N]``
 ``w8a16_gemm_into(activation, weight, weight_scale, out, workspace, *, plan)``
 (``:794-823``) that allocates nothing and never synchronises.
 
-Changed for this build: the weight format is int8 symmetric per output
-channel with a bf16 scale per row (instead of E4M3 with E8M0 128x128 block
-scales), repacked once by ``prepare_int8_weight`` into the tiled layout of
-``dsv4moe_pack_int8``; the automatic split-K policy is the HIP library's
+Two weight formats, each repacked once into the tiled layout of
+``dsv4moe_pack_int8``:
+  * int8 symmetric per output channel with a bf16 scale per row
+    (``prepare_int8_weight``, ``w8a16_gemm_into``; the BASELINE format);
+  * the reference checkpoint's FP8 E4M3 weights with one E8M0 scale per
+    128 x 128 block (``prepare_fp8_block_weight``, ``w8a16_fp8_gemm_into``;
+    E8M0 decode and the reserved-byte preflight of ``:488-513``).
+The automatic split-K policy is the HIP library's
 (``dsv4moe_w8a16_split_k``, sized for its 128/256-row workgroup tiles and
 256 CUs) rather than ``_automatic_split_k`` (``:168-179``), which is tuned for
 32x64 Triton tiles; split_k may also be 16.  The kernels are in
@@ -144,6 +148,50 @@ def prepare_int8_weight(weight: torch.Tensor, scale: torch.Tensor) -> PreparedIn
     return PreparedInt8Weight(packed=packed, scale=scale.contiguous(), n=n, k=k)
 
 
+@dataclass(frozen=True)
+class PreparedFP8BlockWeight:
+    """Tiled FP8 E4M3 weight (uint8 [N*K]) and its E8M0 block scales
+    (uint8 [ceil(N/128), K/128])."""
+
+    packed: torch.Tensor
+    scale: torch.Tensor
+    n: int
+    k: int
+
+
+def validate_e8m0_scale_values(name: str, scale: torch.Tensor) -> None:
+    """Cold preflight rejecting the reserved E8M0 byte 255 (``:488-500``);
+    synchronises, so it belongs to load time."""
+
+    codes = scale.view(torch.uint8) if scale.dtype == torch.float8_e8m0fnu else scale
+    if codes.dtype != torch.uint8:
+        raise TypeError(f"{name} must be uint8 or float8_e8m0fnu, got {scale.dtype}")
+    if bool((codes == 255).any().item()):
+        raise ValueError(f"{name} contains reserved E8M0 byte 255")
+
+
+def prepare_fp8_block_weight(weight: torch.Tensor, scale: torch.Tensor) -> PreparedFP8BlockWeight:
+    """Load-time repack of a row-major FP8 E4M3 [N, K] weight (float8_e4m3fn
+    or its uint8 codes) with E8M0 scales [ceil(N/128), K/128] (float8_e8m0fnu
+    or uint8 codes), the checkpoint's block-scaled format."""
+
+    if not isinstance(weight, torch.Tensor) or not isinstance(scale, torch.Tensor):
+        raise TypeError("weight and scale must be tensors")
+    if weight.dtype not in (torch.float8_e4m3fn, torch.uint8) or weight.ndim != 2:
+        raise TypeError("weight must be float8_e4m3fn (or its uint8 codes) [N, K]")
+    n, k = weight.shape
+    if k % BLOCK_K:
+        raise ValueError(f"K={k} must be a multiple of {BLOCK_K}")
+    if scale.dtype not in (torch.float8_e8m0fnu, torch.uint8) or tuple(scale.shape) != ((n + 127) // 128, k // 128):
+        raise TypeError(f"scale must be float8_e8m0fnu (or uint8 codes) [{(n + 127) // 128}, {k // 128}]")
+    if weight.device != scale.device:
+        raise ValueError("weight and scale must share a device")
+    validate_e8m0_scale_values("scale", scale)
+    codes = scale.view(torch.uint8) if scale.dtype == torch.float8_e8m0fnu else scale
+    packed = ops.pack_fp8(weight.contiguous())
+    return PreparedFP8BlockWeight(packed=packed, scale=codes.contiguous(), n=n, k=k)
+
+
 def _check_tensor(name, tensor, *, shape, dtype, device) -> None:
     if not isinstance(tensor, torch.Tensor):
         raise TypeError(f"{name} must be a tensor")
@@ -214,15 +262,41 @@ def w8a16_gemm_into(activation: torch.Tensor, weight: torch.Tensor, weight_scale
                           workspace if plan.split_k > 1 else None, n=plan.n, split_k=plan.split_k)
 
 
-def w8a16_linear(activation: torch.Tensor, prepared: PreparedInt8Weight, *, split_k: int | None = None
-                 ) -> torch.Tensor:
-    """Allocating convenience wrapper (cold paths and tests)."""
+def w8a16_fp8_gemm_into(activation: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                        out: torch.Tensor, workspace: torch.Tensor, *, plan: GemmPlan) -> None:
+    """out = bf16(activation . bf16(q * 2^(e-127))^T) for FP8 E4M3 weights with
+    E8M0 128 x 128 block scales (``prepare_fp8_block_weight``) into
+    caller-owned storage; no allocation, no synchronisation."""
+
+    if not isinstance(plan, GemmPlan):
+        raise TypeError("plan must be GemmPlan")
+    if not isinstance(activation, torch.Tensor):
+        raise TypeError("activation must be a tensor")
+    device = activation.device
+    _check_tensor("activation", activation, shape=plan.activation_shape, dtype=ACTIVATION_DTYPE, device=device)
+    _check_tensor("weight", weight, shape=plan.weight_shape, dtype=torch.uint8, device=device)
+    _check_tensor("weight_scale", weight_scale, shape=((plan.n + 127) // 128, plan.k // BLOCK_K),
+                  dtype=torch.uint8, device=device)
+    _check_tensor("out", out, shape=plan.output_shape, dtype=OUTPUT_DTYPE, device=device)
+    _check_tensor("workspace", workspace, shape=plan.workspace_shape, dtype=WORKSPACE_DTYPE, device=device)
+    if device.type != "cuda":
+        raise ValueError(f"linear tensors must be device tensors, got {device}")
+    ops.w8a16_fp8_linear_into(activation, weight, weight_scale, out,
+                              workspace if plan.split_k > 1 else None, n=plan.n, split_k=plan.split_k)
+
+
+def w8a16_linear(activation: torch.Tensor, prepared, *, split_k: int | None = None) -> torch.Tensor:
+    """Allocating convenience wrapper (cold paths and tests) for either
+    prepared format."""
 
     m = activation.shape[0]
     plan = make_gemm_plan(m, prepared.n, prepared.k, split_k=split_k)
     out = torch.empty(plan.output_shape, dtype=OUTPUT_DTYPE, device=activation.device)
     ws = allocate_workspace(plan, activation.device)
-    w8a16_gemm_into(activation, prepared.packed, prepared.scale, out, ws, plan=plan)
+    if isinstance(prepared, PreparedFP8BlockWeight):
+        w8a16_fp8_gemm_into(activation, prepared.packed, prepared.scale, out, ws, plan=plan)
+    else:
+        w8a16_gemm_into(activation, prepared.packed, prepared.scale, out, ws, plan=plan)
     return out
 
 
@@ -232,14 +306,18 @@ __all__ = [
     "GemmPlan",
     "LAYOUT_CONTRACT",
     "OUTPUT_DTYPE",
+    "PreparedFP8BlockWeight",
     "PreparedInt8Weight",
     "SUPPORTED_SPLIT_K",
     "WORKSPACE_DTYPE",
     "allocate_workspace",
     "make_gemm_plan",
+    "prepare_fp8_block_weight",
     "prepare_int8_weight",
+    "validate_e8m0_scale_values",
     "validate_non_alias_tensors",
     "validate_w8a16_tensors",
+    "w8a16_fp8_gemm_into",
     "w8a16_gemm_into",
     "w8a16_linear",
 ]

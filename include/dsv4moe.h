@@ -265,6 +265,26 @@ int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, con
                          size_t workspace_bytes, uint16_t* out, void* stream);
 
 /*
+ * W8A16 dense linear over the reference checkpoint's weight format: FP8 E4M3
+ * codes with one E8M0 scale per 128 x 128 block,
+ *   out[M,N] = bf16( a[M,K] . bf16(q[N,K] * 2^(e[n/128][k/128] - 127))^T ),
+ * fp32 accumulation.  Replaces w8a16_gemm_into with its checkpoint FP8
+ * weights (experiments/C1F-integrated-block/weight_only_linear.py:537-598,
+ * E8M0 decode :488-513: byte 0 is 2^-127, 255 reserved) and
+ * dequant_fp8_block (runtime/dsv4_direct/moe_forward.py:158-176).
+ *   wq      the E4M3 bytes [n, k] packed by dsv4moe_pack_int8 (a byte
+ *           permutation; it packs any 1-byte format)
+ *   ws8     E8M0 bytes [ceil(n/128), k/128], row-major; 255 must not occur
+ *           (the reference rejects it in a cold preflight; the Python wrapper
+ *           does the same at load time)
+ *   split_k, workspace, out: as dsv4moe_w8a16_linear (same split policy).
+ * m >= 0, n % 16 == 0, k % 128 == 0, k <= 32768, m*k*2 and n*k below 2^31.
+ */
+int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
+                             const uint8_t* ws8, int32_t split_k, float* workspace, size_t workspace_bytes,
+                             uint16_t* out, void* stream);
+
+/*
  * W4A8 variant of dsv4moe_experts_w4a16 on the gfx950 fp8 MFMA
  * (v_mfma_scale_f32_16x16x128_f8f6f4, unit block scales).  Replaces the vLLM
  * _fused_marlin_moe call with input_dtype = float8_e4m3fn

@@ -72,6 +72,7 @@ __all__ = [
     "dequant_mxfp4",
     "error_metrics",
     "exp_f32",
+    "dequant_fp8_block",
     "fp8_e4m3_decode",
     "fp8_e4m3_encode",
     "fp8_e4m3_round",
@@ -93,6 +94,7 @@ __all__ = [
     "softmax_f32",
     "sqrtsoftplus_f32",
     "unpack_int4_rows",
+    "w8a16_fp8_linear_f32",
     "w8a16_linear_f32",
 ]
 
@@ -793,6 +795,30 @@ def automatic_split_k(m: int, n: int, k: int, block_m: int = 32, block_n: int = 
     if tiles < 96 and k_blocks >= 16:
         return 2
     return 1
+
+
+def dequant_fp8_block(codes, scale_codes, block: int = 128) -> np.ndarray:
+    """``dequant_fp8_block`` (``moe_forward.py:158-176``): FP8 E4M3 codes
+    [N, K] times the E8M0 scale of their ``block`` x ``block`` block
+    (scale_codes [ceil(N/block), ceil(K/block)]), in float32."""
+
+    c = np.asarray(codes, dtype=np.uint8)
+    n, k = c.shape
+    s = decode_e8m0(scale_codes)
+    if s.shape != (-(-n // block), -(-k // block)):
+        raise ValueError(f"FP8 block scale shape {s.shape} does not match weight {c.shape}")
+    expanded = np.repeat(np.repeat(s, block, axis=0), block, axis=1)[:n, :k]
+    with np.errstate(over="ignore"):  # large scales overflow to inf, as in the reference's fp32 product
+        return (fp8_e4m3_decode(c) * expanded).astype(F32)
+
+
+def w8a16_fp8_linear_f32(a, codes, scale_codes) -> np.ndarray:
+    """C = A . bf16(dequant_fp8_block(Q, s))^T in fp32: the FP8 checkpoint path
+    of ``weight_only_linear.py:560-598``, which rounds the scaled weight to
+    bf16 before the bf16 MMA (fp32 accumulation)."""
+
+    w = bf16_round(dequant_fp8_block(codes, scale_codes))
+    return (np.asarray(a, dtype=F32) @ w.T).astype(F32)
 
 
 def w8a16_linear_f32(a, q_int8, scale_bits) -> np.ndarray:

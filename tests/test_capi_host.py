@@ -152,3 +152,22 @@ def test_synthetic_generators_are_seeded():
     ids = S.zipf_ids(8192, 256, 6, device="cpu")
     counts = np.bincount(ids.numpy().reshape(-1), minlength=256)
     assert counts.max() / counts.mean() > 10  # heavy skew (hottest expert >> mean)
+
+
+def test_w8a16_fp8_validation_and_e8m0_preflight():
+    from gaiban_lite_amd import weight_only_linear as L
+
+    fake = ctypes.c_void_p(0x1000)
+    args = lambda m, n, k, split, ws_bytes: (fake, m, n, k, fake, fake, split, fake, ws_bytes, fake, None)
+    assert "multiple of 16" in _einval("dsv4moe_w8a16_fp8_linear", *args(4, 40, 4096, 1, 0))
+    assert "multiple of 128" in _einval("dsv4moe_w8a16_fp8_linear", *args(4, 64, 4000, 1, 0))
+    assert "k must be <= 32768" in _einval("dsv4moe_w8a16_fp8_linear", *args(4, 64, 32896, 1, 0))
+    assert "null" in _einval("dsv4moe_w8a16_fp8_linear", fake, 4, 64, 4096, None, fake, 1, None, 0, fake, None)
+    assert _lib.load().dsv4moe_w8a16_fp8_linear(fake, 0, 64, 4096, fake, fake, 1, None, 0, fake, None) == _lib.DSV4MOE_OK
+    # the reference's cold preflight: the reserved E8M0 byte 255 is rejected at load time
+    codes = torch.zeros((128, 256), dtype=torch.uint8)
+    bad = torch.tensor([[127, 255]], dtype=torch.uint8)
+    with pytest.raises(ValueError, match="255"):
+        L.prepare_fp8_block_weight(codes, bad)
+    with pytest.raises(TypeError, match="scale"):
+        L.prepare_fp8_block_weight(codes, torch.zeros((1, 1), dtype=torch.uint8))

@@ -203,3 +203,47 @@ def test_mxfp4_source_is_dequant_then_matmul():
             code = (w13[ex, n, k // 2] >> (4 * (k % 2))) & 0xF
             assert w[n, k] == table[code] * np.float32(2.0 ** (int(s13[ex, n, k // 32]) - 127))
         assert src.w2(ex).shape == (h, i)
+
+
+def test_fp8_block_dequant_matches_torch_fp8_dtypes():
+    """dequant_fp8_block (moe_forward.py:158-176) = torch's float8_e4m3fn decode
+    times torch's float8_e8m0fnu decode of the block's scale, including a
+    ragged last row block, scale byte 0 (2^-127) and every finite E4M3 code."""
+
+    import torch
+
+    rng = np.random.default_rng(11)
+    n, k = 300, 384  # 3 row blocks (the last holds 44 rows), 3 K blocks
+    codes = rng.integers(0, 256, size=(n, k), dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C  # no NaN codes
+    codes[0, :254] = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], dtype=np.uint8)
+    scales = rng.integers(100, 140, size=(3, 3), dtype=np.uint8)
+    scales[1, 2] = 0
+    scales[2, 0] = 254
+    got = O.dequant_fp8_block(codes, scales)
+    w = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float()
+    s = torch.from_numpy(scales.copy()).view(torch.float8_e8m0fnu).float()
+    ref = (w * s.repeat_interleave(128, 0).repeat_interleave(128, 1)[:n, :k]).numpy()
+    np.testing.assert_array_equal(got, ref)
+    with pytest.raises(ValueError):
+        O.dequant_fp8_block(codes, scales[:2])
+
+
+def test_w8a16_fp8_linear_oracle_against_scalar_loop():
+    """A . bf16(Q * 2^(e-127))^T (weight_only_linear.py:583-590) on a tiny shape."""
+
+    rng = np.random.default_rng(12)
+    a = O.bf16_round(rng.standard_normal((3, 256)).astype(np.float32))
+    codes = rng.integers(0, 0x7E, size=(5, 256), dtype=np.uint8)  # positive finite E4M3
+    codes[::2] |= 0x80                                           # and some negative
+    scales = np.array([[120, 131]], dtype=np.uint8)
+    got = O.w8a16_fp8_linear_f32(a, codes, scales)
+    dec = O.fp8_e4m3_decode(codes)
+    ref = np.zeros((3, 5))
+    for m in range(3):
+        for n_ in range(5):
+            for c in range(256):
+                wv = float(O.bf16_round(np.array([dec[n_, c] * 2.0 ** (int(scales[0, c // 128]) - 127)],
+                                                 dtype=np.float32))[0])
+                ref[m, n_] += float(a[m, c]) * wv
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
