@@ -239,6 +239,7 @@ def main() -> int:
         secondary["decode_graph"] = bench_graph(layer, S, dev, [1, 8, T], H, E)
         secondary["w4a8"] = bench_w4a8(pkg, resident, gate, cfg, dev, T, args)
         secondary["mxfp4"] = bench_mxfp4(pkg, gate, cfg, dev, T, args)
+        secondary["fp8_shared"] = bench_shared_fp8(pkg, gate, cfg, dev, T, args)
         secondary["w8a16_linear"] = bench_w8a16(pkg, dev)
         secondary["w8a16_fp8_block_linear"] = bench_w8a16(pkg, dev, fmt="fp8")
 
@@ -469,6 +470,42 @@ def bench_mxfp4(pkg, gate, cfg, dev, T, args):
         log(f"[bench] mxfp4 prefill T={tp}: {out[f'prefill_T{tp}']}")
     del layer, res
     torch.cuda.empty_cache()
+    return out
+
+
+def bench_shared_fp8(pkg, gate, cfg, dev, T, args):
+    """The FLASH layer with int4-g128 routed experts and the shared expert in
+    the checkpoint's FP8 block format (dense W8A16 linears adding into the
+    routed sum) at the decode T and the prefill size."""
+
+    import dataclasses
+
+    import torch
+
+    S, ops = pkg.synthetic, pkg.ops
+    E, H, I = cfg.experts, cfg.hidden_size, cfg.intermediate_size
+    routed_shape = dataclasses.replace(S.FLASH, has_shared=False)
+    w = S.make_checkpoint_experts(routed_shape, seed=args.seed, device=dev)
+    sw = [S.make_fp8_block_linear(n, k, seed=args.seed + j, device=dev)
+          for j, (n, k) in enumerate(((I, H), (I, H), (H, I)))]
+    shared = pkg.ResidentFP8SharedExpert.from_checkpoint(sw[0][0], sw[0][1], sw[1][0], sw[1][1], sw[2][0], sw[2][1])
+    res = pkg.ResidentInt4MoEWeights.from_checkpoint_layout(*w, experts=E, has_shared=False, shared_fp8=shared)
+    del w, sw
+    ts = [T] + ([args.prefill_tokens] if args.prefill_tokens else [])
+    layer = pkg.TP4MoE(config=cfg, resident=res, gate=gate, device=dev, global_row_shapes=ts)
+    out = {"shared_fp8_bytes": shared.resident_bytes}
+    for t in ts:
+        x = S.make_hidden(t, H, seed=8000 + t, device=dev).view(1, t, H)
+        lg = S.make_logits(t, E, seed=8500 + t, device=dev)
+        for _ in range(3):
+            layer.forward_tensor(x, router_logits=lg)
+        n = 100 if t == T else args.prefill_steps
+        ms = cuda_timer(lambda i: layer.forward_tensor(x, router_logits=lg), n)
+        out[f"T{t}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1)}
+        log(f"[bench] fp8 shared expert T={t}: {out[f'T{t}']}")
+        del x, lg
+    del layer, res, shared
+    torch.cuda.synchronize()
     return out
 
 

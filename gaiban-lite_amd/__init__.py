@@ -43,6 +43,7 @@ from .moe_runtime import (  # noqa: F401
     TP4MoEConfig,
 )
 from .weights import (  # noqa: F401
+    ResidentFP8SharedExpert,
     ResidentInt4MoEWeights,
     ResidentMXFP4MoEWeights,
     int4_g128_expert_bytes,

@@ -75,6 +75,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_w8a16_workspace_bytes": (_sz, [_i64, _i64, _i32]),
     "dsv4moe_w8a16_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),
     "dsv4moe_w8a16_fp8_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),
+    "dsv4moe_shared_fp8_workspace_bytes": (_sz, [_i64, _i32, _i32]),
+    "dsv4moe_shared_fp8_add": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _p, ctypes.c_float, _p, _p, _sz,
+                                              _p]),
 }
 
 _lock = threading.Lock()

@@ -101,7 +101,10 @@ int32_t dsv4_w8a16_split_k(int64_t, int64_t, int64_t);
 size_t dsv4_w8a16_workspace_bytes(int64_t, int64_t, int32_t);
 int dsv4_launch_pack_int8(const int8_t*, int64_t, int64_t, uint8_t*, hipStream_t);
 int dsv4_launch_w8a16(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, const uint16_t*,
-                      const uint8_t*, int32_t, float*, uint16_t*, hipStream_t);
+                      const uint8_t*, int32_t, float*, uint16_t*, hipStream_t, int accumulate);
+size_t dsv4_shared_fp8_workspace_bytes(int64_t, int, int);
+int dsv4_launch_shared_fp8_add(const uint16_t*, int64_t, int, int, const uint8_t*, const uint8_t*, const uint8_t*,
+                               const uint8_t*, float, uint16_t*, void*, hipStream_t);
 
 using dsv4host::clear_error;
 using dsv4host::set_error;
@@ -502,7 +505,7 @@ int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, con
   if (rc != DSV4MOE_OK || m == 0) return rc;
   DSV4_REQUIRE(aligned(ws, 8), "w8a16_linear: ws must be 8-byte aligned");
   return dsv4_launch_w8a16(a, m, n, k, wq, ws, nullptr, split_k, workspace, out,
-                           static_cast<hipStream_t>(stream));
+                           static_cast<hipStream_t>(stream), 0);
 }
 
 int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
@@ -513,7 +516,36 @@ int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k,
   if (rc != DSV4MOE_OK || m == 0) return rc;
   DSV4_REQUIRE(k <= 32768, "w8a16_fp8_linear: k must be <= 32768, got %lld", (long long)k);
   return dsv4_launch_w8a16(a, m, n, k, wq, nullptr, ws8, split_k, workspace, out,
-                           static_cast<hipStream_t>(stream));
+                           static_cast<hipStream_t>(stream), 0);
+}
+
+size_t dsv4moe_shared_fp8_workspace_bytes(int64_t tokens, int32_t hidden, int32_t inter) {
+  if (tokens < 0 || hidden <= 0 || inter <= 0 || hidden % 128 || inter % 128) return 0;
+  return dsv4_shared_fp8_workspace_bytes(tokens, hidden, inter);
+}
+
+int dsv4moe_shared_fp8_add(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter, const uint8_t* w13q,
+                           const uint8_t* w13s8, const uint8_t* w2q, const uint8_t* w2s8, float clamp_limit,
+                           uint16_t* out, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(tokens >= 0, "shared_fp8_add: tokens must be >= 0");
+  DSV4_REQUIRE(hidden > 0 && hidden % 128 == 0 && hidden <= 32768 && inter > 0 && inter % 128 == 0 &&
+                   inter <= 32768,
+               "shared_fp8_add: hidden and inter must be multiples of 128 in [128, 32768], got %d, %d", hidden,
+               inter);
+  DSV4_REQUIRE(!(clamp_limit < 0.0f) && clamp_limit < 3.0e38f, "shared_fp8_add: clamp_limit must be >= 0 and finite");
+  DSV4_REQUIRE(tokens * (int64_t)hidden * 2 < (int64_t)1 << 31 && tokens * (int64_t)inter * 4 < (int64_t)1 << 31 &&
+                   (int64_t)hidden * inter * 2 < (int64_t)1 << 31,
+               "shared_fp8_add: sizes must keep every operand below 2^31 bytes");
+  if (tokens == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(x && w13q && w13s8 && w2q && w2s8 && out && workspace, "shared_fp8_add: null pointer");
+  DSV4_REQUIRE(aligned(x, 16) && aligned(w13q, 16) && aligned(w2q, 16) && aligned(out, 8) && aligned(workspace, 256),
+               "shared_fp8_add: x, w13q, w2q 16-byte aligned, out 8-byte, workspace 256-byte aligned");
+  const size_t need = dsv4_shared_fp8_workspace_bytes(tokens, hidden, inter);
+  DSV4_REQUIRE(workspace_bytes >= need, "shared_fp8_add: workspace of %zu bytes is below the %zu needed",
+               workspace_bytes, need);
+  return dsv4_launch_shared_fp8_add(x, tokens, hidden, inter, w13q, w13s8, w2q, w2s8, clamp_limit, out, workspace,
+                                    static_cast<hipStream_t>(stream));
 }
 
 size_t dsv4moe_experts_w4a8_workspace_bytes(int64_t tokens, int32_t topk, int32_t hidden, int32_t inter,

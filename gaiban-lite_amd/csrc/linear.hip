@@ -23,6 +23,7 @@
 // two MFMA 16x16x32 steps (bytes 0-7: K 16j..16j+7, bytes 8-15: K 16j+8..+15,
 // j = l/16); the activation fragments use the same K assignment, so the
 // product is the plain dot product over a permuted K order.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -50,7 +51,22 @@ struct LinearParams {
   int tiles_m;
   uint16_t* out;
   float* partial;  // [split][M][N] when split > 1
+  int accumulate;  // out = bf16(out + bf16(result)) instead of bf16(result)
 };
+
+// The bf16 written for result v: bf16(v), or with accumulation the bf16 sum
+// of the existing output and bf16(v) (torch.add of two bf16 tensors).
+__device__ __forceinline__ u32x2 finish_bf16x4(const float (&v)[4], const uint16_t* old, bool accumulate) {
+  u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  if (accumulate) {
+    const u32x2 prev = *reinterpret_cast<const u32x2*>(old);
+    o[0] = pack_bf16x2(__uint_as_float(prev[0] << 16) + __uint_as_float(o[0] << 16),
+                       __uint_as_float(prev[0] & 0xFFFF0000u) + __uint_as_float(o[0] & 0xFFFF0000u));
+    o[1] = pack_bf16x2(__uint_as_float(prev[1] << 16) + __uint_as_float(o[1] << 16),
+                       __uint_as_float(prev[1] & 0xFFFF0000u) + __uint_as_float(o[1] & 0xFFFF0000u));
+  }
+  return o;
+}
 
 // 8 int8 weights (two dwords, K order) -> 8 bf16.  Every int8 is exact in
 // bf16; the signed byte converts through v_cvt_f32_i32 (SDWA byte select) and
@@ -243,8 +259,8 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = acc[r][c][e] * sc[e];
       if (p.split == 1) {
-        const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        *reinterpret_cast<u32x2*>(p.out + tok * p.n + n) = o;
+        uint16_t* dst = p.out + tok * p.n + n;
+        *reinterpret_cast<u32x2*>(dst) = finish_bf16x4(v, dst, p.accumulate != 0);
       } else {
         float* dst = p.partial + ((int64_t)sp * p.m + tok) * p.n + n;
         *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
@@ -255,7 +271,7 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
 
 // out[m][n] = bf16(sum over splits, in split order, of partial[s][m][n]).
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* partial, int split, int64_t mn,
-                                                           uint16_t* out) {
+                                                           uint16_t* out, int accumulate) {
   const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 4 elements each
   if (q * 4 >= mn) return;
   f32x4 s = *reinterpret_cast<const f32x4*>(partial + q * 4);
@@ -266,7 +282,36 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* partial,
     s[2] += v[2];
     s[3] += v[3];
   }
-  *reinterpret_cast<u32x2*>(out + q * 4) = u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
+  const float v[4] = {s[0], s[1], s[2], s[3]};
+  *reinterpret_cast<u32x2*>(out + q * 4) = finish_bf16x4(v, out + q * 4, accumulate != 0);
+}
+
+// Shared-expert SwiGLU over bf16 linear outputs (shared_bf16_partial,
+// runtime/dsv4_direct/moe_runtime.py:246-263): per row the first `inter`
+// columns are the gate, the next `inter` the up projection;
+// h = bf16(silu(min(gate, L)) * clamp(up, -L, L)) in fp32 (no clamp for L = 0).
+__global__ __launch_bounds__(256) void swiglu_rows_kernel(const uint16_t* __restrict__ gu, int64_t rows, int inter,
+                                                          float clamp_limit, uint16_t* __restrict__ h) {
+  const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 4 columns each
+  const int quads = inter / 4;
+  if (q >= rows * quads) return;
+  const int64_t r = q / quads;
+  const int c = (int)(q % quads) * 4;
+  const u32x2 g = *reinterpret_cast<const u32x2*>(gu + r * 2 * inter + c);
+  const u32x2 u = *reinterpret_cast<const u32x2*>(gu + r * 2 * inter + inter + c);
+  float out[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t gw = g[e >> 1], uw = u[e >> 1];
+    float gt = (e & 1) ? __uint_as_float(gw & 0xFFFF0000u) : __uint_as_float(gw << 16);
+    float up = (e & 1) ? __uint_as_float(uw & 0xFFFF0000u) : __uint_as_float(uw << 16);
+    if (clamp_limit > 0.0f) {
+      gt = fminf(gt, clamp_limit);
+      up = fminf(fmaxf(up, -clamp_limit), clamp_limit);
+    }
+    out[e] = silu_f(gt) * up;
+  }
+  *reinterpret_cast<u32x2*>(h + r * inter + c) = u32x2{pack_bf16x2(out[0], out[1]), pack_bf16x2(out[2], out[3])};
 }
 
 // Row-major int8 [N][K] -> 1 KiB tiles (16 rows x 64 K); one thread per 16 bytes.
@@ -333,7 +378,7 @@ int dsv4_launch_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed
 // ws (int8 format, bf16 [N]) or ws8 (FP8 format, E8M0 [ceil(N/128)][K/128]): exactly one is set.
 int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
                       const uint16_t* ws, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
-                      hipStream_t stream) {
+                      hipStream_t stream, int accumulate) {
   int r, c;
   w8a16_geometry(m, &r, &c);
   LinearParams p;
@@ -352,6 +397,7 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
   p.tiles_m = (int)((m + 16 * c - 1) / (16 * c));
   p.out = out;
   p.partial = workspace;
+  p.accumulate = accumulate;
   if (ws8 != nullptr)
     launch_w8a16_kernel<true>(p, r, c, stream);
   else
@@ -360,8 +406,57 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
   if (split > 1) {
     const int64_t quads = m * n / 4;
     hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
-                       workspace, split, m * n, out);
+                       workspace, split, m * n, out, accumulate);
     DSV4_CHECK_LAUNCH("split_reduce_kernel");
   }
   return DSV4MOE_OK;
+}
+
+// Workspace of the FP8-block shared expert: gate|up bf16 [T][2I], h bf16
+// [T][I], split-K partials fp32 (the larger of the two linears' needs), each
+// 256-byte aligned.
+struct SharedFp8Workspace {
+  uint16_t* gu;
+  uint16_t* h;
+  float* partial;
+  int32_t split13, split2;
+  size_t bytes;
+};
+static SharedFp8Workspace carve_shared_fp8(void* base, int64_t tokens, int hidden, int inter) {
+  auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  SharedFp8Workspace w{};
+  w.split13 = dsv4_w8a16_split_k(tokens, 2 * (int64_t)inter, hidden);
+  w.split2 = dsv4_w8a16_split_k(tokens, hidden, inter);
+  const size_t gu = align((size_t)tokens * 2 * inter * 2);
+  const size_t h = align((size_t)tokens * inter * 2);
+  const size_t part = std::max(dsv4_w8a16_workspace_bytes(tokens, 2 * (int64_t)inter, w.split13),
+                               dsv4_w8a16_workspace_bytes(tokens, hidden, w.split2));
+  uint8_t* p = static_cast<uint8_t*>(base);
+  w.gu = reinterpret_cast<uint16_t*>(p);
+  w.h = reinterpret_cast<uint16_t*>(p + gu);
+  w.partial = reinterpret_cast<float*>(p + gu + h);
+  w.bytes = gu + h + align(part);
+  return w;
+}
+
+size_t dsv4_shared_fp8_workspace_bytes(int64_t tokens, int hidden, int inter) {
+  return tokens > 0 ? carve_shared_fp8(nullptr, tokens, hidden, inter).bytes : 0;
+}
+
+// out[T][H] (bf16, the routed sum) <- bf16(out + shared(x)), the shared expert
+// as three dense steps over FP8-block weights: gate|up = bf16(x . W13^T),
+// SwiGLU -> h bf16, bf16(h . W2^T) added into out.
+int dsv4_launch_shared_fp8_add(const uint16_t* x, int64_t tokens, int hidden, int inter, const uint8_t* w13q,
+                               const uint8_t* w13s8, const uint8_t* w2q, const uint8_t* w2s8, float clamp_limit,
+                               uint16_t* out, void* workspace, hipStream_t stream) {
+  if (tokens == 0) return DSV4MOE_OK;
+  const SharedFp8Workspace w = carve_shared_fp8(workspace, tokens, hidden, inter);
+  int rc = dsv4_launch_w8a16(x, tokens, 2 * (int64_t)inter, hidden, w13q, nullptr, w13s8, w.split13, w.partial, w.gu,
+                             stream, 0);
+  if (rc != DSV4MOE_OK) return rc;
+  const int64_t quads = tokens * (inter / 4);
+  hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, w.gu, tokens,
+                     inter, clamp_limit, w.h);
+  DSV4_CHECK_LAUNCH("swiglu_rows_kernel");
+  return dsv4_launch_w8a16(w.h, tokens, hidden, inter, w2q, nullptr, w2s8, w.split2, w.partial, out, stream, 1);
 }

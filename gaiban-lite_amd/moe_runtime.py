@@ -159,6 +159,7 @@ class _LayerBuffers:
     block_size_m: int
     ready_event: Any
     gathered_input_ids: torch.Tensor | None = None
+    shared_workspace: torch.Tensor | None = None  # FP8-block shared expert
     has_completion_event: bool = False
     state: str = "free"
 
@@ -267,7 +268,8 @@ class TP4MoE:
             config.experts, config.hidden_size, config.intermediate_size
         ):
             raise ValueError("resident expert geometry does not match the config")
-        if resident.has_shared != bool(config.shared_experts):
+        shared_fp8 = getattr(resident, "shared_fp8", None)
+        if (resident.has_shared or shared_fp8 is not None) != bool(config.shared_experts):
             raise ValueError("resident shared-expert presence does not match the config")
         if resident.device != device:
             raise ValueError("resident weights must live on the configured device")
@@ -302,6 +304,10 @@ class TP4MoE:
         self.group = group
         self._marlin_input_dtype = marlin_input_dtype
         self._mxfp4 = isinstance(resident, ResidentMXFP4MoEWeights)
+        # shared expert: inside the grouped kernels (expert index E of the routed
+        # stack) or, in the checkpoint FP8 format, as dense linears after them
+        self._shared_fp8 = getattr(resident, "shared_fp8", None)
+        self._grouped_shared = bool(config.shared_experts) and self._shared_fp8 is None
         self._gate_weight = gate.weight.to(torch.bfloat16).contiguous()
         self._gate_bias = None if gate.bias is None else gate.bias.float().contiguous()
         self.overlap_stats: dict[str, int] = {
@@ -341,6 +347,14 @@ class TP4MoE:
                     self._register_shape(int(rows), slot)
         self._validate_provider_storage()
 
+    def _add_shared_fp8(self, flat: torch.Tensor, buffers: "_LayerBuffers") -> None:
+        """output <- bf16(routed + shared(flat)) for an FP8-block shared expert
+        (``moe_runtime.py:1860-1873``: shared_bf16_partial, then torch.add)."""
+
+        if self._shared_fp8 is not None:
+            ops.shared_fp8_add_into(flat, self._shared_fp8, clamp_limit=self.config.clamp_limit,
+                                    out=buffers.output, workspace=buffers.shared_workspace)
+
     # ------------------------------------------------------------ buffers
     def _register_shape(self, rows: int, slot: int) -> None:
         cfg = self.config
@@ -352,7 +366,7 @@ class TP4MoE:
         bs = ops.block_size_m(rows, cfg.topk, cfg.experts, 1 if self._marlin_input_dtype else 2)
         template = torch.empty(rows, cfg.topk, dtype=torch.int32, device=self.device)
         ws_fn = ops.experts_w4a8_workspace_bytes if self._marlin_input_dtype else ops.experts_workspace_bytes
-        ws_bytes = ws_fn(rows, cfg.topk, cfg.hidden_size, cfg.intermediate_size, bool(cfg.shared_experts))
+        ws_bytes = ws_fn(rows, cfg.topk, cfg.hidden_size, cfg.intermediate_size, self._grouped_shared)
         self._buffers[key] = _LayerBuffers(
             workspace=torch.empty(ws_bytes, dtype=torch.uint8, device=self.device),
             logits=torch.empty(rows, cfg.experts, dtype=torch.float32, device=self.device),
@@ -366,6 +380,11 @@ class TP4MoE:
             gathered_input_ids=(
                 torch.empty(rows, dtype=torch.int64, device=self.device)
                 if self.route_kind == "hash" else None
+            ),
+            shared_workspace=(
+                torch.empty(ops.shared_fp8_workspace_bytes(rows, cfg.hidden_size, cfg.intermediate_size),
+                            dtype=torch.uint8, device=self.device)
+                if self._shared_fp8 is not None else None
             ),
         )
 
@@ -598,13 +617,14 @@ class TP4MoE:
                         route_scale=cfg.route_scale, w13q=self.resident.w13_q,
                         w13s=self.resident.w13_s, w2q=self.resident.w2_q, w2s=self.resident.w2_s,
                         experts=cfg.experts, inter=cfg.intermediate_size,
-                        has_shared=bool(cfg.shared_experts), clamp_limit=cfg.clamp_limit,
+                        has_shared=self._grouped_shared, clamp_limit=cfg.clamp_limit,
                         block_size=buffers.block_size_m, ids=buffers.route_ids,
                         weights=buffers.route_weights, margin=buffers.margin,
                         sorted_token_ids=a.sorted_token_ids, expert_ids=a.expert_ids,
                         num_tokens_post_padded=a.num_tokens_post_padded, out=buffers.output,
                         workspace=buffers.workspace,
                     )
+                    self._add_shared_fp8(flat, buffers)
                     return buffers.route_weights, buffers.route_ids, buffers.margin, {}
                 sel_ids = sel_scores = None
                 if self.route_kind == "hash":
@@ -668,14 +688,16 @@ class TP4MoE:
                 experts_into(
                     flat, w13q=self.resident.w13_q, w13s=self.resident.w13_s,
                     w2q=self.resident.w2_q, w2s=self.resident.w2_s, experts=cfg.experts,
-                    inter=cfg.intermediate_size, has_shared=bool(cfg.shared_experts),
+                    inter=cfg.intermediate_size, has_shared=self._grouped_shared,
                     route_weights=route_weights, sorted_token_ids=a.sorted_token_ids,
                     expert_ids=a.expert_ids, num_tokens_post_padded=a.num_tokens_post_padded,
                     block_size=buffers.block_size_m, clamp_limit=cfg.clamp_limit,
                     out=buffers.output, workspace=buffers.workspace,
                 )
                 # routed experts, shared expert and the add run in the same fused launch chain
+                # (an FP8-block shared expert as dense linears that add into the routed sum)
                 mark("moe_routed_done")
+                self._add_shared_fp8(flat, buffers)
                 mark("moe_shared_done")
                 mark("moe_combine_done")
                 digests = {}

@@ -417,3 +417,25 @@ def w8a16_fp8_linear_into(a: torch.Tensor, wq: torch.Tensor, ws8: torch.Tensor, 
         ws_bytes = workspace.numel() * 4
     call("dsv4moe_w8a16_fp8_linear", ptr(a), m, n, k, ptr(wq), ptr(ws8), int(split_k), ptr(workspace),
          ws_bytes, ptr(out), _lib.current_stream(dev))
+
+
+def shared_fp8_workspace_bytes(tokens: int, hidden: int, inter: int) -> int:
+    return int(_lib.load().dsv4moe_shared_fp8_workspace_bytes(tokens, hidden, inter))
+
+
+def shared_fp8_add_into(x: torch.Tensor, shared, *, clamp_limit: float, out: torch.Tensor,
+                        workspace: torch.Tensor) -> None:
+    """out <- bf16(out + shared(x)) with the FP8-block shared expert
+    (``ResidentFP8SharedExpert``; ``dsv4moe_shared_fp8_add``)."""
+
+    tokens, hidden = x.shape
+    dev = x.device
+    inter = shared.intermediate_size
+    _check("x", x, dtype=torch.bfloat16, device=dev)
+    _check("out", out, dtype=torch.bfloat16, shape=(tokens, hidden), device=dev)
+    _check("workspace", workspace, dtype=torch.uint8, device=dev)
+    if shared.hidden_size != hidden:
+        raise ValueError("shared expert hidden size does not match x")
+    call("dsv4moe_shared_fp8_add", ptr(x), tokens, hidden, inter, ptr(shared.w13_q), ptr(shared.w13_s),
+         ptr(shared.w2_q), ptr(shared.w2_s), float(clamp_limit), ptr(out), ptr(workspace), workspace.numel(),
+         _lib.current_stream(dev))

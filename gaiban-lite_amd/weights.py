@@ -28,6 +28,101 @@ from . import ops
 GROUP = 128
 
 
+@dataclass
+class ResidentFP8SharedExpert:
+    """The shared expert in the checkpoint's FP8 format (``SharedExpertSlice``,
+    ``runtime/dsv4_direct/ops/marlin_moe.py:42-74``): E4M3 weights with one
+    E8M0 scale per 128 x 128 block, repacked once into the W8A16 tile layout
+    (``dsv4moe_pack_int8``, a byte permutation).  Runs as dense W8A16 linears
+    (``dsv4moe_shared_fp8_add``), outside the grouped expert kernels.
+
+      w13_q  uint8 [2I*H]           W13 = [W1; W3] [2I, H]
+      w13_s  uint8 [2I/128, H/128]  E8M0 (W1's block rows, then W3's)
+      w2_q   uint8 [H*I]            W2 [H, I]
+      w2_s   uint8 [H/128, I/128]
+    """
+
+    w13_q: torch.Tensor
+    w13_s: torch.Tensor
+    w2_q: torch.Tensor
+    w2_s: torch.Tensor
+    hidden_size: int
+    intermediate_size: int
+
+    @property
+    def device(self) -> torch.device:
+        return self.w13_q.device
+
+    @property
+    def resident_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.w13_q, self.w13_s, self.w2_q, self.w2_s))
+
+    def validate(self) -> None:
+        h, i = self.hidden_size, self.intermediate_size
+        if h % GROUP or i % GROUP:
+            raise ValueError("FP8 shared expert needs hidden and intermediate sizes that are multiples of 128")
+        expected = {
+            "w13_q": ((2 * i * h,), torch.uint8),
+            "w13_s": ((2 * i // GROUP, h // GROUP), torch.uint8),
+            "w2_q": ((h * i,), torch.uint8),
+            "w2_s": ((h // GROUP, i // GROUP), torch.uint8),
+        }
+        for name, (shape, dtype) in expected.items():
+            t = getattr(self, name)
+            if tuple(t.shape) != shape or t.dtype != dtype:
+                raise ValueError(f"{name} must be {dtype} {shape}, got {t.dtype} {tuple(t.shape)}")
+            if not t.is_contiguous() or t.device != self.w13_q.device:
+                raise ValueError(f"{name} must be contiguous on {self.w13_q.device}")
+
+    @classmethod
+    def from_checkpoint(cls, w1, s1, w3, s3, w2, s2) -> "ResidentFP8SharedExpert":
+        """``w1``/``w3`` [I, H] and ``w2`` [H, I] float8_e4m3fn (or their uint8
+        codes); ``s1``/``s3`` [I/128, H/128] and ``s2`` [H/128, I/128]
+        float8_e8m0fnu (or uint8 codes).  Rejects the reserved E8M0 byte 255
+        (a synchronising load-time check, as the reference's preflight)."""
+
+        from .weight_only_linear import validate_e8m0_scale_values
+
+        def codes(t):
+            return t.view(torch.uint8) if t.dtype in (torch.float8_e4m3fn, torch.float8_e8m0fnu) else t
+
+        w1, w3, w2 = codes(w1), codes(w3), codes(w2)
+        s1, s3, s2 = codes(s1), codes(s3), codes(s2)
+        for name, t in (("w1", w1), ("w3", w3), ("w2", w2), ("s1", s1), ("s3", s3), ("s2", s2)):
+            if t.dtype != torch.uint8 or t.ndim != 2:
+                raise TypeError(f"{name} must be a 2-D FP8 (or uint8) tensor")
+        inter, hidden = w1.shape
+        if w3.shape != (inter, hidden) or w2.shape != (hidden, inter):
+            raise ValueError("w1/w3 must be [I, H] and w2 [H, I]")
+        if inter % GROUP or hidden % GROUP:
+            raise ValueError("hidden and intermediate sizes must be multiples of 128")
+        for name, t, shape in (("s1", s1, (inter // GROUP, hidden // GROUP)), ("s3", s3, (inter // GROUP, hidden // GROUP)),
+                               ("s2", s2, (hidden // GROUP, inter // GROUP))):
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name} must be [{shape[0]}, {shape[1]}]")
+            validate_e8m0_scale_values(name, t)
+        w13 = torch.cat([w1, w3], dim=0).contiguous()
+        out = cls(ops.pack_int8(w13.view(torch.int8)), torch.cat([s1, s3], dim=0).contiguous(),
+                  ops.pack_int8(w2.contiguous().view(torch.int8)), s2.contiguous(), hidden, inter)
+        out.validate()
+        return out
+
+
+def _validate_shared_fp8(resident) -> None:
+    sh = resident.shared_fp8
+    if sh is None:
+        return
+    if not isinstance(sh, ResidentFP8SharedExpert):
+        raise TypeError("shared_fp8 must be ResidentFP8SharedExpert")
+    if resident.has_shared:
+        raise ValueError("a shared expert is either in the routed stack (has_shared) or in FP8, not both")
+    if (sh.hidden_size, sh.intermediate_size) != (resident.hidden_size, resident.intermediate_size):
+        raise ValueError("FP8 shared expert geometry does not match the routed experts")
+    if sh.device != resident.w13_q.device:
+        raise ValueError("FP8 shared expert must live on the routed experts' device")
+    sh.validate()
+
+
 def int4_g128_expert_bytes(hidden: int, inter: int) -> int:
     """Bytes of one expert's weights plus scales: 3*H*I/2 + 3*H*(I/128)*2."""
 
@@ -48,6 +143,7 @@ class ResidentInt4MoEWeights:
     checkpoint_id: str | None = None
     marlin_input_dtype: torch.dtype | None = None
     weight_format: str = "int4_g128"
+    shared_fp8: ResidentFP8SharedExpert | None = None  # shared expert in the checkpoint FP8 format
 
     @property
     def device(self) -> torch.device:
@@ -78,6 +174,7 @@ class ResidentInt4MoEWeights:
                 raise ValueError(f"{name} must be {dtype} {shape}, got {t.dtype} {tuple(t.shape)}")
             if not t.is_contiguous() or t.device != self.w13_q.device:
                 raise ValueError(f"{name} must be contiguous on {self.w13_q.device}")
+        _validate_shared_fp8(self)
 
     @classmethod
     def from_checkpoint_layout(
@@ -92,6 +189,7 @@ class ResidentInt4MoEWeights:
         layer_id: int | None = None,
         checkpoint_id: str | None = None,
         marlin_input_dtype: torch.dtype | None = None,
+        shared_fp8: ResidentFP8SharedExpert | None = None,
     ) -> "ResidentInt4MoEWeights":
         """Repack stacked checkpoint-layout experts on the device.
 
@@ -109,7 +207,7 @@ class ResidentInt4MoEWeights:
         q13, s13 = ops.pack_int4_g128(w13_packed.contiguous(), w13_scale.contiguous(), gated=True)
         q2, s2 = ops.pack_int4_g128(w2_packed.contiguous(), w2_scale.contiguous(), gated=False)
         out = cls(q13, s13, q2, s2, experts, hidden, inter, has_shared, layer_id, checkpoint_id,
-                  marlin_input_dtype)
+                  marlin_input_dtype, shared_fp8=shared_fp8)
         out.validate()
         return out
 
@@ -145,6 +243,7 @@ class ResidentMXFP4MoEWeights:
     checkpoint_id: str | None = None
     marlin_input_dtype: torch.dtype | None = None
     weight_format: str = "mxfp4_g32"
+    shared_fp8: ResidentFP8SharedExpert | None = None  # shared expert in the checkpoint FP8 format
 
     @property
     def device(self) -> torch.device:
@@ -177,6 +276,7 @@ class ResidentMXFP4MoEWeights:
                 raise ValueError(f"{name} must be {dtype} {shape}, got {t.dtype} {tuple(t.shape)}")
             if not t.is_contiguous() or t.device != self.w13_q.device:
                 raise ValueError(f"{name} must be contiguous on {self.w13_q.device}")
+        _validate_shared_fp8(self)
 
     @classmethod
     def from_checkpoint_layout(
@@ -190,6 +290,7 @@ class ResidentMXFP4MoEWeights:
         has_shared: bool,
         layer_id: int | None = None,
         checkpoint_id: str | None = None,
+        shared_fp8: ResidentFP8SharedExpert | None = None,
     ) -> "ResidentMXFP4MoEWeights":
         """Repack stacked checkpoint-layout experts on the device.
 
@@ -209,10 +310,11 @@ class ResidentMXFP4MoEWeights:
             raise ValueError("expert count does not match the stacked tensors")
         q13, s13 = ops.pack_mxfp4_g32(as_u8(w13_packed).contiguous(), as_u8(w13_scale).contiguous(), gated=True)
         q2, s2 = ops.pack_mxfp4_g32(as_u8(w2_packed).contiguous(), as_u8(w2_scale).contiguous(), gated=False)
-        out = cls(q13, s13, q2, s2, experts, hidden, inter, has_shared, layer_id, checkpoint_id)
+        out = cls(q13, s13, q2, s2, experts, hidden, inter, has_shared, layer_id, checkpoint_id,
+                  shared_fp8=shared_fp8)
         out.validate()
         return out
 
 
-__all__ = ["ResidentInt4MoEWeights", "ResidentMXFP4MoEWeights", "int4_g128_expert_bytes",
-           "mxfp4_g32_expert_bytes"]
+__all__ = ["ResidentFP8SharedExpert", "ResidentInt4MoEWeights", "ResidentMXFP4MoEWeights",
+           "int4_g128_expert_bytes", "mxfp4_g32_expert_bytes"]

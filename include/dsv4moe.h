@@ -285,6 +285,31 @@ int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k,
                              uint16_t* out, void* stream);
 
 /*
+ * Shared expert over the checkpoint's FP8 E4M3 / E8M0 128x128-block weights,
+ * added into the routed output:
+ *   out[T,H] <- bf16( out + shared(x) ),
+ *   shared(x) = bf16( bf16( silu(min(g, L)) * clamp(u, -L, L) ) . W2^T ),
+ *   g | u     = bf16( x . W13^T ),  W13 = [W1; W3] (gate rows, then up rows),
+ * bf16 products of the exactly dequantised weights with fp32 accumulation,
+ * no clamp when L = 0.  Replaces prepare_shared_bf16 / shared_bf16_partial
+ * and the routed + shared add (runtime/dsv4_direct/moe_runtime.py:238-263,
+ * 1865-1873; dequant_fp8_block, moe_forward.py:158-176): the same three
+ * bf16 roundings and the same final torch.add of two bf16 tensors.
+ *   w13q   E4M3 bytes of W13 [2I, H] packed by dsv4moe_pack_int8
+ *   w13s8  E8M0 bytes [2I/128, H/128] (rows of W1's blocks, then W3's)
+ *   w2q    E4M3 bytes of W2 [H, I] packed by dsv4moe_pack_int8
+ *   w2s8   E8M0 bytes [H/128, I/128]
+ *   out    bf16 [T, H], read and written (holds the routed sum on entry)
+ *   workspace  dsv4moe_shared_fp8_workspace_bytes(T, H, I) bytes, 256-byte aligned
+ * hidden and inter: multiples of 128 up to 32768.  Four to six launches
+ * (two W8A16 linears with their split-K reductions, one SwiGLU).
+ */
+size_t dsv4moe_shared_fp8_workspace_bytes(int64_t tokens, int32_t hidden, int32_t inter);
+int dsv4moe_shared_fp8_add(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter, const uint8_t* w13q,
+                           const uint8_t* w13s8, const uint8_t* w2q, const uint8_t* w2s8, float clamp_limit,
+                           uint16_t* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * W4A8 variant of dsv4moe_experts_w4a16 on the gfx950 fp8 MFMA
  * (v_mfma_scale_f32_16x16x128_f8f6f4, unit block scales).  Replaces the vLLM
  * _fused_marlin_moe call with input_dtype = float8_e4m3fn

@@ -94,6 +94,7 @@ __all__ = [
     "softmax_f32",
     "sqrtsoftplus_f32",
     "unpack_int4_rows",
+    "shared_fp8_bf16",
     "w8a16_fp8_linear_f32",
     "w8a16_linear_f32",
 ]
@@ -563,7 +564,8 @@ def dequant_mxfp4(packed, scale_codes) -> np.ndarray:
 
 
 def _silu(g: np.ndarray) -> np.ndarray:
-    return (g / (F32(1.0) + np.exp(-g.astype(F32)))).astype(F32)
+    with np.errstate(over="ignore"):  # exp(-g) = inf for very negative g gives silu = -0
+        return (g / (F32(1.0) + np.exp(-g.astype(F32)))).astype(F32)
 
 
 def _swiglu(g: np.ndarray, u: np.ndarray, clamp_limit: float) -> np.ndarray:
@@ -819,6 +821,25 @@ def w8a16_fp8_linear_f32(a, codes, scale_codes) -> np.ndarray:
 
     w = bf16_round(dequant_fp8_block(codes, scale_codes))
     return (np.asarray(a, dtype=F32) @ w.T).astype(F32)
+
+
+def shared_fp8_bf16(x, w1, s1, w3, s3, w2, s2, clamp_limit: float) -> np.ndarray:
+    """``prepare_shared_bf16`` + ``shared_bf16_partial``
+    (``moe_runtime.py:238-263``) on FP8-block checkpoint weights: the weights
+    dequantised and rounded to bf16, then three bf16 linears with fp32
+    accumulation -- gate = bf16(x W1^T) clamped above at L, up = bf16(x W3^T)
+    clamped to [-L, L], h = bf16(silu(gate) * up), out = bf16(h W2^T) -- as
+    float32 values on the bf16 grid.  ``clamp_limit`` 0 disables the clamps
+    (this build's convention for the routed experts too)."""
+
+    x = np.asarray(x, dtype=F32)
+    wb1 = bf16_round(dequant_fp8_block(w1, s1))
+    wb3 = bf16_round(dequant_fp8_block(w3, s3))
+    wb2 = bf16_round(dequant_fp8_block(w2, s2))
+    gate = bf16_round(x @ wb1.T)
+    up = bf16_round(x @ wb3.T)
+    h = bf16_round(_swiglu(gate, up, clamp_limit))
+    return bf16_round(h @ wb2.T)
 
 
 def w8a16_linear_f32(a, q_int8, scale_bits) -> np.ndarray:

@@ -247,3 +247,40 @@ def test_w8a16_fp8_linear_oracle_against_scalar_loop():
                                                  dtype=np.float32))[0])
                 ref[m, n_] += float(a[m, c]) * wv
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_shared_fp8_oracle_matches_reference_op_order_in_torch():
+    """shared_fp8_bf16 equals the reference's torch sequence
+    (moe_runtime.py:238-263: dequant_fp8_block -> bf16, F.linear in bf16,
+    .float().clamp, F.silu, .to(bf16), F.linear) bit for bit.  Operands are
+    small dyadic values, so every fp32 sum is exact and the accumulation order
+    cannot matter; gate and up exceed the clamp for some entries."""
+
+    import torch
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(21)
+    t, h, i, lim = 5, 256, 128, 3.0
+    enc = O.fp8_e4m3_encode
+    vals = np.array([-8, -4, -3, -2, -1, -0.5, 0, 0.5, 1, 2, 3, 4, 8], dtype=np.float32)
+    w1 = enc(rng.choice(vals, size=(i, h)).astype(np.float32))
+    w3 = enc(rng.choice(vals, size=(i, h)).astype(np.float32))
+    w2 = enc(rng.choice(vals, size=(h, i)).astype(np.float32))
+    s1 = np.full((1, 2), 123, dtype=np.uint8)   # 2^-4
+    s3 = np.array([[124, 122]], dtype=np.uint8)
+    s2 = np.full((2, 1), 121, dtype=np.uint8)
+    x = (rng.integers(-4, 5, size=(t, h)) * 0.25).astype(np.float32)
+    got = O.shared_fp8_bf16(x, w1, s1, w3, s3, w2, s2, lim)
+
+    def dq(c, s):
+        wv = torch.from_numpy(c.copy()).view(torch.float8_e4m3fn).float()
+        sv = torch.from_numpy(s.copy()).view(torch.float8_e8m0fnu).float()
+        return (wv * sv.repeat_interleave(128, 0).repeat_interleave(128, 1)).to(torch.bfloat16)
+
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    gate = F.linear(xb, dq(w1, s1)).float().clamp(max=lim)
+    up = F.linear(xb, dq(w3, s3)).float().clamp(min=-lim, max=lim)
+    assert float(gate.max()) == lim and float(up.abs().max()) == lim  # the clamps bite
+    act = (F.silu(gate) * up).to(torch.bfloat16)
+    ref = F.linear(act, dq(w2, s2)).float().numpy()
+    np.testing.assert_allclose(got, ref, rtol=2e-3, atol=0)
