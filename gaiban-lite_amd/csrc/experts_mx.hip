@@ -195,9 +195,12 @@ __global__ __launch_bounds__(256, 4) void mx_decode_kernel(ExpertGemmParams p) {
 // As the int4 prefill kernel: alignment blocks of up to 64 token slots,
 // workgroup tile 64 slots x 256 weight rows (wavefront w: strip pairs
 // p0 = tile*8 + 2w and p0 + 1), work items (block, tile) in XCD-grouped order
-// (prefill_item), token tile, weight tiles and scales copied into LDS by
-// inline-asm DMA, double buffered, one explicit wait and one barrier per
-// group.  Per group a wavefront converts 16 weight operands (64 conversions)
+// (prefill_item).  The token tile is copied into LDS by inline-asm DMA,
+// double buffered; each wavefront's weight tiles and scale words (private to
+// it) are loaded straight into registers one group ahead, so LDS carries only
+// the shared operand (32 KiB per workgroup, 160 VGPRs: three workgroups per
+// CU).  One explicit wait and one barrier per group.  Per group a wavefront
+// converts 16 weight operands (64 conversions)
 // and issues 64 MFMAs into its 16 accumulator tiles.
 template <int STAGE>
 __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, int total_blocks) {
@@ -205,8 +208,6 @@ __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, 
   constexpr int C = 4;
   constexpr int kSlots = 64;
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kSlots * 256];
-  __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * kTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];  // the wavefront's two pairs' 128-byte blocks
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
@@ -238,18 +239,48 @@ __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, 
   // weight tiles: pair p, group g, member m at byte ((p*groups + g)*2 + m) * 1 KiB
   const uint32_t w_off0 = (uint32_t)(p0 * groups) * 2048 + lane * 16;
   const uint32_t w_off1 = (uint32_t)((p0 + 1) * groups) * 2048 + lane * 16;
-  // scales: 128 bytes per (pair, group); lane l copies 4 bytes of pair p0 + l/32
-  const uint32_t s_off = (uint32_t)((p0 + (lane >> 5)) * groups) * 128 + (lane & 31) * 4;
+  // scales: 128 bytes per (pair, group); strip r = 2j + m of this row at
+  // byte 128 j + (r16*2 + m)*4 of the group's block: one 8-byte word per pair
+  const uint32_t s_off0 = (uint32_t)(p0 * groups) * 128 + (lane & 15) * 8;
+  const uint32_t s_off1 = (uint32_t)((p0 + 1) * groups) * 128 + (lane & 15) * 8;
 
   auto issue = [&](int g, int buf) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       lds_copy16(act_rsrc, lds_addr(&xs[buf][(16 * wave + 4 * q) * 256]), dma_off[q], g * 256);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][0]), w_off0, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][kTileBytes]), w_off0 + kTileBytes, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][2 * kTileBytes]), w_off1, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][3 * kTileBytes]), w_off1 + kTileBytes, g * 2048);
-    lds_copy4(s_rsrc, lds_addr(&scl[buf][wave][0]), s_off, g * 128);
+  };
+  // The weight tiles and scales are private to the wavefront: loaded straight
+  // into registers, one group ahead (no LDS traffic for them).
+  struct WRegs {
+    u32x4 w[R];
+    u32x2 s[2];
+  };
+  // Loads into registers as inline asm: the compiler neither counts them in
+  // its own vmcnt waits (compiler-visible loads made it wait for the token
+  // copies issued after them) nor lets uses move above wait_weights, which
+  // takes the registers as in/out operands.  The registers in flight must not
+  // be touched in between: the kernel must compile without spills
+  // (tests/test_kernel_resources.py checks the compiled code object).
+  auto load_weights = [&](int g, WRegs& o) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t gw = __builtin_amdgcn_readfirstlane((uint32_t)g * 2048u);
+    const uint32_t gs = __builtin_amdgcn_readfirstlane((uint32_t)g * 128u);
+    const uint32_t w0b = w_off0 + kTileBytes, w1b = w_off1 + kTileBytes;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(o.w[0]) : "v"(w_off0), "s"(w_rsrc), "s"(gw));
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(o.w[1]) : "v"(w0b), "s"(w_rsrc), "s"(gw));
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(o.w[2]) : "v"(w_off1), "s"(w_rsrc), "s"(gw));
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(o.w[3]) : "v"(w1b), "s"(w_rsrc), "s"(gw));
+    asm volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen" : "=v"(o.s[0]) : "v"(s_off0), "s"(s_rsrc), "s"(gs));
+    asm volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen" : "=v"(o.s[1]) : "v"(s_off1), "s"(s_rsrc), "s"(gs));
+#endif
+  };
+  auto wait_weights = [&](WRegs& o) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(o.w[0]), "+v"(o.w[1]), "+v"(o.w[2]), "+v"(o.w[3]), "+v"(o.s[0]), "+v"(o.s[1])
+                 :
+                 : "memory");
+#endif
   };
 
   f32x4 acc[R][C];
@@ -261,16 +292,11 @@ __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, 
   const int sw = lane & 15;
   // One group: prefetch group g+1 into the other buffers (unless last), then
   // 16 operand conversions and 64 MFMAs from buffer u.
-  auto step = [&](int g, auto u_c, auto prefetch_c) {
+  auto step = [&](int g, auto u_c, auto prefetch_c, const WRegs& cur, WRegs& nxt) {
     constexpr int u = decltype(u_c)::value;
-    if constexpr (decltype(prefetch_c)::value) issue(g + 1, (u + 1) & 1);
-    u32x4 wv[R];
-    uint32_t sv[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      wv[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]);
-      // strip r = 2j + m: pair j's block at 128 j, this row's dword at (r16*2 + m)*4
-      sv[r] = *reinterpret_cast<const uint32_t*>(&scl[u][wave][128 * (r >> 1) + (sw * 2 + (r & 1)) * 4]);
+    if constexpr (decltype(prefetch_c)::value) {
+      issue(g + 1, (u + 1) & 1);
+      load_weights(g + 1, nxt);
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -281,12 +307,15 @@ __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, 
         bfr[ct] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][(ct * 16 + sw) * 256 + part]));
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const bf16x8 a = dequant_mxfp4(wv[r][d], e8m0_operand(sv[r], d));
+        const bf16x8 a = dequant_mxfp4(cur.w[r][d], e8m0_operand(cur.s[r >> 1][r & 1], d));
 #pragma unroll
         for (int ct = 0; ct < C; ++ct) acc[r][ct] = mfma_bf16(a, bfr[ct], acc[r][ct]);
       }
     }
-    lds_dma_wait_all();  // this wavefront's copies of group g + 1 have landed
+    if constexpr (decltype(prefetch_c)::value)
+      wait_weights(nxt);  // this wavefront's copies and loads of group g + 1 have landed
+    else
+      lds_dma_wait_all();
     __syncthreads();     // ... and everyone's; buffer u is free again
   };
   using U0 = std::integral_constant<int, 0>;
@@ -294,16 +323,18 @@ __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, 
   using PF = std::true_type;
   using NOPF = std::false_type;
 
+  WRegs wa, wb;
   issue(0, 0);
-  lds_dma_wait_all();
+  load_weights(0, wa);
+  wait_weights(wa);
   __syncthreads();
   // groups is even (checked on the host); the last group issues no prefetch
   for (int g0 = 0; g0 + 2 < groups; g0 += 2) {
-    step(g0, U0{}, PF{});
-    step(g0 + 1, U1{}, PF{});
+    step(g0, U0{}, PF{}, wa, wb);
+    step(g0 + 1, U1{}, PF{}, wb, wa);
   }
-  step(groups - 2, U0{}, PF{});
-  step(groups - 1, U1{}, NOPF{});
+  step(groups - 2, U0{}, PF{}, wa, wb);
+  step(groups - 1, U1{}, NOPF{}, wb, wa);
 
   if constexpr (STAGE == 1) {
     const float lim = p.clamp_limit;
