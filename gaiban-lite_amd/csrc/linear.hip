@@ -332,7 +332,9 @@ template <bool FP8>
 static void launch_w8a16_kernel(const LinearParams& p, int r, int c, hipStream_t stream) {
   const int items = p.split * p.tiles_m * p.tiles_n;
   const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
-  if (r == 4) hipLaunchKernelGGL((w8a16_kernel<4, 8, FP8>), grid, dim3(256), 0, stream, p);
+  if (r == 4 && c == 8) hipLaunchKernelGGL((w8a16_kernel<4, 8, FP8>), grid, dim3(256), 0, stream, p);
+  else if (r == 4 && c == 4) hipLaunchKernelGGL((w8a16_kernel<4, 4, FP8>), grid, dim3(256), 0, stream, p);
+  else if (r == 2 && c == 8) hipLaunchKernelGGL((w8a16_kernel<2, 8, FP8>), grid, dim3(256), 0, stream, p);
   else if (c == 1) hipLaunchKernelGGL((w8a16_kernel<2, 1, FP8>), grid, dim3(256), 0, stream, p);
   else if (c == 2) hipLaunchKernelGGL((w8a16_kernel<2, 2, FP8>), grid, dim3(256), 0, stream, p);
   else hipLaunchKernelGGL((w8a16_kernel<2, 4, FP8>), grid, dim3(256), 0, stream, p);
@@ -342,18 +344,21 @@ static void launch_w8a16_kernel(const LinearParams& p, int r, int c, hipStream_t
 
 using namespace dsv4;
 
-// Geometry of the instance chosen for M: (R strips per wavefront, C token tiles).
-static void w8a16_geometry(int64_t m, int* r, int* c) {
+// Geometry of the instance chosen for (M, N): (R strips per wavefront, C
+// token tiles).  Above 64 tokens the 256 x 128 tile, unless it leaves fewer
+// than 512 workgroups (it would need a split-K reduction): then 256 x 64.
+static void w8a16_geometry(int64_t m, int64_t n, int* r, int* c) {
   if (m <= 16) { *r = 2; *c = 1; }
   else if (m <= 32) { *r = 2; *c = 2; }
   else if (m <= 64) { *r = 2; *c = 4; }
-  else { *r = 4; *c = 8; }
+  else if (((n + 255) / 256) * ((m + 127) / 128) >= 512) { *r = 4; *c = 8; }
+  else { *r = 4; *c = 4; }
 }
 
 int32_t dsv4_w8a16_split_k(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0) return -1;
   int r, c;
-  w8a16_geometry(m, &r, &c);
+  w8a16_geometry(m, n, &r, &c);
   const int64_t tiles = ((n + 64 * r - 1) / (64 * r)) * ((m + 16 * c - 1) / (16 * c));
   const int64_t wins = k / kWin;
   int split = 1;
@@ -380,7 +385,7 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
                       const uint16_t* ws, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
                       hipStream_t stream, int accumulate) {
   int r, c;
-  w8a16_geometry(m, &r, &c);
+  w8a16_geometry(m, n, &r, &c);
   LinearParams p;
   p.a = a;
   p.m = m;
