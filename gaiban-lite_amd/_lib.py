@@ -45,6 +45,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_route_hash": (ctypes.c_int, [_p, _p, _i64, _p, _i64, _i32, _i32, _f32, _p, _p, _p, _p]),
     "dsv4moe_gate_logits": (ctypes.c_int, [_p, _p, _i64, _i32, _i32, _p, _p]),
     "dsv4moe_align": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p]),
+    "dsv4moe_align_workspace_bytes": (_sz, [_i64, _i32, _i32]),
+    "dsv4moe_align_ws": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _sz, _p]),
     "dsv4moe_pack_int4_g128": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p]),
     "dsv4moe_experts_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "dsv4moe_experts_w4a16": (

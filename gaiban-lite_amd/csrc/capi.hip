@@ -85,6 +85,13 @@ int dsv4_launch_prologue(int32_t, const float*, const float*, int64_t, int32_t, 
 // Largest token count routed inside the one-workgroup prologue (one token per
 // wavefront); above it the wide route kernel runs first.
 constexpr int64_t kPrologueRouteMaxTokens = 16;
+int dsv4_launch_align_multi(const int32_t*, int64_t, int32_t, int32_t, int32_t*, int64_t, int32_t*, int64_t,
+                            int32_t*, int32_t*, const uint16_t*, int64_t, int32_t, float*, hipStream_t);
+size_t dsv4_align_scratch_bytes(int64_t, int32_t);
+int32_t* dsv4_experts_align_scratch(void*, int64_t, int, int, int, int, size_t*);
+// Fewest flat route ids aligned by the two-launch split over chunks; below it
+// one workgroup aligns them all in one launch.
+constexpr int64_t kAlignMultiMinAssignments = 8192;
 
 int dsv4_launch_pack_mxfp4(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, int, uint8_t*, uint8_t*,
                            hipStream_t);
@@ -263,24 +270,58 @@ int dsv4moe_gate_logits(const uint16_t* x, const uint16_t* wg, int64_t tokens, i
                                  static_cast<hipStream_t>(stream));
 }
 
+static int validate_align(const char* who, const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts,
+                          int32_t block_size, const int32_t* sorted_token_ids, int64_t capacity,
+                          const int32_t* expert_ids, int64_t num_blocks, const int32_t* num_tokens_post_padded) {
+  DSV4_REQUIRE(tokens > 0 && topk > 0, "%s: route ids must be non-empty [tokens, topk]", who);
+  DSV4_REQUIRE(experts >= 1 && experts <= 1024, "%s: experts must be in [1, 1024]", who);
+  DSV4_REQUIRE(block_size > 0 && block_size <= 1024, "%s: bad block_size %d", who, block_size);
+  const int64_t a = tokens * topk;
+  DSV4_REQUIRE(a <= 0x7FFFFFFFLL, "%s: assignments exceed int32", who);
+  const int64_t cap = max_padded(a, experts, block_size);
+  DSV4_REQUIRE(cap <= 0x7FFFFFFFLL, "%s: capacity exceeds int32", who);
+  DSV4_REQUIRE(capacity == cap, "%s: capacity %lld != max_padded_tokens %lld", who, (long long)capacity,
+               (long long)cap);
+  DSV4_REQUIRE(num_blocks == (cap + block_size - 1) / block_size, "%s: expert_ids length mismatch", who);
+  DSV4_REQUIRE(ids && sorted_token_ids && expert_ids && num_tokens_post_padded, "%s: null pointer", who);
+  return DSV4MOE_OK;
+}
+
 int dsv4moe_align(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts,
                   int32_t block_size, int32_t* sorted_token_ids, int64_t capacity,
                   int32_t* expert_ids, int64_t num_blocks, int32_t* num_tokens_post_padded,
                   void* stream) {
   clear_error();
-  DSV4_REQUIRE(tokens > 0 && topk > 0, "align: route ids must be non-empty [tokens, topk]");
-  DSV4_REQUIRE(experts >= 1 && experts <= 1024, "align: experts must be in [1, 1024]");
-  DSV4_REQUIRE(block_size > 0 && block_size <= 1024, "align: bad block_size %d", block_size);
-  const int64_t a = tokens * topk;
-  DSV4_REQUIRE(a <= 0x7FFFFFFFLL, "align: assignments exceed int32");
-  const int64_t cap = max_padded(a, experts, block_size);
-  DSV4_REQUIRE(cap <= 0x7FFFFFFFLL, "align: capacity exceeds int32");
-  DSV4_REQUIRE(capacity == cap, "align: capacity %lld != max_padded_tokens %lld",
-               (long long)capacity, (long long)cap);
-  DSV4_REQUIRE(num_blocks == (cap + block_size - 1) / block_size, "align: expert_ids length mismatch");
-  DSV4_REQUIRE(ids && sorted_token_ids && expert_ids && num_tokens_post_padded, "align: null pointer");
-  return dsv4_launch_align(ids, a, experts, block_size, sorted_token_ids, capacity, expert_ids,
+  const int rc = validate_align("align", ids, tokens, topk, experts, block_size, sorted_token_ids, capacity,
+                                expert_ids, num_blocks, num_tokens_post_padded);
+  if (rc != DSV4MOE_OK) return rc;
+  return dsv4_launch_align(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
                            num_blocks, num_tokens_post_padded, static_cast<hipStream_t>(stream));
+}
+
+size_t dsv4moe_align_workspace_bytes(int64_t tokens, int32_t topk, int32_t experts) {
+  if (tokens <= 0 || topk <= 0 || experts < 1 || experts > 1024) return 0;
+  const int64_t a = tokens * topk;
+  return a >= kAlignMultiMinAssignments ? dsv4_align_scratch_bytes(a, experts) : 0;
+}
+
+int dsv4moe_align_ws(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts, int32_t block_size,
+                     int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids, int64_t num_blocks,
+                     int32_t* num_tokens_post_padded, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const int rc = validate_align("align_ws", ids, tokens, topk, experts, block_size, sorted_token_ids, capacity,
+                                expert_ids, num_blocks, num_tokens_post_padded);
+  if (rc != DSV4MOE_OK) return rc;
+  const size_t need = dsv4moe_align_workspace_bytes(tokens, topk, experts);
+  DSV4_REQUIRE(workspace_bytes >= need, "align_ws: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  DSV4_REQUIRE(need == 0 || (workspace && aligned(workspace, 4)), "align_ws: workspace must be 4-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (need == 0)
+    return dsv4_launch_align(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
+                             num_blocks, num_tokens_post_padded, s);
+  return dsv4_launch_align_multi(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
+                                 num_blocks, num_tokens_post_padded, static_cast<int32_t*>(workspace), nullptr,
+                                 tokens, 0, nullptr, s);
 }
 
 int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, int64_t batch,
@@ -443,9 +484,19 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
     dsv4host::prof_stamp(dsv4host::kStampRoute, s);
   }
   float* xsum = dsv4_experts_xsum(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0);
-  rc = dsv4_launch_prologue(route_in_prologue ? 1 : 0, logits, bias, tokens, experts, topk, score_func, route_scale,
-                            ids, weights, margin, block_size, sorted_token_ids, capacity, expert_ids, nblocks,
-                            num_tokens_post_padded, x, hidden, xsum, s);
+  if (tokens * topk >= kAlignMultiMinAssignments) {
+    // Many ids: the two-launch alignment, row sums beside the counting, its
+    // scratch in the (not yet used) contribution region of the workspace.
+    size_t room = 0;
+    int32_t* scratch = dsv4_experts_align_scratch(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0, &room);
+    DSV4_REQUIRE(room >= dsv4_align_scratch_bytes(tokens * topk, experts), "layer_w4a16: align scratch too small");
+    rc = dsv4_launch_align_multi(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
+                                 nblocks, num_tokens_post_padded, scratch, x, tokens, hidden, xsum, s);
+  } else {
+    rc = dsv4_launch_prologue(route_in_prologue ? 1 : 0, logits, bias, tokens, experts, topk, score_func,
+                              route_scale, ids, weights, margin, block_size, sorted_token_ids, capacity, expert_ids,
+                              nblocks, num_tokens_post_padded, x, hidden, xsum, s);
+  }
   if (rc != DSV4MOE_OK) return rc;
   if (route_in_prologue) dsv4host::prof_stamp(dsv4host::kStampRoute, s);
   dsv4host::prof_stamp(dsv4host::kStampAlign, s);

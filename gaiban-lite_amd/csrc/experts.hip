@@ -526,6 +526,16 @@ float* dsv4_experts_xsum(void* workspace, int64_t tokens, int topk, int hidden, 
   return carve_workspace(workspace, tokens, topk, hidden, inter, has_shared).xsum;
 }
 
+// Scratch for an alignment that runs before the experts: the contribution
+// region, which the experts path writes only after it has read the alignment.
+int32_t* dsv4_experts_align_scratch(void* workspace, int64_t tokens, int topk, int hidden, int inter,
+                                    int has_shared, size_t* bytes) {
+  const ExpertWorkspace w = carve_workspace(workspace, tokens, topk, hidden, inter, has_shared);
+  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
+  *bytes = sizeof(float) * (size_t)rows * hidden;
+  return reinterpret_cast<int32_t*>(w.contrib);
+}
+
 int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int inter,
                               int experts, int topk, const uint8_t* w13q, const uint16_t* w13s,
                               const uint8_t* w2q, const uint16_t* w2s, int has_shared,

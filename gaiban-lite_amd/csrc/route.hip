@@ -317,25 +317,7 @@ __global__ __launch_bounds__(kAlignThreads) void prologue_kernel(PrologueArgs a)
                 a.expert_ids, a.num_blocks, a.ntpp);
     return;
   }
-  const int chunks = a.hidden / 64;
-  const int64_t n = a.tokens * chunks;
-  for (int64_t idx = (int64_t)(blockIdx.x - 1) * kAlignThreads + threadIdx.x; idx < n;
-       idx += (int64_t)(gridDim.x - 1) * kAlignThreads) {
-    const int64_t r = idx / chunks;
-    const int c = (int)(idx % chunks);
-    const uint16_t* src = a.x + r * a.hidden + c * 64;
-    float sum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 64; e += 8) {
-      const u32x4 v = load16(src + e);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        sum += __uint_as_float(v[q] << 16);
-        sum += __uint_as_float(v[q] & 0xFFFF0000u);
-      }
-    }
-    a.xsum[idx] = sum;
-  }
+  row_sums_part(a.x, a.tokens, a.hidden, a.xsum, blockIdx.x - 1, gridDim.x - 1);
 }
 
 __global__ __launch_bounds__(256) void route_hash_kernel(

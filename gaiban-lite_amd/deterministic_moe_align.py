@@ -3,8 +3,10 @@
 Drop-in for ``runtime/dsv4_direct/deterministic_moe_align.py``: same dataclass,
 same capacity rule, same validation, same output layout (the public
 ``moe_align_block_size`` ABI).  The layout is computed by one workgroup of the
-HIP kernel ``align_kernel`` (ballot-ranked stable permutation), with no host
-read of route-dependent data.
+HIP kernel ``align_kernel`` (ballot-ranked stable permutation), or for many
+ids by the chunk-count and chunk-scatter kernels over a temporary scratch
+tensor (in place of the reference's torch temporaries), with no host read of
+route-dependent data.
 """
 
 from __future__ import annotations
@@ -81,6 +83,7 @@ def deterministic_moe_align_block_size(
         )
     _validate_output(output, topk_ids=topk_ids, block_size=block_size, num_experts=num_experts)
     ids = topk_ids if topk_ids.dtype == torch.int32 else topk_ids.to(torch.int32)
+    scratch_bytes = ops.align_workspace_bytes(ids.shape[0], ids.shape[1], num_experts)
     ops.align_into(
         ids,
         block_size=block_size,
@@ -88,6 +91,7 @@ def deterministic_moe_align_block_size(
         sorted_token_ids=output.sorted_token_ids,
         expert_ids=output.expert_ids,
         num_tokens_post_padded=output.num_tokens_post_padded,
+        workspace=(torch.empty(scratch_bytes, dtype=torch.uint8, device=ids.device) if scratch_bytes else None),
     )
     return output
 

@@ -664,10 +664,13 @@ class TP4MoE:
                     )
                 provider = self._owned_alignment_provider
                 if provider is None:
+                    # the experts workspace is idle until the experts launches, which
+                    # follow on the same stream: it holds the split alignment's scratch
                     ops.align_into(
                         route_ids, block_size=buffers.block_size_m, num_experts=cfg.experts,
                         sorted_token_ids=a.sorted_token_ids, expert_ids=a.expert_ids,
                         num_tokens_post_padded=a.num_tokens_post_padded,
+                        workspace=buffers.workspace,
                     )
                 else:
                     try:

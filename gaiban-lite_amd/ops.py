@@ -153,6 +153,12 @@ def gate_logits_into(x: torch.Tensor, weight: torch.Tensor, logits: torch.Tensor
          _lib.current_stream(dev))
 
 
+def align_workspace_bytes(tokens: int, topk: int, experts: int) -> int:
+    """Scratch bytes of the workgroup-split alignment (0: one workgroup aligns)."""
+
+    return int(_lib.load().dsv4moe_align_workspace_bytes(tokens, topk, experts))
+
+
 def align_into(
     ids: torch.Tensor,
     *,
@@ -161,17 +167,30 @@ def align_into(
     sorted_token_ids: torch.Tensor,
     expert_ids: torch.Tensor,
     num_tokens_post_padded: torch.Tensor,
+    workspace: torch.Tensor | None = None,
 ) -> None:
+    """Deterministic alignment; with a ``workspace`` of at least
+    ``align_workspace_bytes`` bytes, many ids are aligned by the
+    workgroup-split kernels (same output bits)."""
+
     tokens, topk = ids.shape
     dev = ids.device
     _check("topk_ids", ids, dtype=torch.int32, device=dev)
     _check("sorted_token_ids", sorted_token_ids, dtype=torch.int32, device=dev)
     _check("expert_ids", expert_ids, dtype=torch.int32, device=dev)
     _check("num_tokens_post_padded", num_tokens_post_padded, dtype=torch.int32, shape=(1,), device=dev)
+    if workspace is None:
+        call(
+            "dsv4moe_align", ptr(ids), tokens, topk, num_experts, block_size, ptr(sorted_token_ids),
+            sorted_token_ids.numel(), ptr(expert_ids), expert_ids.numel(),
+            ptr(num_tokens_post_padded), _lib.current_stream(dev),
+        )
+        return
+    _check("workspace", workspace, dtype=torch.uint8, device=dev)
     call(
-        "dsv4moe_align", ptr(ids), tokens, topk, num_experts, block_size, ptr(sorted_token_ids),
+        "dsv4moe_align_ws", ptr(ids), tokens, topk, num_experts, block_size, ptr(sorted_token_ids),
         sorted_token_ids.numel(), ptr(expert_ids), expert_ids.numel(),
-        ptr(num_tokens_post_padded), _lib.current_stream(dev),
+        ptr(num_tokens_post_padded), ptr(workspace), workspace.numel(), _lib.current_stream(dev),
     )
 
 

@@ -137,6 +137,22 @@ int dsv4moe_align(const int32_t* ids, int64_t tokens, int32_t topk, int32_t expe
                   void* stream);
 
 /*
+ * The same alignment (same outputs, bit for bit) split over workgroups when
+ * tokens * topk >= 8192: one launch counts chunks of the ids into the
+ * workspace, a second scatters each chunk from the summed counts.  The
+ * workspace replaces the reference's torch temporaries of
+ * deterministic_moe_align_block_size (deterministic_moe_align.py:95-106); its
+ * size is dsv4moe_align_workspace_bytes (0 below the split threshold, then the
+ * call is dsv4moe_align and workspace may be NULL; at most 262400 bytes).
+ * The workspace needs no initial contents.
+ */
+size_t dsv4moe_align_workspace_bytes(int64_t tokens, int32_t topk, int32_t experts);
+int dsv4moe_align_ws(const int32_t* ids, int64_t tokens, int32_t topk, int32_t experts,
+                     int32_t block_size, int32_t* sorted_token_ids, int64_t capacity,
+                     int32_t* expert_ids, int64_t num_blocks, int32_t* num_tokens_post_padded,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Repack int4 group-128 weights from the checkpoint layout into the
  * pair-interleaved tiled layout the expert kernels stream.  Replaces the
  * load-time Marlin repack (runtime/dsv4_direct/ops/marlin_moe.py:173-223).

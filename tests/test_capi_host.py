@@ -71,6 +71,31 @@ def test_validation_rejects_before_launch():
                                   ws - 1, None)
 
 
+def test_align_workspace_policy_and_validation():
+    """The split alignment needs [chunks][experts + 1] int32 of scratch, chunks
+    of >= 4096 ids (multiples of 1024), at most 64 chunks; below 8192 ids one
+    workgroup aligns and no scratch is needed."""
+
+    lib = _lib.load()
+    assert lib.dsv4moe_align_workspace_bytes(1365, 6, 256) == 0        # 8190 ids
+    assert lib.dsv4moe_align_workspace_bytes(1024, 8, 256) == 2 * 257 * 4   # 8192 ids: 2 x 4096
+    assert lib.dsv4moe_align_workspace_bytes(8192, 6, 256) == 12 * 257 * 4  # 49152 ids: 12 x 4096
+    assert lib.dsv4moe_align_workspace_bytes(2049, 6, 8) == 4 * 9 * 4       # 12294 ids: 4 x 4096 (last ragged)
+    assert lib.dsv4moe_align_workspace_bytes(1 << 20, 8, 1024) == 64 * 1025 * 4  # capped at 64 chunks
+    assert lib.dsv4moe_align_workspace_bytes(0, 6, 256) == 0
+    fake = ctypes.c_void_p(0x1000)
+    t, k, e, bs = 8192, 6, 256, 64
+    cap = O.max_padded_tokens(t * k, e, bs)
+    nb = (cap + bs - 1) // bs
+    need = lib.dsv4moe_align_workspace_bytes(t, k, e)
+    assert "workspace" in _einval("dsv4moe_align_ws", fake, t, k, e, bs, fake, cap, fake, nb, fake,
+                                  fake, need - 1, None)
+    assert "workspace" in _einval("dsv4moe_align_ws", fake, t, k, e, bs, fake, cap, fake, nb, fake,
+                                  None, need, None)
+    assert "capacity" in _einval("dsv4moe_align_ws", fake, t, k, e, bs, fake, cap - 1, fake, nb, fake,
+                                 fake, need, None)
+
+
 def test_w8a16_validation_and_split_policy():
     fake = ctypes.c_void_p(0x1000)
     lib = _lib.load()

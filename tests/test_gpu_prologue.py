@@ -1,8 +1,10 @@
 """The fused layer entry point (``dsv4moe_layer_w4a16``), whose prologue launch
 aligns the route ids and sums the activation rows in one launch, and for
 T <= 16 also routes (one workgroup routes every token and aligns the ids it
-wrote; the others sum the activation rows).  Token counts on both sides of
-that threshold, three score functions, 8 / 256 / 1024 experts.
+wrote; the others sum the activation rows); from 8192 route ids on, the
+alignment is split over workgroups (chunk counts beside the row sums, then
+chunk scatters).  Token counts on both sides of both thresholds, three score
+functions, 8 / 256 / 1024 experts.
 
 Checked bit for bit against the oracle's router (``model.py:564-584``,
 ``moe_forward.py:80-87``) and closed-form alignment
@@ -109,3 +111,17 @@ def test_layer_entry_1024_experts(tokens):
     shape = S.LayerShape(experts=1024, hidden=512, inter=512, topk=8, has_shared=True)
     print(f"[prologue] E=1024 k=8 T={tokens}", flush=True)
     check(*run_layer(shape, tokens, "sigmoid", seed=300 + tokens))
+
+
+@pytest.mark.parametrize("shape,tokens", [
+    (S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True), 1366),
+    (S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True), 3000),
+    (S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True), 4096),
+])
+def test_layer_entry_split_alignment(shape, tokens):
+    """tokens * topk >= 8192: the layer aligns with the two-launch split (row
+    sums beside the chunk counts, scratch in the workspace's contribution
+    region); the staged chain aligns in one workgroup.  Same bits."""
+
+    print(f"[prologue] split align E={shape.experts} k={shape.topk} T={tokens}", flush=True)
+    check(*run_layer(shape, tokens, "sqrtsoftplus", seed=400 + tokens, route_scale=2.5, clamp=10.0))
