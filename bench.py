@@ -242,6 +242,7 @@ def main() -> int:
         secondary["fp8_shared"] = bench_shared_fp8(pkg, gate, cfg, dev, T, args)
         secondary["w8a16_linear"] = bench_w8a16(pkg, dev)
         secondary["w8a16_fp8_block_linear"] = bench_w8a16(pkg, dev, fmt="fp8")
+        secondary["w8a8_block_fp8_linear"] = bench_block_fp8(pkg, dev)
 
     # ------------------------------------------------------------ CPU baseline
     cpu = None
@@ -551,6 +552,52 @@ def bench_w8a16(pkg, dev, fmt="int8"):
             out[f"M{m}_N{n}"] = entry
             log(f"[bench] w8a16 {fmt} M={m} N={n}: {entry}")
             del a, o, ws
+        del prep
+    return out
+
+
+def bench_block_fp8(pkg, dev):
+    """Block-FP8 W8A8 dense linear (fp8_linear.py): K = 4096, N in {4096, 1024,
+    16384}, M in {1, 64, 8192}; the bf16 -> E4M3 activation quantiser and the
+    GEMM timed separately (the reference launches them separately)."""
+
+    import torch
+
+    F = pkg.fp8_linear
+    L = pkg.weight_only_linear
+    S = pkg.synthetic
+    out = {}
+    k = 4096
+    for n in (4096, 1024, 16384):
+        q, s = S.make_fp8_block_linear(n, k, device=dev)
+        prep = L.prepare_fp8_block_weight(q, s)
+        del q
+        for m in (1, 64, 8192):
+            x = S.make_hidden(m, k, seed=7000 + m, device=dev)
+            qp = F.make_quantization_plan(m, k)
+            aq = torch.empty(qp.quantized_shape, dtype=F.FP8_DTYPE, device=dev)
+            a_s = torch.empty(qp.scale_shape, dtype=F.E8M0_DTYPE, device=dev)
+            plan = F.make_gemm_plan(m, n, k)
+            o = torch.empty(plan.output_shape, dtype=torch.bfloat16, device=dev)
+            ws = torch.empty(plan.workspace_shape, dtype=torch.float32, device=dev)
+            it = 50 if m < 8192 else 10
+            quant = lambda i: F.activation_quant_into(x, aq, a_s, plan=qp)
+            gemm = lambda i: F.block_fp8_gemm_into(aq, a_s, prep, None, o, ws, plan=plan)
+            for _ in range(3):
+                quant(0)
+                gemm(0)
+            q_ms = cuda_timer(quant, it)
+            ms = cuda_timer(gemm, it)
+            byts = n * k + prep.scale.numel() + m * k + m * (k // 128) + 2 * m * n
+            fl = 2.0 * m * n * k
+            entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2), "quant_us": round(q_ms * 1e3, 2),
+                     "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+            entry["frac_of_peak"] = (round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if m <= 64
+                                     else round(fl / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4))
+            entry["bound"] = "hbm" if m <= 64 else "mfma (fp8)"
+            out[f"M{m}_N{n}"] = entry
+            log(f"[bench] w8a8 block fp8 M={m} N={n}: {entry}")
+            del x, aq, a_s, o, ws
         del prep
     return out
 

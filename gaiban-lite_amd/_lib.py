@@ -46,6 +46,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_gate_logits": (ctypes.c_int, [_p, _p, _i64, _i32, _i32, _p, _p]),
     "dsv4moe_align": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p]),
     "dsv4moe_align_workspace_bytes": (_sz, [_i64, _i32, _i32]),
+    "dsv4moe_act_quant_block_fp8": (ctypes.c_int, [_p, _i32, _i64, _i64, _p, _p, _p]),
+    "dsv4moe_block_fp8_split_k": (_i32, [_i64, _i64, _i64]),
+    "dsv4moe_block_fp8_workspace_bytes": (_sz, [_i64, _i64, _i32]),
+    "dsv4moe_block_fp8_gemm": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),
     "dsv4moe_align_ws": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _sz, _p]),
     "dsv4moe_pack_int4_g128": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p]),
     "dsv4moe_experts_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),

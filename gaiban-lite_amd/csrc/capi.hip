@@ -105,6 +105,10 @@ int dsv4_launch_experts_w4a8(const uint16_t*, int64_t, int, int, int, int, const
                              const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
                              uint16_t*, void*, hipStream_t);
 int32_t dsv4_w8a16_split_k(int64_t, int64_t, int64_t);
+int32_t dsv4_block_fp8_split_k(int64_t, int64_t, int64_t);
+int dsv4_launch_act_quant_block_fp8(const void*, int32_t, int64_t, int64_t, uint8_t*, uint8_t*, hipStream_t);
+int dsv4_launch_block_fp8_gemm(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, const uint8_t*,
+                               const uint8_t*, int32_t, float*, uint16_t*, hipStream_t);
 size_t dsv4_w8a16_workspace_bytes(int64_t, int64_t, int32_t);
 int dsv4_launch_pack_int8(const int8_t*, int64_t, int64_t, uint8_t*, hipStream_t);
 int dsv4_launch_w8a16(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, const uint16_t*,
@@ -568,6 +572,53 @@ int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k,
   DSV4_REQUIRE(k <= 32768, "w8a16_fp8_linear: k must be <= 32768, got %lld", (long long)k);
   return dsv4_launch_w8a16(a, m, n, k, wq, nullptr, ws8, split_k, workspace, out,
                            static_cast<hipStream_t>(stream), 0);
+}
+
+int32_t dsv4moe_block_fp8_split_k(int64_t m, int64_t n, int64_t k) { return dsv4_block_fp8_split_k(m, n, k); }
+
+size_t dsv4moe_block_fp8_workspace_bytes(int64_t m, int64_t n, int32_t split_k) {
+  if (m <= 0 || n <= 0 || split_k <= 1) return 0;
+  return (size_t)split_k * (size_t)m * (size_t)n * sizeof(float);
+}
+
+int dsv4moe_act_quant_block_fp8(const void* x, int32_t x_dtype, int64_t m, int64_t k, uint8_t* q, uint8_t* scale,
+                                void* stream) {
+  clear_error();
+  DSV4_REQUIRE(x_dtype >= 0 && x_dtype <= 2, "act_quant_block_fp8: x_dtype must be 0 (bf16), 1 (fp16) or 2 (fp32)");
+  DSV4_REQUIRE(m >= 0, "act_quant_block_fp8: m must be >= 0");
+  DSV4_REQUIRE(k > 0 && k % 128 == 0, "act_quant_block_fp8: k must be a positive multiple of 128, got %lld",
+               (long long)k);
+  DSV4_REQUIRE(m * (k / 128) * 16 < (int64_t)1 << 38, "act_quant_block_fp8: m * k too large");
+  if (m == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(x && q && scale, "act_quant_block_fp8: null pointer");
+  DSV4_REQUIRE(aligned(x, 16) && aligned(q, 8), "act_quant_block_fp8: x 16-byte, q 8-byte aligned");
+  return dsv4_launch_act_quant_block_fp8(x, x_dtype, m, k, q, scale, static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_block_fp8_gemm(const uint8_t* a, const uint8_t* a_scale, int64_t m, int64_t n, int64_t k,
+                           const uint8_t* wq, const uint8_t* w_scale, int32_t split_k, float* workspace,
+                           size_t workspace_bytes, uint16_t* out, void* stream) {
+  clear_error();
+  const char* who = "block_fp8_gemm";
+  DSV4_REQUIRE(m >= 0, "%s: m must be >= 0", who);
+  DSV4_REQUIRE(n > 0 && n % 16 == 0, "%s: n must be a positive multiple of 16, got %lld", who, (long long)n);
+  DSV4_REQUIRE(k > 0 && k % 128 == 0 && k <= 32768, "%s: k must be a multiple of 128 in [128, 32768], got %lld", who,
+               (long long)k);
+  DSV4_REQUIRE(split_k == 1 || split_k == 2 || split_k == 4 || split_k == 8,
+               "%s: split_k must be one of 1, 2, 4, 8, got %d", who, split_k);
+  DSV4_REQUIRE(split_k <= k / 128, "%s: split_k=%d exceeds K-block count %lld", who, split_k, (long long)(k / 128));
+  DSV4_REQUIRE(m * k < (int64_t)1 << 31 && n * k < (int64_t)1 << 31, "%s: m*k and n*k must be below 2^31", who);
+  if (m == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(a && a_scale && wq && w_scale && out, "%s: null pointer", who);
+  DSV4_REQUIRE(aligned(a, 16) && aligned(wq, 16) && aligned(out, 8),
+               "%s: a and wq must be 16-byte aligned, out 8-byte aligned", who);
+  const size_t need = dsv4moe_block_fp8_workspace_bytes(m, n, split_k);
+  DSV4_REQUIRE(workspace_bytes >= need, "%s: workspace of %zu bytes is below the %zu needed", who, workspace_bytes,
+               need);
+  DSV4_REQUIRE(need == 0 || (workspace && aligned(workspace, 16)), "%s: split_k > 1 needs a 16-byte aligned workspace",
+               who);
+  return dsv4_launch_block_fp8_gemm(a, a_scale, m, n, k, wq, w_scale, split_k, workspace, out,
+                                    static_cast<hipStream_t>(stream));
 }
 
 size_t dsv4moe_shared_fp8_workspace_bytes(int64_t tokens, int32_t hidden, int32_t inter) {

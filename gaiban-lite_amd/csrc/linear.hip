@@ -1,4 +1,6 @@
-// W8A16 dense linear for gfx950: C[M,N] = bf16( A[M,K] . W[N,K]^T ), A bf16,
+// Dense linears for gfx950 over 1-byte weights.
+//
+// W8A16: C[M,N] = bf16( A[M,K] . W[N,K]^T ), A bf16,
 // fp32 accumulation, with W in one of two formats:
 //   * int8 symmetric per output channel, W = Q * s[n] (s bf16);
 //   * FP8 E4M3 with one E8M0 scale per 128 x 128 block, W = Q * 2^(e-127),
@@ -328,6 +330,271 @@ __global__ __launch_bounds__(256) void pack_int8_kernel(const uint8_t* src, int6
   *reinterpret_cast<u32x4*>(dst + c * 16) = *reinterpret_cast<const u32x4*>(src + row * k + col);
 }
 
+// ------------------------------------------------------------ block-FP8 W8A8
+// Restates runtime/dsv4_direct/fp8_linear.py:354-497: activations quantised
+// per row and 128-K block to E4M3 with a power-of-two E8M0 scale, weights in
+// the checkpoint's E4M3 / E8M0 128 x 128 block format, and per K block
+// C += (A_blk . W_blk^T) * 2^(ea-127) * 2^(ew-127) in fp32, one bf16 rounding
+// (split-K: fp32 partials reduced in split order).  gfx950 applies both block
+// scales inside the MFMA: v_mfma_scale_f32_16x16x128_f8f6f4 takes one E8M0
+// byte per lane for its row of A (weights: the row block's scale, uniform over
+// the wavefront) and its column of B (tokens: the token's scale), so the MFMA
+// adds exactly 2^(ea-127) * 2^(ew-127) times the block dot product.
+
+typedef __attribute__((ext_vector_type(8))) int i32x8;
+
+__device__ __forceinline__ f32x4 mfma_fp8_block(i32x8 w, i32x8 t, f32x4 c, int scale_w, int scale_t) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w, t, c, 0, 0, 0, scale_w, 0, scale_t);
+}
+
+// Activation quantiser (fp8_linear.py:354-392): per row and 128-K block,
+// s = max(amax, 1e-4) * fp32(1/448); its E8M0 exponent is rounded up to a
+// power of two (biased exponent + 1 when the mantissa is nonzero, clamped to
+// [1, 254]); q = e4m3(clamp(x / 2^(e-127), -448, 448)) (round to nearest
+// even).  16 lanes per block, 8 K values per lane; X is bf16 (0), fp16 (1) or
+// fp32 (2).
+template <int X>
+__device__ __forceinline__ void load_act8(const void* x, int64_t idx, float (&f)[8]) {
+  if constexpr (X == 2) {
+    const u32x4 a = load16(static_cast<const float*>(x) + idx);
+    const u32x4 b = load16(static_cast<const float*>(x) + idx + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[e] = __uint_as_float(a[e]);
+      f[4 + e] = __uint_as_float(b[e]);
+    }
+  } else {
+    const u32x4 v = load16(static_cast<const uint16_t*>(x) + idx);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (X == 0) {
+        f[2 * e] = __uint_as_float(v[e] << 16);
+        f[2 * e + 1] = __uint_as_float(v[e] & 0xFFFF0000u);
+      } else {
+        f[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v[e] & 0xFFFFu));
+        f[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(v[e] >> 16));
+      }
+    }
+  }
+}
+
+template <int X>
+__global__ __launch_bounds__(256) void act_quant_block_fp8_kernel(const void* __restrict__ x, int64_t m, int k,
+                                                                  uint8_t* __restrict__ q,
+                                                                  uint8_t* __restrict__ scale) {
+  const int kblocks = k / 128;
+  const int64_t blk = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // (row, K block)
+  if (blk >= m * kblocks) return;  // 16-lane groups leave together
+  const int sub = threadIdx.x & 15;
+  const int64_t row = blk / kblocks;
+  const int kb = (int)(blk % kblocks);
+  const int64_t idx = row * k + kb * 128 + sub * 8;
+  float f[8];
+  load_act8<X>(x, idx, f);
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  const uint32_t bits = __float_as_uint(fmaxf(amax, 1.0e-4f) * (1.0f / 448.0f));
+  int e8 = (int)((bits >> 23) & 0xFF) + ((bits & 0x7FFFFF) != 0 ? 1 : 0);
+  e8 = min(254, max(1, e8));
+  const float s = __uint_as_float((uint32_t)e8 << 23);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / s, -448.0f), 448.0f);
+  int lo = 0, hi = 0;
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], lo, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], lo, true);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4], f[5], hi, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6], f[7], hi, true);
+  *reinterpret_cast<u32x2*>(q + idx) = u32x2{(uint32_t)lo, (uint32_t)hi};
+  if (sub == 0) scale[row * kblocks + kb] = (uint8_t)e8;
+}
+
+struct BlockFp8Params {
+  const uint8_t* a;    // E4M3 [M][K], row-major
+  const uint8_t* as;   // E8M0 [M][K/128]
+  int64_t m;
+  int n;
+  int k;
+  const uint8_t* wq;   // E4M3 in 1 KiB tiles (16 rows x 64 K)
+  const uint8_t* ws8;  // E8M0 [ceil(N/128)][K/128]
+  int kblocks;
+  int split;
+  int kb_per_split;
+  int tiles_n;
+  int tiles_m;
+  uint16_t* out;
+  float* partial;      // [split][M][N] when split > 1
+};
+
+// Workgroup tile: 64*R output channels x 16*C tokens over one K split, one
+// 128-K block per step.  Per step, buffer_load ... lds copies the token tile
+// (16C rows x 128 B, part q of row t at q ^ swz128(t)) and each wavefront's R
+// weight strips (two 1 KiB tiles each: K windows 2kb and 2kb+1) into LDS,
+// double buffered.  A lane's 32-byte MFMA operand is K 16j..16j+15 and
+// 64+16j..64+16j+15 of the block (j = lane/16) for both operands.
+template <int R, int C>
+__global__ __launch_bounds__(256, 2) void w8a8_block_kernel(BlockFp8Params p) {
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * C * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * 2048];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  // XCD-aware item order, as in w8a16_kernel
+  const int items = p.split * p.tiles_m * p.tiles_n;
+  const int per_xcd = (items + kLinXcds - 1) / kLinXcds;
+  const int item = (blockIdx.x % kLinXcds) * per_xcd + blockIdx.x / kLinXcds;
+  if (item >= items) return;
+  const int tn = item % p.tiles_n;
+  const int tm = (item / p.tiles_n) % p.tiles_m;
+  const int sp = item / (p.tiles_n * p.tiles_m);
+
+  const int kb_begin = sp * p.kb_per_split;
+  const int kb_end = min(p.kblocks, kb_begin + p.kb_per_split);
+  const int nk = kb_end - kb_begin;  // may be 0 for a trailing split: it writes zeros
+  const int wins = p.k / kWin;
+  const int strips = p.n >> 4;
+  const int strip0 = tn * 4 * R + wave * R;
+
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.a, (short)0, (int)(p.m * p.k), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wq, (short)0, (int)((int64_t)p.n * p.k), kLinRsrcFlags);
+
+  constexpr int kActDma = 2 * C;
+  constexpr int kActPerWave = (kActDma + 3) / 4;
+  uint32_t a_off[kActPerWave];
+#pragma unroll
+  for (int i = 0; i < kActPerWave; ++i) {
+    const int q = wave + 4 * i;
+    const int row = q * 8 + (lane >> 3);
+    const int64_t tok = (int64_t)tm * 16 * C + row;
+    const int part = (lane & 7) ^ swz128(row);
+    a_off[i] = (q < kActDma && tok < p.m) ? (uint32_t)(tok * p.k + part * 16) : kLinOob;
+  }
+  uint32_t w_off[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+  // the wavefront's R strips lie in one 128-row scale block (R divides 8);
+  // lane i holds the E8M0 bytes of K blocks i, 64 + i, 128 + i, 192 + i
+  uint32_t srow[4] = {0, 0, 0, 0};
+  {
+    const uint8_t* row = p.ws8 + (int64_t)(min(strip0, strips - 1) >> 3) * p.kblocks;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (64 * q + lane < p.kblocks) srow[q] = row[64 * q + lane];
+  }
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+  // activation scale rows of this lane's tokens (127 = 2^0 past the last token)
+  const uint8_t* srow_t[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int64_t tok = (int64_t)tm * 16 * C + c * 16 + n16;
+    srow_t[c] = tok < p.m ? p.as + tok * p.kblocks : nullptr;
+  }
+
+  auto issue = [&](int kb, int buf) {
+#pragma unroll
+    for (int i = 0; i < kActPerWave; ++i) {
+      const int q = wave + 4 * i;
+      if (q < kActDma) lds_dma16(a_rsrc, (lds_void_ptr)&xs[buf][q * 1024], a_off[i], kb * 128);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 2048], w_off[r], (2 * kb) * 1024);
+      lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 2048 + 1024], w_off[r], (2 * kb + 1) * 1024);
+    }
+  };
+
+  f32x4 acc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto step = [&](int kb, auto u_c, auto pf_c) {
+    constexpr int u = decltype(u_c)::value;
+    int st[C];  // token scales, loaded before this step's prefetch is issued
+#pragma unroll
+    for (int c = 0; c < C; ++c) st[c] = srow_t[c] != nullptr ? (int)srow_t[c][kb] : 127;
+    if constexpr (decltype(pf_c)::value) issue(kb + 1, u ^ 1);
+    const uint32_t word = kb < 64 ? srow[0] : (kb < 128 ? srow[1] : (kb < 192 ? srow[2] : srow[3]));
+    const int sw = __builtin_amdgcn_readlane((int)word, kb & 63);
+    i32x8 wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * 2048 + lane * 16]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * 2048 + 1024 + lane * 16]);
+      wv[r] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int row = c * 16 + n16;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((j ^ swz128(row)) * 16)]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + (((4 + j) ^ swz128(row)) * 16)]);
+      const i32x8 tv = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][c] = mfma_fp8_block(wv[r], tv, acc[r][c], sw, st[c]);
+    }
+    __syncthreads();
+  };
+  using U0 = std::integral_constant<int, 0>;
+  using U1 = std::integral_constant<int, 1>;
+  using PF = std::true_type;
+  using NOPF = std::false_type;
+
+  if (nk > 0) {
+    issue(kb_begin, 0);
+    __syncthreads();
+    int i = 0;
+    for (; i + 2 < nk; i += 2) {
+      step(kb_begin + i, U0{}, PF{});
+      step(kb_begin + i + 1, U1{}, PF{});
+    }
+    // the last step issues no prefetch, so no LDS DMA is in flight at exit
+    if (nk - i == 2) {
+      step(kb_begin + i, U0{}, PF{});
+      step(kb_begin + i + 1, U1{}, NOPF{});
+    } else {
+      step(kb_begin + i, U0{}, NOPF{});
+    }
+  }
+
+  // epilogue: lane holds channels 16*strip + 4*j + (0..3) of token c*16 + n16
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int strip = strip0 + r;
+    if (strip >= strips) continue;
+    const int n = strip * 16 + 4 * j;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t tok = (int64_t)tm * 16 * C + c * 16 + n16;
+      if (tok >= p.m) continue;
+      const float v[4] = {acc[r][c][0], acc[r][c][1], acc[r][c][2], acc[r][c][3]};
+      if (p.split == 1) {
+        uint16_t* dst = p.out + tok * p.n + n;
+        *reinterpret_cast<u32x2*>(dst) = finish_bf16x4(v, dst, false);
+      } else {
+        float* dst = p.partial + ((int64_t)sp * p.m + tok) * p.n + n;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+      }
+    }
+  }
+}
+
+static void launch_w8a8_block_kernel(const BlockFp8Params& p, int r, int c, hipStream_t stream) {
+  const int items = p.split * p.tiles_m * p.tiles_n;
+  const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
+  if (r == 2 && c == 8) hipLaunchKernelGGL((w8a8_block_kernel<2, 8>), grid, dim3(256), 0, stream, p);
+  else if (r == 4 && c == 4) hipLaunchKernelGGL((w8a8_block_kernel<4, 4>), grid, dim3(256), 0, stream, p);
+  else if (c == 1) hipLaunchKernelGGL((w8a8_block_kernel<2, 1>), grid, dim3(256), 0, stream, p);
+  else if (c == 2) hipLaunchKernelGGL((w8a8_block_kernel<2, 2>), grid, dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL((w8a8_block_kernel<2, 4>), grid, dim3(256), 0, stream, p);
+}
+
 template <bool FP8>
 static void launch_w8a16_kernel(const LinearParams& p, int r, int c, hipStream_t stream) {
   const int items = p.split * p.tiles_m * p.tiles_n;
@@ -412,6 +679,73 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
     const int64_t quads = m * n / 4;
     hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
                        workspace, split, m * n, out, accumulate);
+    DSV4_CHECK_LAUNCH("split_reduce_kernel");
+  }
+  return DSV4MOE_OK;
+}
+
+// Block-FP8 W8A8 geometry: (R, C) = (2, 1 | 2 | 4) up to 64 tokens, then
+// 128 channels x 128 tokens; split-K widened (powers of two up to 8, >= 2 K
+// blocks per split) while the grid is below 512 workgroups.
+static void w8a8_geometry(int64_t m, int* r, int* c) {
+  *r = 2;
+  if (m <= 16) *c = 1;
+  else if (m <= 32) *c = 2;
+  else if (m <= 64) *c = 4;
+  else *c = 8;
+}
+
+int32_t dsv4_block_fp8_split_k(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return -1;
+  int r, c;
+  w8a8_geometry(m, &r, &c);
+  const int64_t tiles = ((n + 64 * r - 1) / (64 * r)) * ((m + 16 * c - 1) / (16 * c));
+  const int64_t kblocks = k / 128;
+  int split = 1;
+  while (split < 8 && tiles * split < 512 && kblocks / (split * 2) >= 2) split *= 2;
+  return split;
+}
+
+int dsv4_launch_act_quant_block_fp8(const void* x, int32_t x_dtype, int64_t m, int64_t k, uint8_t* q, uint8_t* scale,
+                                    hipStream_t stream) {
+  const int64_t threads = m * (k / 128) * 16;
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if (x_dtype == 0)
+    hipLaunchKernelGGL(act_quant_block_fp8_kernel<0>, grid, dim3(256), 0, stream, x, m, (int)k, q, scale);
+  else if (x_dtype == 1)
+    hipLaunchKernelGGL(act_quant_block_fp8_kernel<1>, grid, dim3(256), 0, stream, x, m, (int)k, q, scale);
+  else
+    hipLaunchKernelGGL(act_quant_block_fp8_kernel<2>, grid, dim3(256), 0, stream, x, m, (int)k, q, scale);
+  DSV4_CHECK_LAUNCH("act_quant_block_fp8_kernel");
+  return DSV4MOE_OK;
+}
+
+int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, int64_t n, int64_t k,
+                               const uint8_t* wq, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
+                               hipStream_t stream) {
+  int r, c;
+  w8a8_geometry(m, &r, &c);
+  BlockFp8Params p;
+  p.a = a;
+  p.as = as;
+  p.m = m;
+  p.n = (int)n;
+  p.k = (int)k;
+  p.wq = wq;
+  p.ws8 = ws8;
+  p.kblocks = (int)(k / 128);
+  p.split = split;
+  p.kb_per_split = (p.kblocks + split - 1) / split;
+  p.tiles_n = (int)((n + 64 * r - 1) / (64 * r));
+  p.tiles_m = (int)((m + 16 * c - 1) / (16 * c));
+  p.out = out;
+  p.partial = workspace;
+  launch_w8a8_block_kernel(p, r, c, stream);
+  DSV4_CHECK_LAUNCH("w8a8_block_kernel");
+  if (split > 1) {
+    const int64_t quads = m * n / 4;
+    hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
+                       workspace, split, m * n, out, 0);
     DSV4_CHECK_LAUNCH("split_reduce_kernel");
   }
   return DSV4MOE_OK;

@@ -438,6 +438,61 @@ def w8a16_fp8_linear_into(a: torch.Tensor, wq: torch.Tensor, ws8: torch.Tensor, 
          ws_bytes, ptr(out), _lib.current_stream(dev))
 
 
+_X_DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def act_quant_block_fp8_into(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor) -> None:
+    """Per-row, per-128-K block E4M3 quantisation with E8M0 power-of-two
+    scales (``dsv4moe_act_quant_block_fp8``); q uint8 [m, k], scale uint8
+    [m, k/128]."""
+
+    if x.ndim != 2:
+        raise ValueError("x must be [m, k]")
+    if x.dtype not in _X_DTYPE_CODES:
+        raise TypeError(f"x must be bfloat16, float16 or float32, got {x.dtype}")
+    m, k = x.shape
+    dev = x.device
+    _check("x", x, dtype=x.dtype, device=dev)
+    _check("quantized_out", q, dtype=torch.uint8, shape=(m, k), device=dev)
+    _check("scale_out", scale, dtype=torch.uint8, shape=(m, k // 128), device=dev)
+    call("dsv4moe_act_quant_block_fp8", ptr(x), _X_DTYPE_CODES[x.dtype], m, k, ptr(q), ptr(scale),
+         _lib.current_stream(dev))
+
+
+def block_fp8_split_k(m: int, n: int, k: int) -> int:
+    split = int(_lib.load().dsv4moe_block_fp8_split_k(m, n, k))
+    if split < 1:
+        raise ValueError("m, n and k must be positive")
+    return split
+
+
+def block_fp8_workspace_bytes(m: int, n: int, split_k: int) -> int:
+    return int(_lib.load().dsv4moe_block_fp8_workspace_bytes(m, n, split_k))
+
+
+def block_fp8_gemm_into(a: torch.Tensor, a_scale: torch.Tensor, wq: torch.Tensor, ws8: torch.Tensor,
+                        out: torch.Tensor, workspace: torch.Tensor | None, *, n: int, split_k: int) -> None:
+    """Block-FP8 W8A8 GEMM (``dsv4moe_block_fp8_gemm``): a E4M3 uint8 [m, k]
+    with E8M0 a_scale [m, k/128]; wq the ``pack_fp8`` tiles of W [n, k] with
+    E8M0 ws8 [ceil(n/128), k/128]; out bf16 [m, n]."""
+
+    if a.ndim != 2:
+        raise ValueError("activation must be [m, k]")
+    m, k = a.shape
+    dev = a.device
+    _check("activation", a, dtype=torch.uint8, device=dev)
+    _check("activation_scale", a_scale, dtype=torch.uint8, shape=(m, k // 128), device=dev)
+    _check("weight", wq, dtype=torch.uint8, shape=(n * k,), device=dev)
+    _check("weight_scale", ws8, dtype=torch.uint8, shape=((n + 127) // 128, k // 128), device=dev)
+    _check("out", out, dtype=torch.bfloat16, shape=(m, n), device=dev)
+    ws_bytes = 0
+    if workspace is not None:
+        _check("workspace", workspace, dtype=torch.float32, device=dev)
+        ws_bytes = workspace.numel() * 4
+    call("dsv4moe_block_fp8_gemm", ptr(a), ptr(a_scale), m, n, k, ptr(wq), ptr(ws8), int(split_k),
+         ptr(workspace), ws_bytes, ptr(out), _lib.current_stream(dev))
+
+
 def shared_fp8_workspace_bytes(tokens: int, hidden: int, inter: int) -> int:
     return int(_lib.load().dsv4moe_shared_fp8_workspace_bytes(tokens, hidden, inter))
 

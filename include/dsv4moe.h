@@ -301,6 +301,39 @@ int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k,
                              uint16_t* out, void* stream);
 
 /*
+ * Block-FP8 W8A8 activation quantiser.  Replaces activation_quant_into
+ * (runtime/dsv4_direct/fp8_linear.py:523-569, kernel :354-392).
+ *   x      [m, k] row-major, x_dtype 0 = bf16, 1 = fp16, 2 = fp32
+ *   q      E4M3 bytes [m, k] row-major (out)
+ *   scale  E8M0 bytes [m, k/128] (out): per row and 128-K block,
+ *          e = ceil-to-power-of-two exponent of max(amax, 1e-4) * fp32(1/448),
+ *          clamped to [1, 254]; q = e4m3(clamp(x / 2^(e-127), -448, 448))
+ * k a multiple of 128.
+ */
+int dsv4moe_act_quant_block_fp8(const void* x, int32_t x_dtype, int64_t m, int64_t k, uint8_t* q,
+                                uint8_t* scale, void* stream);
+
+/*
+ * Block-FP8 W8A8 GEMM.  Replaces block_fp8_gemm_into
+ * (runtime/dsv4_direct/fp8_linear.py:572-684, kernels :395-497) and the
+ * automatic split of make_gemm_plan (:206-251):
+ *   out[m, n] = bf16( sum over 128-K blocks kb of
+ *                     (A_kb . W_kb^T) * 2^(a_scale[m, kb] - 127) * 2^(w_scale[n/128, kb] - 127) )
+ *   a        E4M3 [m, k] row-major, a_scale E8M0 [m, k/128] (dsv4moe_act_quant_block_fp8)
+ *   wq       E4M3 weights [n, k] packed by dsv4moe_pack_int8 (1 KiB tiles)
+ *   w_scale  E8M0 [ceil(n/128), k/128] (the checkpoint's block scales; byte 0 = 2^-127)
+ *   split_k  1, 2, 4 or 8; > 1 needs dsv4moe_block_fp8_workspace_bytes bytes of
+ *            fp32 [split, m, n] workspace, reduced in split order
+ * n a multiple of 16, k a multiple of 128 up to 32768, m*k and n*k below 2^31.
+ * dsv4moe_block_fp8_split_k returns this library's split for (m, n, k).
+ */
+int32_t dsv4moe_block_fp8_split_k(int64_t m, int64_t n, int64_t k);
+size_t dsv4moe_block_fp8_workspace_bytes(int64_t m, int64_t n, int32_t split_k);
+int dsv4moe_block_fp8_gemm(const uint8_t* a, const uint8_t* a_scale, int64_t m, int64_t n, int64_t k,
+                           const uint8_t* wq, const uint8_t* w_scale, int32_t split_k, float* workspace,
+                           size_t workspace_bytes, uint16_t* out, void* stream);
+
+/*
  * Shared expert over the checkpoint's FP8 E4M3 / E8M0 128x128-block weights,
  * added into the routed output:
  *   out[T,H] <- bf16( out + shared(x) ),

@@ -62,7 +62,9 @@ __all__ = [
     "ExpertSource",
     "MXFP4ExpertSource",
     "RouteResult",
+    "act_quant_block_fp8",
     "act_quant_per_token_fp8",
+    "block_fp8_gemm_f32",
     "automatic_split_k",
     "bf16_bits_to_f32",
     "bf16_round",
@@ -821,6 +823,51 @@ def w8a16_fp8_linear_f32(a, codes, scale_codes) -> np.ndarray:
 
     w = bf16_round(dequant_fp8_block(codes, scale_codes))
     return (np.asarray(a, dtype=F32) @ w.T).astype(F32)
+
+
+def act_quant_block_fp8(x) -> tuple[np.ndarray, np.ndarray]:
+    """``_activation_quant_kernel`` (``fp8_linear.py:354-392``): per row and
+    128-K block, s = max(amax, 1e-4) * fp32(1/448) in fp32; the E8M0 exponent
+    is its biased exponent plus 1 when the mantissa is nonzero (the next power
+    of two at or above s), clamped to [1, 254]; q = e4m3(clamp(x / 2^(e-127),
+    -448, 448)).  x: float32 values (bf16 / fp16 inputs widen exactly).
+    Returns (E4M3 codes uint8 [M, K], E8M0 bytes uint8 [M, K/128])."""
+
+    xf = np.asarray(x, dtype=F32)
+    m, k = xf.shape
+    if k % 128:
+        raise ValueError("k must be a multiple of 128")
+    blocks = xf.reshape(m, k // 128, 128)
+    amax = np.abs(blocks).max(axis=-1)
+    unrounded = (np.maximum(amax, F32(1.0e-4)) * F32(1.0 / 448.0)).astype(F32)
+    bits = unrounded.view(np.uint32)
+    e = ((bits >> 23) & 0xFF).astype(np.int64) + ((bits & 0x7FFFFF) != 0)
+    e = np.clip(e, 1, 254)
+    scale = (e.astype(np.uint32) << np.uint32(23)).view(F32)
+    q = np.clip(blocks / scale[..., None], F32(-448.0), F32(448.0)).astype(F32)
+    codes = fp8_e4m3_encode(fp8_e4m3_round(q)).reshape(m, k)
+    return codes, e.astype(np.uint8)
+
+
+def block_fp8_gemm_f32(a_codes, a_scale, w_codes, w_scale) -> np.ndarray:
+    """``_block_fp8_gemm_kernel`` (``fp8_linear.py:395-424``) in exact-product
+    fp32 form: C = sum over 128-K blocks of (A_blk . W_blk^T) * 2^(ea-127) *
+    2^(ew-127), accumulated in float64 and returned as float32 (the kernel
+    rounds the fp32 sum to bf16).  a_codes E4M3 [M, K], a_scale E8M0
+    [M, K/128], w_codes E4M3 [N, K], w_scale E8M0 [ceil(N/128), K/128]."""
+
+    a = fp8_e4m3_decode(a_codes).astype(np.float64)
+    w = fp8_e4m3_decode(w_codes).astype(np.float64)
+    m, k = a.shape
+    n = w.shape[0]
+    sa = decode_e8m0(a_scale).astype(np.float64)               # [M, KB]
+    sw = decode_e8m0(w_scale).astype(np.float64)               # [NB, KB]
+    sw_rows = np.repeat(sw, 128, axis=0)[:n]                   # [N, KB]
+    out = np.zeros((m, n), dtype=np.float64)
+    for kb in range(k // 128):
+        blk = a[:, kb * 128:(kb + 1) * 128] @ w[:, kb * 128:(kb + 1) * 128].T
+        out += blk * sa[:, kb:kb + 1] * sw_rows[None, :, kb]
+    return out.astype(F32)
 
 
 def shared_fp8_bf16(x, w1, s1, w3, s3, w2, s2, clamp_limit: float) -> np.ndarray:

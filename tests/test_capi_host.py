@@ -121,6 +121,50 @@ def test_w8a16_validation_and_split_policy():
     assert lib.dsv4moe_w8a16_split_k(0, 4096, 4096) == -1
 
 
+def test_block_fp8_validation_and_split_policy():
+    fake = ctypes.c_void_p(0x1000)
+    lib = _lib.load()
+    g = lambda m, n, k, split, ws: (fake, fake, m, n, k, fake, fake, split, fake, ws, fake, None)
+    assert "multiple of 16" in _einval("dsv4moe_block_fp8_gemm", *g(4, 40, 4096, 1, 0))
+    assert "multiple of 128" in _einval("dsv4moe_block_fp8_gemm", *g(4, 64, 4000, 1, 0))
+    assert "split_k" in _einval("dsv4moe_block_fp8_gemm", *g(4, 64, 4096, 16, 1 << 30))
+    assert "K-block" in _einval("dsv4moe_block_fp8_gemm", *g(4, 64, 256, 4, 1 << 30))
+    need = lib.dsv4moe_block_fp8_workspace_bytes(4, 64, 2)
+    assert need == 2 * 4 * 64 * 4 and lib.dsv4moe_block_fp8_workspace_bytes(4, 64, 1) == 0
+    assert "workspace" in _einval("dsv4moe_block_fp8_gemm", *g(4, 64, 4096, 2, need - 1))
+    assert "x_dtype" in _einval("dsv4moe_act_quant_block_fp8", fake, 3, 4, 128, fake, fake, None)
+    assert "multiple of 128" in _einval("dsv4moe_act_quant_block_fp8", fake, 0, 4, 100, fake, fake, None)
+    assert lib.dsv4moe_block_fp8_gemm(*g(0, 64, 4096, 1, 0)) == _lib.DSV4MOE_OK
+    # this library's split: a power of two in [1, 8] leaving >= 2 K blocks per split,
+    # raised only while the grid is below 512 workgroups
+    for m in (1, 16, 17, 64, 65, 8192):
+        for n in (1024, 4096, 16384):
+            split = lib.dsv4moe_block_fp8_split_k(m, n, 4096)
+            assert split in (1, 2, 4, 8) and 32 // split >= 2
+    assert lib.dsv4moe_block_fp8_split_k(8192, 4096, 4096) == 1
+    assert lib.dsv4moe_block_fp8_split_k(1, 4096, 4096) == 8
+    assert lib.dsv4moe_block_fp8_split_k(0, 4096, 4096) == -1
+
+
+def test_block_fp8_plans_mirror_reference_contract():
+    from gaiban_lite_amd import fp8_linear as F
+
+    qp = F.make_quantization_plan(33, 512)
+    assert qp.quantized_shape == (33, 512) and qp.scale_shape == (33, 4) and qp.grid == (3, 4)
+    gp = F.make_gemm_plan(64, 1024, 4096, split_k=4)
+    assert gp.workspace_shape == (4, 64, 1024) and gp.workspace_bytes == 4 * 64 * 1024 * 4
+    assert gp.weight_scale_shape == (8, 32) and gp.k_blocks_per_split == 8 and gp.dispatch == "split_k_reduce"
+    assert F.make_gemm_plan(8192, 4096, 4096).split_k == 1
+    for bad in (dict(split_k=3), dict(split_k=16), dict(split_k=True)):
+        with pytest.raises(ValueError):
+            F.make_gemm_plan(64, 1024, 4096, **bad)
+    with pytest.raises(ValueError):
+        F.make_gemm_plan(64, 1024, 4000)
+    with pytest.raises(ValueError):
+        F.make_quantization_plan(4, 256, block_m=3)
+    assert F.primitive_contract()["supported_split_k"] == [1, 2, 4, 8]
+
+
 def test_workspace_formula():
     # x row sums (per 64 columns) + h + h row sums + fp32 contributions, each 256-byte aligned
     t, k, h, i = 64, 6, 4096, 2048
