@@ -244,6 +244,7 @@ class ResidentMXFP4MoEWeights:
     marlin_input_dtype: torch.dtype | None = None
     weight_format: str = "mxfp4_g32"
     shared_fp8: ResidentFP8SharedExpert | None = None  # shared expert in the checkpoint FP8 format
+    load_seconds: float | None = None  # set by the checkpoint loader
 
     @property
     def device(self) -> torch.device:
