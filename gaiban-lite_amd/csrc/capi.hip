@@ -610,8 +610,8 @@ int dsv4moe_block_fp8_gemm(const uint8_t* a, const uint8_t* a_scale, int64_t m, 
   DSV4_REQUIRE(m * k < (int64_t)1 << 31 && n * k < (int64_t)1 << 31, "%s: m*k and n*k must be below 2^31", who);
   if (m == 0) return DSV4MOE_OK;
   DSV4_REQUIRE(a && a_scale && wq && w_scale && out, "%s: null pointer", who);
-  DSV4_REQUIRE(aligned(a, 16) && aligned(wq, 16) && aligned(out, 8),
-               "%s: a and wq must be 16-byte aligned, out 8-byte aligned", who);
+  DSV4_REQUIRE(aligned(a, 16) && aligned(wq, 16) && aligned(out, 8) && aligned(a_scale, 4),
+               "%s: a and wq must be 16-byte aligned, a_scale 4-byte, out 8-byte aligned", who);
   const size_t need = dsv4moe_block_fp8_workspace_bytes(m, n, split_k);
   DSV4_REQUIRE(workspace_bytes >= need, "%s: workspace of %zu bytes is below the %zu needed", who, workspace_bytes,
                need);

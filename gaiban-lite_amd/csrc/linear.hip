@@ -585,11 +585,175 @@ __global__ __launch_bounds__(256, 2) void w8a8_block_kernel(BlockFp8Params p) {
   }
 }
 
+// Many tokens: a three-stage pipeline through LDS.  Per K block, inline-asm
+// buffer_load ... lds copies the token tile (16C rows x 128 B, part q of row t
+// at q ^ swz128(t)), each wavefront's R weight strips (2 KiB each) and the
+// tokens' E8M0 scale dwords (the 4-block group holding block kb; K % 512 == 0)
+// two blocks ahead of the compute; one s_waitcnt vmcnt(n) (n = one step's
+// copies, left in flight) and a barrier publish the next block.  No register
+// holds data in flight, so nothing the compiler moves can read it early.
+template <int R, int C>
+__global__ __launch_bounds__(256, 1) void w8a8_block_prefill_kernel(BlockFp8Params p) {
+  constexpr int kTokBytes = 16 * C * 128;
+  constexpr int kScaleTok = 16 * C / 4;  // tokens per wavefront's scale copy
+  __shared__ __attribute__((aligned(16))) uint8_t xs[3][kTokBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[3][4][R * 2048];
+  __shared__ __attribute__((aligned(16))) uint32_t scs[3][4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+
+  const int items = p.split * p.tiles_m * p.tiles_n;
+  const int per_xcd = (items + kLinXcds - 1) / kLinXcds;
+  const int item = (blockIdx.x % kLinXcds) * per_xcd + blockIdx.x / kLinXcds;
+  if (item >= items) return;
+  const int tn = item % p.tiles_n;
+  const int tm = (item / p.tiles_n) % p.tiles_m;
+  const int sp = item / (p.tiles_n * p.tiles_m);
+
+  const int kb_begin = sp * p.kb_per_split;
+  const int kb_end = min(p.kblocks, kb_begin + p.kb_per_split);
+  const int nk = kb_end - kb_begin;
+  const int wins = p.k / kWin;
+  const int strips = p.n >> 4;
+  const int strip0 = tn * 4 * R + wave * R;
+  const int64_t tok0 = (int64_t)tm * 16 * C;
+
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.a, (short)0, (int)(p.m * p.k), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t as_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.as, (short)0, (int)(p.m * p.kblocks), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wq, (short)0, (int)((int64_t)p.n * p.k), kLinRsrcFlags);
+
+  constexpr int kActDma = 2 * C;
+  static_assert(kActDma % 4 == 0, "every wavefront issues the same number of token copies");
+  constexpr int kActPerWave = kActDma / 4;
+  uint32_t a_off[kActPerWave];
+#pragma unroll
+  for (int i = 0; i < kActPerWave; ++i) {
+    const int q = wave + 4 * i;
+    const int row = q * 8 + (lane >> 3);
+    const int64_t tok = tok0 + row;
+    const int part = (lane & 7) ^ swz128(row);
+    a_off[i] = tok < p.m ? (uint32_t)(tok * p.k + part * 16) : kLinOob;
+  }
+  uint32_t w_off[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+  // scale dword of token tok0 + kScaleTok * wave + lane (lanes past kScaleTok
+  // or past the last token read out of range into unused slots)
+  const int64_t stok = tok0 + kScaleTok * wave + lane;
+  const uint32_t s_off = (lane < kScaleTok && stok < p.m) ? (uint32_t)(stok * p.kblocks) : kLinOob;
+  uint32_t srow[4] = {0, 0, 0, 0};
+  {
+    const uint8_t* row = p.ws8 + (int64_t)(min(strip0, strips - 1) >> 3) * p.kblocks;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (64 * q + lane < p.kblocks) srow[q] = row[64 * q + lane];
+  }
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+
+  constexpr int kStepLoads = kActPerWave + 2 * R + 1;
+  static_assert(kStepLoads < 64, "vmcnt range");
+  auto issue = [&](int kb, int buf) {
+#pragma unroll
+    for (int i = 0; i < kActPerWave; ++i)
+      lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + 4 * i) * 1024]), a_off[i], kb * 128);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 2048]), w_off[r], (2 * kb) * 1024);
+      lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 2048 + 1024]), w_off[r], (2 * kb + 1) * 1024);
+    }
+    lds_copy4(as_rsrc, lds_addr(&scs[buf][wave][0]), s_off, kb & ~3);
+  };
+
+  f32x4 acc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Step kb: issue block kb + 2 into buffer (u + 2) % 3 (released by step
+  // kb - 1's barrier), compute block kb from buffer u, wait for block kb + 1.
+  auto step = [&](int kb, auto u_c) {
+    constexpr int u = decltype(u_c)::value;
+    const bool issue2 = kb + 2 < kb_end;
+    if (issue2) issue(kb + 2, (u + 2) % 3);
+    const uint32_t word = kb < 64 ? srow[0] : (kb < 128 ? srow[1] : (kb < 192 ? srow[2] : srow[3]));
+    const int sw = __builtin_amdgcn_readlane((int)word, kb & 63);
+    i32x8 wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * 2048 + lane * 16]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * 2048 + 1024 + lane * 16]);
+      wv[r] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int row = c * 16 + n16;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((j ^ swz128(row)) * 16)]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + (((4 + j) ^ swz128(row)) * 16)]);
+      const i32x8 tv = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      const int st = (int)((scs[u][row / kScaleTok][row % kScaleTok] >> (8 * (kb & 3))) & 0xFF);
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][c] = mfma_fp8_block(wv[r], tv, acc[r][c], sw, st);
+    }
+    if (issue2)
+      lds_dma_wait_keep<kStepLoads>();  // this wavefront's copies of block kb + 1 have landed
+    else
+      lds_dma_wait_all();
+    __syncthreads();  // ... and everyone's; buffer u is free again
+  };
+  using U0 = std::integral_constant<int, 0>;
+  using U1 = std::integral_constant<int, 1>;
+  using U2 = std::integral_constant<int, 2>;
+
+  if (nk > 0) {
+    issue(kb_begin, 0);
+    if (nk > 1) {
+      issue(kb_begin + 1, 1);
+      lds_dma_wait_keep<kStepLoads>();
+    } else {
+      lds_dma_wait_all();
+    }
+    __syncthreads();
+    // the last two steps issue nothing, and the last waits for everything,
+    // so no copy is outstanding at exit
+    for (int i = 0; i < nk; i += 3) {
+      step(kb_begin + i, U0{});
+      if (i + 1 < nk) step(kb_begin + i + 1, U1{});
+      if (i + 2 < nk) step(kb_begin + i + 2, U2{});
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int strip = strip0 + r;
+    if (strip >= strips) continue;
+    const int n = strip * 16 + 4 * j;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t tok = tok0 + c * 16 + n16;
+      if (tok >= p.m) continue;
+      const float v[4] = {acc[r][c][0], acc[r][c][1], acc[r][c][2], acc[r][c][3]};
+      if (p.split == 1) {
+        uint16_t* dst = p.out + tok * p.n + n;
+        *reinterpret_cast<u32x2*>(dst) = finish_bf16x4(v, dst, false);
+      } else {
+        float* dst = p.partial + ((int64_t)sp * p.m + tok) * p.n + n;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+      }
+    }
+  }
+}
+
 static void launch_w8a8_block_kernel(const BlockFp8Params& p, int r, int c, hipStream_t stream) {
   const int items = p.split * p.tiles_m * p.tiles_n;
   const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
-  if (r == 2 && c == 8) hipLaunchKernelGGL((w8a8_block_kernel<2, 8>), grid, dim3(256), 0, stream, p);
-  else if (r == 4 && c == 4) hipLaunchKernelGGL((w8a8_block_kernel<4, 4>), grid, dim3(256), 0, stream, p);
+  if (r == 4 && c == 8) hipLaunchKernelGGL((w8a8_block_prefill_kernel<4, 8>), grid, dim3(256), 0, stream, p);
+  else if (r == 4 && c == 4) hipLaunchKernelGGL((w8a8_block_prefill_kernel<4, 4>), grid, dim3(256), 0, stream, p);
   else if (c == 1) hipLaunchKernelGGL((w8a8_block_kernel<2, 1>), grid, dim3(256), 0, stream, p);
   else if (c == 2) hipLaunchKernelGGL((w8a8_block_kernel<2, 2>), grid, dim3(256), 0, stream, p);
   else hipLaunchKernelGGL((w8a8_block_kernel<2, 4>), grid, dim3(256), 0, stream, p);
@@ -684,21 +848,26 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
   return DSV4MOE_OK;
 }
 
-// Block-FP8 W8A8 geometry: (R, C) = (2, 1 | 2 | 4) up to 64 tokens, then
-// 128 channels x 128 tokens; split-K widened (powers of two up to 8, >= 2 K
+// Block-FP8 W8A8 geometry: (R, C) = (2, 1 | 2 | 4) up to 64 tokens or when
+// K % 512 != 0 (w8a8_block_kernel), then the three-stage kernel with 256
+// channels x 128 tokens, or x 64 tokens when that leaves fewer than 512
+// workgroups; split-K widened (powers of two up to 8, >= 2 K
 // blocks per split) while the grid is below 512 workgroups.
-static void w8a8_geometry(int64_t m, int* r, int* c) {
+static void w8a8_geometry(int64_t m, int64_t n, int64_t k, int* r, int* c) {
   *r = 2;
   if (m <= 16) *c = 1;
   else if (m <= 32) *c = 2;
-  else if (m <= 64) *c = 4;
-  else *c = 8;
+  else if (m <= 64 || k % 512 != 0) *c = 4;
+  else {
+    *r = 4;
+    *c = ((n + 255) / 256) * ((m + 127) / 128) >= 512 ? 8 : 4;
+  }
 }
 
 int32_t dsv4_block_fp8_split_k(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0) return -1;
   int r, c;
-  w8a8_geometry(m, &r, &c);
+  w8a8_geometry(m, n, k, &r, &c);
   const int64_t tiles = ((n + 64 * r - 1) / (64 * r)) * ((m + 16 * c - 1) / (16 * c));
   const int64_t kblocks = k / 128;
   int split = 1;
@@ -724,7 +893,7 @@ int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, i
                                const uint8_t* wq, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
                                hipStream_t stream) {
   int r, c;
-  w8a8_geometry(m, &r, &c);
+  w8a8_geometry(m, n, k, &r, &c);
   BlockFp8Params p;
   p.a = a;
   p.as = as;

@@ -47,3 +47,71 @@ def test_mxfp4_prefill_kernel_has_no_spills_and_fits_three_workgroups(tmp_path):
         assert m["sgpr_spill_count"] == 0, name
         assert m["vgpr_count"] <= 168, (name, m["vgpr_count"])
         assert m["group_segment_fixed_size"] <= 32768, name
+
+
+def test_w8a8_prefill_kernel_fits_one_workgroup_per_cu(tmp_path):
+    """The block-FP8 W8A8 prefill kernel (three LDS stages of tokens, weight
+    strips and token scales): no spills, and its LDS within the 160 KiB of a
+    gfx950 CU."""
+
+    meta = kernel_metadata(CSRC / "linear.hip", tmp_path)
+    prefill = {k: v for k, v in meta.items() if "w8a8_block_prefill_kernel" in k}
+    assert len(prefill) == 2
+    for name, m in prefill.items():
+        assert m["vgpr_spill_count"] == 0, name
+        assert m["sgpr_spill_count"] == 0, name
+        assert m["group_segment_fixed_size"] <= 160 * 1024, name
+
+
+def inflight_register_reads(asm: str, kernel: str) -> list[str]:
+    """Instructions of `kernel` that read or overwrite a VGPR whose
+    (non-LDS) buffer load has not been waited for by a later s_waitcnt vmcnt
+    (any vmcnt wait is taken to release every load, which can only miss a
+    hazard, never invent one)."""
+
+    start = asm.index(kernel + ":")
+    body = asm[start:asm.index(".Lfunc_end", start)].split("\n")
+
+    def regs(spec):
+        spec = spec.strip()
+        m = re.match(r"v\[(\d+):(\d+)\]", spec)
+        if m:
+            return set(range(int(m.group(1)), int(m.group(2)) + 1))
+        m = re.match(r"v(\d+)$", spec)
+        return {int(m.group(1))} if m else set()
+
+    pending, bad = set(), []
+    for line in body:
+        ins = line.split(";")[0].strip()
+        if not ins or ins.startswith(".") or ins.endswith(":"):
+            continue
+        op = ins.split()[0]
+        args = [a.strip() for a in ins[len(op):].split(",")]
+        if op == "s_waitcnt" and "vmcnt" in ins:
+            pending = set()
+        elif op.startswith("buffer_load") and not ins.endswith("lds"):
+            pending |= regs(args[0])
+        elif op.startswith(("v_", "ds_", "global_", "buffer_")):
+            touched = set().union(*(regs(a) for a in args)) if args else set()
+            if touched & pending:
+                bad.append(ins)
+    return bad
+
+
+def test_mxfp4_prefill_reads_no_register_in_flight(tmp_path):
+    """The MXFP4 prefill kernel's inline-asm weight loads land in registers
+    that nothing may read (a copy, a spill) before its explicit wait."""
+
+    from gaiban_lite_amd import build_ext
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path / "mx.s"
+    subprocess.run([hipcc, *build_ext.HIPCC_FLAGS, f"-I{ROOT / 'include'}", f"-I{CSRC}", "--cuda-device-only",
+                    "-S", str(CSRC / "experts_mx.hip"), "-o", str(out)], check=True, capture_output=True)
+    asm = out.read_text()
+    names = re.findall(r"^(_Z\S*mx_prefill_kernel\S*):", asm, flags=re.M)
+    assert len(names) == 2
+    for name in names:
+        assert inflight_register_reads(asm, name) == [], name
