@@ -452,6 +452,64 @@ int dsv4moe_experts_mxfp4(const uint16_t* x, int64_t tokens, int32_t hidden, int
                                    num_tokens_post_padded, block_size, clamp_limit, out, workspace, s);
 }
 
+// Checks shared by the fused layer entries (who = entry name), after the
+// experts checks.
+static int validate_layer_route(const char* who, const float* logits, int32_t topk, int32_t score_func,
+                                float route_scale, float clamp_limit, const int32_t* ids, const float* weights,
+                                const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                                const int32_t* num_tokens_post_padded) {
+  DSV4_REQUIRE(topk <= 16, "%s: topk must be <= 16", who);
+  DSV4_REQUIRE(score_func == DSV4MOE_SCORE_SIGMOID || score_func == DSV4MOE_SCORE_SOFTMAX ||
+                   score_func == DSV4MOE_SCORE_SQRTSOFTPLUS,
+               "%s: unknown score_func %d", who, score_func);
+  DSV4_REQUIRE(route_scale > 0.0f && route_scale < 3.0e38f, "%s: route_scale must be finite and positive", who);
+  DSV4_REQUIRE(!(clamp_limit < 0.0f) && clamp_limit < 3.0e38f, "%s: clamp_limit must be >= 0 and finite", who);
+  DSV4_REQUIRE(logits && ids && weights && sorted_token_ids && expert_ids && num_tokens_post_padded,
+               "%s: null route/alignment pointer", who);
+  return DSV4MOE_OK;
+}
+
+// Route and align a fused layer call [and sum the activation rows when
+// x_sums is given], by token count: for T <= 16 one prologue launch routes,
+// aligns and sums; up to 8191 route ids the route kernel, then the prologue
+// (align + sums); from 8192 ids the route kernel, then the workgroup-split
+// alignment with the sums beside its counting, its scratch in the (not yet
+// used) contribution region of the experts workspace.
+static int layer_route_align(const char* who, const uint16_t* x_sums, const float* logits, const float* bias,
+                             int64_t tokens, int32_t hidden, int32_t inter, int32_t experts, int32_t topk,
+                             int32_t score_func, float route_scale, int32_t has_shared, int32_t block_size,
+                             int32_t* ids, float* weights, float* margin, int32_t* sorted_token_ids, int64_t capacity,
+                             int32_t* expert_ids, int32_t* num_tokens_post_padded, void* workspace, hipStream_t s) {
+  int rc = DSV4MOE_OK;
+  const int64_t nblocks = (capacity + block_size - 1) / block_size;
+  // (with routing in the prologue the route interval of the profile covers
+  // the whole prologue, and the align interval is empty)
+  const bool route_in_prologue = tokens <= kPrologueRouteMaxTokens;
+  if (!route_in_prologue) {
+    rc = dsv4_launch_route_topk(logits, bias, tokens, experts, topk, score_func, route_scale, ids,
+                                weights, margin, nullptr, nullptr, s);
+    if (rc != DSV4MOE_OK) return rc;
+    dsv4host::prof_stamp(dsv4host::kStampRoute, s);
+  }
+  float* xsum = x_sums != nullptr ? dsv4_experts_xsum(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0)
+                                  : nullptr;
+  if (tokens * topk >= kAlignMultiMinAssignments) {
+    size_t room = 0;
+    int32_t* scratch = dsv4_experts_align_scratch(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0, &room);
+    DSV4_REQUIRE(room >= dsv4_align_scratch_bytes(tokens * topk, experts), "%s: align scratch too small", who);
+    rc = dsv4_launch_align_multi(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
+                                 nblocks, num_tokens_post_padded, scratch, x_sums, tokens, hidden, xsum, s);
+  } else {
+    rc = dsv4_launch_prologue(route_in_prologue ? 1 : 0, logits, bias, tokens, experts, topk, score_func,
+                              route_scale, ids, weights, margin, block_size, sorted_token_ids, capacity, expert_ids,
+                              nblocks, num_tokens_post_padded, x_sums, hidden, xsum, s);
+  }
+  if (rc != DSV4MOE_OK) return rc;
+  if (route_in_prologue) dsv4host::prof_stamp(dsv4host::kStampRoute, s);
+  dsv4host::prof_stamp(dsv4host::kStampAlign, s);
+  return DSV4MOE_OK;
+}
+
 int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bias,
                         int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
                         int32_t topk, int32_t score_func, float route_scale,
@@ -466,48 +524,51 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                             capacity, block_size, out, workspace, workspace_bytes, has_shared,
                             "layer_w4a16");
   if (rc != DSV4MOE_OK || tokens == 0) return rc;
-  DSV4_REQUIRE(topk <= 16, "layer_w4a16: topk must be <= 16");
-  DSV4_REQUIRE(score_func == DSV4MOE_SCORE_SIGMOID || score_func == DSV4MOE_SCORE_SOFTMAX ||
-                   score_func == DSV4MOE_SCORE_SQRTSOFTPLUS,
-               "layer_w4a16: unknown score_func %d", score_func);
-  DSV4_REQUIRE(route_scale > 0.0f && route_scale < 3.0e38f, "layer_w4a16: route_scale must be finite and positive");
-  DSV4_REQUIRE(!(clamp_limit < 0.0f) && clamp_limit < 3.0e38f, "layer_w4a16: clamp_limit must be >= 0 and finite");
-  DSV4_REQUIRE(logits && ids && weights && sorted_token_ids && expert_ids && num_tokens_post_padded,
-               "layer_w4a16: null route/alignment pointer");
+  rc = validate_layer_route("layer_w4a16", logits, topk, score_func, route_scale, clamp_limit, ids, weights,
+                            sorted_token_ids, expert_ids, num_tokens_post_padded);
+  if (rc != DSV4MOE_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   dsv4host::prof_stamp(dsv4host::kStampBegin, s);
-  const int64_t nblocks = (capacity + block_size - 1) / block_size;
-  // One prologue launch aligns the ids and computes the activation row sums;
-  // for small T it also routes (then the route interval of the profile covers
-  // the whole prologue, and the align interval is empty).
-  const bool route_in_prologue = tokens <= kPrologueRouteMaxTokens;
-  if (!route_in_prologue) {
-    rc = dsv4_launch_route_topk(logits, bias, tokens, experts, topk, score_func, route_scale, ids,
-                                weights, margin, nullptr, nullptr, s);
-    if (rc != DSV4MOE_OK) return rc;
-    dsv4host::prof_stamp(dsv4host::kStampRoute, s);
-  }
-  float* xsum = dsv4_experts_xsum(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0);
-  if (tokens * topk >= kAlignMultiMinAssignments) {
-    // Many ids: the two-launch alignment, row sums beside the counting, its
-    // scratch in the (not yet used) contribution region of the workspace.
-    size_t room = 0;
-    int32_t* scratch = dsv4_experts_align_scratch(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0, &room);
-    DSV4_REQUIRE(room >= dsv4_align_scratch_bytes(tokens * topk, experts), "layer_w4a16: align scratch too small");
-    rc = dsv4_launch_align_multi(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
-                                 nblocks, num_tokens_post_padded, scratch, x, tokens, hidden, xsum, s);
-  } else {
-    rc = dsv4_launch_prologue(route_in_prologue ? 1 : 0, logits, bias, tokens, experts, topk, score_func,
-                              route_scale, ids, weights, margin, block_size, sorted_token_ids, capacity, expert_ids,
-                              nblocks, num_tokens_post_padded, x, hidden, xsum, s);
-  }
+  rc = layer_route_align("layer_w4a16", x, logits, bias, tokens, hidden, inter, experts, topk, score_func,
+                         route_scale, has_shared, block_size, ids, weights, margin, sorted_token_ids, capacity,
+                         expert_ids, num_tokens_post_padded, workspace, s);
   if (rc != DSV4MOE_OK) return rc;
-  if (route_in_prologue) dsv4host::prof_stamp(dsv4host::kStampRoute, s);
-  dsv4host::prof_stamp(dsv4host::kStampAlign, s);
   return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
                                    has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
                                    num_tokens_post_padded, block_size, clamp_limit, out, workspace, s,
                                    /*rowsums_ready=*/true);
+}
+
+int dsv4moe_layer_mxfp4(const uint16_t* x, const float* logits, const float* bias,
+                        int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
+                        int32_t topk, int32_t score_func, float route_scale,
+                        const uint8_t* w13q, const uint8_t* w13s, const uint8_t* w2q,
+                        const uint8_t* w2s, int32_t has_shared, float clamp_limit,
+                        int32_t block_size, int32_t* ids, float* weights, float* margin,
+                        int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                        int32_t* num_tokens_post_padded, uint16_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(hidden % 512 == 0 && inter % 512 == 0,
+               "layer_mxfp4: hidden and inter must be multiples of 512 (got %d, %d)", hidden, inter);
+  int rc = validate_experts(x, tokens, hidden, inter, experts, topk, w13q, reinterpret_cast<const uint16_t*>(w13s),
+                            w2q, reinterpret_cast<const uint16_t*>(w2s), capacity, block_size, out, workspace,
+                            workspace_bytes, has_shared, "layer_mxfp4");
+  if (rc != DSV4MOE_OK || tokens == 0) return rc;
+  rc = validate_layer_route("layer_mxfp4", logits, topk, score_func, route_scale, clamp_limit, ids, weights,
+                            sorted_token_ids, expert_ids, num_tokens_post_padded);
+  if (rc != DSV4MOE_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dsv4host::prof_stamp(dsv4host::kStampBegin, s);
+  // the MXFP4 kernels need no activation row sums (the E8M0 scale is exact
+  // inside the conversion)
+  rc = layer_route_align("layer_mxfp4", nullptr, logits, bias, tokens, hidden, inter, experts, topk, score_func,
+                         route_scale, has_shared, block_size, ids, weights, margin, sorted_token_ids, capacity,
+                         expert_ids, num_tokens_post_padded, workspace, s);
+  if (rc != DSV4MOE_OK) return rc;
+  return dsv4_launch_experts_mxfp4(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+                                   has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
+                                   num_tokens_post_padded, block_size, clamp_limit, out, workspace, s);
 }
 
 int dsv4moe_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed, void* stream) {

@@ -601,7 +601,6 @@ class TP4MoE:
                 fused = (
                     self.route_kind == "learned"
                     and self._marlin_input_dtype is None
-                    and not self._mxfp4
                     and override is None
                     and self._owned_alignment_provider is None
                     and self._route_tensor_observer is None
@@ -622,7 +621,7 @@ class TP4MoE:
                         weights=buffers.route_weights, margin=buffers.margin,
                         sorted_token_ids=a.sorted_token_ids, expert_ids=a.expert_ids,
                         num_tokens_post_padded=a.num_tokens_post_padded, out=buffers.output,
-                        workspace=buffers.workspace,
+                        workspace=buffers.workspace, mxfp4=self._mxfp4,
                     )
                     self._add_shared_fp8(flat, buffers)
                     return buffers.route_weights, buffers.route_ids, buffers.margin, {}

@@ -343,7 +343,11 @@ def layer_w4a16_into(
     num_tokens_post_padded: torch.Tensor,
     out: torch.Tensor,
     workspace: torch.Tensor,
+    mxfp4: bool = False,
 ) -> None:
+    """The fused layer entry (``dsv4moe_layer_w4a16``, or with ``mxfp4``
+    ``dsv4moe_layer_mxfp4`` over the MXFP4 residents)."""
+
     tokens, hidden = x.shape
     dev = x.device
     _check("x", x, dtype=torch.bfloat16, device=dev)
@@ -355,7 +359,8 @@ def layer_w4a16_into(
     if bias is not None:
         _check("bias", bias, dtype=torch.float32, shape=(experts,), device=dev)
     call(
-        "dsv4moe_layer_w4a16", ptr(x), ptr(logits), ptr(bias), tokens, hidden, inter, experts,
+        "dsv4moe_layer_mxfp4" if mxfp4 else "dsv4moe_layer_w4a16", ptr(x), ptr(logits), ptr(bias), tokens,
+        hidden, inter, experts,
         topk, score_func_id(score_func), float(route_scale), ptr(w13q), ptr(w13s), ptr(w2q),
         ptr(w2s), int(bool(has_shared)), float(clamp_limit), block_size, ptr(ids), ptr(weights),
         ptr(margin), ptr(sorted_token_ids), sorted_token_ids.numel(), ptr(expert_ids),

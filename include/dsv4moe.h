@@ -254,6 +254,23 @@ int dsv4moe_experts_mxfp4(const uint16_t* x, int64_t tokens, int32_t hidden, int
                           size_t workspace_bytes, void* stream);
 
 /*
+ * Whole MoE layer over MXFP4 experts: route (from logits) -> align ->
+ * experts (dsv4moe_experts_mxfp4) -> combine, as dsv4moe_layer_w4a16 (same
+ * arguments; w13s / w2s are the packed E8M0 bytes).  Replaces
+ * TP4MoE.compute_partial (runtime/dsv4_direct/moe_runtime.py:1714-1888) for
+ * the checkpoint's routed-expert format at world size 1.
+ */
+int dsv4moe_layer_mxfp4(const uint16_t* x, const float* logits, const float* bias,
+                        int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
+                        int32_t topk, int32_t score_func, float route_scale,
+                        const uint8_t* w13q, const uint8_t* w13s, const uint8_t* w2q,
+                        const uint8_t* w2s, int32_t has_shared, float clamp_limit,
+                        int32_t block_size, int32_t* ids, float* weights, float* margin,
+                        int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                        int32_t* num_tokens_post_padded, uint16_t* out, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/*
  * W8A16 dense linear: out[M,N] = bf16( a[M,K] . (q[N,K] * s[N])^T ), int8
  * symmetric per-output-channel weights, bf16 scales, fp32 accumulation.
  * Replaces w8a16_gemm_into / make_gemm_plan / _automatic_split_k

@@ -175,3 +175,37 @@ def test_tp4moe_dropin_mxfp4():
     assert_moe_close(to_np_f32(out.view(64, -1)), ref, what="TP4MoE mxfp4")
     # the staged and the layer path agree with a direct experts call on the same routing
     assert moe.resident.weight_format == "mxfp4_g32"
+
+
+@pytest.mark.parametrize("t", [1, 16, 17, 64, 1400])
+def test_fused_layer_entry_equals_staged_chain(t):
+    """``dsv4moe_layer_mxfp4`` (route [in the prologue for T <= 16], align --
+    split over workgroups from 8192 ids -- and the MXFP4 experts in one call)
+    gives the staged chain's bits, and its routing equals the oracle's."""
+
+    shape = S.LayerShape(experts=64, hidden=512, inter=512, topk=6, has_shared=True)
+    print(f"[mxfp4] fused layer T={t}", flush=True)
+    res, src = layer(shape, seed=2)
+    g = torch.Generator(DEV).manual_seed(31)
+    wg = (torch.randn((shape.experts, shape.hidden), device=DEV, generator=g) * 0.03).to(torch.bfloat16)
+    bias = torch.randn((shape.experts,), device=DEV, generator=g) * 0.05
+    cfg = TP4MoEConfig(hidden_size=shape.hidden, intermediate_size=shape.inter, experts=shape.experts,
+                       topk=shape.topk, route_scale=2.5, clamp_limit=10.0, score_func="sqrtsoftplus",
+                       shared_experts=1)
+    moe = TP4MoE(config=cfg, resident=res, gate=ResidentGateWeights(weight=wg, bias=bias), device=DEV,
+                 global_row_shapes=[t])
+    x = S.make_hidden(t, shape.hidden, seed=t, device=DEV).view(1, t, shape.hidden)
+    lg = S.make_logits(t, shape.experts, seed=t + 5, device=DEV)
+    fused = moe.forward_tensor(x, router_logits=lg).clone()
+    ids_fused = moe._buffers[(t, 0)].route_ids.clone() if (t, 0) in moe._buffers else None
+    staged = moe.forward_tensor(x, router_logits=lg, stage_marker=lambda s: None)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, staged)
+    ref_route = O.route_topk(lg.cpu().numpy(), shape.topk, score_func=O.SCORE_SQRTSOFTPLUS, bias=bias.cpu().numpy(),
+                             route_scale=2.5)
+    if ids_fused is not None:
+        np.testing.assert_array_equal(ids_fused.cpu().numpy(), ref_route.ids)
+    rows = np.arange(t) if t <= 64 else np.sort(np.random.default_rng(t).choice(t, 64, replace=False))
+    ref = O.moe_fp32(to_np_f32(x.view(t, -1)), ref_route.ids, ref_route.weights, src, shared_index=shape.experts,
+                     clamp_limit=10.0, rows=rows)
+    assert_moe_close(to_np_f32(fused.view(t, -1))[rows], ref, what=f"fused mxfp4 T={t}")
