@@ -38,6 +38,8 @@ def build(shape, rows):
     (S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True), 64),
     (S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True), 8),
     (S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True), 64),
+    # 8400 route ids: the workgroup-split alignment (scratch in the workspace)
+    (S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True), 1400),
 ])
 def test_capture_and_replay_matches_eager(shape, rows, use_logits):
     print(f"[graph] E={shape.experts} T={rows} logits={use_logits}", flush=True)
