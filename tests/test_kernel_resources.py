@@ -65,9 +65,11 @@ def test_w8a8_prefill_kernel_fits_one_workgroup_per_cu(tmp_path):
 
 def inflight_register_reads(asm: str, kernel: str) -> list[str]:
     """Instructions of `kernel` that read or overwrite a VGPR whose
-    (non-LDS) buffer load has not been waited for by a later s_waitcnt vmcnt
-    (any vmcnt wait is taken to release every load, which can only miss a
-    hazard, never invent one)."""
+    (non-LDS) buffer load may still be in flight, in program order: vector
+    memory operations complete in issue order and `s_waitcnt vmcnt(n)` leaves
+    only the newest n outstanding.  A read at the end of a loop body is seen
+    with the loads the body left in flight, which is where a copy at the loop's
+    back edge would sit."""
 
     start = asm.index(kernel + ":")
     body = asm[start:asm.index(".Lfunc_end", start)].split("\n")
@@ -80,7 +82,8 @@ def inflight_register_reads(asm: str, kernel: str) -> list[str]:
         m = re.match(r"v(\d+)$", spec)
         return {int(m.group(1))} if m else set()
 
-    pending, bad = set(), []
+    outstanding: list[set[int]] = []  # destination VGPRs of each vector memory op, in issue order
+    bad = []
     for line in body:
         ins = line.split(";")[0].strip()
         if not ins or ins.startswith(".") or ins.endswith(":"):
@@ -88,11 +91,20 @@ def inflight_register_reads(asm: str, kernel: str) -> list[str]:
         op = ins.split()[0]
         args = [a.strip() for a in ins[len(op):].split(",")]
         if op == "s_waitcnt" and "vmcnt" in ins:
-            pending = set()
-        elif op.startswith("buffer_load") and not ins.endswith("lds"):
-            pending |= regs(args[0])
-        elif op.startswith(("v_", "ds_", "global_", "buffer_")):
-            touched = set().union(*(regs(a) for a in args)) if args else set()
+            n = int(re.search(r"vmcnt\((\d+)\)", ins).group(1))
+            outstanding = outstanding[len(outstanding) - n:] if n else []
+            continue
+        pending = set().union(*outstanding) if outstanding else set()
+        touched = set().union(*(regs(a) for a in args)) if args else set()
+        if op.startswith(("buffer_load", "global_load", "scratch_load")):
+            if touched - regs(args[0]) & pending:
+                bad.append(ins)
+            outstanding.append(set() if ins.endswith("lds") else regs(args[0]))
+        elif op.startswith(("buffer_store", "global_store", "scratch_store", "buffer_atomic", "global_atomic")):
+            if touched & pending:
+                bad.append(ins)
+            outstanding.append(set())
+        elif op.startswith(("v_", "ds_")):
             if touched & pending:
                 bad.append(ins)
     return bad
