@@ -16,8 +16,10 @@ fixed-routing figure is reported beside it).
 Also reported on the same line (secondary): decode at T in {1, 8, 256},
 prefill at T in {2048, 4096, 8192}, the W4A8 layer (uniform and Zipf routing,
 T = 64 and 8192), the same layer with MXFP4 experts (the reference
-checkpoint's E2M1 + E8M0 format, T = 64 and 8192), the W8A16 dense linear at
-K = 4096, and the CPU baseline
+checkpoint's E2M1 + E8M0 format, T = 64 and 8192), the FP8-block shared
+expert, the W8A16 (int8 and FP8-block) and block-FP8 W8A8 dense linears at
+K = 4096 (M <= 64 timed as 50 calls captured in a HIP graph, beside the
+launch-bound Python-loop figure), and the CPU baseline
 (the oracle's restatement of the reference torch path timed on this host's
 cores on a bounded sample).
 
@@ -109,6 +111,42 @@ def cuda_timer(fn, n):
     t1.record()
     torch.cuda.synchronize()
     return t0.elapsed_time(t1) / n
+
+
+def graph_timer(fn, n, out):
+    """Per-call GPU time of `fn` (kernels only, no host launch gaps): `n` calls
+    captured into one HIP graph, replayed and timed with events.  The replay's
+    output must equal an eager call's (`out` after each), else None."""
+
+    import torch
+
+    fn(0)
+    torch.cuda.synchronize()
+    want = out.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(n):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    ok = torch.equal(out, want)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(3):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ok = ok and torch.equal(out, want)
+    del graph
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / (3 * n) if ok else None
 
 
 def main() -> int:
@@ -542,10 +580,16 @@ def bench_w8a16(pkg, dev, fmt="int8"):
                 gemm(a, prep.packed, prep.scale, o, ws, plan=plan)
             it = 50 if m < 8192 else 10
             ms = cuda_timer(lambda i: gemm(a, prep.packed, prep.scale, o, ws, plan=plan), it)
+            if m <= 64:  # launch-bound from Python: time the kernels in a graph
+                g_ms = graph_timer(lambda i: gemm(a, prep.packed, prep.scale, o, ws, plan=plan), 50, o)
+                ms_eager, ms = ms, (g_ms if g_ms is not None else ms)
             byts = n * k + scale_bytes + 2 * m * k + 2 * m * n
             fl = 2.0 * m * n * k
             entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2),
                      "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+            if m <= 64:
+                entry["us_eager_python_loop"] = round(ms_eager * 1e3, 2)
+                entry["timing"] = "hip graph of 50 calls" if g_ms is not None else "eager (graph replay mismatch)"
             entry["frac_of_peak"] = (round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if m <= 64
                                      else round(fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
             entry["bound"] = "hbm" if m <= 64 else "mfma"
@@ -588,10 +632,21 @@ def bench_block_fp8(pkg, dev):
                 gemm(0)
             q_ms = cuda_timer(quant, it)
             ms = cuda_timer(gemm, it)
+            if m <= 64:  # launch-bound from Python: time the kernels in a graph
+                g_q = graph_timer(quant, 50, aq.view(torch.uint8))
+                g_ms = graph_timer(gemm, 50, o)
+                ms_eager, q_eager = ms, q_ms
+                ms = g_ms if g_ms is not None else ms
+                q_ms = g_q if g_q is not None else q_ms
             byts = n * k + prep.scale.numel() + m * k + m * (k // 128) + 2 * m * n
             fl = 2.0 * m * n * k
             entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2), "quant_us": round(q_ms * 1e3, 2),
                      "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+            if m <= 64:
+                entry["us_eager_python_loop"] = round(ms_eager * 1e3, 2)
+                entry["quant_us_eager_python_loop"] = round(q_eager * 1e3, 2)
+                entry["timing"] = ("hip graph of 50 calls" if g_ms is not None and g_q is not None
+                                   else "eager (graph replay mismatch)")
             entry["frac_of_peak"] = (round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if m <= 64
                                      else round(fl / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4))
             entry["bound"] = "hbm" if m <= 64 else "mfma (fp8)"
