@@ -793,8 +793,10 @@ int32_t dsv4_w8a16_split_k(int64_t m, int64_t n, int64_t k) {
   const int64_t tiles = ((n + 64 * r - 1) / (64 * r)) * ((m + 16 * c - 1) / (16 * c));
   const int64_t wins = k / kWin;
   int split = 1;
-  // widen over K until about two workgroups per CU, keeping >= 4 windows per split
-  while (split < 16 && tiles * split < 512 && wins / (split * 2) >= 4) split *= 2;
+  // widen over K until about two workgroups per CU, keeping >= 4 windows per
+  // split, at most 8 splits (16 measured slower at M = 1..64: the partial sums
+  // and the fewer windows per split cost more than the extra workgroups gain)
+  while (split < 8 && tiles * split < 512 && wins / (split * 2) >= 4) split *= 2;
   return split;
 }
 

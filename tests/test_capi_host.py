@@ -109,12 +109,12 @@ def test_w8a16_validation_and_split_policy():
     assert "workspace" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 4096, 2, need - 1))
     assert "multiple of 16" in _einval("dsv4moe_pack_int8", fake, 24, 128, fake, None)
     assert lib.dsv4moe_w8a16_linear(fake, 0, 64, 4096, fake, fake, 1, None, 0, fake, None) == _lib.DSV4MOE_OK
-    # this library's policy: a power of two in [1, 16] leaving >= 4 windows of 64 K per split,
+    # this library's policy: a power of two in [1, 8] leaving >= 4 windows of 64 K per split,
     # raised only while the grid is below 512 workgroups
     for m in (1, 16, 17, 64, 65, 8192):
         for n in (1024, 4096, 16384):
             split = lib.dsv4moe_w8a16_split_k(m, n, 4096)
-            assert split in (1, 2, 4, 8, 16)
+            assert split in (1, 2, 4, 8)
             assert 4096 // 64 // split >= 4
     assert lib.dsv4moe_w8a16_split_k(8192, 4096, 4096) == 1
     assert lib.dsv4moe_w8a16_split_k(1, 4096, 4096) > 1
