@@ -592,15 +592,23 @@ __global__ __launch_bounds__(256, 2) void w8a8_block_kernel(BlockFp8Params p) {
 // two blocks ahead of the compute; one s_waitcnt vmcnt(n) (n = one step's
 // copies, left in flight) and a barrier publish the next block.  No register
 // holds data in flight, so nothing the compiler moves can read it early.
-template <int R, int C>
-__global__ __launch_bounds__(256, 1) void w8a8_block_prefill_kernel(BlockFp8Params p) {
-  constexpr int kTokBytes = 16 * C * 128;
-  constexpr int kScaleTok = 16 * C / 4;  // tokens per wavefront's scale copy
+// H = 2: 8 wavefronts (two per SIMD) share each strip group's weights, wave
+// w taking strip group w % 4 and token half w / 4; each copies one of the two
+// 1 KiB weight tiles of its strips.
+template <int R, int C, int H>
+__global__ __launch_bounds__(256 * H, 1) void w8a8_block_prefill_kernel(BlockFp8Params p) {
+  constexpr int kWaves = 4 * H;
+  constexpr int kTokRows = 16 * C * H;
+  constexpr int kTokBytes = kTokRows * 128;
+  constexpr int kScaleTok = kTokRows / kWaves;  // tokens per wavefront's scale copy
+  static_assert(kScaleTok <= 64, "one scale copy per wavefront");
   __shared__ __attribute__((aligned(16))) uint8_t xs[3][kTokBytes];
   __shared__ __attribute__((aligned(16))) uint8_t wts[3][4][R * 2048];
-  __shared__ __attribute__((aligned(16))) uint32_t scs[3][4][64];
+  __shared__ __attribute__((aligned(16))) uint32_t scs[3][kWaves][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int sg = wave & 3;   // strip group
+  const int half = wave >> 2;  // token half (H = 2)
 
   const int items = p.split * p.tiles_m * p.tiles_n;
   const int per_xcd = (items + kLinXcds - 1) / kLinXcds;
@@ -615,8 +623,8 @@ __global__ __launch_bounds__(256, 1) void w8a8_block_prefill_kernel(BlockFp8Para
   const int nk = kb_end - kb_begin;
   const int wins = p.k / kWin;
   const int strips = p.n >> 4;
-  const int strip0 = tn * 4 * R + wave * R;
-  const int64_t tok0 = (int64_t)tm * 16 * C;
+  const int strip0 = tn * 4 * R + sg * R;
+  const int64_t tok0 = (int64_t)tm * kTokRows;
 
   const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.a, (short)0, (int)(p.m * p.k), kLinRsrcFlags);
@@ -625,13 +633,13 @@ __global__ __launch_bounds__(256, 1) void w8a8_block_prefill_kernel(BlockFp8Para
   const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.wq, (short)0, (int)((int64_t)p.n * p.k), kLinRsrcFlags);
 
-  constexpr int kActDma = 2 * C;
-  static_assert(kActDma % 4 == 0, "every wavefront issues the same number of token copies");
-  constexpr int kActPerWave = kActDma / 4;
+  constexpr int kActDma = kTokRows / 8;
+  static_assert(kActDma % kWaves == 0, "every wavefront issues the same number of token copies");
+  constexpr int kActPerWave = kActDma / kWaves;
   uint32_t a_off[kActPerWave];
 #pragma unroll
   for (int i = 0; i < kActPerWave; ++i) {
-    const int q = wave + 4 * i;
+    const int q = wave + kWaves * i;
     const int row = q * 8 + (lane >> 3);
     const int64_t tok = tok0 + row;
     const int part = (lane & 7) ^ swz128(row);
@@ -655,16 +663,18 @@ __global__ __launch_bounds__(256, 1) void w8a8_block_prefill_kernel(BlockFp8Para
   const int n16 = lane & 15;
   const int j = lane >> 4;
 
-  constexpr int kStepLoads = kActPerWave + 2 * R + 1;
+  constexpr int kStepLoads = kActPerWave + 2 * R / H + 1;
   static_assert(kStepLoads < 64, "vmcnt range");
   auto issue = [&](int kb, int buf) {
 #pragma unroll
     for (int i = 0; i < kActPerWave; ++i)
-      lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + 4 * i) * 1024]), a_off[i], kb * 128);
+      lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + kWaves * i) * 1024]), a_off[i], kb * 128);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 2048]), w_off[r], (2 * kb) * 1024);
-      lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 2048 + 1024]), w_off[r], (2 * kb + 1) * 1024);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        if (H == 1 || t == half)
+          lds_copy16(w_rsrc, lds_addr(&wts[buf][sg][r * 2048 + t * 1024]), w_off[r], (2 * kb + t) * 1024);
     }
     lds_copy4(as_rsrc, lds_addr(&scs[buf][wave][0]), s_off, kb & ~3);
   };
@@ -686,13 +696,13 @@ __global__ __launch_bounds__(256, 1) void w8a8_block_prefill_kernel(BlockFp8Para
     i32x8 wv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * 2048 + lane * 16]);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * 2048 + 1024 + lane * 16]);
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(&wts[u][sg][r * 2048 + lane * 16]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(&wts[u][sg][r * 2048 + 1024 + lane * 16]);
       wv[r] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     }
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      const int row = c * 16 + n16;
+      const int row = half * 16 * C + c * 16 + n16;
       const u32x4 lo = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((j ^ swz128(row)) * 16)]);
       const u32x4 hi = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + (((4 + j) ^ swz128(row)) * 16)]);
       const i32x8 tv = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
@@ -735,7 +745,7 @@ __global__ __launch_bounds__(256, 1) void w8a8_block_prefill_kernel(BlockFp8Para
     const int n = strip * 16 + 4 * j;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      const int64_t tok = tok0 + c * 16 + n16;
+      const int64_t tok = tok0 + half * 16 * C + c * 16 + n16;
       if (tok >= p.m) continue;
       const float v[4] = {acc[r][c][0], acc[r][c][1], acc[r][c][2], acc[r][c][3]};
       if (p.split == 1) {
@@ -752,8 +762,8 @@ __global__ __launch_bounds__(256, 1) void w8a8_block_prefill_kernel(BlockFp8Para
 static void launch_w8a8_block_kernel(const BlockFp8Params& p, int r, int c, hipStream_t stream) {
   const int items = p.split * p.tiles_m * p.tiles_n;
   const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
-  if (r == 4 && c == 8) hipLaunchKernelGGL((w8a8_block_prefill_kernel<4, 8>), grid, dim3(256), 0, stream, p);
-  else if (r == 4 && c == 4) hipLaunchKernelGGL((w8a8_block_prefill_kernel<4, 4>), grid, dim3(256), 0, stream, p);
+  if (r == 4 && c == 8) hipLaunchKernelGGL((w8a8_block_prefill_kernel<4, 4, 2>), grid, dim3(512), 0, stream, p);
+  else if (r == 4 && c == 4) hipLaunchKernelGGL((w8a8_block_prefill_kernel<4, 2, 2>), grid, dim3(512), 0, stream, p);
   else if (c == 1) hipLaunchKernelGGL((w8a8_block_kernel<2, 1>), grid, dim3(256), 0, stream, p);
   else if (c == 2) hipLaunchKernelGGL((w8a8_block_kernel<2, 2>), grid, dim3(256), 0, stream, p);
   else hipLaunchKernelGGL((w8a8_block_kernel<2, 4>), grid, dim3(256), 0, stream, p);
