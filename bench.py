@@ -422,7 +422,7 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args):
                 else:
                     ids.copy_(zipf_ids)
                 ops.align_into(ids, block_size=bs, num_experts=E, sorted_token_ids=sorted_ids,
-                               expert_ids=expert_ids, num_tokens_post_padded=ntpp)
+                               expert_ids=expert_ids, num_tokens_post_padded=ntpp, workspace=ws)
                 ops.experts_w4a8_into(x, w13q=resident.w13_q, w13s=resident.w13_s, w2q=resident.w2_q,
                                       w2s=resident.w2_s, experts=E, inter=I, has_shared=True, route_weights=w,
                                       sorted_token_ids=sorted_ids, expert_ids=expert_ids,
