@@ -87,3 +87,39 @@ def test_loaded_layer_matches_oracle(tmp_path):
     sh = [t.cpu().numpy() for t in shared_raw(raw, p, 0, I)]
     want = O.bf16_round(routed + O.shared_fp8_bf16(xf, *sh, 10.0))
     assert_moe_close(to_np_f32(out.view(64, H)), want, what="checkpoint layer")
+
+
+def test_loaded_hash_layer_matches_oracle(tmp_path):
+    """A hash-routed layer (the checkpoint's layers 0-2: gate.tid2eid, no
+    bias) loaded from the safetensors files: token ids pick the experts,
+    sqrt-softplus scores of the gate logits weight them (``moe_forward.py:
+    186-231``); MXFP4 routed experts plus the FP8 shared expert."""
+
+    print("[checkpoint] hash layer forward", flush=True)
+    vocab = 50
+    raw = write_checkpoint(tmp_path, layer_id=1, experts=E, hidden=H, inter=I, seed=6, hash_gate=True, vocab=vocab,
+                           topk=2)
+    res = C.load_resident_mxfp4_layer(stage_root=tmp_path, layer_id=1, hidden_size=H, intermediate_size=I,
+                                      n_experts=E, device=DEV)
+    gate = C.load_gate(stage_root=tmp_path, layer_id=1, experts=E, hidden_size=H, device=DEV)
+    assert gate.route_kind == "hash"
+    cfg = TP4MoEConfig(hidden_size=H, intermediate_size=I, experts=E, topk=2, route_scale=1.5, clamp_limit=10.0,
+                       score_func="sqrtsoftplus", shared_experts=1)
+    layer = TP4MoE(config=cfg, resident=res, gate=gate, device=DEV, global_row_shapes=[48])
+    x = S.make_hidden(48, H, seed=8, device=DEV).view(1, 48, H)
+    input_ids = torch.randint(0, vocab, (1, 48), device=DEV, generator=torch.Generator(DEV).manual_seed(3),
+                              dtype=torch.int64)
+    with layer.observe_route_tensors() as seen:
+        out, _ = layer(x, input_ids_local=input_ids)
+    torch.cuda.synchronize()
+    p = "layers.1.ffn"
+    ref = O.hash_route(seen[0].gate_logits.cpu().numpy(), raw[f"{p}.gate.tid2eid"].numpy(),
+                       input_ids.view(-1).cpu().numpy(), route_scale=1.5)
+    np.testing.assert_array_equal(seen[0].ids.cpu().numpy(), ref.ids)
+    w13, s13, w2, s2 = [t.cpu().numpy() for t in stacked(raw, p, range(E), 0, I)]
+    xf = to_np_f32(x.view(48, H))
+    routed = O.bf16_round(O.moe_fp32(xf, ref.ids, ref.weights, O.MXFP4ExpertSource(w13, s13, w2, s2),
+                                     shared_index=None, clamp_limit=10.0))
+    sh = [t.cpu().numpy() for t in shared_raw(raw, p, 0, I)]
+    want = O.bf16_round(routed + O.shared_fp8_bf16(xf, *sh, 10.0))
+    assert_moe_close(to_np_f32(out.view(48, H)), want, what="checkpoint hash layer")
