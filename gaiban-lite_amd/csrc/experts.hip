@@ -83,9 +83,14 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
   return it;
 }
 
-template <int STAGE>
-__global__ __launch_bounds__(256, 4) void expert_decode_kernel(ExpertGemmParams p) {
+// RING = 4: weights two groups ahead, four workgroups per CU (many items).
+// RING = 8: weights six groups ahead, for launches with fewer items than
+// resident workgroups (T ~ 1), where the bytes in flight per workgroup, not the
+// workgroup count, bound the stream; K must be a multiple of 8 groups.
+template <int STAGE, int RING>
+__global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(ExpertGemmParams p) {
   constexpr int R = 2;
+  constexpr int kAhead = RING - 2;
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * 256];  // part q of slot s at q ^ s
   __shared__ float red[4][16];
   const int lane = threadIdx.x & 63;
@@ -114,12 +119,12 @@ __global__ __launch_bounds__(256, 4) void expert_decode_kernel(ExpertGemmParams 
   int next = item + stride;
   DecodeItem nxt = next < n_items ? decode_item<STAGE>(p, next, routed, tk) : cur;
 
-  // Weights two groups ahead (ring 4), activations + sums one group ahead
-  // (ring 2).  At the end of an item the prefetches continue with the next
-  // item (or re-read the current one when there is none), so every load is
-  // unconditional and the compiler's vmcnt waits stay exact.
-  u32x4 W[4][R];
-  u32x4 S[4];
+  // Weights kAhead groups ahead (ring RING), activations + sums one group
+  // ahead (ring 2).  At the end of an item the prefetches continue with the
+  // next item (or re-read the current one when there is none), so every load
+  // is unconditional and the compiler's vmcnt waits stay exact.
+  u32x4 W[RING][R];
+  u32x4 S[RING];
   float CS[2][2];
   u32x4 xr;
 
@@ -136,8 +141,8 @@ __global__ __launch_bounds__(256, 4) void expert_decode_kernel(ExpertGemmParams 
 
   const uint32_t magic = dequant_magic();
   issue_x(cur, 0, CS[0]);
-  issue_w(cur, 0, W[0], S[0]);
-  issue_w(cur, 1, W[1], S[1]);
+#pragma unroll
+  for (int a = 0; a < kAhead; ++a) issue_w(cur, a, W[a], S[a]);
   *reinterpret_cast<u32x4*>(&xs[0][ld_lds]) = xr;
   __syncthreads();
 
@@ -145,14 +150,15 @@ __global__ __launch_bounds__(256, 4) void expert_decode_kernel(ExpertGemmParams 
     f32x4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int g0 = 0; g0 < groups; g0 += 4) {  // groups % 4 == 0 (checked on the host)
+    for (int g0 = 0; g0 < groups; g0 += RING) {  // groups % RING == 0 (checked on the host)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < RING; ++u) {
         const int g = g0 + u;
         const bool xn = g + 1 >= groups;  // the activation prefetch crosses into the next item
         issue_x(xn ? nxt : cur, xn ? 0 : g + 1, CS[(u + 1) & 1]);
-        const bool wn = g + 2 >= groups;
-        issue_w(wn ? nxt : cur, wn ? g + 2 - groups : g + 2, W[(u + 2) & 3], S[(u + 2) & 3]);
+        const bool wn = g + kAhead >= groups;
+        issue_w(wn ? nxt : cur, wn ? g + kAhead - groups : g + kAhead, W[(u + kAhead) % RING],
+                S[(u + kAhead) % RING]);
         // the MFMA chain starts from -136 * sum_g(x): it yields sum_g(q * x) directly
         const float nc = -kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
         const f32x4 init = {nc, nc, nc, nc};
@@ -499,7 +505,7 @@ using namespace dsv4;
 
 // Resident workgroups of a decode kernel on the current device (CUs x
 // occupancy), cached per device: the persistent grid size.
-template <int STAGE>
+template <int STAGE, int RING>
 static int decode_resident_grid() {
   static int cache[64] = {0};
   int dev = 0;
@@ -507,12 +513,28 @@ static int decode_resident_grid() {
   if (cache[dev] == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, expert_decode_kernel<STAGE>, 256, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, expert_decode_kernel<STAGE, RING>, 256, 0) !=
+            hipSuccess ||
         per_cu <= 0)
       per_cu = 1;
     cache[dev] = cus * per_cu;
   }
   return cache[dev];
+}
+
+// The decode launch of one stage: the deep-ring kernel when every item fits
+// in one wave of resident workgroups (few blocks, T ~ 1) and K allows it,
+// else the four-workgroups-per-CU kernel.  `blocks` bounds the active blocks
+// (the kernel reads the real count from the alignment on the device).
+template <int STAGE>
+static void launch_decode(const ExpertGemmParams& p, int blocks, hipStream_t stream) {
+  const int items = p.n_tiles * blocks;
+  if ((p.k_dim / kGroup) % 8 == 0 && items <= decode_resident_grid<STAGE, 8>()) {
+    hipLaunchKernelGGL((expert_decode_kernel<STAGE, 8>), dim3((unsigned)items), dim3(256), 0, stream, p);
+  } else {
+    const int grid = std::min(items, decode_resident_grid<STAGE, 4>());
+    hipLaunchKernelGGL((expert_decode_kernel<STAGE, 4>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  }
 }
 
 size_t dsv4_experts_workspace_bytes(int64_t tokens, int topk, int hidden, int inter,
@@ -586,8 +608,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.hsum_out = ws.hsum;
   if (decode) {
     p.n_tiles = inter / 64;
-    const int grid = std::min(p.n_tiles * blocks, decode_resident_grid<1>());
-    hipLaunchKernelGGL(expert_decode_kernel<1>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    launch_decode<1>(p, blocks, stream);
   } else {
     p.n_tiles = inter / 128;
     hipLaunchKernelGGL(expert_prefill_kernel<1>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)),
@@ -610,8 +631,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.out_cols = hidden;
   if (decode) {
     p.n_tiles = hidden / 128;
-    const int grid = std::min(p.n_tiles * blocks, decode_resident_grid<2>());
-    hipLaunchKernelGGL(expert_decode_kernel<2>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    launch_decode<2>(p, blocks, stream);
   } else {
     p.n_tiles = hidden / 256;
     hipLaunchKernelGGL(expert_prefill_kernel<2>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)),
