@@ -475,7 +475,8 @@ __global__ __launch_bounds__(256) void row_chunk_sum_kernel(const uint16_t* __re
   out[idx] = s;
 }
 
-// out[t][n] = bf16( sum_{j<k} contrib[t*k+j][n] + contrib[T*k+t][n] ).
+// out[t][n] = bf16( sum_{j<k} contrib[t*k+j][n] + contrib[T*k+t][n] ).  The
+// contributions are read once: nontemporal loads (T=8192: 195 -> 156 us).
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ contrib,
                                                       int64_t tokens, int topk, int hidden,
                                                       int has_shared, uint16_t* __restrict__ out) {
@@ -485,13 +486,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   const int64_t t = idx / vec;
   const int n = (int)(idx % vec) * 4;
   const float* base = contrib + (t * topk) * hidden + n;
-  f32x4 s = *reinterpret_cast<const f32x4*>(base);
+  f32x4 s = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base));
   for (int j = 1; j < topk; ++j) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(base + (int64_t)j * hidden);
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base + (int64_t)j * hidden));
     s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
   }
   if (has_shared) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(contrib + (tokens * topk + t) * hidden + n);
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(contrib + (tokens * topk + t) * hidden + n));
     s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
   }
   u32x2 o = {pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
