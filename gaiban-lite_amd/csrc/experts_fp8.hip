@@ -289,17 +289,19 @@ __global__ __launch_bounds__(256, 4) void expert_fp8_decode_kernel(ExpertGemmPar
 // same strip assignment and work order as the bf16 prefill kernel.  Per
 // group the 64 x 128 B token tile (16-byte part q of slot s at q ^ swz128(s)),
 // the slots' group sums and each wavefront's 4 weight tiles and scales are
-// copied into LDS by buffer_load ... lds, double buffered.
+// copied into LDS by buffer_load ... lds in a three-buffer ring, two groups
+// ahead of the compute (76 KiB per workgroup: still two per CU; one group of
+// 16 MFMAs per wavefront is too short to cover a copy issued one group ahead).
 constexpr int kF8Slots = 64;
 
 template <int STAGE>
 __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmParams p, int total_blocks) {
   constexpr int R = 4;
   constexpr int C = 4;
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kF8Slots * 128];
-  __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * kTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];
-  __shared__ float xsum[2][kF8Slots];
+  __shared__ __attribute__((aligned(16))) uint8_t xs[3][kF8Slots * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[3][4][R * kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t scl[3][4][256];
+  __shared__ float xsum[3][kF8Slots];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
@@ -363,9 +365,18 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
 
   const int sw = lane & 15;
   const int jg = lane >> 4;
-  auto step = [&](int g, auto u_c, auto prefetch_c) {
+  // copies one issue() makes per wavefront (wave 0 also the activation sums)
+  constexpr int kLoads = 2 + 4 + 1;
+  auto wait_step = [&]() {
+    if (wave == 0) lds_dma_wait_keep<kLoads + 1>();
+    else lds_dma_wait_keep<kLoads>();
+  };
+  // Step g: copy group g + 2 into buffer (u + 2) % 3 (released by step g - 1's
+  // barrier), compute group g from buffer u, wait for group g + 1.
+  auto step = [&](int g, auto u_c) {
     constexpr int u = decltype(u_c)::value;
-    if constexpr (decltype(prefetch_c)::value) issue(g + 1, (u + 1) & 1);
+    const bool issue2 = g + 2 < groups;
+    if (issue2) issue(g + 2, (u + 2) % 3);
     i32x8 bfr[C];
 #pragma unroll
     for (int ct = 0; ct < C; ++ct) {
@@ -391,23 +402,29 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * (tmp[ct][i] - corr[ct]);
     }
-    lds_dma_wait_all();  // this wavefront's copies of group g + 1 have landed
-    __syncthreads();     // ... and everyone's; buffer u is free again
+    if (issue2) wait_step();  // this wavefront's copies of group g + 1 have landed
+    else lds_dma_wait_all();
+    __syncthreads();          // ... and everyone's; buffer u is free again
   };
   using U0 = std::integral_constant<int, 0>;
   using U1 = std::integral_constant<int, 1>;
-  using PF = std::true_type;
-  using NOPF = std::false_type;
+  using U2 = std::integral_constant<int, 2>;
 
   issue(0, 0);
-  lds_dma_wait_all();
-  __syncthreads();
-  for (int g0 = 0; g0 + 2 < groups; g0 += 2) {
-    step(g0, U0{}, PF{});
-    step(g0 + 1, U1{}, PF{});
+  if (groups > 1) {
+    issue(1, 1);
+    wait_step();
+  } else {
+    lds_dma_wait_all();
   }
-  step(groups - 2, U0{}, PF{});
-  step(groups - 1, U1{}, NOPF{});
+  __syncthreads();
+  // the last two steps copy nothing and the last waits for everything, so no
+  // copy is outstanding at exit
+  for (int g = 0; g < groups; g += 3) {
+    step(g, U0{});
+    if (g + 1 < groups) step(g + 1, U1{});
+    if (g + 2 < groups) step(g + 2, U2{});
+  }
 
 #pragma unroll
   for (int ct = 0; ct < C; ++ct) {
