@@ -240,3 +240,26 @@ def test_w8a16_fp8_validation_and_e8m0_preflight():
         L.prepare_fp8_block_weight(codes, bad)
     with pytest.raises(TypeError, match="scale"):
         L.prepare_fp8_block_weight(codes, torch.zeros((1, 1), dtype=torch.uint8))
+
+
+def test_block_fp8_mirror_rejects_host_tensors_and_bad_dtypes():
+    """The fp8_linear mirror validates like the reference module before any
+    launch: device placement, dtypes, shapes, and the reserved E8M0 byte."""
+
+    from gaiban_lite_amd import fp8_linear as F
+
+    qp = F.make_quantization_plan(4, 256)
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="device"):
+        F.activation_quant_into(x, torch.empty(4, 256, dtype=F.FP8_DTYPE), torch.empty(4, 2, dtype=F.E8M0_DTYPE),
+                                plan=qp)
+    gp = F.make_gemm_plan(4, 64, 256, split_k=1)
+    with pytest.raises(ValueError, match="device"):
+        F.block_fp8_gemm_into(torch.empty(4, 256, dtype=F.FP8_DTYPE), torch.empty(4, 2, dtype=F.E8M0_DTYPE),
+                              torch.empty(64, 256, dtype=F.FP8_DTYPE), torch.empty(1, 2, dtype=F.E8M0_DTYPE),
+                              torch.empty(4, 64, dtype=torch.bfloat16), torch.empty(0), plan=gp)
+    bad = torch.full((2, 2), 255, dtype=torch.uint8).view(torch.float8_e8m0fnu)
+    with pytest.raises(ValueError, match="255"):
+        F.validate_e8m0_scale_values("w_scale", bad)
+    with pytest.raises(TypeError):
+        F.validate_e8m0_scale_values("w_scale", torch.zeros(2, 2, dtype=torch.uint8))
