@@ -157,3 +157,11 @@ def test_reference_api_round_trip():
                                codes.cpu().numpy(), scales.cpu().numpy())
     for out in (outs[0], outs[2]):
         assert_moe_close(to_np_f32(out), ref, what="reference API")
+
+
+@pytest.mark.parametrize("split", [2, 8])
+def test_prefill_kernel_with_explicit_split(split):
+    """The 8-wavefront prefill kernel over a K split (partials reduced in split order)."""
+
+    rows = np.sort(np.random.default_rng(split).choice(8192, 64, replace=False))
+    run(8192, 4096, 4096, split=split, rows=rows)

@@ -120,3 +120,11 @@ def test_scale_byte_zero_is_two_to_minus_127():
     np.testing.assert_array_equal(out[1], np.full(n, 448.0, dtype=np.float32))
     ref0 = 448.0 * 2.0 ** -127
     assert np.all(np.abs(out[0] - ref0) <= ref0 * 2.0 ** -6)
+
+
+@pytest.mark.parametrize("split", [2, 4])
+def test_prefill_tile_with_explicit_split(split):
+    """The 256 x 128 prefill tile (weights three buffers deep) over a K split."""
+
+    rows = np.sort(np.random.default_rng(split).choice(8192, 64, replace=False))
+    run(8192, 4096, 4096, split=split, rows=rows)
