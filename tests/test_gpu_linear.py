@@ -96,3 +96,10 @@ def test_zero_rows_and_contract_errors():
         L.make_gemm_plan(4, 64, 200)
     with pytest.raises(ValueError):
         L.make_gemm_plan(4, 64, 256, split_k=4)  # 2 K-blocks
+
+
+def test_prefill_tile_with_explicit_split():
+    """The 256 x 128 prefill tile (weights three buffers deep) over a K split."""
+
+    rows = np.sort(np.random.default_rng(7).choice(8192, 64, replace=False))
+    run(8192, 4096, 4096, split=2, rows=rows)
