@@ -477,6 +477,11 @@ __global__ __launch_bounds__(256) void row_chunk_sum_kernel(const uint16_t* __re
 
 // out[t][n] = bf16( sum_{j<k} contrib[t*k+j][n] + contrib[T*k+t][n] ).  The
 // contributions are read once: nontemporal loads (T=8192: 195 -> 156 us).
+// Up to kCombineBatch loads are issued before the first add instead of a
+// loop of load, wait, add; the adds keep the slot order, so the result is the
+// same bits.  Measured gain is small (T=64: 7.0 -> 6.7 us, against a ~6.4 us
+// floor at T=1; T=8192 unchanged).
+constexpr int kCombineBatch = 8;
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ contrib,
                                                       int64_t tokens, int topk, int hidden,
                                                       int has_shared, uint16_t* __restrict__ out) {
@@ -486,14 +491,28 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   const int64_t t = idx / vec;
   const int n = (int)(idx % vec) * 4;
   const float* base = contrib + (t * topk) * hidden + n;
-  f32x4 s = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base));
-  for (int j = 1; j < topk; ++j) {
-    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base + (int64_t)j * hidden));
-    s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
+  f32x4 sh = {0.f, 0.f, 0.f, 0.f};
+  if (has_shared)
+    sh = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(contrib + (tokens * topk + t) * hidden + n));
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < topk; j0 += kCombineBatch) {
+    f32x4 v[kCombineBatch];
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j)
+      if (j0 + j < topk)
+        v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base + (int64_t)(j0 + j) * hidden));
+#pragma unroll
+    for (int j = 0; j < kCombineBatch; ++j) {
+      if (j0 + j >= topk) break;
+      if (j0 + j == 0) {
+        s = v[0];
+      } else {
+        s[0] += v[j][0]; s[1] += v[j][1]; s[2] += v[j][2]; s[3] += v[j][3];
+      }
+    }
   }
   if (has_shared) {
-    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(contrib + (tokens * topk + t) * hidden + n));
-    s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
+    s[0] += sh[0]; s[1] += sh[1]; s[2] += sh[2]; s[3] += sh[3];
   }
   u32x2 o = {pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
   *reinterpret_cast<u32x2*>(out + t * hidden + n) = o;

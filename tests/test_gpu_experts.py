@@ -103,6 +103,13 @@ def test_tiny_shared_expert_layout():
     check_layer(shape, 50, seed=9)
 
 
+@pytest.mark.parametrize("shared", [False, True])
+def test_topk_above_one_combine_batch(shared):
+    """Ten slots per token: the combine reads them in two batches of loads."""
+    shape = S.LayerShape(experts=16, hidden=1024, inter=512, topk=10, has_shared=shared)
+    check_layer(shape, 40, seed=13)
+
+
 @pytest.mark.parametrize("t", [1, 8, 64, 256])
 def test_flash_decode(t):
     rows = np.unique(np.r_[np.arange(min(t, 6)), t - 1])
