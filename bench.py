@@ -99,17 +99,29 @@ def traffic_from_profile():
     return int(m.group(1)) if m else None
 
 
-def cuda_timer(fn, n):
+def cuda_timer(fn, n, per_step=None):
+    """Mean ms per call of `fn` over `n` calls, timed with events on the
+    current stream.  With `per_step` (a list), an event is also recorded
+    after every call and the per-call times are appended to it."""
+
     import torch
 
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(n)] if per_step is not None else None
     torch.cuda.synchronize()
     t0.record()
     for i in range(n):
         fn(i)
+        if marks is not None:
+            marks[i].record()
     t1.record()
     torch.cuda.synchronize()
+    if marks is not None:
+        prev = t0
+        for m in marks:
+            per_step.append(prev.elapsed_time(m))
+            prev = m
     return t0.elapsed_time(t1) / n
 
 
@@ -210,8 +222,10 @@ def main() -> int:
     # timed region: K steps with two HIP events per step around the roofline
     # kernel (stage 1), recorded by the library on the launch stream
     ops.profile_begin(args.steps, intervals=["stage1_w13"])
-    ms = cuda_timer(step, args.steps)
+    step_ms: list[float] = []
+    ms = cuda_timer(step, args.steps, per_step=step_ms)
     roof, ncalls = ops.profile_end()
+    log("[bench] headline per-step ms: " + " ".join(f"{v:.4f}" for v in step_ms))
     # the same steps with all seven stamps (per-kernel breakdown), and with none
     ops.profile_begin(args.steps)
     ms_all = cuda_timer(step, args.steps)

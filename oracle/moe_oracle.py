@@ -54,6 +54,7 @@ import numpy as np
 F32 = np.float32
 
 __all__ = [
+    "BF16_CASTS",
     "FP4_VALUES",
     "SCORE_SIGMOID",
     "SCORE_SOFTMAX",
@@ -629,6 +630,7 @@ def moe_fp32(
     shared_index: int | None = None,
     clamp_limit: float = 0.0,
     rows=None,
+    workers: int = 1,
 ) -> np.ndarray:
     """fp32 dequant oracle of the MoE layer (``a3_numerics.py:56-91``;
     official ``MoE.forward``, ``model.py:629-644``): per expert, gate/up in fp32,
@@ -637,6 +639,9 @@ def moe_fp32(
 
     ``rows`` optionally restricts the output to a subset of token rows (each
     token's output depends only on its own row), returning [len(rows), H].
+    ``workers`` > 1 dequantises and multiplies the experts on a thread pool
+    (numpy releases the GIL); the per-expert results are added in expert order
+    either way.
     """
 
     x = np.asarray(x, dtype=F32)
@@ -647,7 +652,8 @@ def moe_fp32(
         x, ids, weights = x[rows], ids[rows], weights[rows]
     t, h = x.shape
     y = np.zeros((t, h), dtype=F32)
-    for e in np.unique(ids):
+
+    def one_expert(e):
         tok, kk = np.nonzero(ids == e)
         w13 = experts.w13(int(e))
         inter = w13.shape[0] // 2
@@ -655,13 +661,41 @@ def moe_fp32(
         g = xe @ w13[:inter].T
         u = xe @ w13[inter:].T
         act = _swiglu(g, u, clamp_limit) * weights[tok, kk][:, None]
-        y[tok] += act.astype(F32) @ experts.w2(int(e)).T
+        return tok, act.astype(F32) @ experts.w2(int(e)).T
+
+    present = np.unique(ids)
+    if workers > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            parts = pool.map(one_expert, present)
+            for tok, part in parts:
+                y[tok] += part
+    else:
+        for e in present:
+            tok, part = one_expert(e)
+            y[tok] += part
     if shared_index is not None:
         w13 = experts.w13(shared_index)
         inter = w13.shape[0] // 2
         act = _swiglu(x @ w13[:inter].T, x @ w13[inter:].T, clamp_limit)
         y += act @ experts.w2(shared_index).T
     return y.astype(F32)
+
+
+# The bf16 casts of the reference's torch path, by name.  Each entry is
+# ``bf16_round``; the table exists so a CPU test can drop one rounding (plant
+# an op-order mistake in this oracle) and show that the comparison against
+# torch's own bf16 operations detects it.
+BF16_CASTS = {
+    name: bf16_round
+    for name in ("input", "weight", "gemm1_out", "hidden", "gemm2_out", "routed_sum", "shared_gemm1_out",
+                 "shared_hidden", "shared_out", "output")
+}
+
+
+def _cast(name: str, x) -> np.ndarray:
+    return BF16_CASTS[name](x)
 
 
 def moe_bf16_mirror(
@@ -687,7 +721,7 @@ def moe_bf16_mirror(
     ``workers`` > 1 runs the experts on a thread pool (numpy releases the GIL).
     """
 
-    x = bf16_round(np.asarray(x, dtype=F32))
+    x = _cast("input", np.asarray(x, dtype=F32))
     ids = np.asarray(ids)
     weights = np.asarray(weights, dtype=F32)
     if rows is not None:
@@ -699,11 +733,11 @@ def moe_bf16_mirror(
 
     def one_expert(e):
         tok, kk = np.nonzero(ids == e)
-        w13 = bf16_round(experts.w13(int(e)))
+        w13 = _cast("weight", experts.w13(int(e)))
         inter = w13.shape[0] // 2
-        proj = bf16_round(x[tok] @ w13.T)
-        hid = bf16_round(_swiglu(proj[:, :inter], proj[:, inter:], clamp_limit))
-        out = bf16_round(hid @ bf16_round(experts.w2(int(e))).T)
+        proj = _cast("gemm1_out", x[tok] @ w13.T)
+        hid = _cast("hidden", _swiglu(proj[:, :inter], proj[:, inter:], clamp_limit))
+        out = _cast("gemm2_out", hid @ _cast("weight", experts.w2(int(e))).T)
         contrib[tok, kk] = out * weights[tok, kk][:, None]
 
     if workers > 1:
@@ -717,16 +751,16 @@ def moe_bf16_mirror(
     routed = contrib[:, 0].copy()
     for j in range(1, k):
         routed = (routed + contrib[:, j]).astype(F32)
-    routed = bf16_round(routed)
+    routed = _cast("routed_sum", routed)
     if shared_index is None:
         return routed
-    w13 = bf16_round(experts.w13(shared_index))
+    w13 = _cast("weight", experts.w13(shared_index))
     inter = w13.shape[0] // 2
-    proj_g = bf16_round(x @ w13[:inter].T)
-    proj_u = bf16_round(x @ w13[inter:].T)
-    hid = bf16_round(_swiglu(proj_g, proj_u, clamp_limit))
-    shared = bf16_round(hid @ bf16_round(experts.w2(shared_index)).T)
-    return bf16_round(routed + shared)
+    proj_g = _cast("shared_gemm1_out", x @ w13[:inter].T)
+    proj_u = _cast("shared_gemm1_out", x @ w13[inter:].T)
+    hid = _cast("shared_hidden", _swiglu(proj_g, proj_u, clamp_limit))
+    shared = _cast("shared_out", hid @ _cast("weight", experts.w2(shared_index)).T)
+    return _cast("output", routed + shared)
 
 
 # ---------------------------------------------------------------------------

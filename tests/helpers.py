@@ -49,6 +49,44 @@ class DeviceExpertSource(O.ExpertSource):
         return self._get("w2", e)
 
 
+class DeviceMXFP4Source(O.MXFP4ExpertSource):
+    """Oracle accessor over device-resident MXFP4 experts (copied per expert)."""
+
+    def __init__(self, w13, s13, w2, s2):
+        super().__init__(w13, s13, w2, s2)
+        self._cache: dict[tuple[str, int], np.ndarray] = {}
+
+    def _get(self, which: str, e: int) -> np.ndarray:
+        key = (which, e)
+        if key not in self._cache:
+            if len(self._cache) > 64:
+                self._cache.clear()
+            if which == "w13":
+                v = O.dequant_mxfp4(self.w13_packed[e].cpu().numpy(), self.w13_scale[e].cpu().numpy())
+            else:
+                v = O.dequant_mxfp4(self.w2_packed[e].cpu().numpy(), self.w2_scale[e].cpu().numpy())
+            self._cache[key] = v
+        return self._cache[key]
+
+    def w13(self, e: int) -> np.ndarray:
+        return self._get("w13", e)
+
+    def w2(self, e: int) -> np.ndarray:
+        return self._get("w2", e)
+
+
+def block_cover_rows(sorted_token_ids, num_tokens_post_padded: int, block_size: int, tokens: int,
+                     topk: int) -> np.ndarray:
+    """One token of every alignment block (its first real slot), plus the
+    first and last token: a row set on which every expert block of the
+    grouped kernels contributes to some checked output row."""
+
+    s = np.asarray(sorted_token_ids)[:num_tokens_post_padded].reshape(-1, block_size)
+    firsts = s[:, 0]
+    assert (firsts < tokens * topk).all(), "an alignment block starts with padding"
+    return np.unique(np.r_[firsts // topk, 0, tokens - 1])
+
+
 def moe_errors(out, ref) -> dict:
     o = np.asarray(out, dtype=np.float64)
     r = np.asarray(ref, dtype=np.float64)

@@ -20,39 +20,13 @@ from gaiban_lite_amd import (
     synthetic as S,
 )
 from gaiban_lite_amd.deterministic_moe_align import deterministic_moe_align_block_size
-from helpers import assert_moe_close, np_tile_pack_mxfp4, to_np_f32
+from helpers import DeviceMXFP4Source, assert_moe_close, np_tile_pack_mxfp4, to_np_f32
 
 pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda:0")
 SMALL = S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True)
 _LAYERS: dict = {}
-
-
-class DeviceMXFP4Source(O.MXFP4ExpertSource):
-    """Oracle accessor over device-resident MXFP4 experts (copied per expert)."""
-
-    def __init__(self, w13, s13, w2, s2):
-        super().__init__(w13, s13, w2, s2)
-        self._cache = {}
-
-    def _get(self, which, e):
-        key = (which, e)
-        if key not in self._cache:
-            if len(self._cache) > 64:
-                self._cache.clear()
-            if which == "w13":
-                v = O.dequant_mxfp4(self.w13_packed[e].cpu().numpy(), self.w13_scale[e].cpu().numpy())
-            else:
-                v = O.dequant_mxfp4(self.w2_packed[e].cpu().numpy(), self.w2_scale[e].cpu().numpy())
-            self._cache[key] = v
-        return self._cache[key]
-
-    def w13(self, e):
-        return self._get("w13", e)
-
-    def w2(self, e):
-        return self._get("w2", e)
 
 
 def layer(shape, seed=0, scale_fn=None):
