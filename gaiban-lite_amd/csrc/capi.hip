@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -569,6 +570,82 @@ int dsv4moe_layer_mxfp4(const uint16_t* x, const float* logits, const float* bia
   return dsv4_launch_experts_mxfp4(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
                                    has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
                                    num_tokens_post_padded, block_size, clamp_limit, out, workspace, s);
+}
+
+// ------------------------------------------------ allocation-free layer entry
+// dsv4moe_layer_w4a16_noalloc keeps the experts workspace in this static
+// device array instead of a caller buffer.  Every GPU the library runs on
+// holds its own copy, at its own address, until the process ends.  In host
+// code `scratch` names a host-side stand-in, never the device memory: the
+// address passed to the kernels comes from hipGetSymbolAddress, taken once
+// per device with that device current and kept in g_noalloc_scratch.  The
+// array keeps the last call's contents; nothing in it needs to start at zero
+// (each call writes every workspace region before reading it).  Calls that
+// overlap on one GPU share the array and race.
+static __device__ __align__(256) unsigned char scratch[DSV4MOE_NOALLOC_SCRATCH_BYTES];
+
+static constexpr int kMaxScratchDevices = 64;
+static std::mutex g_noalloc_mutex;
+static void* g_noalloc_scratch[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on the device that runs `stream`.
+static int noalloc_scratch_address(hipStream_t stream, void** address) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    set_error("layer_w4a16_noalloc: hipGetDevice: %s", hipGetErrorString(err));
+    return DSV4MOE_EHIP;
+  }
+  if (stream != nullptr) {
+    hipDevice_t stream_dev = -1;
+    err = hipStreamGetDevice(stream, &stream_dev);
+    if (err != hipSuccess) {
+      set_error("layer_w4a16_noalloc: hipStreamGetDevice: %s", hipGetErrorString(err));
+      return DSV4MOE_EHIP;
+    }
+    DSV4_REQUIRE(stream_dev == dev, "layer_w4a16_noalloc: the stream runs on device %d but device %d is current",
+                 (int)stream_dev, dev);
+  }
+  DSV4_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "layer_w4a16_noalloc: device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+  if (g_noalloc_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      set_error("layer_w4a16_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                hipGetErrorString(err));
+      return DSV4MOE_EHIP;
+    }
+    g_noalloc_scratch[dev] = p;
+  }
+  *address = g_noalloc_scratch[dev];
+  return DSV4MOE_OK;
+}
+
+int dsv4moe_layer_w4a16_noalloc(const uint16_t* x, const float* logits, const float* bias,
+                                int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
+                                int32_t topk, int32_t score_func, float route_scale,
+                                const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
+                                const uint16_t* w2s, int32_t has_shared, float clamp_limit,
+                                int32_t block_size, int32_t* ids, float* weights, float* margin,
+                                int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                                int32_t* num_tokens_post_padded, uint16_t* out, void* stream) {
+  clear_error();
+  if (tokens == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(tokens > 0 && topk > 0 && hidden > 0 && inter > 0,
+               "layer_w4a16_noalloc: tokens, topk, hidden and inter must be positive");
+  const size_t need = dsv4_experts_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0);
+  DSV4_REQUIRE(need <= (size_t)DSV4MOE_NOALLOC_SCRATCH_BYTES,
+               "layer_w4a16_noalloc: %lld tokens need %zu bytes of workspace, more than the %zu-byte static "
+               "scratch; call dsv4moe_layer_w4a16 with a caller workspace",
+               (long long)tokens, need, (size_t)DSV4MOE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = noalloc_scratch_address(static_cast<hipStream_t>(stream), &ws);
+  if (rc != DSV4MOE_OK) return rc;
+  return dsv4moe_layer_w4a16(x, logits, bias, tokens, hidden, inter, experts, topk, score_func, route_scale, w13q,
+                             w13s, w2q, w2s, has_shared, clamp_limit, block_size, ids, weights, margin,
+                             sorted_token_ids, capacity, expert_ids, num_tokens_post_padded, out, ws,
+                             (size_t)DSV4MOE_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int dsv4moe_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed, void* stream) {

@@ -222,6 +222,28 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                         size_t workspace_bytes, void* stream);
 
 /*
+ * No counterpart in the reference.  The fused W4A16 layer call for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the arguments and results of
+ * dsv4moe_layer_w4a16 without the workspace, which the library keeps in a
+ * static device array of DSV4MOE_NOALLOC_SCRATCH_BYTES on each GPU it runs
+ * on (held until the process ends).  Calls whose workspace need
+ * (dsv4moe_experts_workspace_bytes) exceeds it fail with DSV4MOE_EINVAL before
+ * any launch: at H=4096, I=2048, top-6 with the shared expert that is above
+ * 464 tokens.  Calls that overlap on one GPU share the array and race.  The
+ * stream must belong to the current device.  Allocates nothing.
+ */
+#define DSV4MOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int dsv4moe_layer_w4a16_noalloc(const uint16_t* x, const float* logits, const float* bias,
+                                int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
+                                int32_t topk, int32_t score_func, float route_scale,
+                                const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
+                                const uint16_t* w2s, int32_t has_shared, float clamp_limit,
+                                int32_t block_size, int32_t* ids, float* weights, float* margin,
+                                int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                                int32_t* num_tokens_post_padded, uint16_t* out, void* stream);
+
+/*
  * MXFP4 experts: E2M1 codes with one E8M0 scale per 32 K, the checkpoint
  * format of the reference's routed experts (runtime/dsv4_direct/moe_forward.py:
  * 23-40,115-155; the MXFP4 Marlin path of ops/marlin_moe.py:173-223 and
