@@ -564,8 +564,11 @@ def bench_shared_fp8(pkg, gate, cfg, dev, T, args):
 
 def bench_w8a16(pkg, dev, fmt="int8"):
     """W8A16 dense linear, K = 4096, N in {4096, 1024, 16384}, M in {1, 64, 8192};
-    fmt "int8" (per-channel bf16 scales) or "fp8" (E4M3 with E8M0 128x128
-    block scales, the reference checkpoint's format)."""
+    fmt "int8" (per-channel bf16 scales, ``w8a16_int8_gemm_into``) or "fp8"
+    (E4M3 with E8M0 128x128 block scales, the reference checkpoint's format:
+    ``w8a16_gemm_into``), each on the weight as stored (row-major [N, K]) and
+    on the load-time tiles (``w8a16_prepared_gemm_into``, reported as
+    ``us_tiled``)."""
 
     import torch
 
@@ -577,47 +580,56 @@ def bench_w8a16(pkg, dev, fmt="int8"):
         if fmt == "fp8":
             q, s = S.make_fp8_block_linear(n, k, device=dev)
             prep = L.prepare_fp8_block_weight(q, s)
-            gemm = L.w8a16_fp8_gemm_into
+            w, ws_ = q.view(torch.float8_e4m3fn), s.view(torch.float8_e8m0fnu)
+            gemm = L.w8a16_gemm_into
             scale_bytes = s.numel()
         else:
             q, s = S.make_int8_linear(n, k, device=dev)
             prep = L.prepare_int8_weight(q, s)
-            gemm = L.w8a16_gemm_into
+            w, ws_ = q, s
+            gemm = L.w8a16_int8_gemm_into
             scale_bytes = 2 * n
-        del q
         for m in (1, 64, 8192):
             a = S.make_hidden(m, k, seed=6000 + m, device=dev)
             plan = L.make_gemm_plan(m, n, k)
             o = torch.empty(plan.output_shape, dtype=torch.bfloat16, device=dev)
-            ws = L.allocate_workspace(plan, dev)
-            for _ in range(3):
-                gemm(a, prep.packed, prep.scale, o, ws, plan=plan)
-            it = 50 if m < 8192 else 10
-            ms = cuda_timer(lambda i: gemm(a, prep.packed, prep.scale, o, ws, plan=plan), it)
-            if m <= 64:  # launch-bound from Python: time the kernels in a graph
-                g_ms = graph_timer(lambda i: gemm(a, prep.packed, prep.scale, o, ws, plan=plan), 50, o)
-                ms_eager, ms = ms, (g_ms if g_ms is not None else ms)
+            wsp = L.allocate_workspace(plan, dev)
+            calls = {"rowmajor": lambda i: gemm(a, w, ws_, o, wsp, plan=plan),
+                     "tiled": lambda i: L.w8a16_prepared_gemm_into(a, prep, o, wsp, plan=plan)}
+            times, eager = {}, {}
+            for layout, fn in calls.items():
+                for _ in range(3):
+                    fn(0)
+                it = 50 if m < 8192 else 10
+                ms = cuda_timer(fn, it)
+                if m <= 64:  # launch-bound from Python: time the kernels in a graph
+                    g_ms = graph_timer(fn, 50, o)
+                    eager[layout], ms = ms, (g_ms if g_ms is not None else ms)
+                times[layout] = ms
+            ms = times["rowmajor"]
             byts = n * k + scale_bytes + 2 * m * k + 2 * m * n
             fl = 2.0 * m * n * k
-            entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2),
+            entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2), "us_tiled": round(times["tiled"] * 1e3, 2),
                      "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
             if m <= 64:
-                entry["us_eager_python_loop"] = round(ms_eager * 1e3, 2)
-                entry["timing"] = "hip graph of 50 calls" if g_ms is not None else "eager (graph replay mismatch)"
+                entry["us_eager_python_loop"] = round(eager["rowmajor"] * 1e3, 2)
+                entry["timing"] = "hip graph of 50 calls"
             entry["frac_of_peak"] = (round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if m <= 64
                                      else round(fl / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4))
             entry["bound"] = "hbm" if m <= 64 else "mfma"
             out[f"M{m}_N{n}"] = entry
             log(f"[bench] w8a16 {fmt} M={m} N={n}: {entry}")
-            del a, o, ws
-        del prep
+            del a, o, wsp
+        del prep, q, w
     return out
 
 
 def bench_block_fp8(pkg, dev):
     """Block-FP8 W8A8 dense linear (fp8_linear.py): K = 4096, N in {4096, 1024,
     16384}, M in {1, 64, 8192}; the bf16 -> E4M3 activation quantiser and the
-    GEMM timed separately (the reference launches them separately)."""
+    GEMM timed separately (the reference launches them separately); the GEMM
+    on the checkpoint weight as stored and on the load-time tiles
+    (``us_tiled``)."""
 
     import torch
 
@@ -629,7 +641,7 @@ def bench_block_fp8(pkg, dev):
     for n in (4096, 1024, 16384):
         q, s = S.make_fp8_block_linear(n, k, device=dev)
         prep = L.prepare_fp8_block_weight(q, s)
-        del q
+        w, w_s = q.view(torch.float8_e4m3fn), s.view(torch.float8_e8m0fnu)
         for m in (1, 64, 8192):
             x = S.make_hidden(m, k, seed=7000 + m, device=dev)
             qp = F.make_quantization_plan(m, k)
@@ -640,34 +652,40 @@ def bench_block_fp8(pkg, dev):
             ws = torch.empty(plan.workspace_shape, dtype=torch.float32, device=dev)
             it = 50 if m < 8192 else 10
             quant = lambda i: F.activation_quant_into(x, aq, a_s, plan=qp)
-            gemm = lambda i: F.block_fp8_gemm_into(aq, a_s, prep, None, o, ws, plan=plan)
-            for _ in range(3):
-                quant(0)
-                gemm(0)
+            gemms = {"rowmajor": lambda i: F.block_fp8_gemm_into(aq, a_s, w, w_s, o, ws, plan=plan),
+                     "tiled": lambda i: F.block_fp8_gemm_into(aq, a_s, prep, None, o, ws, plan=plan)}
+            quant(0)
             q_ms = cuda_timer(quant, it)
-            ms = cuda_timer(gemm, it)
-            if m <= 64:  # launch-bound from Python: time the kernels in a graph
+            if m <= 64:
+                q_eager = q_ms
                 g_q = graph_timer(quant, 50, aq.view(torch.uint8))
-                g_ms = graph_timer(gemm, 50, o)
-                ms_eager, q_eager = ms, q_ms
-                ms = g_ms if g_ms is not None else ms
                 q_ms = g_q if g_q is not None else q_ms
+            times, eager = {}, {}
+            for layout, fn in gemms.items():
+                for _ in range(3):
+                    fn(0)
+                ms = cuda_timer(fn, it)
+                if m <= 64:  # launch-bound from Python: time the kernels in a graph
+                    g_ms = graph_timer(fn, 50, o)
+                    eager[layout], ms = ms, (g_ms if g_ms is not None else ms)
+                times[layout] = ms
+            ms = times["rowmajor"]
             byts = n * k + prep.scale.numel() + m * k + m * (k // 128) + 2 * m * n
             fl = 2.0 * m * n * k
-            entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2), "quant_us": round(q_ms * 1e3, 2),
+            entry = {"split_k": plan.split_k, "us": round(ms * 1e3, 2), "us_tiled": round(times["tiled"] * 1e3, 2),
+                     "quant_us": round(q_ms * 1e3, 2),
                      "hbm_gbs": round(byts / (ms * 1e-3) / 1e9, 1), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
             if m <= 64:
-                entry["us_eager_python_loop"] = round(ms_eager * 1e3, 2)
+                entry["us_eager_python_loop"] = round(eager["rowmajor"] * 1e3, 2)
                 entry["quant_us_eager_python_loop"] = round(q_eager * 1e3, 2)
-                entry["timing"] = ("hip graph of 50 calls" if g_ms is not None and g_q is not None
-                                   else "eager (graph replay mismatch)")
+                entry["timing"] = "hip graph of 50 calls"
             entry["frac_of_peak"] = (round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4) if m <= 64
                                      else round(fl / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4))
             entry["bound"] = "hbm" if m <= 64 else "mfma (fp8)"
             out[f"M{m}_N{n}"] = entry
             log(f"[bench] w8a8 block fp8 M={m} N={n}: {entry}")
             del x, aq, a_s, o, ws
-        del prep
+        del prep, q, w
     return out
 
 

@@ -16,7 +16,7 @@ from __future__ import annotations
 
 import sys
 
-from . import _lib, build_ext, ops, synthetic, weights  # noqa: F401
+from . import _lib, build_ext, contracts, linear_plan, ops, synthetic, weights  # noqa: F401
 from . import checkpoint, deterministic_moe_align, fp8_linear, moe_forward, moe_runtime, weight_only_linear  # noqa: F401
 from .deterministic_moe_align import (  # noqa: F401
     DeterministicMoEAlignment,
@@ -36,7 +36,10 @@ from .moe_forward import (  # noqa: F401
 )
 from .moe_runtime import (  # noqa: F401
     MoELayer,
+    MoERouteCaptureBuffer,
+    MoERouteCaptureEvidence,
     MoERouteOverride,
+    MoERouteTensors,
     MoETrace,
     ResidentGateWeights,
     TP4MoE,

@@ -22,6 +22,8 @@ DSV4MOE_EHIP = 2
 SCORE_FUNCS = {"sigmoid": 0, "softmax": 1, "sqrtsoftplus": 2}
 PAIR_PLAIN = 0
 PAIR_GATED = 1
+WEIGHT_TILED = 0
+WEIGHT_ROWMAJOR = 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -49,7 +51,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_act_quant_block_fp8": (ctypes.c_int, [_p, _i32, _i64, _i64, _p, _p, _p]),
     "dsv4moe_block_fp8_split_k": (_i32, [_i64, _i64, _i64]),
     "dsv4moe_block_fp8_workspace_bytes": (_sz, [_i64, _i64, _i32]),
-    "dsv4moe_block_fp8_gemm": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),
+    "dsv4moe_block_fp8_gemm": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _p, _i32, _p, _i32, _p, _sz, _p, _p]),
     "dsv4moe_align_ws": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _sz, _p]),
     "dsv4moe_pack_int4_g128": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p]),
     "dsv4moe_experts_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
@@ -89,8 +91,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_act_quant_fp8": (ctypes.c_int, [_p, _i64, _i32, _p, _p, _p, _p]),
     "dsv4moe_w8a16_split_k": (_i32, [_i64, _i64, _i64]),
     "dsv4moe_w8a16_workspace_bytes": (_sz, [_i64, _i64, _i32]),
-    "dsv4moe_w8a16_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),
-    "dsv4moe_w8a16_fp8_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p, _i32, _p, _sz, _p, _p]),
+    "dsv4moe_w8a16_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i32, _p, _i32, _p, _sz, _p, _p]),
+    "dsv4moe_w8a16_fp8_linear": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i32, _p, _i32, _p, _sz, _p, _p]),
     "dsv4moe_shared_fp8_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "dsv4moe_shared_fp8_add": (ctypes.c_int, [_p, _i64, _i32, _i32, _p, _p, _p, _p, ctypes.c_float, _p, _p, _sz,
                                               _p]),

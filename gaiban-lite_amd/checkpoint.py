@@ -63,49 +63,51 @@ def load_weight_map(stage_root: Path) -> tuple[dict[str, str], dict[str, Any]]:
 
 
 class ShardReader:
-    """Resolves tensor keys through the index weight_map and caches open
-    safetensors handles (``marlin_moe.py:225-262``)."""
+    """Tensors of a checkpoint, found only through the index ``weight_map``
+    (the Flash runtime's sole shard-resolution rule, ``marlin_moe.py:225-262``).
+
+    Each shard file is opened at most once, on first use, and stays open
+    until ``close()`` (or the end of a ``with`` block).  A key the index does
+    not list raises KeyError; a listed file outside the checkpoint directory
+    raises CheckpointContractError."""
 
     def __init__(self, stage_root: Path, weight_map: dict[str, str]):
-        self._root = Path(stage_root)
-        self._weight_map = weight_map
-        self._handles: dict[str, Any] = {}
+        self._root = Path(stage_root).resolve()
+        self._file_of = dict(weight_map)
+        self._open_files: dict[str, Any] = {}
 
-    def _handle(self, key: str) -> Any:
-        try:
-            filename = self._weight_map[key]
-        except KeyError as error:
-            raise KeyError(f"tensor key not in index weight_map: {key}") from error
-        handle = self._handles.get(filename)
-        if handle is None:
+    def _shard(self, key: str) -> Any:
+        name = self._file_of.get(key)
+        if name is None:
+            raise KeyError(f"{key!r} is not listed in the index weight_map")
+        shard = self._open_files.get(name)
+        if shard is None:
+            path = (self._root / name).resolve()
+            if self._root not in path.parents:
+                raise CheckpointContractError(f"weight_map names a file outside the checkpoint: {name}")
             from safetensors import safe_open
 
-            path = (self._root / filename).resolve()
-            if self._root.resolve() not in path.parents:
-                raise CheckpointContractError(f"weight_map names a file outside the checkpoint: {filename}")
-            handle = safe_open(str(path), framework="pt", device="cpu")
-            self._handles[filename] = handle
-        return handle
+            shard = self._open_files[name] = safe_open(str(path), framework="pt", device="cpu")
+        return shard
 
     def get_slice(self, key: str) -> Any:
-        return self._handle(key).get_slice(key)
+        return self._shard(key).get_slice(key)
 
     def get_tensor(self, key: str) -> torch.Tensor:
-        return self._handle(key).get_tensor(key)
+        return self._shard(key).get_tensor(key)
 
     def read(self, key: str, index: Any = None) -> torch.Tensor:
-        """The tensor, or the slice ``index`` of it, as a contiguous CPU tensor."""
+        """The tensor, or its slice ``index``, as a contiguous CPU tensor."""
 
-        if index is None:
-            return self.get_tensor(key).contiguous()
-        return self.get_slice(key)[index].contiguous()
+        t = self.get_tensor(key) if index is None else self.get_slice(key)[index]
+        return t.contiguous()
 
     def close(self) -> None:
-        for handle in self._handles.values():
-            close = getattr(handle, "close", None)
-            if callable(close):
-                close()
-        self._handles.clear()
+        shards, self._open_files = list(self._open_files.values()), {}
+        for shard in shards:
+            closer = getattr(shard, "close", None)
+            if callable(closer):
+                closer()
 
     def __enter__(self) -> "ShardReader":
         return self

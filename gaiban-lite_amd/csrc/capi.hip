@@ -109,11 +109,11 @@ int32_t dsv4_w8a16_split_k(int64_t, int64_t, int64_t);
 int32_t dsv4_block_fp8_split_k(int64_t, int64_t, int64_t);
 int dsv4_launch_act_quant_block_fp8(const void*, int32_t, int64_t, int64_t, uint8_t*, uint8_t*, hipStream_t);
 int dsv4_launch_block_fp8_gemm(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, const uint8_t*,
-                               const uint8_t*, int32_t, float*, uint16_t*, hipStream_t);
+                               const uint8_t*, int32_t, float*, uint16_t*, hipStream_t, int w_rowmajor);
 size_t dsv4_w8a16_workspace_bytes(int64_t, int64_t, int32_t);
 int dsv4_launch_pack_int8(const int8_t*, int64_t, int64_t, uint8_t*, hipStream_t);
 int dsv4_launch_w8a16(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, const uint16_t*,
-                      const uint8_t*, int32_t, float*, uint16_t*, hipStream_t, int accumulate);
+                      const uint8_t*, int32_t, float*, uint16_t*, hipStream_t, int accumulate, int w_rowmajor);
 size_t dsv4_shared_fp8_workspace_bytes(int64_t, int, int);
 int dsv4_launch_shared_fp8_add(const uint16_t*, int64_t, int, int, const uint8_t*, const uint8_t*, const uint8_t*,
                                const uint8_t*, float, uint16_t*, void*, hipStream_t);
@@ -141,7 +141,7 @@ extern "C" {
 
 const char* dsv4moe_last_error(void) { return dsv4host::g_error; }
 
-int32_t dsv4moe_abi_version(void) { return 1; }
+int32_t dsv4moe_abi_version(void) { return 2; }
 
 int dsv4moe_profile_begin(int32_t max_calls) {
   return dsv4moe_profile_begin_stamps(max_calls, (1u << dsv4host::kNumStamps) - 1u);
@@ -667,9 +667,11 @@ size_t dsv4moe_w8a16_workspace_bytes(int64_t m, int64_t n, int32_t split_k) {
 
 // Shared checks of the two W8A16 entry points (who = entry name).
 static int validate_w8a16(const char* who, const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
-                          const void* scales, int32_t split_k, float* workspace, size_t workspace_bytes,
-                          uint16_t* out) {
+                          int32_t weight_layout, const void* scales, int32_t split_k, float* workspace,
+                          size_t workspace_bytes, uint16_t* out) {
   DSV4_REQUIRE(m >= 0, "%s: m must be >= 0", who);
+  DSV4_REQUIRE(weight_layout == DSV4MOE_WEIGHT_TILED || weight_layout == DSV4MOE_WEIGHT_ROWMAJOR,
+               "%s: unknown weight_layout %d", who, weight_layout);
   DSV4_REQUIRE(n > 0 && n % 16 == 0, "%s: n must be a positive multiple of 16, got %lld", who, (long long)n);
   DSV4_REQUIRE(k > 0 && k % 128 == 0, "%s: k must be a positive multiple of 128, got %lld", who, (long long)k);
   DSV4_REQUIRE(split_k == 1 || split_k == 2 || split_k == 4 || split_k == 8 || split_k == 16,
@@ -691,25 +693,27 @@ static int validate_w8a16(const char* who, const uint16_t* a, int64_t m, int64_t
 }
 
 int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
-                         const uint16_t* ws, int32_t split_k, float* workspace,
+                         int32_t weight_layout, const uint16_t* ws, int32_t split_k, float* workspace,
                          size_t workspace_bytes, uint16_t* out, void* stream) {
   clear_error();
-  int rc = validate_w8a16("w8a16_linear", a, m, n, k, wq, ws, split_k, workspace, workspace_bytes, out);
+  int rc = validate_w8a16("w8a16_linear", a, m, n, k, wq, weight_layout, ws, split_k, workspace, workspace_bytes,
+                          out);
   if (rc != DSV4MOE_OK || m == 0) return rc;
   DSV4_REQUIRE(aligned(ws, 8), "w8a16_linear: ws must be 8-byte aligned");
   return dsv4_launch_w8a16(a, m, n, k, wq, ws, nullptr, split_k, workspace, out,
-                           static_cast<hipStream_t>(stream), 0);
+                           static_cast<hipStream_t>(stream), 0, weight_layout == DSV4MOE_WEIGHT_ROWMAJOR);
 }
 
 int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
-                             const uint8_t* ws8, int32_t split_k, float* workspace, size_t workspace_bytes,
-                             uint16_t* out, void* stream) {
+                             int32_t weight_layout, const uint8_t* ws8, int32_t split_k, float* workspace,
+                             size_t workspace_bytes, uint16_t* out, void* stream) {
   clear_error();
-  int rc = validate_w8a16("w8a16_fp8_linear", a, m, n, k, wq, ws8, split_k, workspace, workspace_bytes, out);
+  int rc = validate_w8a16("w8a16_fp8_linear", a, m, n, k, wq, weight_layout, ws8, split_k, workspace,
+                          workspace_bytes, out);
   if (rc != DSV4MOE_OK || m == 0) return rc;
   DSV4_REQUIRE(k <= 32768, "w8a16_fp8_linear: k must be <= 32768, got %lld", (long long)k);
   return dsv4_launch_w8a16(a, m, n, k, wq, nullptr, ws8, split_k, workspace, out,
-                           static_cast<hipStream_t>(stream), 0);
+                           static_cast<hipStream_t>(stream), 0, weight_layout == DSV4MOE_WEIGHT_ROWMAJOR);
 }
 
 int32_t dsv4moe_block_fp8_split_k(int64_t m, int64_t n, int64_t k) { return dsv4_block_fp8_split_k(m, n, k); }
@@ -734,11 +738,13 @@ int dsv4moe_act_quant_block_fp8(const void* x, int32_t x_dtype, int64_t m, int64
 }
 
 int dsv4moe_block_fp8_gemm(const uint8_t* a, const uint8_t* a_scale, int64_t m, int64_t n, int64_t k,
-                           const uint8_t* wq, const uint8_t* w_scale, int32_t split_k, float* workspace,
-                           size_t workspace_bytes, uint16_t* out, void* stream) {
+                           const uint8_t* wq, int32_t weight_layout, const uint8_t* w_scale, int32_t split_k,
+                           float* workspace, size_t workspace_bytes, uint16_t* out, void* stream) {
   clear_error();
   const char* who = "block_fp8_gemm";
   DSV4_REQUIRE(m >= 0, "%s: m must be >= 0", who);
+  DSV4_REQUIRE(weight_layout == DSV4MOE_WEIGHT_TILED || weight_layout == DSV4MOE_WEIGHT_ROWMAJOR,
+               "%s: unknown weight_layout %d", who, weight_layout);
   DSV4_REQUIRE(n > 0 && n % 16 == 0, "%s: n must be a positive multiple of 16, got %lld", who, (long long)n);
   DSV4_REQUIRE(k > 0 && k % 128 == 0 && k <= 32768, "%s: k must be a multiple of 128 in [128, 32768], got %lld", who,
                (long long)k);
@@ -756,7 +762,7 @@ int dsv4moe_block_fp8_gemm(const uint8_t* a, const uint8_t* a_scale, int64_t m, 
   DSV4_REQUIRE(need == 0 || (workspace && aligned(workspace, 16)), "%s: split_k > 1 needs a 16-byte aligned workspace",
                who);
   return dsv4_launch_block_fp8_gemm(a, a_scale, m, n, k, wq, w_scale, split_k, workspace, out,
-                                    static_cast<hipStream_t>(stream));
+                                    static_cast<hipStream_t>(stream), weight_layout == DSV4MOE_WEIGHT_ROWMAJOR);
 }
 
 size_t dsv4moe_shared_fp8_workspace_bytes(int64_t tokens, int32_t hidden, int32_t inter) {

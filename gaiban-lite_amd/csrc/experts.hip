@@ -56,7 +56,7 @@ struct DecodeItem {
   uint32_t ld_base;    // loader thread: activation row offset of its slot (or out of range)
   uint32_t sum_base;   // lane: row-sum offset of its slot (or out of range)
   int64_t rowid;       // lane: row id of its slot, -1 if padded
-  int n0;
+  int n0;  bool poison;         // the block names no valid expert (NaN contributions)
 };
 
 template <int STAGE>
@@ -74,6 +74,7 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
   it.ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
+  it.poison = b.poison;
   it.rowid = slot_rowid(p, b, lane & 15, tk);
   const int64_t arow = act_row_of<STAGE>(it.rowid, tk, p.topk);
   it.sum_base = arow >= 0 ? (uint32_t)(arow * sums_per_row * 4) : kOobOffset;
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(E
       }
     } else {
       if (rowid >= 0) {
-        const float wr = rowid < tk ? p.route_w[rowid] : 1.0f;
+        const float wr = cur.poison ? __builtin_nanf("") : (rowid < tk ? p.route_w[rowid] : 1.0f);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
@@ -439,7 +440,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
     for (int ct = 0; ct < C; ++ct) {
       const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
       if (rowid < 0) continue;
-      const float wr = rowid < tk ? p.route_w[rowid] : 1.0f;
+      const float wr = contrib_weight(p, b, rowid, tk);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int n = n0 + 64 * wave + 16 * r + 4 * (lane >> 4);
@@ -481,8 +482,12 @@ __global__ __launch_bounds__(256) void row_chunk_sum_kernel(const uint16_t* __re
 // loop of load, wait, add; the adds keep the slot order, so the result is the
 // same bits.  Measured gain is small (T=64: 7.0 -> 6.7 us, against a ~6.4 us
 // floor at T=1; T=8192 unchanged).
+// An alignment that reports a negative padded count (the alignment kernel's
+// answer to a route id outside [0, experts)) ran no routed block, so the
+// contributions were never written: every output is NaN instead.
 constexpr int kCombineBatch = 8;
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ contrib,
+                                                      const int32_t* __restrict__ ntpp,
                                                       int64_t tokens, int topk, int hidden,
                                                       int has_shared, uint16_t* __restrict__ out) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -490,6 +495,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
   if (idx >= tokens * vec) return;
   const int64_t t = idx / vec;
   const int n = (int)(idx % vec) * 4;
+  if (ntpp[0] < 0) {
+    *reinterpret_cast<u32x2*>(out + t * hidden + n) = u32x2{0x7FC07FC0u, 0x7FC07FC0u};
+    return;
+  }
   const float* base = contrib + (t * topk) * hidden + n;
   f32x4 sh = {0.f, 0.f, 0.f, 0.f};
   if (has_shared)
@@ -609,6 +618,8 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   p.block_size = block_size;
   p.shared_block_size = shared_bs;
   p.max_blocks = max_blocks;
+  p.full_blocks = (int)(capacity / block_size);
+  p.experts = experts;
   p.tokens = tokens;
   p.topk = topk;
   p.shared_expert = has_shared ? experts : -1;
@@ -660,17 +671,17 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   DSV4_CHECK_LAUNCH("expert stage 2");
   dsv4host::prof_stamp(dsv4host::kStampStage2, stream);
 
-  const int rc = dsv4_launch_combine(ws.contrib, tokens, topk, hidden, has_shared, out, stream);
+  const int rc = dsv4_launch_combine(ws.contrib, ntpp, tokens, topk, hidden, has_shared, out, stream);
   if (rc != DSV4MOE_OK) return rc;
   dsv4host::prof_stamp(dsv4host::kStampCombine, stream);
   return DSV4MOE_OK;
 }
 
-int dsv4_launch_combine(const float* contrib, int64_t tokens, int topk, int hidden, int has_shared,
-                        uint16_t* out, hipStream_t stream) {
+int dsv4_launch_combine(const float* contrib, const int32_t* ntpp, int64_t tokens, int topk, int hidden,
+                        int has_shared, uint16_t* out, hipStream_t stream) {
   const int64_t n = tokens * (hidden / 4);
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                     contrib, tokens, topk, hidden, has_shared, out);
+                     contrib, ntpp, tokens, topk, hidden, has_shared, out);
   DSV4_CHECK_LAUNCH("combine_kernel");
   return DSV4MOE_OK;
 }

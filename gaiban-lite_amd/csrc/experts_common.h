@@ -26,7 +26,9 @@ struct ExpertGemmParams {
   const int32_t* ntpp;
   int block_size;
   int shared_block_size; // token slots per shared-expert block
-  int max_blocks;
+  int max_blocks;        // ceil(capacity / block_size): routed blocks before the shared ones
+  int full_blocks;       // capacity / block_size: routed blocks that lie inside `sorted`
+  int experts;           // routed experts: a block expert id outside [0, experts) is poisoned
   int n_tiles;
   int64_t tokens;
   int topk;
@@ -46,22 +48,39 @@ struct BlockInfo {
   int64_t slot_base;
   bool shared;
   bool active;
+  bool poison;  // the alignment names no valid expert: results of this block are NaN
 };
 
+// The alignment comes from the caller (or a caller's provider), so it is not
+// trusted for addressing: a routed block is active only below both the padded
+// count and the blocks that fit the capacity, and an active block whose expert
+// id is outside [0, experts) reads expert 0's weights (in bounds) and marks its
+// stage-2 contributions NaN, so the damage shows in the output.
 __device__ __forceinline__ BlockInfo block_info(const ExpertGemmParams& p, int blk) {
   BlockInfo b;
   b.shared = blk >= p.max_blocks;
   b.active = true;
+  b.poison = false;
   if (!b.shared) {
     const int total = p.ntpp[0];
-    b.active = total > 0 && (int64_t)blk * p.block_size < total;
-    b.expert = b.active ? p.expert_ids[blk] : 0;
+    b.active = total > 0 && blk < p.full_blocks && (int64_t)blk * p.block_size < total;
+    const int e = b.active ? p.expert_ids[blk] : 0;
+    b.poison = (unsigned)e >= (unsigned)p.experts;
+    b.expert = b.poison ? 0 : e;
     b.slot_base = (int64_t)blk * p.block_size;
   } else {
     b.expert = p.shared_expert;
     b.slot_base = (int64_t)(blk - p.max_blocks) * p.shared_block_size;
   }
   return b;
+}
+
+// Stage-2 multiplier of a contribution row: the route weight (1 for the
+// shared expert), NaN in a poisoned block.
+__device__ __forceinline__ float contrib_weight(const ExpertGemmParams& p, const BlockInfo& b, int64_t rowid,
+                                               int64_t tk) {
+  const float w = rowid < tk ? p.route_w[rowid] : 1.0f;
+  return b.poison ? __builtin_nanf("") : w;
 }
 
 // Row id (index into h / contrib) of token column `col` of a block, -1 if padded.
@@ -95,7 +114,8 @@ __device__ __forceinline__ void scale4(u32x2 sv, float (&sc)[4]) {
 // N tiles.
 __device__ __forceinline__ int decode_routed_blocks(const ExpertGemmParams& p) {
   const int total = p.ntpp[0];
-  return total > 0 ? (total + p.block_size - 1) / p.block_size : 0;
+  const int blocks = total > 0 ? (total + p.block_size - 1) / p.block_size : 0;
+  return blocks < p.full_blocks ? blocks : p.full_blocks;
 }
 
 __device__ __forceinline__ int decode_items(const ExpertGemmParams& p, int routed) {
@@ -168,5 +188,5 @@ inline ExpertWorkspace carve_workspace(void* base, int64_t tokens, int topk, int
 }
 
 // Host launchers shared by the expert paths (experts.hip).
-int dsv4_launch_combine(const float* contrib, int64_t tokens, int topk, int hidden, int has_shared,
-                        uint16_t* out, hipStream_t stream);
+int dsv4_launch_combine(const float* contrib, const int32_t* ntpp, int64_t tokens, int topk, int hidden,
+                        int has_shared, uint16_t* out, hipStream_t stream);

@@ -141,7 +141,7 @@ struct Fp8DecodeItem {
   uint32_t sum_base;  // lane: group-sum offset of its slot (or out of range)
   int64_t rowid;      // lane: row id of its slot, -1 if padded
   int64_t arow;       // lane: activation row of its slot, -1 if padded
-  int n0;
+  int n0;  bool poison;         // the block names no valid expert (NaN contributions)
 };
 
 template <int STAGE>
@@ -159,6 +159,7 @@ __device__ __forceinline__ Fp8DecodeItem fp8_decode_item(const ExpertGemmParams&
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
   it.ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
+  it.poison = b.poison;
   it.rowid = slot_rowid(p, b, lane & 15, tk);
   it.arow = act_row_of<STAGE>(it.rowid, tk, p.topk);
   it.sum_base = it.arow >= 0 ? (uint32_t)(it.arow * groups * 4) : kOobOffset;
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(256, 4) void expert_fp8_decode_kernel(ExpertGemmPar
         *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) =
             u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
       } else {
-        const float wm = (rowid < tk ? p.route_w[rowid] : 1.0f) * mult;
+        const float wm = (cur.poison ? __builtin_nanf("") : (rowid < tk ? p.route_w[rowid] : 1.0f)) * mult;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
@@ -452,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
             u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
       }
     } else {
-      const float wm = (rowid < tk ? p.route_w[rowid] : 1.0f) * mult;
+      const float wm = contrib_weight(p, b, rowid, tk) * mult;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int n = n0 + 64 * wave + 16 * r + 4 * jg;
@@ -581,6 +582,8 @@ int dsv4_launch_experts_w4a8(const uint16_t* x, int64_t tokens, int hidden, int 
   p.block_size = block_size;
   p.shared_block_size = shared_bs;
   p.max_blocks = max_blocks;
+  p.full_blocks = (int)(capacity / block_size);
+  p.experts = experts;
   p.tokens = tokens;
   p.topk = topk;
   p.shared_expert = has_shared ? experts : -1;
@@ -622,7 +625,7 @@ int dsv4_launch_experts_w4a8(const uint16_t* x, int64_t tokens, int hidden, int 
   DSV4_CHECK_LAUNCH("expert fp8 stage 2");
   dsv4host::prof_stamp(dsv4host::kStampStage2, stream);
 
-  const int rc = dsv4_launch_combine(ws.contrib, tokens, topk, hidden, has_shared, out, stream);
+  const int rc = dsv4_launch_combine(ws.contrib, ntpp, tokens, topk, hidden, has_shared, out, stream);
   if (rc != DSV4MOE_OK) return rc;
   dsv4host::prof_stamp(dsv4host::kStampCombine, stream);
   return DSV4MOE_OK;

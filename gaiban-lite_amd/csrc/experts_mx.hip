@@ -57,7 +57,7 @@ struct MxItem {
   const uint8_t* ws;   // this lane's 8 scale bytes of the pair's first group
   uint32_t ld_base;    // loader thread: activation row offset of its slot (or out of range)
   int64_t rowid;       // lane: row id of its slot, -1 if padded
-  int n0;
+  int n0;  bool poison;         // the block names no valid expert (NaN contributions)
 };
 
 template <int STAGE>
@@ -74,6 +74,7 @@ __device__ __forceinline__ MxItem mx_item(const ExpertGemmParams& p, int item, i
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
   it.ws = p.ws8 + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 128 + (lane & 15) * 8;
+  it.poison = b.poison;
   it.rowid = slot_rowid(p, b, lane & 15, tk);
   const int ld_slot = threadIdx.x >> 4;
   const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
@@ -173,7 +174,7 @@ __global__ __launch_bounds__(256, 4) void mx_decode_kernel(ExpertGemmParams p) {
       }
     } else {
       if (rowid >= 0) {
-        const float wr = rowid < tk ? p.route_w[rowid] : 1.0f;
+        const float wr = cur.poison ? __builtin_nanf("") : (rowid < tk ? p.route_w[rowid] : 1.0f);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
@@ -365,7 +366,7 @@ __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, 
     for (int ct = 0; ct < C; ++ct) {
       const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
       if (rowid < 0) continue;
-      const float wr = rowid < tk ? p.route_w[rowid] : 1.0f;
+      const float wr = contrib_weight(p, b, rowid, tk);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int n = n0 + 64 * wave + 16 * r + 4 * (lane >> 4);
@@ -421,6 +422,8 @@ int dsv4_launch_experts_mxfp4(const uint16_t* x, int64_t tokens, int hidden, int
   p.block_size = block_size;
   p.shared_block_size = shared_bs;
   p.max_blocks = max_blocks;
+  p.full_blocks = (int)(capacity / block_size);
+  p.experts = experts;
   p.tokens = tokens;
   p.topk = topk;
   p.shared_expert = has_shared ? experts : -1;
@@ -471,7 +474,7 @@ int dsv4_launch_experts_mxfp4(const uint16_t* x, int64_t tokens, int hidden, int
   DSV4_CHECK_LAUNCH("mxfp4 expert stage 2");
   dsv4host::prof_stamp(dsv4host::kStampStage2, stream);
 
-  const int rc = dsv4_launch_combine(ws.contrib, tokens, topk, hidden, has_shared, out, stream);
+  const int rc = dsv4_launch_combine(ws.contrib, ntpp, tokens, topk, hidden, has_shared, out, stream);
   if (rc != DSV4MOE_OK) return rc;
   dsv4host::prof_stamp(dsv4host::kStampCombine, stream);
   return DSV4MOE_OK;

@@ -54,7 +54,21 @@ struct LinearParams {
   uint16_t* out;
   float* partial;  // [split][M][N] when split > 1
   int accumulate;  // out = bf16(out + bf16(result)) instead of bf16(result)
+  int w_rowmajor;  // weights as the checkpoint's row-major [N][K] bytes instead of 1 KiB tiles
 };
+
+// Byte offset of lane `lane`'s 16 weight bytes in 64-K window 0 of 16-row
+// strip `strip`, in either weight layout: 1 KiB tiles (dsv4moe_pack_int8 /
+// pack_fp8: the strip's tiles are contiguous, lane l at 16 l) or the
+// checkpoint's row-major [N][K] bytes (lane l reads row 16 strip + l % 16,
+// K 16 (l / 16) .. +15).  Both put the same bytes in the same LDS slots,
+// since a buffer_load ... lds copy places lane l's 16 bytes at 16 l whatever
+// address it read.  The step to the next window is weight_window_step.
+__device__ __forceinline__ uint32_t weight_lane_offset(int rowmajor, int strip, int lane, int k, int wins) {
+  return rowmajor ? (uint32_t)(((int64_t)strip * 16 + (lane & 15)) * k + (lane >> 4) * 16)
+                  : (uint32_t)((int64_t)strip * wins * 1024 + lane * 16);
+}
+__device__ __forceinline__ int weight_window_step(int rowmajor) { return rowmajor ? 64 : 1024; }
 
 // The bf16 written for result v: bf16(v), or with accumulation the bf16 sum
 // of the existing output and bf16(v) (torch.add of two bf16 tensors).
@@ -150,10 +164,11 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
     const int part = (lane & 7) ^ swz128(row);
     a_off[i] = (q < kActDma && tok < p.m) ? (uint32_t)(tok * p.k * 2 + part * 16) : kLinOob;
   }
+  const int wstep = weight_window_step(p.w_rowmajor);
   uint32_t w_off[R];
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+    w_off[r] = strip0 + r < strips ? weight_lane_offset(p.w_rowmajor, strip0 + r, lane, p.k, wins) : kLinOob;
   // FP8: the wavefront's R strips lie in one 128-row scale block (R divides
   // 8); lane i holds the E8M0 bytes of K blocks i, 64 + i, 128 + i, 192 + i,
   // loaded before any copy is in flight (K <= 32768, checked on the host)
@@ -172,7 +187,7 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
       if (q < kActDma) lds_dma16(a_rsrc, (lds_void_ptr)&xs[buf][q * 1024], a_off[i], win * 128);
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 1024], w_off[r], win * 1024);
+    for (int r = 0; r < R; ++r) lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 1024], w_off[r], win * wstep);
   };
 
   f32x4 acc[R][C];
@@ -325,10 +340,11 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel3(LinearParams p) {
     const int part = (lane & 7) ^ swz128(row);
     a_off[i] = (q < kActDma && tok < p.m) ? (uint32_t)(tok * p.k * 2 + part * 16) : kLinOob;
   }
+  const int wstep = weight_window_step(p.w_rowmajor);
   uint32_t w_off[R];
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+    w_off[r] = strip0 + r < strips ? weight_lane_offset(p.w_rowmajor, strip0 + r, lane, p.k, wins) : kLinOob;
   // FP8: the wavefront's R strips lie in one 128-row scale block (R divides
   // 8); lane i holds the E8M0 bytes of K blocks i, 64 + i, 128 + i, 192 + i,
   // loaded before any copy is in flight (K <= 32768, checked on the host)
@@ -347,7 +363,7 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel3(LinearParams p) {
     for (int i = 0; i < kActPerWave; ++i)
       lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + 4 * i) * 1024]), a_off[i], win * 128);
 #pragma unroll
-    for (int r = 0; r < R; ++r) lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 1024]), w_off[r], win * 1024);
+    for (int r = 0; r < R; ++r) lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 1024]), w_off[r], win * wstep);
   };
 
   f32x4 acc[R][C];
@@ -500,10 +516,11 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel_w3(LinearParams p) {
     const int part = (lane & 7) ^ swz128(row);
     a_off[i] = (q < kActDma && tok < p.m) ? (uint32_t)(tok * p.k * 2 + part * 16) : kLinOob;
   }
+  const int wstep = weight_window_step(p.w_rowmajor);
   uint32_t w_off[R];
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+    w_off[r] = strip0 + r < strips ? weight_lane_offset(p.w_rowmajor, strip0 + r, lane, p.k, wins) : kLinOob;
   // FP8: the wavefront's R strips lie in one 128-row scale block (R divides
   // 8); lane i holds the E8M0 bytes of K blocks i, 64 + i, 128 + i, 192 + i,
   // loaded before any copy is in flight (K <= 32768, checked on the host)
@@ -523,7 +540,7 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel_w3(LinearParams p) {
   };
   auto issue_w = [&](int win, int buf) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 1024]), w_off[r], win * 1024);
+    for (int r = 0; r < R; ++r) lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 1024]), w_off[r], win * wstep);
   };
 
   f32x4 acc[R][C];
@@ -791,6 +808,7 @@ struct BlockFp8Params {
   int tiles_m;
   uint16_t* out;
   float* partial;      // [split][M][N] when split > 1
+  int w_rowmajor;      // weights as the checkpoint's row-major [N][K] bytes instead of 1 KiB tiles
 };
 
 // Workgroup tile: 64*R output channels x 16*C tokens over one K split, one
@@ -838,10 +856,11 @@ __global__ __launch_bounds__(256, 2) void w8a8_block_kernel(BlockFp8Params p) {
     const int part = (lane & 7) ^ swz128(row);
     a_off[i] = (q < kActDma && tok < p.m) ? (uint32_t)(tok * p.k + part * 16) : kLinOob;
   }
+  const int wstep = weight_window_step(p.w_rowmajor);
   uint32_t w_off[R];
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+    w_off[r] = strip0 + r < strips ? weight_lane_offset(p.w_rowmajor, strip0 + r, lane, p.k, wins) : kLinOob;
   // the wavefront's R strips lie in one 128-row scale block (R divides 8);
   // lane i holds the E8M0 bytes of K blocks i, 64 + i, 128 + i, 192 + i
   uint32_t srow[4] = {0, 0, 0, 0};
@@ -869,8 +888,8 @@ __global__ __launch_bounds__(256, 2) void w8a8_block_kernel(BlockFp8Params p) {
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 2048], w_off[r], (2 * kb) * 1024);
-      lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 2048 + 1024], w_off[r], (2 * kb + 1) * 1024);
+      lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 2048], w_off[r], (2 * kb) * wstep);
+      lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 2048 + 1024], w_off[r], (2 * kb + 1) * wstep);
     }
   };
 
@@ -1010,10 +1029,11 @@ __global__ __launch_bounds__(256 * H, 1) void w8a8_block_prefill_kernel(BlockFp8
     const int part = (lane & 7) ^ swz128(row);
     a_off[i] = tok < p.m ? (uint32_t)(tok * p.k + part * 16) : kLinOob;
   }
+  const int wstep = weight_window_step(p.w_rowmajor);
   uint32_t w_off[R];
 #pragma unroll
   for (int r = 0; r < R; ++r)
-    w_off[r] = strip0 + r < strips ? (uint32_t)((int64_t)(strip0 + r) * wins * 1024 + lane * 16) : kLinOob;
+    w_off[r] = strip0 + r < strips ? weight_lane_offset(p.w_rowmajor, strip0 + r, lane, p.k, wins) : kLinOob;
   // scale dword of token tok0 + kScaleTok * wave + lane (lanes past kScaleTok
   // or past the last token read out of range into unused slots)
   const int64_t stok = tok0 + kScaleTok * wave + lane;
@@ -1039,7 +1059,7 @@ __global__ __launch_bounds__(256 * H, 1) void w8a8_block_prefill_kernel(BlockFp8
 #pragma unroll
       for (int t = 0; t < 2; ++t)
         if (H == 1 || t == half)
-          lds_copy16(w_rsrc, lds_addr(&wts[buf][sg][r * 2048 + t * 1024]), w_off[r], (2 * kb + t) * 1024);
+          lds_copy16(w_rsrc, lds_addr(&wts[buf][sg][r * 2048 + t * 1024]), w_off[r], (2 * kb + t) * wstep);
     }
     lds_copy4(as_rsrc, lds_addr(&scs[buf][wave][0]), s_off, kb & ~3);
   };
@@ -1191,7 +1211,7 @@ int dsv4_launch_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed
 // ws (int8 format, bf16 [N]) or ws8 (FP8 format, E8M0 [ceil(N/128)][K/128]): exactly one is set.
 int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
                       const uint16_t* ws, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
-                      hipStream_t stream, int accumulate) {
+                      hipStream_t stream, int accumulate, int w_rowmajor) {
   int r, c;
   w8a16_geometry(m, n, &r, &c);
   LinearParams p;
@@ -1211,6 +1231,7 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
   p.out = out;
   p.partial = workspace;
   p.accumulate = accumulate;
+  p.w_rowmajor = w_rowmajor;
   if (ws8 != nullptr)
     launch_w8a16_kernel<true>(p, r, c, stream);
   else
@@ -1268,7 +1289,7 @@ int dsv4_launch_act_quant_block_fp8(const void* x, int32_t x_dtype, int64_t m, i
 
 int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, int64_t n, int64_t k,
                                const uint8_t* wq, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
-                               hipStream_t stream) {
+                               hipStream_t stream, int w_rowmajor) {
   int r, c;
   w8a8_geometry(m, n, k, &r, &c);
   BlockFp8Params p;
@@ -1286,6 +1307,7 @@ int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, i
   p.tiles_m = (int)((m + 16 * c - 1) / (16 * c));
   p.out = out;
   p.partial = workspace;
+  p.w_rowmajor = w_rowmajor;
   launch_w8a8_block_kernel(p, r, c, stream);
   DSV4_CHECK_LAUNCH("w8a8_block_kernel");
   if (split > 1) {
@@ -1337,11 +1359,11 @@ int dsv4_launch_shared_fp8_add(const uint16_t* x, int64_t tokens, int hidden, in
   if (tokens == 0) return DSV4MOE_OK;
   const SharedFp8Workspace w = carve_shared_fp8(workspace, tokens, hidden, inter);
   int rc = dsv4_launch_w8a16(x, tokens, 2 * (int64_t)inter, hidden, w13q, nullptr, w13s8, w.split13, w.partial, w.gu,
-                             stream, 0);
+                             stream, 0, 0);
   if (rc != DSV4MOE_OK) return rc;
   const int64_t quads = tokens * (inter / 4);
   hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, w.gu, tokens,
                      inter, clamp_limit, w.h);
   DSV4_CHECK_LAUNCH("swiglu_rows_kernel");
-  return dsv4_launch_w8a16(w.h, tokens, hidden, inter, w2q, nullptr, w2s8, w.split2, w.partial, out, stream, 1);
+  return dsv4_launch_w8a16(w.h, tokens, hidden, inter, w2q, nullptr, w2s8, w.split2, w.partial, out, stream, 1, 0);
 }

@@ -1,22 +1,24 @@
-"""Block-FP8 W8A8 dense linear on the HIP kernels.
+"""Block-FP8 W8A8 dense linear with the interface of
+``runtime/dsv4_direct/fp8_linear.py``.
 
-Drop-in for ``runtime/dsv4_direct/fp8_linear.py``: the same constants, plan
-dataclasses, validation and caller-owned storage (``activation_quant_into``,
-``block_fp8_gemm_into``), computed by ``act_quant_block_fp8_kernel`` and
-``w8a8_block_kernel`` (gfx950 block-scaled fp8 MFMA, both E8M0 block scales
-applied inside the MFMA) instead of Triton.
+The reference quantises activations per row and 128-K block to E4M3 with a
+power-of-two E8M0 scale (``activation_quant_into``, ``:523-569``) and runs
+the GEMM over the checkpoint's E4M3 weight [N, K] with its E8M0 128 x 128
+block scales, applying both scales per K block in fp32, with optional
+deterministic split-K (``block_fp8_gemm_into``, ``:572-684``).  Here both
+steps are HIP kernels: ``act_quant_block_fp8_kernel`` and the GEMM on
+gfx950's block-scaled fp8 MFMA, which multiplies the two E8M0 scales into
+each 128-K block product itself.
 
-Differences a caller sees:
-* the weight is the ``PreparedFP8BlockWeight`` of
-  ``weight_only_linear.prepare_fp8_block_weight`` (a load-time byte
-  permutation of the checkpoint tensor into 1 KiB MFMA tiles).  A raw
-  checkpoint ``float8_e4m3fn [N, K]`` tensor is accepted too and repacked on
-  every call, which allocates;
-* ``make_gemm_plan``'s automatic split follows this library's policy
-  (``dsv4moe_block_fp8_split_k``: widen K while the grid is below 512
-  workgroups), not the Triton tile count; explicit values are validated as
-  in the reference, and the workspace shape follows the chosen split;
-* N must be a multiple of 16 and K at most 32768.
+Kept: the module constants, ``QuantizationPlan`` / ``GemmPlan`` /
+``GemmTuning`` with their fields, the two ``*_into`` entry points with
+caller-owned storage, ``primitive_contract`` and
+``validate_e8m0_scale_values``, and the exception classes of every check.
+This build's own: the split policy (``dsv4moe_block_fp8_split_k``), the
+kernels, and one extension -- ``block_fp8_gemm_into`` also takes a
+``PreparedFP8BlockWeight`` (the weight repacked into MFMA tiles at load time)
+in place of the raw weight, with ``weight_scale`` None; the output bits are
+the same.  N must be a multiple of 16 and K at most 32768.
 """
 
 from __future__ import annotations
@@ -26,18 +28,27 @@ from typing import Final
 
 import torch
 
+from . import contracts as C
 from . import ops
-from .weight_only_linear import PreparedFP8BlockWeight, prepare_fp8_block_weight
+from .linear_plan import (
+    BLOCK_K,
+    DEFAULT_GEMM_TUNING,
+    SUPPORTED_SPLIT_K,
+    WEIGHT_BLOCK_N,
+    GemmPlan,
+    GemmTuning,
+    build_plan,
+)
+from .weight_only_linear import PreparedFP8BlockWeight
 
 SCHEMA: Final = "dsv4.e1b2g.block_fp8_primitives.v1"
 FP8_DTYPE: Final = torch.float8_e4m3fn
 E8M0_DTYPE: Final = torch.float8_e8m0fnu
 OUTPUT_DTYPE: Final = torch.bfloat16
-WEIGHT_BLOCK_N: Final = 128
-BLOCK_K: Final = 128
 FP8_MAX: Final = 448.0
 MIN_ACTIVATION_AMAX: Final = 1.0e-4
-SUPPORTED_SPLIT_K: Final = (1, 2, 4, 8)
+ACTIVATION_DTYPES: Final = (torch.bfloat16, torch.float16, torch.float32)
+QUANT_BLOCK_M_CHOICES: Final = (1, 2, 4, 8, 16, 32)
 
 LAYOUT_CONTRACT: Final = {
     "activation": "row_major[M,K]",
@@ -53,157 +64,46 @@ LAYOUT_CONTRACT: Final = {
 }
 
 
-def _ceil_div(value: int, divisor: int) -> int:
-    return (value + divisor - 1) // divisor
-
-
-def _positive_dimension(name: str, value: int) -> int:
-    if isinstance(value, bool) or not isinstance(value, int) or value <= 0:
-        raise ValueError(f"{name} must be a positive integer, got {value!r}")
-    return value
-
-
 @dataclass(frozen=True)
 class QuantizationPlan:
-    """Activation block quantisation layout (``fp8_linear.py:53-71``)."""
+    """Shapes of one activation quantisation (reference ``:53-71``): the
+    quantised copy [M, K], one E8M0 scale per row and K block [M, K/128],
+    and the reference's launch grid for ``block_m`` rows per program."""
 
     m: int
     k: int
     block_m: int = 16
     block_k: int = BLOCK_K
 
-    @property
-    def quantized_shape(self) -> tuple[int, int]:
-        return (self.m, self.k)
-
-    @property
-    def scale_shape(self) -> tuple[int, int]:
-        return (self.m, self.k // self.block_k)
-
-    @property
-    def grid(self) -> tuple[int, int]:
-        return (_ceil_div(self.m, self.block_m), self.k // self.block_k)
-
-
-@dataclass(frozen=True)
-class GemmTuning:
-    """The reference's Triton tile parameters (``:74-81``); validated and kept
-    for plan identity, the HIP kernel picks its own tiles."""
-
-    block_m: int = 32
-    block_n: int = 64
-    num_warps: int = 4
-    num_stages: int = 3
-
-
-DEFAULT_GEMM_TUNING: Final = GemmTuning()
-
-
-@dataclass(frozen=True)
-class GemmPlan:
-    """Dispatch decision and caller-owned workspace contract (``:87-153``)."""
-
-    m: int
-    n: int
-    k: int
-    split_k: int
-    tuning: GemmTuning = DEFAULT_GEMM_TUNING
-
-    @property
-    def activation_shape(self) -> tuple[int, int]:
-        return (self.m, self.k)
-
-    @property
-    def activation_scale_shape(self) -> tuple[int, int]:
-        return (self.m, self.k // BLOCK_K)
-
-    @property
-    def weight_shape(self) -> tuple[int, int]:
-        return (self.n, self.k)
-
-    @property
-    def weight_scale_shape(self) -> tuple[int, int]:
-        return (_ceil_div(self.n, WEIGHT_BLOCK_N), self.k // BLOCK_K)
-
-    @property
-    def output_shape(self) -> tuple[int, int]:
-        return (self.m, self.n)
-
-    @property
-    def output_grid(self) -> tuple[int, int]:
-        return (_ceil_div(self.m, self.tuning.block_m), _ceil_div(self.n, self.tuning.block_n))
-
-    @property
-    def gemm_grid(self) -> tuple[int, ...]:
-        return self.output_grid if self.split_k == 1 else (*self.output_grid, self.split_k)
-
-    @property
-    def k_blocks_per_split(self) -> int:
-        return _ceil_div(self.k // BLOCK_K, self.split_k)
-
-    @property
-    def workspace_shape(self) -> tuple[int, ...]:
-        return (0,) if self.split_k == 1 else (self.split_k, self.m, self.n)
-
-    @property
-    def workspace_elements(self) -> int:
-        return 0 if self.split_k == 1 else self.split_k * self.m * self.n
-
-    @property
-    def workspace_bytes(self) -> int:
-        return self.workspace_elements * 4
-
-    @property
-    def dispatch(self) -> str:
-        return "full_k" if self.split_k == 1 else "split_k_reduce"
+    quantized_shape = property(lambda self: (self.m, self.k))
+    scale_shape = property(lambda self: (self.m, self.k // self.block_k))
+    grid = property(lambda self: (-(-self.m // self.block_m), self.k // self.block_k))
 
 
 def make_quantization_plan(m: int, k: int, *, block_m: int = 16) -> QuantizationPlan:
-    """``make_quantization_plan`` (``:168-183``)."""
+    """Validated quantisation plan (reference ``:166-181``); ValueError for
+    any bad dimension."""
 
-    m = _positive_dimension("m", m)
-    k = _positive_dimension("k", k)
-    block_m = _positive_dimension("block_m", block_m)
+    m, k, block_m = (C.positive_int(name, v) for name, v in (("m", m), ("k", k), ("block_m", block_m)))
     if k % BLOCK_K:
-        raise ValueError(f"k must be divisible by {BLOCK_K}, got {k}")
-    if block_m not in (1, 2, 4, 8, 16, 32):
-        raise ValueError(f"unsupported quantization block_m={block_m}")
+        raise ValueError(f"k={k} is not a multiple of {BLOCK_K}")
+    if block_m not in QUANT_BLOCK_M_CHOICES:
+        raise ValueError(f"block_m={block_m} is not one of {QUANT_BLOCK_M_CHOICES}")
     return QuantizationPlan(m=m, k=k, block_m=block_m)
-
-
-def _validate_tuning(tuning: GemmTuning) -> None:
-    if tuning.block_m not in (16, 32, 64):
-        raise ValueError(f"unsupported GEMM block_m={tuning.block_m}")
-    if tuning.block_n not in (32, 64, 128):
-        raise ValueError(f"unsupported GEMM block_n={tuning.block_n}")
-    if tuning.num_warps not in (4, 8):
-        raise ValueError(f"unsupported GEMM num_warps={tuning.num_warps}")
-    if tuning.num_stages not in (2, 3, 4):
-        raise ValueError(f"unsupported GEMM num_stages={tuning.num_stages}")
 
 
 def make_gemm_plan(m: int, n: int, k: int, *, split_k: int | None = None,
                    tuning: GemmTuning = DEFAULT_GEMM_TUNING) -> GemmPlan:
-    """``make_gemm_plan`` (``:218-240``); the automatic split is this
-    library's (``ops.block_fp8_split_k``)."""
+    """One GEMM geometry (reference ``:207-234``); the automatic split is this
+    library's policy for its kernel tiles."""
 
-    m = _positive_dimension("m", m)
-    n = _positive_dimension("n", n)
-    k = _positive_dimension("k", k)
-    _validate_tuning(tuning)
-    if k % BLOCK_K:
-        raise ValueError(f"k must be divisible by {BLOCK_K}, got {k}")
-    selected = ops.block_fp8_split_k(m, n, k) if split_k is None else split_k
-    if isinstance(selected, bool) or selected not in SUPPORTED_SPLIT_K:
-        raise ValueError(f"split_k must be one of {SUPPORTED_SPLIT_K}, got {selected!r}")
-    if selected > k // BLOCK_K:
-        raise ValueError(f"split_k={selected} exceeds K-block count {k // BLOCK_K}")
-    return GemmPlan(m=m, n=n, k=k, split_k=selected, tuning=tuning)
+    return build_plan(m, n, k, split_k=split_k, tuning=tuning, policy=ops.block_fp8_split_k)
 
 
 def primitive_contract() -> dict[str, object]:
-    """JSON-friendly identity (``:243-270``)."""
+    """A JSON-friendly description of the primitives (reference ``:237-261``)."""
 
+    tuning = DEFAULT_GEMM_TUNING
     return {
         "schema": SCHEMA,
         "block_k": BLOCK_K,
@@ -211,106 +111,88 @@ def primitive_contract() -> dict[str, object]:
         "fp8_dtype": str(FP8_DTYPE),
         "scale_dtypes": [str(E8M0_DTYPE)],
         "supported_split_k": list(SUPPORTED_SPLIT_K),
-        "default_tuning": {
-            "block_m": DEFAULT_GEMM_TUNING.block_m,
-            "block_n": DEFAULT_GEMM_TUNING.block_n,
-            "num_warps": DEFAULT_GEMM_TUNING.num_warps,
-            "num_stages": DEFAULT_GEMM_TUNING.num_stages,
-        },
+        "default_tuning": {f: getattr(tuning, f) for f in ("block_m", "block_n", "num_warps", "num_stages")},
         "layout": dict(LAYOUT_CONTRACT),
         "caller_preallocated": ["activation_quantized", "activation_scale", "output", "workspace"],
         "cuda_graph_friendly": True,
     }
 
 
-def _check_tensor(name: str, tensor: torch.Tensor, *, shape: tuple[int, ...],
-                  dtypes: tuple[torch.dtype, ...], device: torch.device) -> None:
-    if not isinstance(tensor, torch.Tensor):
-        raise TypeError(f"{name} must be a tensor")
-    if tuple(tensor.shape) != shape:
-        raise ValueError(f"{name} shape must be {shape}, got {tuple(tensor.shape)}")
-    if tensor.dtype not in dtypes:
-        expected = ", ".join(str(d) for d in dtypes)
-        raise TypeError(f"{name} dtype must be one of ({expected}), got {tensor.dtype}")
-    if tensor.device != device:
-        raise ValueError(f"{name} must be on {device}, got {tensor.device}")
-    if not tensor.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
+def _e8m0(name: str, value, shape, device) -> torch.Tensor:
+    """A caller's E8M0 tensor as its uint8 byte view."""
 
-
-def _scale_codes(scale: torch.Tensor) -> torch.Tensor:
-    if scale.dtype != E8M0_DTYPE:
-        raise TypeError(f"scale must use {E8M0_DTYPE}, got {scale.dtype}")
-    return scale.view(torch.uint8)
+    return C.tensor(name, value, shape=shape, dtype=E8M0_DTYPE, device=device, contiguous=True).view(torch.uint8)
 
 
 def validate_e8m0_scale_values(name: str, scale: torch.Tensor) -> None:
-    """Reject the reserved E8M0 NaN byte once, outside captured paths (``:301-309``)."""
+    """Cold preflight against the reserved E8M0 byte 255 (reference
+    ``:296-309``): ValueError for a bad name or the byte, TypeError unless the
+    tensor is ``float8_e8m0fnu``.  Reads the device."""
 
     if not isinstance(name, str) or not name:
-        raise ValueError("scale preflight requires a non-empty name")
-    if scale.dtype != E8M0_DTYPE:
-        raise TypeError(f"{name} must use {E8M0_DTYPE}, got {scale.dtype}")
-    if bool((scale.view(torch.uint8) == 255).any().item()):
-        raise ValueError(f"{name} contains reserved E8M0 byte 255")
+        raise ValueError("validate_e8m0_scale_values needs a non-empty name")
+    C.tensor(name, scale, dtype=E8M0_DTYPE)
+    C.no_reserved_e8m0(name, scale)
+
+
+def _on_gpu(name: str, t) -> torch.device:
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        where = t.device if isinstance(t, torch.Tensor) else type(t).__name__
+        raise ValueError(f"{name} must be a device tensor, got {where}")
+    return t.device
 
 
 def activation_quant_into(x: torch.Tensor, quantized_out: torch.Tensor, scale_out: torch.Tensor, *,
                           plan: QuantizationPlan) -> None:
-    """Quantise ``x`` into caller-owned FP8 and power-of-two scale buffers
-    (``activation_quant_into``, ``:523-569``)."""
+    """E4M3 codes and E8M0 scales of ``x`` into caller-owned tensors."""
 
-    if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
-        raise ValueError("x must be a device tensor")
-    _check_tensor("x", x, shape=plan.quantized_shape, dtypes=(torch.bfloat16, torch.float16, torch.float32),
-                  device=x.device)
-    _check_tensor("quantized_out", quantized_out, shape=plan.quantized_shape, dtypes=(FP8_DTYPE,), device=x.device)
-    _check_tensor("scale_out", scale_out, shape=plan.scale_shape, dtypes=(E8M0_DTYPE,), device=x.device)
-    ops.act_quant_block_fp8_into(x, quantized_out.view(torch.uint8), _scale_codes(scale_out))
+    device = _on_gpu("x", x)
+    C.tensor("x", x, shape=plan.quantized_shape, dtype=ACTIVATION_DTYPES, device=device, contiguous=True)
+    q = C.tensor("quantized_out", quantized_out, shape=plan.quantized_shape, dtype=FP8_DTYPE, device=device,
+                 contiguous=True)
+    s = _e8m0("scale_out", scale_out, plan.scale_shape, device)
+    ops.act_quant_block_fp8_into(x, q.view(torch.uint8), s)
 
 
 def block_fp8_gemm_into(activation: torch.Tensor, activation_scale: torch.Tensor,
-                        weight: PreparedFP8BlockWeight | torch.Tensor, weight_scale: torch.Tensor | None,
+                        weight: torch.Tensor | PreparedFP8BlockWeight, weight_scale: torch.Tensor | None,
                         out: torch.Tensor, workspace: torch.Tensor, *, plan: GemmPlan) -> None:
-    """Full-K or deterministic split-K block-FP8 GEMM into ``out``
-    (``block_fp8_gemm_into``, ``:572-684``)."""
+    """Full-K or split-K block-FP8 GEMM into ``out``; the raw checkpoint
+    weight is read as stored (no repack, no allocation)."""
 
-    if not isinstance(activation, torch.Tensor) or activation.device.type != "cuda":
-        raise ValueError("activation must be a device tensor")
-    device = activation.device
-    _check_tensor("activation", activation, shape=plan.activation_shape, dtypes=(FP8_DTYPE,), device=device)
-    _check_tensor("activation_scale", activation_scale, shape=plan.activation_scale_shape, dtypes=(E8M0_DTYPE,),
-                  device=device)
+    device = _on_gpu("activation", activation)
+    a = C.tensor("activation", activation, shape=plan.activation_shape, dtype=FP8_DTYPE, device=device,
+                 contiguous=True)
+    a_scale = _e8m0("activation_scale", activation_scale, plan.activation_scale_shape, device)
     if isinstance(weight, PreparedFP8BlockWeight):
         if (weight.n, weight.k) != plan.weight_shape:
-            raise ValueError(f"weight shape must be {plan.weight_shape}, got {(weight.n, weight.k)}")
-        if weight_scale is not None:
-            _check_tensor("weight_scale", weight_scale, shape=plan.weight_scale_shape, dtypes=(E8M0_DTYPE,),
-                          device=device)
-            if not torch.equal(_scale_codes(weight_scale), weight.scale):
-                raise ValueError("weight_scale differs from the prepared weight's scales")
-        prepared = weight
+            raise ValueError(f"prepared weight is {(weight.n, weight.k)}, the plan needs {plan.weight_shape}")
+        w_bytes, w_scale = weight.packed, weight.scale
+        if weight_scale is not None and not torch.equal(_e8m0("weight_scale", weight_scale,
+                                                               plan.weight_scale_shape, device), w_scale):
+            raise ValueError("weight_scale differs from the prepared weight's scales")
     else:
-        _check_tensor("weight", weight, shape=plan.weight_shape, dtypes=(FP8_DTYPE,), device=device)
-        _check_tensor("weight_scale", weight_scale, shape=plan.weight_scale_shape, dtypes=(E8M0_DTYPE,),
-                      device=device)
-        prepared = prepare_fp8_block_weight(weight, weight_scale)
-    _check_tensor("out", out, shape=plan.output_shape, dtypes=(OUTPUT_DTYPE,), device=device)
-    _check_tensor("workspace", workspace, shape=plan.workspace_shape, dtypes=(torch.float32,), device=device)
-    ops.block_fp8_gemm_into(
-        activation.view(torch.uint8), _scale_codes(activation_scale), prepared.packed, prepared.scale, out,
-        workspace if plan.split_k > 1 else None, n=plan.n, split_k=plan.split_k,
-    )
+        w_bytes = C.tensor("weight", weight, shape=plan.weight_shape, dtype=FP8_DTYPE, device=device,
+                           contiguous=True)
+        w_scale = _e8m0("weight_scale", weight_scale, plan.weight_scale_shape, device)
+    C.tensor("out", out, shape=plan.output_shape, dtype=OUTPUT_DTYPE, device=device, contiguous=True)
+    C.tensor("workspace", workspace, shape=plan.workspace_shape, dtype=torch.float32, device=device,
+             contiguous=True)
+    ops.block_fp8_gemm_into(a.view(torch.uint8), a_scale, w_bytes, w_scale, out,
+                            workspace if plan.split_k > 1 else None, n=plan.n, split_k=plan.split_k)
 
 
 __all__ = [
+    "ACTIVATION_DTYPES",
     "BLOCK_K",
     "DEFAULT_GEMM_TUNING",
     "E8M0_DTYPE",
     "FP8_DTYPE",
+    "FP8_MAX",
     "GemmPlan",
     "GemmTuning",
     "LAYOUT_CONTRACT",
+    "MIN_ACTIVATION_AMAX",
     "OUTPUT_DTYPE",
     "QuantizationPlan",
     "SCHEMA",

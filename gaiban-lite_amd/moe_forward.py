@@ -18,6 +18,7 @@ from typing import Any
 
 import torch
 
+from . import contracts as C
 from . import ops
 
 FP4_VALUES = (
@@ -155,23 +156,19 @@ def hash_gate_forward(
 ) -> HashGateForwardTensors:
     """Token-id router of layers 0-2 (``moe_forward.py:186-231``)."""
 
-    if x.ndim != 2 or weight.ndim != 2 or tid2eid.ndim != 2:
-        raise ValueError("x/weight/tid2eid must have ranks 2/2/2")
+    x = C.tensor("x", x, ndim=2)
+    weight = C.tensor("gate weight", weight, ndim=2)
+    tid2eid = C.tensor("tid2eid", tid2eid, ndim=2)
     experts, hidden = weight.shape
     if x.shape[1] != hidden:
-        raise ValueError(f"x hidden size {x.shape[1]} != gate hidden size {hidden}")
-    if input_ids.ndim != 1 or input_ids.shape[0] != x.shape[0]:
-        raise ValueError("input_ids must contain one token ID per gate row")
-    if input_ids.dtype != torch.int64 or tid2eid.dtype != torch.int64:
-        raise TypeError("hash input IDs and tid2eid must be int64")
-    if tid2eid.shape[1] <= 0 or tid2eid.shape[1] >= experts:
-        raise ValueError("tid2eid top-k width must be positive and smaller than experts")
-    if x.device != weight.device or x.device != tid2eid.device:
-        raise ValueError("hash gate tensors must share one device")
-    if input_ids.device != x.device:
-        raise ValueError("hash gate input IDs must share the gate device")
-    if not math.isfinite(route_scale) or route_scale <= 0:
-        raise ValueError("route_scale must be finite and positive")
+        raise ValueError(f"x has hidden size {x.shape[1]}, the gate {hidden}")
+    C.tensor("input_ids", input_ids, shape=(x.shape[0],))
+    C.tensor("input_ids", input_ids, dtype=torch.int64)
+    C.tensor("tid2eid", tid2eid, dtype=torch.int64)
+    if not 0 < tid2eid.shape[1] < experts:
+        raise ValueError(f"tid2eid routes {tid2eid.shape[1]} experts per token; need 1 .. {experts - 1}")
+    C.same_device("hash gate tensors", (x, weight, tid2eid, input_ids))
+    C.finite_positive("route_scale", route_scale)
     logits = gate_logits(x, weight)
     topk = tid2eid.shape[1]
     ids = torch.empty((x.shape[0], topk), dtype=torch.int32, device=x.device)

@@ -26,6 +26,7 @@ from typing import Any, Callable, Iterable, Iterator
 
 import torch
 
+from . import contracts as C
 from . import ops
 from .deterministic_moe_align import (
     DeterministicMoEAlignment,
@@ -175,48 +176,57 @@ def _tensor_digest(*tensors: torch.Tensor) -> str:
 def _snapshot_route_override(
     value: MoERouteOverride, *, rows: int, config: TP4MoEConfig, device: torch.device
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Validate and own an injected route (``moe_runtime.py:418-476``)."""
+    """An owned, validated copy of an injected route (the contract of the
+    reference's override path, ``moe_runtime.py:418-476``): ids int32 and
+    weights fp32, both [rows, k] on the layer's device; ids unique per row
+    and inside [0, experts); weights finite, positive, and for renormalised
+    score functions summing to route_scale per row.  Reads the device."""
 
     if not isinstance(value, MoERouteOverride):
-        raise TypeError("route_override must be a MoERouteOverride")
-    ids, weights = value.ids, value.weights
-    if not isinstance(ids, torch.Tensor) or not isinstance(weights, torch.Tensor):
-        raise TypeError("route override IDs and weights must be tensors")
-    shape = (rows, config.topk)
-    if tuple(ids.shape) != shape or tuple(weights.shape) != shape:
-        raise ValueError(f"route override IDs/weights must have shape {shape}")
-    if ids.dtype != torch.int32 or weights.dtype != torch.float32:
-        raise TypeError("route override requires INT32 IDs and FP32 weights")
-    if ids.device != device or weights.device != device:
-        raise ValueError("route override tensors must use the configured device")
-    if not ids.is_contiguous() or not weights.is_contiguous():
-        raise ValueError("route override tensors must be contiguous")
-    if ids.requires_grad or weights.requires_grad:
-        raise ValueError("route override tensors must not require gradients")
-    ids = ids.detach().clone(memory_format=torch.contiguous_format)
-    weights = weights.detach().clone(memory_format=torch.contiguous_format)
-    if not bool(torch.isfinite(weights).all().item()):
-        raise ValueError("route override weights must be finite")
-    if bool((weights <= 0).any().item()):
-        raise ValueError("route override weights must be strictly positive")
-    minimum, maximum = int(ids.min().item()), int(ids.max().item())
-    if minimum < 0 or maximum >= config.experts:
-        raise ValueError(
-            f"route override expert range [{minimum}, {maximum}] is outside [0, {config.experts})"
-        )
-    ordered = ids.sort(dim=1).values
-    if bool((ordered[:, 1:] == ordered[:, :-1]).any().item()):
-        raise ValueError("route override rows must contain unique expert IDs")
-    if config.score_func != "softmax":
-        row_sums = weights.sum(dim=1)
-        err = float((row_sums - float(config.route_scale)).abs().max().item())
-        tol = 8.0 * torch.finfo(torch.float32).eps * max(1.0, abs(float(config.route_scale)))
-        if err > tol:
-            raise ValueError(
-                "route override weights must sum to route_scale per row; "
-                f"max_abs_error={err}, tolerance={tol}"
-            )
+        raise TypeError(f"route_override: expected MoERouteOverride, got {type(value).__name__}")
+    want = (rows, config.topk)
+    ids = C.tensor("route_override.ids", value.ids, shape=want, dtype=torch.int32, device=device,
+                   contiguous=True, no_grad=True).detach().clone()
+    weights = C.tensor("route_override.weights", value.weights, shape=want, dtype=torch.float32, device=device,
+                       contiguous=True, no_grad=True).detach().clone()
+    C.route_weights("route_override.weights", weights,
+                    row_sum=None if config.score_func == "softmax" else float(config.route_scale))
+    C.expert_table("route_override.ids", ids, experts=config.experts)
     return ids, weights
+
+
+@dataclass(frozen=True)
+class MoERouteCaptureBuffer:
+    """Stable device storage that a captured layer call writes its effective
+    route into (``moe_runtime.py:121-136``): ids int32 [rows, k] (-1 until
+    written), weights fp32 [rows, k], and a device generation counter that
+    every call adds one to."""
+
+    global_rows: int
+    slot: int
+    owner_id: int
+    ids: torch.Tensor
+    weights: torch.Tensor
+    generation: torch.Tensor
+    tensor_pointers: tuple[int, int, int]
+
+    @property
+    def resident_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.ids, self.weights, self.generation))
+
+
+@dataclass(frozen=True)
+class MoERouteCaptureEvidence:
+    """A host copy of one capture buffer taken outside replay
+    (``moe_runtime.py:138-148``)."""
+
+    global_rows: int
+    slot: int
+    ids: torch.Tensor
+    weights: torch.Tensor
+    generation: int
+    device_tensor_pointers: tuple[int, int, int]
+    route_digest: str
 
 
 class TP4MoE:
@@ -243,8 +253,10 @@ class TP4MoE:
     ) -> None:
         config.validate()
         device = torch.device(device)
-        if device.type != "cuda":
-            raise ValueError("TP4MoE runs on a GPU device")
+        if device.type not in ("cuda", "cpu"):
+            raise ValueError(f"TP4MoE runs on a GPU device, not {device}")
+        # A layer built on the CPU supports the host-side lifecycle only
+        # (registration, capture bindings, validation); every call raises.
         if rank != 0:
             raise ValueError("single-GPU layer: rank must be 0")
         if group is not None:
@@ -324,6 +336,12 @@ class TP4MoE:
             if not callable(alignment_provider):
                 raise TypeError("alignment_provider must be callable")
         self._owned_alignment_provider = alignment_provider
+        # the provider the next calls use: the owned one, or None (the built-in
+        # alignment) inside bind_alignment_provider_for_capture(None, ...)
+        self._active_alignment_provider = alignment_provider
+        self._capture_lease: frozenset[tuple[int, int]] | None = None
+        self._route_captures: dict[tuple[int, int], MoERouteCaptureBuffer] = {}
+        self._route_capture_tensors: dict[tuple[int, int], tuple[torch.Tensor, ...]] = {}
         self._alignment_provider_poisoned = False
         self._alignment_provider_tensors = self._snapshot_provider_tensors(alignment_provider)
         if slots_per_shape < 1:
@@ -408,41 +426,39 @@ class TP4MoE:
 
     # ------------------------------------------------- alignment provider
     def _snapshot_provider_tensors(self, provider) -> tuple[torch.Tensor, ...]:
+        """The provider's own storage (``storage_tensors()``, reference
+        ``moe_runtime.py:631-666``): a tuple of non-empty, contiguous,
+        gradient-free tensors on the layer's device, each the whole of its
+        allocation, no two sharing one."""
+
         if provider is None:
             return ()
-        storage_tensors = getattr(provider, "storage_tensors", None)
-        if not callable(storage_tensors):
-            raise TypeError("alignment_provider must expose callable storage_tensors")
-        observed = storage_tensors()
-        if not isinstance(observed, tuple):
-            raise TypeError("alignment_provider.storage_tensors() must return a tuple")
-        pointers: set[int] = set()
-        for tensor in observed:
-            if not isinstance(tensor, torch.Tensor):
-                raise TypeError("alignment provider storage must contain only tensors")
-            if tensor.device != self.device:
-                raise ValueError("alignment provider storage device differs")
-            if tensor.numel() <= 0 or not tensor.is_contiguous():
-                raise ValueError("alignment provider storage must be nonempty and contiguous")
-            if tensor.requires_grad:
-                raise ValueError("alignment provider storage must not require gradients")
-            storage = tensor.untyped_storage()
-            if tensor.storage_offset() != 0 or storage.nbytes() != tensor.numel() * tensor.element_size():
-                raise ValueError("alignment provider tensors must own their complete storage")
-            pointer = int(storage.data_ptr())
-            if pointer in pointers:
-                raise ValueError("alignment provider storage tensors must not alias")
-            pointers.add(pointer)
-        return observed
+        lister = getattr(provider, "storage_tensors", None)
+        if not callable(lister):
+            raise TypeError("alignment_provider must expose a callable storage_tensors()")
+        owned = lister()
+        if not isinstance(owned, tuple):
+            raise TypeError(f"alignment_provider.storage_tensors() returned {type(owned).__name__}, not a tuple")
+        named = {f"alignment provider storage[{i}]": t for i, t in enumerate(owned)}
+        for name, t in named.items():
+            C.tensor(name, t, device=self.device, contiguous=True, no_grad=True, nonempty=True)
+            C.owns_whole_storage(name, t)
+        C.distinct_storages(named, what="alignment provider storage")
+        return owned
 
-    def _runtime_storage_pointers(self) -> set[int]:
+    def _runtime_tensors(self) -> list[torch.Tensor]:
         tensors = [self.resident.w13_q, self.resident.w13_s, self.resident.w2_q, self.resident.w2_s,
                    self.gate.weight]
         for b in self._buffers.values():
             tensors += [b.workspace, b.logits, b.route_ids, b.route_weights, b.margin, b.output,
                         b.alignment.sorted_token_ids, b.alignment.expert_ids,
                         b.alignment.num_tokens_post_padded]
-        return {int(t.untyped_storage().data_ptr()) for t in tensors}
+        for owned in self._route_capture_tensors.values():
+            tensors += list(owned)
+        return tensors
+
+    def _runtime_storage_pointers(self) -> set[int]:
+        return {int(t.untyped_storage().data_ptr()) for t in self._runtime_tensors()}
 
     def _validate_provider_storage(self) -> None:
         if self._owned_alignment_provider is None:
@@ -461,6 +477,223 @@ class TP4MoE:
         for b in self._buffers.values():
             b.state = "poisoned"
 
+    def _require_healthy(self) -> None:
+        if self._alignment_provider_poisoned:
+            raise RuntimeError("MoE alignment-provider lifecycle is poisoned; restart required")
+
+    def _lifecycle(self, keys) -> dict[tuple[int, int], tuple[str, bool, int]]:
+        return {key: (self._buffers[key].state, self._buffers[key].has_completion_event,
+                      id(self._buffers[key].ready_event)) for key in keys}
+
+    @contextmanager
+    def bind_alignment_provider_for_capture(self, provider: Callable[..., object] | None, *,
+                                            buffer_keys: Iterable[tuple[int, int]]) -> Iterator[None]:
+        """Choose the alignment path (the owned provider, or None for the
+        built-in alignment) for one fresh graph capture of the listed
+        (rows, slot) buffers (reference ``moe_runtime.py:825-978``).
+
+        On entry every slot must be free and each listed slot must have had
+        its completion event reset; calls to unlisted slots are refused while
+        the lease is held.  On exit the listed slots must be free with a new
+        completion event (the captured call recorded it) and every other slot
+        untouched; a failed capture must leave every slot as it was.  Any
+        violation, and any change of the provider's storage, poisons the
+        layer (RuntimeError; a restart is required).  Graphs captured before
+        keep the path they captured.
+        """
+
+        if provider is not None and provider is not self._owned_alignment_provider:
+            raise ValueError("the capture provider must be None or the layer's own alignment provider")
+        self._require_healthy()
+        if self._capture_lease is not None:
+            raise RuntimeError("alignment-provider capture bindings cannot be nested")
+        keys = tuple(buffer_keys)
+        if not keys:
+            raise ValueError("a capture binding needs at least one (rows, slot) key")
+        for key in keys:
+            if not (isinstance(key, tuple) and len(key) == 2
+                    and all(isinstance(v, int) and not isinstance(v, bool) for v in key)):
+                raise TypeError(f"capture binding keys are (rows, slot) integer pairs, got {key!r}")
+            if key not in self._buffers:
+                raise ValueError(f"capture binding key {key} is not a registered (rows, slot)")
+        if len(set(keys)) != len(keys):
+            raise ValueError("capture binding keys must be unique")
+        busy = {k: b.state for k, b in self._buffers.items() if b.state != "free"}
+        if busy:
+            raise RuntimeError(f"a capture binding needs every slot free; busy: {busy}")
+        stale = [k for k in keys if self._buffers[k].has_completion_event]
+        if stale:
+            raise RuntimeError(f"reset the completion events of {stale} before binding them for capture")
+        before = self._lifecycle(self._buffers)
+        try:
+            self._validate_provider_storage()
+        except Exception as exc:
+            self._poison_alignment_runtime()
+            raise RuntimeError("alignment-provider storage changed; restart required") from exc
+        previous = self._active_alignment_provider
+        self._active_alignment_provider = provider
+        self._capture_lease = frozenset(keys)
+        completed = False
+        try:
+            yield
+            completed = True
+        finally:
+            self._active_alignment_provider = previous
+            self._capture_lease = None
+            after = self._lifecycle(self._buffers)
+            problems = []
+            for key in self._buffers:
+                if completed and key in keys:
+                    state, has_event, event = after[key]
+                    if state != "free" or not has_event or event != before[key][2]:
+                        problems.append(f"{key}: captured slot ended {state}, completion event {has_event}")
+                elif after[key] != before[key]:
+                    problems.append(f"{key}: lifecycle changed from {before[key]} to {after[key]}")
+            try:
+                self._validate_provider_storage()
+            except Exception as exc:  # noqa: BLE001 - reported with the rest
+                problems.append(f"provider storage: {exc}")
+            if problems:
+                self._poison_alignment_runtime()
+                raise RuntimeError("capture binding left the layer inconsistent: " + "; ".join(problems))
+
+    # ------------------------------------------------------ route capture
+    @property
+    def registered_route_capture_slots(self) -> dict[int, tuple[int, ...]]:
+        rows = sorted({r for r, _ in self._route_captures})
+        return {r: tuple(sorted(s for rr, s in self._route_captures if rr == r)) for r in rows}
+
+    def register_route_capture(self, global_rows: int, slot: int = 0) -> MoERouteCaptureBuffer:
+        """Allocate the stable route target of one (rows, slot) before a
+        graph capture (reference ``moe_runtime.py:1017-1089``): every later
+        call of that slot copies its effective route (ids, weights) there and
+        adds one to the device generation, with no host read."""
+
+        self._require_healthy()
+        if self._capture_lease is not None:
+            raise RuntimeError("route captures cannot be registered during a capture binding")
+        if not all(isinstance(v, int) and not isinstance(v, bool) for v in (global_rows, slot)):
+            raise TypeError("route capture rows and slot must be integers")
+        key = (global_rows, slot)
+        if key not in self._buffers:
+            raise ValueError(f"route capture {key} has no registered buffers; registered={self.registered_slots}")
+        if key in self._route_captures:
+            raise RuntimeError(f"a route capture for {key} is already registered")
+        shape = (global_rows, self.config.topk)
+        owned = (torch.full(shape, -1, dtype=torch.int32, device=self.device),
+                 torch.zeros(shape, dtype=torch.float32, device=self.device),
+                 torch.zeros(1, dtype=torch.int64, device=self.device))
+        capture = MoERouteCaptureBuffer(global_rows=global_rows, slot=slot, owner_id=id(self), ids=owned[0],
+                                        weights=owned[1], generation=owned[2],
+                                        tensor_pointers=tuple(int(t.data_ptr()) for t in owned))
+        self._route_captures[key] = capture
+        self._route_capture_tensors[key] = owned
+        try:
+            self._check_route_capture(key, capture)
+        except BaseException:
+            del self._route_captures[key], self._route_capture_tensors[key]
+            raise
+        try:
+            self._validate_provider_storage()
+        except BaseException as exc:
+            del self._route_captures[key], self._route_capture_tensors[key]
+            self._poison_alignment_runtime()
+            raise RuntimeError("registering a route capture broke the provider storage; restart required") from exc
+        return capture
+
+    def _check_route_capture(self, key: tuple[int, int], capture: MoERouteCaptureBuffer) -> None:
+        """The registered capture object and its tensors are unchanged and
+        share storage with nothing else of the layer."""
+
+        if not isinstance(capture, MoERouteCaptureBuffer):
+            raise TypeError("route capture has the wrong type")
+        owned = self._route_capture_tensors.get(key)
+        if owned is None or self._route_captures.get(key) is not capture:
+            raise ValueError(f"route capture {key} is not the one registered")
+        if (capture.owner_id, capture.global_rows, capture.slot) != (id(self), *key):
+            raise ValueError(f"route capture {key} belongs to another layer or slot")
+        shape = (key[0], self.config.topk)
+        expected = (("ids", capture.ids, shape, torch.int32), ("weights", capture.weights, shape, torch.float32),
+                    ("generation", capture.generation, (1,), torch.int64))
+        for (name, t, want, dtype), mine in zip(expected, owned):
+            if t is not mine:
+                raise ValueError(f"route capture {key}: {name} was replaced")
+            C.tensor(f"route capture {name}", t, shape=want, dtype=dtype, device=self.device, contiguous=True,
+                     no_grad=True, dtype_error=ValueError)
+        if tuple(int(t.data_ptr()) for t in owned) != capture.tensor_pointers:
+            raise ValueError(f"route capture {key}: storage moved")
+        mine = {int(t.untyped_storage().data_ptr()) for t in owned}
+        if len(mine) != 3:
+            raise ValueError(f"route capture {key}: its tensors share storage")
+        others = [t for k, ts in self._route_capture_tensors.items() if k != key for t in ts]
+        for b in self._buffers.values():
+            others += [b.workspace, b.output, b.route_ids, b.route_weights, b.alignment.sorted_token_ids,
+                       b.alignment.expert_ids, b.alignment.num_tokens_post_padded]
+        if mine & {int(t.untyped_storage().data_ptr()) for t in others}:
+            raise ValueError(f"route capture {key}: storage aliases another buffer of the layer")
+
+    def route_capture_buffer(self, global_rows: int, slot: int = 0) -> MoERouteCaptureBuffer:
+        key = (global_rows, slot)
+        capture = self._route_captures.get(key)
+        if capture is None:
+            raise ValueError(f"no route capture is registered for {key}")
+        self._check_route_capture(key, capture)
+        return capture
+
+    def snapshot_route_capture(self, global_rows: int, slot: int = 0, *,
+                               expected_generation: int) -> MoERouteCaptureEvidence:
+        """A host copy of the capture buffer (reference
+        ``moe_runtime.py:1190-1227``); synchronises, so it belongs outside
+        replay and timed regions.  The device generation must equal
+        ``expected_generation`` before and after the copy."""
+
+        if isinstance(expected_generation, bool) or not isinstance(expected_generation, int) \
+                or expected_generation <= 0:
+            raise ValueError("expected_generation must be a positive integer")
+        capture = self.route_capture_buffer(global_rows, slot)
+        seen = int(capture.generation.item())
+        if seen == 0:
+            raise RuntimeError("the route capture has not recorded a route yet")
+        if seen != expected_generation:
+            raise RuntimeError(f"route capture generation is {seen}, expected {expected_generation}")
+        ids = capture.ids.detach().cpu().clone()
+        weights = capture.weights.detach().cpu().clone()
+        if int(capture.generation.item()) != expected_generation:
+            raise RuntimeError("the route capture changed while it was being copied")
+        return MoERouteCaptureEvidence(global_rows=global_rows, slot=slot, ids=ids, weights=weights,
+                                       generation=seen, device_tensor_pointers=capture.tensor_pointers,
+                                       route_digest=_tensor_digest(ids, weights))
+
+    def reset_route_capture_generation(self, global_rows: int, slot: int = 0) -> None:
+        """Zero the device generation in place (after graph setup / warm-up)."""
+
+        self.route_capture_buffer(global_rows, slot).generation.zero_()
+
+    def _capture_route(self, key: tuple[int, int], weights: torch.Tensor,
+                       ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Copy the effective route into the registered capture buffer on the
+        current stream and return the buffer's tensors, which the rest of the
+        call then uses (reference ``moe_runtime.py:1237-1283``)."""
+
+        for k, cap in self._route_captures.items():
+            self._check_route_capture(k, cap)
+        capture = self._route_captures[key]
+        want = (key[0], self.config.topk)
+        C.tensor("effective route ids", ids, shape=want, dtype=torch.int32, device=self.device, contiguous=True,
+                 dtype_error=ValueError)
+        C.tensor("effective route weights", weights, shape=want, dtype=torch.float32, device=self.device,
+                 contiguous=True, dtype_error=ValueError)
+        sources = {int(ids.untyped_storage().data_ptr()), int(weights.untyped_storage().data_ptr())}
+        if len(sources) != 2:
+            raise ValueError("effective route ids and weights share storage")
+        targets = {int(t.untyped_storage().data_ptr()) for ts in self._route_capture_tensors.values() for t in ts}
+        if sources & targets:
+            raise ValueError("the effective route already lives in a route capture buffer")
+        capture.ids.copy_(ids)
+        capture.weights.copy_(weights)
+        capture.generation.add_(1)
+        return capture.weights, capture.ids
+
     # ----------------------------------------------------- lifecycle
     def slot_completion_status(self, global_rows: int, slot: int) -> dict[str, Any]:
         key = (global_rows, slot)
@@ -470,8 +703,9 @@ class TP4MoE:
         return {"state": b.state, "has_completion_event": b.has_completion_event}
 
     def reset_free_slot_completion_event(self, global_rows: int, slot: int) -> None:
-        if self._alignment_provider_poisoned:
-            raise RuntimeError("MoE alignment-provider lifecycle is poisoned; restart required")
+        self._require_healthy()
+        if self._capture_lease is not None:
+            raise RuntimeError("slot completion events cannot be reset during a capture binding")
         key = (global_rows, slot)
         if key not in self._buffers:
             raise ValueError(f"global row/slot {key} was not pre-registered")
@@ -490,15 +724,16 @@ class TP4MoE:
 
     @contextmanager
     def observe_route_tensors(self, *, capture_local_input: bool = False) -> Iterator[list[MoERouteTensors]]:
-        if not isinstance(capture_local_input, bool):
-            raise TypeError("capture_local_input must be bool")
+        """Collect the route tensors of every call inside the block (reference
+        ``moe_runtime.py:1318-1335``), optionally with a copy of the input."""
+
+        C.boolean("capture_local_input", capture_local_input)
         if self._route_tensor_observer is not None:
-            raise RuntimeError("route tensor observation cannot be nested")
-        observed: list[MoERouteTensors] = []
-        self._route_tensor_observer = observed
+            raise RuntimeError("route tensor observation is already active")
+        self._route_tensor_observer = collected = []
         self._route_observer_captures_local_input = capture_local_input
         try:
-            yield observed
+            yield collected
         finally:
             self._route_tensor_observer = None
             self._route_observer_captures_local_input = False
@@ -556,6 +791,11 @@ class TP4MoE:
                 if not input_ids_local.is_contiguous():
                     raise ValueError("input_ids_local must be contiguous")
                 local_ids = input_ids_local.view(-1)
+                # an id outside the table would route to expert -1; the kernels
+                # would then poison the output with NaN, but an eager call fails
+                # here first (one host read; skipped while a graph is captured)
+                if local_ids.device.type != "cuda" or not torch.cuda.is_current_stream_capturing():
+                    C.ids_below("input_ids_local", local_ids, int(self.gate.tid2eid.shape[0]))
             shape = tuple(hidden_local.shape)
             flat = hidden_local.reshape(-1, cfg.hidden_size).contiguous()
             rows = flat.shape[0]
@@ -572,13 +812,16 @@ class TP4MoE:
                 raise ValueError(
                     f"global row/slot {key} was not pre-registered; registered={self.registered_slots}"
                 )
-            if self._alignment_provider_poisoned:
-                raise RuntimeError("MoE alignment-provider lifecycle is poisoned; restart required")
+            self._require_healthy()
+            if self._capture_lease is not None and key not in self._capture_lease:
+                raise RuntimeError(f"MoE buffer slot {key} is outside the active graph-capture binding")
             b = self._buffers[key]
             if b.state != "free":
                 raise RuntimeError(
                     f"MoE buffer slot {key} is {b.state}; worker restart is required after a poisoned slot"
                 )
+            if self.device.type != "cuda":
+                raise ValueError("this TP4MoE was built on the CPU for host-side checks; it computes on a GPU")
             return shape, flat, local_ids, override, b
 
         shape, flat, local_ids, override, buffers = run_local("prepare MoE input", prepare_input)
@@ -598,12 +841,14 @@ class TP4MoE:
                 route_source = "native"
                 margin = None
                 a = buffers.alignment
+                capture_key = (flat.shape[0], slot)
                 fused = (
                     self.route_kind == "learned"
                     and self._marlin_input_dtype is None
                     and override is None
-                    and self._owned_alignment_provider is None
+                    and self._active_alignment_provider is None
                     and self._route_tensor_observer is None
+                    and capture_key not in self._route_captures
                     and stage_marker is None
                 )
                 if self.route_kind == "learned" and router_logits is None:
@@ -661,7 +906,9 @@ class TP4MoE:
                             route_source=route_source,
                         )
                     )
-                provider = self._owned_alignment_provider
+                if capture_key in self._route_captures:
+                    route_weights, route_ids = self._capture_route(capture_key, route_weights, route_ids)
+                provider = self._active_alignment_provider
                 if provider is None:
                     # the experts workspace is idle until the experts launches, which
                     # follow on the same stream: it holds the split alignment's scratch
@@ -775,6 +1022,8 @@ MoELayer = TP4MoE
 __all__ = [
     "FLASH_CONFIG",
     "MoELayer",
+    "MoERouteCaptureBuffer",
+    "MoERouteCaptureEvidence",
     "MoERouteOverride",
     "MoERouteTensors",
     "MoETrace",

@@ -404,42 +404,61 @@ def w8a16_workspace_bytes(m: int, n: int, split_k: int) -> int:
     return int(_lib.load().dsv4moe_w8a16_workspace_bytes(m, n, split_k))
 
 
+def _weight_bytes(name: str, wq: torch.Tensor, n: int, k: int, dev) -> tuple[torch.Tensor, int]:
+    """A 1-byte weight as uint8 and its layout code: [n, k] (any 1-byte dtype:
+    the checkpoint's bytes, row-major) or flat [n*k] uint8 (the tiles of
+    ``pack_int8`` / ``pack_fp8``)."""
+
+    if wq.dim() == 2:
+        if wq.element_size() != 1:
+            raise TypeError(f"{name} must have 1-byte elements, got {wq.dtype}")
+        _check(name, wq, dtype=wq.dtype, shape=(n, k), device=dev)
+        return wq.view(torch.uint8), _lib.WEIGHT_ROWMAJOR
+    _check(name, wq, dtype=torch.uint8, shape=(n * k,), device=dev)
+    return wq, _lib.WEIGHT_TILED
+
+
 def w8a16_linear_into(a: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, out: torch.Tensor,
                       workspace: torch.Tensor | None, *, n: int, split_k: int) -> None:
+    """int8 weights with bf16 per-channel scales ``ws`` [n]
+    (``dsv4moe_w8a16_linear``); ``wq`` int8 [n, k] row-major or the flat
+    ``pack_int8`` tiles."""
+
     if a.ndim != 2:
         raise ValueError("activation must be [m, k]")
     m, k = a.shape
     dev = a.device
     _check("activation", a, dtype=torch.bfloat16, device=dev)
-    _check("weight", wq, dtype=torch.uint8, shape=(n * k,), device=dev)
+    wq, layout = _weight_bytes("weight", wq, n, k, dev)
     _check("weight_scale", ws, dtype=torch.bfloat16, shape=(n,), device=dev)
     _check("out", out, dtype=torch.bfloat16, shape=(m, n), device=dev)
     ws_bytes = 0
     if workspace is not None:
         _check("workspace", workspace, dtype=torch.float32, device=dev)
         ws_bytes = workspace.numel() * 4
-    call("dsv4moe_w8a16_linear", ptr(a), m, n, k, ptr(wq), ptr(ws), int(split_k), ptr(workspace),
+    call("dsv4moe_w8a16_linear", ptr(a), m, n, k, ptr(wq), layout, ptr(ws), int(split_k), ptr(workspace),
          ws_bytes, ptr(out), _lib.current_stream(dev))
 
 
 def w8a16_fp8_linear_into(a: torch.Tensor, wq: torch.Tensor, ws8: torch.Tensor, out: torch.Tensor,
                           workspace: torch.Tensor | None, *, n: int, split_k: int) -> None:
-    """FP8 E4M3 weights (packed by ``pack_fp8``) with E8M0 128 x 128 block
-    scales ``ws8`` uint8 [ceil(n/128), k/128] (``dsv4moe_w8a16_fp8_linear``)."""
+    """FP8 E4M3 weights with E8M0 128 x 128 block scales ``ws8`` uint8
+    [ceil(n/128), k/128] (``dsv4moe_w8a16_fp8_linear``); ``wq`` the
+    checkpoint's E4M3 [n, k] as stored, or the flat ``pack_fp8`` tiles."""
 
     if a.ndim != 2:
         raise ValueError("activation must be [m, k]")
     m, k = a.shape
     dev = a.device
     _check("activation", a, dtype=torch.bfloat16, device=dev)
-    _check("weight", wq, dtype=torch.uint8, shape=(n * k,), device=dev)
+    wq, layout = _weight_bytes("weight", wq, n, k, dev)
     _check("weight_scale", ws8, dtype=torch.uint8, shape=((n + 127) // 128, k // 128), device=dev)
     _check("out", out, dtype=torch.bfloat16, shape=(m, n), device=dev)
     ws_bytes = 0
     if workspace is not None:
         _check("workspace", workspace, dtype=torch.float32, device=dev)
         ws_bytes = workspace.numel() * 4
-    call("dsv4moe_w8a16_fp8_linear", ptr(a), m, n, k, ptr(wq), ptr(ws8), int(split_k), ptr(workspace),
+    call("dsv4moe_w8a16_fp8_linear", ptr(a), m, n, k, ptr(wq), layout, ptr(ws8), int(split_k), ptr(workspace),
          ws_bytes, ptr(out), _lib.current_stream(dev))
 
 
@@ -478,8 +497,9 @@ def block_fp8_workspace_bytes(m: int, n: int, split_k: int) -> int:
 def block_fp8_gemm_into(a: torch.Tensor, a_scale: torch.Tensor, wq: torch.Tensor, ws8: torch.Tensor,
                         out: torch.Tensor, workspace: torch.Tensor | None, *, n: int, split_k: int) -> None:
     """Block-FP8 W8A8 GEMM (``dsv4moe_block_fp8_gemm``): a E4M3 uint8 [m, k]
-    with E8M0 a_scale [m, k/128]; wq the ``pack_fp8`` tiles of W [n, k] with
-    E8M0 ws8 [ceil(n/128), k/128]; out bf16 [m, n]."""
+    with E8M0 a_scale [m, k/128]; wq W [n, k] (the checkpoint's E4M3 bytes
+    as stored, or the flat ``pack_fp8`` tiles) with E8M0 ws8
+    [ceil(n/128), k/128]; out bf16 [m, n]."""
 
     if a.ndim != 2:
         raise ValueError("activation must be [m, k]")
@@ -487,14 +507,14 @@ def block_fp8_gemm_into(a: torch.Tensor, a_scale: torch.Tensor, wq: torch.Tensor
     dev = a.device
     _check("activation", a, dtype=torch.uint8, device=dev)
     _check("activation_scale", a_scale, dtype=torch.uint8, shape=(m, k // 128), device=dev)
-    _check("weight", wq, dtype=torch.uint8, shape=(n * k,), device=dev)
+    wq, layout = _weight_bytes("weight", wq, n, k, dev)
     _check("weight_scale", ws8, dtype=torch.uint8, shape=((n + 127) // 128, k // 128), device=dev)
     _check("out", out, dtype=torch.bfloat16, shape=(m, n), device=dev)
     ws_bytes = 0
     if workspace is not None:
         _check("workspace", workspace, dtype=torch.float32, device=dev)
         ws_bytes = workspace.numel() * 4
-    call("dsv4moe_block_fp8_gemm", ptr(a), ptr(a_scale), m, n, k, ptr(wq), ptr(ws8), int(split_k),
+    call("dsv4moe_block_fp8_gemm", ptr(a), ptr(a_scale), m, n, k, ptr(wq), layout, ptr(ws8), int(split_k),
          ptr(workspace), ws_bytes, ptr(out), _lib.current_stream(dev))
 
 

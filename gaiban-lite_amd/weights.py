@@ -23,6 +23,7 @@ from dataclasses import dataclass
 
 import torch
 
+from . import contracts as C
 from . import ops
 
 GROUP = 128
@@ -298,6 +299,8 @@ class ResidentMXFP4MoEWeights:
         ``w13_packed`` [E', 2I, H/2] u8 (E2M1, low nibble = even k),
         ``w13_scale`` [E', 2I, H/32] u8 (E8M0, or torch.float8_e8m0fnu viewed as
         bytes), ``w2_packed`` [E', H, I/2] u8, ``w2_scale`` [E', H, I/32] u8.
+        The reserved scale byte 255 (NaN in the reference's decode) is
+        rejected with ValueError; the check reads the device (load time).
         """
 
         def as_u8(t):
@@ -309,6 +312,8 @@ class ResidentMXFP4MoEWeights:
             raise ValueError("w2_packed must be [E', H, I/2] matching w13_packed")
         if e_tot != experts + (1 if has_shared else 0):
             raise ValueError("expert count does not match the stacked tensors")
+        C.no_reserved_e8m0("w13_scale", w13_scale)
+        C.no_reserved_e8m0("w2_scale", w2_scale)
         q13, s13 = ops.pack_mxfp4_g32(as_u8(w13_packed).contiguous(), as_u8(w13_scale).contiguous(), gated=True)
         q2, s2 = ops.pack_mxfp4_g32(as_u8(w2_packed).contiguous(), as_u8(w2_scale).contiguous(), gated=False)
         out = cls(q13, s13, q2, s2, experts, hidden, inter, has_shared, layer_id, checkpoint_id,

@@ -293,6 +293,17 @@ int dsv4moe_layer_mxfp4(const uint16_t* x, const float* logits, const float* bia
                         size_t workspace_bytes, void* stream);
 
 /*
+ * Weight layouts of the dense linears (argument weight_layout):
+ *   DSV4MOE_WEIGHT_ROWMAJOR  the checkpoint's bytes as stored, row-major [n, k]
+ *                            (what the reference's entry points take);
+ *   DSV4MOE_WEIGHT_TILED     the load-time repack of dsv4moe_pack_int8 /
+ *                            dsv4moe_pack_fp8 (1 KiB tiles, below).
+ * Both feed the same kernels and give the same bits.
+ */
+#define DSV4MOE_WEIGHT_TILED 0
+#define DSV4MOE_WEIGHT_ROWMAJOR 1
+
+/*
  * W8A16 dense linear: out[M,N] = bf16( a[M,K] . (q[N,K] * s[N])^T ), int8
  * symmetric per-output-channel weights, bf16 scales, fp32 accumulation.
  * Replaces w8a16_gemm_into / make_gemm_plan / _automatic_split_k
@@ -306,7 +317,8 @@ int dsv4moe_layer_mxfp4(const uint16_t* x, const float* logits, const float* bia
  * dsv4moe_w8a16_workspace_bytes: split*m*n*4 when split > 1, else 0.
  * dsv4moe_w8a16_linear:
  *   a       bf16 [m, k]
- *   wq      packed int8 (dsv4moe_pack_int8), ws bf16 [n]
+ *   wq      int8 [n, k] in weight_layout (row-major, or packed by dsv4moe_pack_int8)
+ *   ws      bf16 [n]
  *   split_k 1, 2, 4, 8 or 16 (<= k/128); > 1 uses workspace fp32 [split, m, n],
  *           partials reduced in split order before the single bf16 rounding
  *   out     bf16 [m, n]
@@ -316,7 +328,7 @@ int dsv4moe_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed, vo
 int32_t dsv4moe_w8a16_split_k(int64_t m, int64_t n, int64_t k);
 size_t dsv4moe_w8a16_workspace_bytes(int64_t m, int64_t n, int32_t split_k);
 int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
-                         const uint16_t* ws, int32_t split_k, float* workspace,
+                         int32_t weight_layout, const uint16_t* ws, int32_t split_k, float* workspace,
                          size_t workspace_bytes, uint16_t* out, void* stream);
 
 /*
@@ -327,7 +339,8 @@ int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, con
  * weights (experiments/C1F-integrated-block/weight_only_linear.py:537-598,
  * E8M0 decode :488-513: byte 0 is 2^-127, 255 reserved) and
  * dequant_fp8_block (runtime/dsv4_direct/moe_forward.py:158-176).
- *   wq      the E4M3 bytes [n, k] packed by dsv4moe_pack_int8 (a byte
+ *   wq      the E4M3 bytes [n, k] in weight_layout: as stored in the
+ *           checkpoint (row-major), or packed by dsv4moe_pack_int8 (a byte
  *           permutation; it packs any 1-byte format)
  *   ws8     E8M0 bytes [ceil(n/128), k/128], row-major; 255 must not occur
  *           (the reference rejects it in a cold preflight; the Python wrapper
@@ -336,8 +349,8 @@ int dsv4moe_w8a16_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, con
  * m >= 0, n % 16 == 0, k % 128 == 0, k <= 32768, m*k*2 and n*k below 2^31.
  */
 int dsv4moe_w8a16_fp8_linear(const uint16_t* a, int64_t m, int64_t n, int64_t k, const uint8_t* wq,
-                             const uint8_t* ws8, int32_t split_k, float* workspace, size_t workspace_bytes,
-                             uint16_t* out, void* stream);
+                             int32_t weight_layout, const uint8_t* ws8, int32_t split_k, float* workspace,
+                             size_t workspace_bytes, uint16_t* out, void* stream);
 
 /*
  * Block-FP8 W8A8 activation quantiser.  Replaces activation_quant_into
@@ -359,7 +372,8 @@ int dsv4moe_act_quant_block_fp8(const void* x, int32_t x_dtype, int64_t m, int64
  *   out[m, n] = bf16( sum over 128-K blocks kb of
  *                     (A_kb . W_kb^T) * 2^(a_scale[m, kb] - 127) * 2^(w_scale[n/128, kb] - 127) )
  *   a        E4M3 [m, k] row-major, a_scale E8M0 [m, k/128] (dsv4moe_act_quant_block_fp8)
- *   wq       E4M3 weights [n, k] packed by dsv4moe_pack_int8 (1 KiB tiles)
+ *   wq       E4M3 weights [n, k] in weight_layout (the checkpoint's row-major
+ *            bytes, or packed by dsv4moe_pack_int8 into 1 KiB tiles)
  *   w_scale  E8M0 [ceil(n/128), k/128] (the checkpoint's block scales; byte 0 = 2^-127)
  *   split_k  1, 2, 4 or 8; > 1 needs dsv4moe_block_fp8_workspace_bytes bytes of
  *            fp32 [split, m, n] workspace, reduced in split order
@@ -369,8 +383,8 @@ int dsv4moe_act_quant_block_fp8(const void* x, int32_t x_dtype, int64_t m, int64
 int32_t dsv4moe_block_fp8_split_k(int64_t m, int64_t n, int64_t k);
 size_t dsv4moe_block_fp8_workspace_bytes(int64_t m, int64_t n, int32_t split_k);
 int dsv4moe_block_fp8_gemm(const uint8_t* a, const uint8_t* a_scale, int64_t m, int64_t n, int64_t k,
-                           const uint8_t* wq, const uint8_t* w_scale, int32_t split_k, float* workspace,
-                           size_t workspace_bytes, uint16_t* out, void* stream);
+                           const uint8_t* wq, int32_t weight_layout, const uint8_t* w_scale, int32_t split_k,
+                           float* workspace, size_t workspace_bytes, uint16_t* out, void* stream);
 
 /*
  * Shared expert over the checkpoint's FP8 E4M3 / E8M0 128x128-block weights,

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in dsv4moe.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.dsv4moe_abi_version() == 1
+    assert lib.dsv4moe_abi_version() == 2
 
 
 def test_host_policy_functions_match_oracle():
@@ -99,7 +99,8 @@ def test_align_workspace_policy_and_validation():
 def test_w8a16_validation_and_split_policy():
     fake = ctypes.c_void_p(0x1000)
     lib = _lib.load()
-    args = lambda m, n, k, split, ws_bytes: (fake, m, n, k, fake, fake, split, fake, ws_bytes, fake, None)
+    args = lambda m, n, k, split, ws_bytes, layout=0: (fake, m, n, k, fake, layout, fake, split, fake, ws_bytes,
+                                                       fake, None)
     assert "multiple of 16" in _einval("dsv4moe_w8a16_linear", *args(4, 40, 4096, 1, 0))
     assert "multiple of 128" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 4000, 1, 0))
     assert "split_k" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 4096, 3, 1 << 30))
@@ -107,8 +108,12 @@ def test_w8a16_validation_and_split_policy():
     need = lib.dsv4moe_w8a16_workspace_bytes(4, 64, 2)
     assert need == 2 * 4 * 64 * 4 and lib.dsv4moe_w8a16_workspace_bytes(4, 64, 1) == 0
     assert "workspace" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 4096, 2, need - 1))
+    assert "weight_layout" in _einval("dsv4moe_w8a16_linear", *args(4, 64, 4096, 1, 0, layout=2))
+    assert "weight_layout" in _einval("dsv4moe_w8a16_fp8_linear", *args(4, 64, 4096, 1, 0, layout=-1))
     assert "multiple of 16" in _einval("dsv4moe_pack_int8", fake, 24, 128, fake, None)
-    assert lib.dsv4moe_w8a16_linear(fake, 0, 64, 4096, fake, fake, 1, None, 0, fake, None) == _lib.DSV4MOE_OK
+    for layout in (_lib.WEIGHT_TILED, _lib.WEIGHT_ROWMAJOR):
+        assert lib.dsv4moe_w8a16_linear(fake, 0, 64, 4096, fake, layout, fake, 1, None, 0, fake,
+                                        None) == _lib.DSV4MOE_OK
     # this library's policy: a power of two in [1, 8] leaving >= 4 windows of 64 K per split,
     # raised only while the grid is below 512 workgroups
     for m in (1, 16, 17, 64, 65, 8192):
@@ -124,7 +129,7 @@ def test_w8a16_validation_and_split_policy():
 def test_block_fp8_validation_and_split_policy():
     fake = ctypes.c_void_p(0x1000)
     lib = _lib.load()
-    g = lambda m, n, k, split, ws: (fake, fake, m, n, k, fake, fake, split, fake, ws, fake, None)
+    g = lambda m, n, k, split, ws, layout=0: (fake, fake, m, n, k, fake, layout, fake, split, fake, ws, fake, None)
     assert "multiple of 16" in _einval("dsv4moe_block_fp8_gemm", *g(4, 40, 4096, 1, 0))
     assert "multiple of 128" in _einval("dsv4moe_block_fp8_gemm", *g(4, 64, 4000, 1, 0))
     assert "split_k" in _einval("dsv4moe_block_fp8_gemm", *g(4, 64, 4096, 16, 1 << 30))
@@ -132,6 +137,7 @@ def test_block_fp8_validation_and_split_policy():
     need = lib.dsv4moe_block_fp8_workspace_bytes(4, 64, 2)
     assert need == 2 * 4 * 64 * 4 and lib.dsv4moe_block_fp8_workspace_bytes(4, 64, 1) == 0
     assert "workspace" in _einval("dsv4moe_block_fp8_gemm", *g(4, 64, 4096, 2, need - 1))
+    assert "weight_layout" in _einval("dsv4moe_block_fp8_gemm", *g(4, 64, 4096, 1, 0, layout=7))
     assert "x_dtype" in _einval("dsv4moe_act_quant_block_fp8", fake, 3, 4, 128, fake, fake, None)
     assert "multiple of 128" in _einval("dsv4moe_act_quant_block_fp8", fake, 0, 4, 100, fake, fake, None)
     assert lib.dsv4moe_block_fp8_gemm(*g(0, 64, 4096, 1, 0)) == _lib.DSV4MOE_OK
@@ -201,14 +207,14 @@ def test_route_override_validation_cpu():
     got_ids, got_w = R._snapshot_route_override(R.MoERouteOverride(ids, w), rows=2, config=cfg, device=cpu)
     assert torch.equal(got_ids, ids) and got_ids.data_ptr() != ids.data_ptr()
     bad = [
-        (torch.tensor([[0, 0], [2, 3]], dtype=torch.int32), w, "unique"),
+        (torch.tensor([[0, 0], [2, 3]], dtype=torch.int32), w, "same expert twice"),
         (torch.tensor([[0, 9], [2, 3]], dtype=torch.int32), w, "outside"),
-        (ids, torch.tensor([[0.7, 0.7], [1.0, 0.5]]), "sum to route_scale"),
+        (ids, torch.tensor([[0.7, 0.7], [1.0, 0.5]]), "sum to 1.5"),
         (ids, torch.tensor([[1.5, 0.0], [1.0, 0.5]]), "strictly positive"),
-        (ids.long(), w, "INT32"),
+        (ids.long(), w, "int32"),
     ]
     for i, ww, msg in bad:
-        with pytest.raises((ValueError, TypeError), match=msg):
+        with pytest.raises(TypeError if i.dtype != torch.int32 else ValueError, match=msg):
             R._snapshot_route_override(R.MoERouteOverride(i, ww), rows=2, config=cfg, device=cpu)
 
 
@@ -227,12 +233,14 @@ def test_w8a16_fp8_validation_and_e8m0_preflight():
     from gaiban_lite_amd import weight_only_linear as L
 
     fake = ctypes.c_void_p(0x1000)
-    args = lambda m, n, k, split, ws_bytes: (fake, m, n, k, fake, fake, split, fake, ws_bytes, fake, None)
+    args = lambda m, n, k, split, ws_bytes, layout=0: (fake, m, n, k, fake, layout, fake, split, fake, ws_bytes,
+                                                       fake, None)
     assert "multiple of 16" in _einval("dsv4moe_w8a16_fp8_linear", *args(4, 40, 4096, 1, 0))
     assert "multiple of 128" in _einval("dsv4moe_w8a16_fp8_linear", *args(4, 64, 4000, 1, 0))
     assert "k must be <= 32768" in _einval("dsv4moe_w8a16_fp8_linear", *args(4, 64, 32896, 1, 0))
-    assert "null" in _einval("dsv4moe_w8a16_fp8_linear", fake, 4, 64, 4096, None, fake, 1, None, 0, fake, None)
-    assert _lib.load().dsv4moe_w8a16_fp8_linear(fake, 0, 64, 4096, fake, fake, 1, None, 0, fake, None) == _lib.DSV4MOE_OK
+    assert "null" in _einval("dsv4moe_w8a16_fp8_linear", fake, 4, 64, 4096, None, 0, fake, 1, None, 0, fake, None)
+    assert _lib.load().dsv4moe_w8a16_fp8_linear(fake, 0, 64, 4096, fake, 1, fake, 1, None, 0, fake,
+                                                None) == _lib.DSV4MOE_OK
     # the reference's cold preflight: the reserved E8M0 byte 255 is rejected at load time
     codes = torch.zeros((128, 256), dtype=torch.uint8)
     bad = torch.tensor([[127, 255]], dtype=torch.uint8)

@@ -25,7 +25,7 @@ def test_weight_map_and_slices(tmp_path):
         s = r.read("layers.3.ffn.shared_experts.w1.scale")
         assert s.dtype == torch.float8_e8m0fnu and torch.equal(s.view(torch.uint8),
                                                                raw["layers.3.ffn.shared_experts.w1.scale"].view(torch.uint8))
-        with pytest.raises(KeyError, match="not in index"):
+        with pytest.raises(KeyError, match="not listed in the index"):
             r.read("layers.3.ffn.experts.9.w1.weight")
 
 

@@ -31,12 +31,14 @@ def quant(x: torch.Tensor):
     return q, s
 
 
-def gemm(q, s, prep, split=None):
+def gemm(q, s, prep, split=None, raw=None):
+    """The GEMM over the prepared tiles, or with ``raw`` (the E4M3 [n, k]
+    bytes as stored) over the checkpoint layout."""
     m, k = q.shape
     split = ops.block_fp8_split_k(m, prep.n, k) if split is None else split
     out = torch.empty((m, prep.n), dtype=torch.bfloat16, device=DEV)
     ws = torch.empty(max(ops.block_fp8_workspace_bytes(m, prep.n, split) // 4, 1), dtype=torch.float32, device=DEV)
-    ops.block_fp8_gemm_into(q, s, prep.packed, prep.scale, out, ws, n=prep.n, split_k=split)
+    ops.block_fp8_gemm_into(q, s, prep.packed if raw is None else raw, prep.scale, out, ws, n=prep.n, split_k=split)
     return out
 
 
@@ -80,9 +82,12 @@ def test_one_hot_reads_back_weights_and_scales(split):
     a = np.zeros((m, k), dtype=np.uint8)
     a[np.arange(m), cols] = 0x38  # e4m3 1.0
     a_s = rng.integers(118, 136, size=(m, 4), dtype=np.uint8)  # a scale per (token, K block)
-    prep = L.prepare_fp8_block_weight(torch.from_numpy(w).to(DEV), torch.from_numpy(ws).to(DEV))
+    w_d = torch.from_numpy(w).to(DEV)
+    prep = L.prepare_fp8_block_weight(w_d, torch.from_numpy(ws).to(DEV))
     out = gemm(torch.from_numpy(a).to(DEV), torch.from_numpy(a_s).to(DEV), prep, split)
+    raw = gemm(torch.from_numpy(a).to(DEV), torch.from_numpy(a_s).to(DEV), prep, split, raw=w_d)
     torch.cuda.synchronize()
+    assert torch.equal(raw, out)
     wd = O.dequant_fp8_block(w, ws)                                    # W * 2^(ew-127), exact
     sa = O.decode_e8m0(a_s)[np.arange(m), cols // 128]                 # the scale of the K block read
     want = O.bf16_round((wd[:, cols] * sa[None, :]).T) + np.float32(0.0)
@@ -96,7 +101,9 @@ def run(m, n, k, *, split=None, seed=3, rows=None):
     q, s = quant(x)
     prep = L.prepare_fp8_block_weight(codes, scales)
     out = gemm(q, s, prep, split)
+    raw = gemm(q, s, prep, split, raw=codes)
     torch.cuda.synchronize()
+    assert torch.equal(raw, out), "checkpoint-layout and tiled weights differ"
     rows = np.arange(m) if rows is None else rows
     ref = O.block_fp8_gemm_f32(q.cpu().numpy()[rows], s.cpu().numpy()[rows], codes.cpu().numpy(),
                                scales.cpu().numpy())

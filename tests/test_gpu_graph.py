@@ -84,3 +84,54 @@ def test_capture_and_replay_matches_eager(shape, rows, use_logits):
     assert layer.slot_completion_status(rows, 0)["state"] == "free"
     del graph
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("rows", [8, 64])
+def test_route_capture_inside_a_bound_graph(rows):
+    """The reference's capture protocol (``moe_runtime.py:825-978,1017-1227``):
+    register the route capture, reset the slot's completion event, capture the
+    call inside ``bind_alignment_provider_for_capture(None, ...)``, reset the
+    generation after warm-up, replay with new inputs; each replay writes the
+    effective route into the capture buffer and adds one to the device
+    generation, and ``snapshot_route_capture`` returns it -- equal to the
+    route of an eager call of the same input, and the output equal too."""
+
+    import oracle as O
+
+    shape = S.LayerShape(experts=64, hidden=512, inter=512, topk=6, has_shared=True)
+    print(f"[graph] route capture T={rows}", flush=True)
+    layer = build(shape, [rows])
+    cap = layer.register_route_capture(rows, 0)
+    xs = [S.make_hidden(rows, shape.hidden, seed=80 + i, device=DEV).view(1, rows, shape.hidden) for i in range(4)]
+    lgs = [S.make_logits(rows, shape.experts, seed=90 + i, device=DEV) for i in range(4)]
+    x_s, lg_s = xs[0].clone(), lgs[0].clone()
+    side = torch.cuda.Stream(DEV)
+    side.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            layer.forward_tensor(x_s, router_logits=lg_s, slot=0)
+    torch.cuda.current_stream(DEV).wait_stream(side)
+    torch.cuda.synchronize()
+    assert int(cap.generation.item()) == 2
+    layer.reset_free_slot_completion_event(rows, 0)
+    graph = torch.cuda.CUDAGraph()
+    with layer.bind_alignment_provider_for_capture(None, buffer_keys=[(rows, 0)]):
+        with torch.cuda.graph(graph):
+            out_s = layer.forward_tensor(x_s, router_logits=lg_s, slot=0)
+    torch.cuda.synchronize()
+    layer.reset_route_capture_generation(rows, 0)
+    for i in range(1, 4):
+        x_s.copy_(xs[i])
+        lg_s.copy_(lgs[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        ev = layer.snapshot_route_capture(rows, 0, expected_generation=i)
+        ref = O.route_topk(lgs[i].cpu().numpy(), shape.topk, score_func=O.SCORE_SQRTSOFTPLUS,
+                           bias=layer.gate.bias.cpu().numpy(), route_scale=2.5)
+        assert torch.equal(ev.ids, torch.from_numpy(ref.ids))
+        assert torch.equal(ev.weights, torch.from_numpy(ref.weights))
+        eager = layer.forward_tensor(xs[i], router_logits=lgs[i], slot=1)
+        torch.cuda.synchronize()
+        assert torch.equal(out_s, eager), f"replay {i} differs from the eager call"
+    del graph
+    torch.cuda.synchronize()

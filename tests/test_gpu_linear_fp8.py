@@ -7,6 +7,11 @@ M in {1, 64, 8192}), every split-K width and ragged M, N (last row block
 partial).  A one-hot activation reads single weights back, which pins the
 conversion bit for bit: byte order inside each lane, the scale block of every
 strip and window, and scales from 2^-100 to 2^40.
+
+Every case runs the reference's own entry (``w8a16_gemm_into`` on the
+checkpoint's ``float8_e4m3fn`` weight and ``float8_e8m0fnu`` scales as
+stored) and the load-time tiled variant (``w8a16_prepared_gemm_into``); the
+two must give the same output bits.
 """
 
 import numpy as np
@@ -37,7 +42,9 @@ def run(m, n, k, *, split=None, seed=3, rows=None):
     a = torch.randn((m, k), device=DEV, generator=torch.Generator(DEV).manual_seed(seed + 100)).to(torch.bfloat16)
     prep = L.prepare_fp8_block_weight(codes, scales)
     out = L.w8a16_linear(a, prep, split_k=split)
+    raw = L.w8a16_linear(a, codes.view(torch.float8_e4m3fn), scales.view(torch.float8_e8m0fnu), split_k=split)
     torch.cuda.synchronize()
+    assert torch.equal(raw, out), "checkpoint-layout and tiled weights differ"
     rows = np.arange(m) if rows is None else rows
     ref = O.w8a16_fp8_linear_f32(to_np_f32(a)[rows], codes.cpu().numpy(), scales.cpu().numpy())
     err = assert_moe_close(to_np_f32(out)[rows], ref, what=f"fp8 M={m} N={n} split={split}")
@@ -69,9 +76,12 @@ def test_one_hot_reads_back_every_weight_exactly(split):
     a = np.zeros((m, k), dtype=np.float32)
     a[np.arange(m), cols] = 1.0
     at = torch.from_numpy(a).to(DEV).to(torch.bfloat16)
-    prep = L.prepare_fp8_block_weight(torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV))
+    codes_d, scales_d = torch.from_numpy(codes).to(DEV), torch.from_numpy(scales).to(DEV)
+    prep = L.prepare_fp8_block_weight(codes_d, scales_d)
     out = L.w8a16_linear(at, prep, split_k=split)
+    raw = L.w8a16_linear(at, codes_d.view(torch.float8_e4m3fn), scales_d.view(torch.float8_e8m0fnu), split_k=split)
     torch.cuda.synchronize()
+    assert torch.equal(raw, out)
     # + 0.0: a sum that starts at +0 turns the -0 of code 0x80 into +0
     want = O.bf16_round(O.dequant_fp8_block(codes, scales))[:, cols].T + np.float32(0.0)
     got = to_np_f32(out)
@@ -90,7 +100,7 @@ def test_prefill_shapes_row_subset(n):
     run(8192, n, 4096, rows=rows)
 
 
-@pytest.mark.parametrize("split", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("split", [1, 2, 4, 8])
 def test_every_split_width(split):
     run(64, 1024, 4096, split=split)
 
@@ -128,3 +138,36 @@ def test_prefill_tile_with_explicit_split(split):
 
     rows = np.sort(np.random.default_rng(split).choice(8192, 64, replace=False))
     run(8192, 4096, 4096, split=split, rows=rows)
+
+
+def test_reference_call_sequence():
+    """The reference module's own sequence (``weight_only_linear.py:182-221,
+    406-513,794-823``): plan, metadata validation, non-alias preflight, the
+    E8M0 preflight, then the hot call into caller-owned storage, repeated
+    without allocation; bad calls raise before any launch."""
+
+    m, n, k = 64, 1024, 4096
+    codes, scales = S.make_fp8_block_linear(n, k, seed=9, device=DEV)
+    weight, scale = codes.view(torch.float8_e4m3fn), scales.view(torch.float8_e8m0fnu)
+    a = torch.randn((m, k), device=DEV, generator=torch.Generator(DEV).manual_seed(9)).to(torch.bfloat16)
+    plan = L.make_gemm_plan(m, n, k)
+    out = torch.empty(plan.output_shape, dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(plan.workspace_shape, dtype=torch.float32, device=DEV)
+    assert plan.weight_shape == (n, k) and plan.weight_scale_shape == (n // 128, k // 128)
+    L.validate_fp8_weight_only_tensors(a, weight, scale, out, ws, plan=plan)
+    L.validate_non_alias_tensors({"activation": a, "weight": weight, "weight_scale": scale, "out": out,
+                                  "workspace": ws})
+    L.validate_e8m0_scale_values("weight_scale", scale)
+    L.w8a16_gemm_into(a, weight, scale, out, ws, plan=plan)
+    first = out.clone()
+    L.fp8_weight_only_linear_into(a, weight, scale, out, ws, plan=plan)
+    torch.cuda.synchronize()
+    assert torch.equal(out, first)
+    ref = O.w8a16_fp8_linear_f32(to_np_f32(a), codes.cpu().numpy(), scales.cpu().numpy())
+    assert_moe_close(to_np_f32(out), ref, what="reference sequence")
+    with pytest.raises(TypeError):  # tiled bytes are not the checkpoint contract
+        L.w8a16_gemm_into(a, codes, scale, out, ws, plan=plan)
+    with pytest.raises(TypeError):
+        L.w8a16_gemm_into(a, weight, scales, out, ws, plan=plan)
+    with pytest.raises(ValueError):
+        L.validate_non_alias_tensors({"out": out, "alias": out[:1]})
