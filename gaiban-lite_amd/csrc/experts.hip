@@ -56,7 +56,8 @@ struct DecodeItem {
   uint32_t ld_base;    // loader thread: activation row offset of its slot (or out of range)
   uint32_t sum_base;   // lane: row-sum offset of its slot (or out of range)
   int64_t rowid;       // lane: row id of its slot, -1 if padded
-  int n0;  bool poison;         // the block names no valid expert (NaN contributions)
+  int n0;
+  float wmul;          // 1, or NaN when the block names no valid expert (stage-2 multiplier)
 };
 
 template <int STAGE>
@@ -74,7 +75,7 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
   it.ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
-  it.poison = b.poison;
+  it.wmul = b.poison ? __builtin_nanf("") : 1.0f;
   it.rowid = slot_rowid(p, b, lane & 15, tk);
   const int64_t arow = act_row_of<STAGE>(it.rowid, tk, p.topk);
   it.sum_base = arow >= 0 ? (uint32_t)(arow * sums_per_row * 4) : kOobOffset;
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(E
       }
     } else {
       if (rowid >= 0) {
-        const float wr = cur.poison ? __builtin_nanf("") : (rowid < tk ? p.route_w[rowid] : 1.0f);
+        const float wr = (rowid < tk ? p.route_w[rowid] : 1.0f) * cur.wmul;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);

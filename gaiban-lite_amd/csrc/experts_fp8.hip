@@ -141,7 +141,8 @@ struct Fp8DecodeItem {
   uint32_t sum_base;  // lane: group-sum offset of its slot (or out of range)
   int64_t rowid;      // lane: row id of its slot, -1 if padded
   int64_t arow;       // lane: activation row of its slot, -1 if padded
-  int n0;  bool poison;         // the block names no valid expert (NaN contributions)
+  int n0;
+  float wmul;          // 1, or NaN when the block names no valid expert (stage-2 multiplier)
 };
 
 template <int STAGE>
@@ -159,7 +160,7 @@ __device__ __forceinline__ Fp8DecodeItem fp8_decode_item(const ExpertGemmParams&
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
   it.ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
-  it.poison = b.poison;
+  it.wmul = b.poison ? __builtin_nanf("") : 1.0f;
   it.rowid = slot_rowid(p, b, lane & 15, tk);
   it.arow = act_row_of<STAGE>(it.rowid, tk, p.topk);
   it.sum_base = it.arow >= 0 ? (uint32_t)(it.arow * groups * 4) : kOobOffset;
@@ -268,7 +269,7 @@ __global__ __launch_bounds__(256, 4) void expert_fp8_decode_kernel(ExpertGemmPar
         *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) =
             u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
       } else {
-        const float wm = (cur.poison ? __builtin_nanf("") : (rowid < tk ? p.route_w[rowid] : 1.0f)) * mult;
+        const float wm = (rowid < tk ? p.route_w[rowid] : 1.0f) * cur.wmul * mult;
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);

@@ -57,7 +57,8 @@ struct MxItem {
   const uint8_t* ws;   // this lane's 8 scale bytes of the pair's first group
   uint32_t ld_base;    // loader thread: activation row offset of its slot (or out of range)
   int64_t rowid;       // lane: row id of its slot, -1 if padded
-  int n0;  bool poison;         // the block names no valid expert (NaN contributions)
+  int n0;
+  float wmul;          // 1, or NaN when the block names no valid expert (stage-2 multiplier)
 };
 
 template <int STAGE>
@@ -74,7 +75,7 @@ __device__ __forceinline__ MxItem mx_item(const ExpertGemmParams& p, int item, i
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
   it.ws = p.ws8 + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 128 + (lane & 15) * 8;
-  it.poison = b.poison;
+  it.wmul = b.poison ? __builtin_nanf("") : 1.0f;
   it.rowid = slot_rowid(p, b, lane & 15, tk);
   const int ld_slot = threadIdx.x >> 4;
   const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(256, 4) void mx_decode_kernel(ExpertGemmParams p) {
       }
     } else {
       if (rowid >= 0) {
-        const float wr = cur.poison ? __builtin_nanf("") : (rowid < tk ? p.route_w[rowid] : 1.0f);
+        const float wr = (rowid < tk ? p.route_w[rowid] : 1.0f) * cur.wmul;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
