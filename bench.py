@@ -13,15 +13,22 @@ the shared expert -> owning output clone) with inputs resident in HBM.  Inputs
 rotate through a pool of seeded batches so every step routes differently (a
 fixed-routing figure is reported beside it).
 
-Also reported on the same line (secondary): decode at T in {1, 8, 256},
-prefill at T in {2048, 4096, 8192}, the W4A8 layer (uniform and Zipf routing,
-T = 64 and 8192), the same layer with MXFP4 experts (the reference
-checkpoint's E2M1 + E8M0 format, T = 64 and 8192), the FP8-block shared
+Order of the run: the prefill lines (T = 8192, then 2048 and 4096: TFLOP/s
+and fraction of the bf16 peak, with a ``prefill_roofline`` block for the
+grouped w13 kernel) come first, then the decode headline (W warm-up steps, K
+timed steps with per-step times on stderr and in ``per_step_ms``), then the
+secondary lines: decode at T in {1, 8, 256}, decode as HIP-graph replays, the
+W4A8 layer (uniform and Zipf routing, T = 64 and 8192), the layer with MXFP4
+experts (the reference checkpoint's E2M1 + E8M0 format), the FP8-block shared
 expert, the W8A16 (int8 and FP8-block) and block-FP8 W8A8 dense linears at
 K = 4096 (M <= 64 timed as 50 calls captured in a HIP graph, beside the
-launch-bound Python-loop figure), and the CPU baseline
-(the oracle's restatement of the reference torch path timed on this host's
-cores on a bounded sample).
+launch-bound Python-loop figure), and last the CPU baseline (the torch
+restatement of the reference's dense path on this host's cores, one batch per
+configuration).  ``env`` records versions, the device and the shader clock
+read right after the headline region.
+
+``--profile-run FMT:T:N`` only builds the layer and runs N calls (the program
+for ``rocprofv3 --pmc`` passes).
 
 ``--copy-calibration`` instead runs a plain 512 MiB device copy (torch
 ``copy_``) 5 times: the reference kernel for scaling the FETCH_SIZE /
@@ -65,10 +72,10 @@ def parse():
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--secondary", type=int, default=1, help="0 skips the extra decode/prefill/W4A8/W8A16 lines")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline")
-    ap.add_argument("--cpu-tokens", type=int, default=64)
-    ap.add_argument("--cpu-batches", type=int, default=6)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--profile-run", default=None, metavar="FMT:T:N",
+                    help="only run N layer calls (FMT int4|mxfp4|w4a8, T tokens) for rocprofv3 counter passes")
     return ap.parse_args()
 
 
@@ -99,17 +106,84 @@ def traffic_from_profile():
     return int(m.group(1)) if m else None
 
 
-def cuda_timer(fn, n, per_step=None):
+def read_sclk_sysfs():
+    """The active shader-clock level of the GPU from the driver's sysfs table
+    (``pp_dpm_sclk``; fast, no subprocess), or None when it is not readable."""
+
+    import glob
+
+    for path in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
+        try:
+            text = Path(path).read_text()
+        except OSError:
+            continue
+        for line in text.splitlines():
+            if line.strip().endswith("*"):
+                m = re.search(r"(\d+)\s*M[Hh]z", line)
+                if m:
+                    return {"mhz": int(m.group(1)), "source": path}
+    return None
+
+
+def read_sclk():
+    """The GPU shader clock as the system management tool reports it (MHz),
+    or None when no tool answers within a few seconds."""
+
+    import shutil
+    import subprocess
+
+    for cmd in (["amd-smi", "metric", "--clock", "--json"], ["rocm-smi", "--showclocks"]):
+        if not shutil.which(cmd[0]):
+            continue
+        try:
+            out = subprocess.run(cmd, capture_output=True, text=True, timeout=8).stdout
+        except Exception:  # noqa: BLE001 - the witness is optional
+            continue
+        m = re.search(r"sclk[^0-9]*?(\d+)\s*M[Hh]z", out) or re.search(r'"GFX_0".*?"clk":\s*\{?[^0-9]*(\d+)', out, re.S)
+        if m:
+            return {"mhz": int(m.group(1)), "tool": cmd[0]}
+    return None
+
+
+def environment(torch, sclk_busy=None, sclk_end=None):
+    """Versions and device of the run (a witness for the peak figures used)."""
+
+    props = torch.cuda.get_device_properties(0)
+    rocm = None
+    for path in ("/opt/rocm/.info/version", "/opt/rocm/.info/version-dev"):
+        try:
+            rocm = Path(path).read_text().strip()
+            break
+        except OSError:
+            pass
+    return {
+        "torch": torch.__version__,
+        "hip": getattr(torch.version, "hip", None),
+        "rocm": rocm,
+        "device": torch.cuda.get_device_name(0),
+        "arch": getattr(props, "gcnArchName", None),
+        "compute_units": props.multi_processor_count,
+        "hbm_bytes": props.total_memory,
+        "sclk_during_decode": sclk_busy,
+        "sclk_at_end": sclk_end,
+        "host_cpus": os.cpu_count(),
+    }
+
+
+def cuda_timer(fn, n, per_step=None, sync_before=True):
     """Mean ms per call of `fn` over `n` calls, timed with events on the
     current stream.  With `per_step` (a list), an event is also recorded
-    after every call and the per-call times are appended to it."""
+    after every call and the per-call times are appended to it.  With
+    `sync_before` False the timed calls queue right behind the work already
+    on the stream (no idle gap before the first event)."""
 
     import torch
 
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(n)] if per_step is not None else None
-    torch.cuda.synchronize()
+    if sync_before:
+        torch.cuda.synchronize()
     t0.record()
     for i in range(n):
         fn(i)
@@ -176,6 +250,8 @@ def main() -> int:
     import torch
 
     pkg = importlib.import_module("gaiban-lite_amd")
+    if args.profile_run:
+        return profile_run(pkg, args.profile_run, args.seed)
     S = pkg.synthetic
     ops = pkg.ops
     dev = torch.device("cuda:0")
@@ -210,11 +286,82 @@ def main() -> int:
              for lg in lgs]
         return xs, lgs, d
 
+    # ------------------------------------------------------------- prefill
+    # Timed before the decode headline: a GPU that has just been idle (fresh
+    # process, weights generated with host syncs between launches) runs its
+    # first ~25 decode steps up to 30% slow while it ramps up (per-step times
+    # fall from 0.59 to 0.46 ms); the prefill lines bring it to its steady
+    # state, so the headline measures the sustained decode rate.
+    prefill = None
+    prefill_lines = {}
+    if prefill_ts:
+        for tp in prefill_ts:
+            xp = S.make_hidden(tp, H, seed=3000, device=dev).view(1, tp, H)
+            lp = S.make_logits(tp, E, seed=3001, device=dev)
+            for _ in range(2):
+                layer.forward_tensor(xp, router_logits=lp)
+            ops.profile_begin(args.prefill_steps)
+            pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps)
+            pk, _ = ops.profile_end()
+            flops = 6.0 * tp * (K + 1) * H * I
+            mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
+            prefill_lines[tp] = {
+                "tokens": tp,
+                "ms_per_step": round(pms, 4),
+                "tokens_per_s": round(tp / (pms * 1e-3), 1),
+                "tflops": round(flops / (pms * 1e-3) / 1e12, 2),
+                "frac_of_bf16_peak": round(flops / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                "grouped_gemm_tflops": round(flops / (mm_ms * 1e-3) / 1e12, 2),
+                "stage1_ms": round(pk["stage1_w13"], 4),
+                "stage2_ms": round(pk["stage2_w2"], 4),
+                "combine_ms": round(pk["combine"], 4),
+            }
+            log(f"[bench] prefill T={tp}: {prefill_lines[tp]} kernels {pk}")
+            del xp, lp
+        tp = prefill_ts[0]
+        prefill = prefill_lines[tp]
+        # the dominant prefill kernel: grouped w13 + SwiGLU, 2 T (k+1) (2I) H flops per launch
+        st1_flops = 2.0 * tp * (K + 1) * (2 * I) * H
+        st1 = prefill["stage1_ms"]
+        secondary_prefill_roofline = {
+            "kernel": f"expert_prefill_kernel<1> (w13 + SwiGLU), prefill T={tp}",
+            "bound": "mfma",
+            "achieved": round(st1_flops / (st1 * 1e-3) / 1e12, 1),
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(st1_flops / (st1 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "algorithmic_flops_per_launch": int(st1_flops),
+            "launch_ms": st1,
+            "launches_timed": args.prefill_steps,
+        }
+
     # ------------------------------------------------------------- decode
+    # Inputs of every decode line are prepared first (host reads included).
+    # The timed decode work then runs as one stream: the T=256 line (its
+    # ms_per_step, timed with events), the headline's warm-up and the
+    # headline's K timed steps, with no host synchronisation in between.  The
+    # HBM-bound decode reaches its sustained rate only after ~10 ms of memory
+    # traffic: the GPU's power management lowers clocks during idle or
+    # compute-only stretches and raises them under load, so steps that start
+    # after an idle gap run up to ~20% slow at first (per-step times falling
+    # from ~0.53 to ~0.45 ms over 20 steps), while steps queued behind other
+    # decode work run at the sustained rate from the first one.
     xs, lgs, distinct = pools(T, args.pool, 1000)
+    other = {t: pools(t, 8, 4000 + t) for t in decode_ts[1:]} if args.secondary else {}
+    lead_t = 256 if 256 in other else None
+    torch.cuda.synchronize()
+    if lead_t:
+        xt, lt, _ = other[lead_t]
+        lead_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        lead_n = 100
+        lead_ev[0].record()
+        for i in range(lead_n):
+            layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8])
+        lead_ev[1].record()
     for i in range(args.warmup):
         layer.forward_tensor(xs[i % args.pool], router_logits=lgs[i % args.pool])
-    torch.cuda.synchronize()
+    sclk_busy = read_sclk_sysfs()  # read while the queued decode work runs
 
     def step(i):
         layer.forward_tensor(xs[i % args.pool], router_logits=lgs[i % args.pool])
@@ -223,15 +370,17 @@ def main() -> int:
     # kernel (stage 1), recorded by the library on the launch stream
     ops.profile_begin(args.steps, intervals=["stage1_w13"])
     step_ms: list[float] = []
-    ms = cuda_timer(step, args.steps, per_step=step_ms)
+    ms = cuda_timer(step, args.steps, per_step=step_ms, sync_before=False)
     roof, ncalls = ops.profile_end()
+    lead_ms = lead_ev[0].elapsed_time(lead_ev[1]) / lead_n if lead_t else None
     log("[bench] headline per-step ms: " + " ".join(f"{v:.4f}" for v in step_ms))
     # the same steps with all seven stamps (per-kernel breakdown), and with none
     ops.profile_begin(args.steps)
-    ms_all = cuda_timer(step, args.steps)
+    ms_all = cuda_timer(step, args.steps, sync_before=False)
     kern, _ = ops.profile_end()
-    ms_plain = cuda_timer(step, args.steps)
-    ms_fixed = cuda_timer(lambda i: layer.forward_tensor(xs[0], router_logits=lgs[0]), args.steps)
+    ms_plain = cuda_timer(step, args.steps, sync_before=False)
+    ms_fixed = cuda_timer(lambda i: layer.forward_tensor(xs[0], router_logits=lgs[0]), args.steps,
+                          sync_before=False)
     d_mean = float(np.mean([distinct[i % args.pool] for i in range(args.steps)]))
     stage1_bytes = (d_mean + 1) * b13 + T * H * 2 + (T * K + T) * I * 2
     st1_ms = roof["stage1_w13"]
@@ -243,11 +392,15 @@ def main() -> int:
     if args.secondary:
         dec = {}
         for t in decode_ts[1:]:
-            xt, lt, dt_ = pools(t, 8, 4000 + t)
-            for i in range(5):
-                layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8])
+            xt, lt, dt_ = other[t]
             n = 100
-            ms_t = cuda_timer(lambda i: layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8]), n)
+            if t == lead_t:
+                ms_t = lead_ms
+            else:
+                for i in range(5):
+                    layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8])
+                ms_t = cuda_timer(lambda i: layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8]), n,
+                                  sync_before=False)
             ops.profile_begin(n)
             cuda_timer(lambda i: layer.forward_tensor(xt[i % 8], router_logits=lt[i % 8]), n)
             kt, _ = ops.profile_end()
@@ -259,32 +412,6 @@ def main() -> int:
                            "kernel_ms": {k: round(v, 4) for k, v in kt.items()}}
             log(f"[bench] decode T={t}: {dec[str(t)]}")
         secondary["decode_other_T"] = dec
-
-    # ------------------------------------------------------------- prefill
-    prefill = None
-    if prefill_ts:
-        prefill = {}
-        for tp in prefill_ts:
-            xp = S.make_hidden(tp, H, seed=3000, device=dev).view(1, tp, H)
-            lp = S.make_logits(tp, E, seed=3001, device=dev)
-            for _ in range(2):
-                layer.forward_tensor(xp, router_logits=lp)
-            ops.profile_begin(args.prefill_steps)
-            pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps)
-            pk, _ = ops.profile_end()
-            flops = 6.0 * tp * (K + 1) * H * I
-            mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
-            entry = {
-                "ms_per_step": round(pms, 4),
-                "tokens_per_s": round(tp / (pms * 1e-3), 1),
-                "layer_tflops": round(flops / (pms * 1e-3) / 1e12, 2),
-                "layer_frac_of_bf16_peak": round(flops / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-                "grouped_gemm_tflops": round(flops / (mm_ms * 1e-3) / 1e12, 2),
-                "kernel_ms": {k: round(v, 4) for k, v in pk.items()},
-            }
-            prefill[str(tp)] = entry
-            log(f"[bench] prefill T={tp}: {entry}")
-            del xp, lp
 
     # -------------------------------------------------------- W4A8 and W8A16
     if args.secondary:
@@ -299,7 +426,7 @@ def main() -> int:
     # ------------------------------------------------------------ CPU baseline
     cpu = None
     if args.cpu_baseline:
-        cpu = cpu_baseline(pkg, w13, s13, w2, s2, lgs, xs, args.cpu_tokens, args.cpu_batches, E, K)
+        cpu = cpu_baseline(pkg, w13, s13, w2, s2, args.seed)
 
     traffic = traffic_from_profile()
     line = {
@@ -345,8 +472,12 @@ def main() -> int:
             "launches_timed": ncalls,
         },
         "prefill": prefill,
+        "prefill_roofline": secondary_prefill_roofline if prefill_ts else None,
+        "prefill_other_T": {str(t): v for t, v in prefill_lines.items() if prefill_ts and t != prefill_ts[0]},
+        "per_step_ms": [round(v, 4) for v in step_ms],
         **secondary,
         "cpu_baseline": cpu,
+        "env": environment(torch, sclk_busy=sclk_busy, sclk_end=read_sclk()),
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -689,66 +820,91 @@ def bench_block_fp8(pkg, dev):
     return out
 
 
-def cpu_baseline(pkg, w13, s13, w2, s2, lgs, xs, tokens, batches, E, K):
-    """The oracle's restatement of the reference torch MoE path
-    (dense_moe.py:289-354 op order, bf16 dequant-then-matmul, plus the shared
-    expert and add), timed on the host over `batches` decode batches of
-    `tokens` rows each: router, alignment and all touched experts."""
+def cpu_baseline(pkg, w13, s13, w2, s2, seed):
+    """The reference's torch path, restated in ``oracle/torch_path.py`` (the
+    gate of ``moe_forward.py:80-87``, ``DenseRoutedExecutor``
+    ``ops/dense_moe.py:289-354`` in bf16 with its chunk-of-8 dequantisation,
+    ``shared_bf16_partial`` and the add), timed on this host's cores
+    (``torch.set_num_threads(os.cpu_count())``): one batch each of C1 (the
+    tiny layer, T=64), C2 at T in {1, 8, 64, 256} and C3 at T=2048, on the
+    same weights as the GPU run (copied to the host before timing).
+    ``value`` is C2 at T=64, the headline configuration."""
 
-    import numpy as np
     import torch
 
     try:
-        import oracle as O
+        from oracle import torch_path as TP
     except Exception as exc:  # pragma: no cover
         log(f"[bench] cpu baseline unavailable: {exc}")
         return None
-    from threadpoolctl import threadpool_limits
-
-    cores = min(os.cpu_count() or 1, 16)
-    batches = min(batches, len(xs))
-    data = []
-    touched = set()
-    for b in range(batches):
-        lg = lgs[b][:tokens].cpu().numpy()
-        xn = xs[b].view(-1, xs[b].shape[-1])[:tokens].float().cpu().numpy()
-        data.append((lg, xn))
-        touched |= set(np.unique(O.route_topk(lg, K, score_func=O.SCORE_SIGMOID).ids).tolist())
-    touched |= {E}
-    host = {}
-    for e in sorted(touched):  # resident weights: copied before the timed region
-        host[e] = (w13[e].cpu().numpy(), s13[e].contiguous().view(torch.int16).cpu().numpy().view(np.uint16),
-                   w2[e].cpu().numpy(), s2[e].contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
-
-    class HostSource(O.ExpertSource):
-        def __init__(self):
-            super().__init__(None, None, None, None)
-
-        def w13(self, e):
-            return O.dequant_int4_g128(host[e][0], host[e][1])
-
-        def w2(self, e):
-            return O.dequant_int4_g128(host[e][2], host[e][3])
-
-    src = HostSource()
-    with threadpool_limits(limits=1):
+    S = pkg.synthetic
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    flash = TP.StackedExperts(w13.cpu(), s13.cpu(), w2.cpu(), s2.cpu())
+    tiny = TP.StackedExperts(*S.make_checkpoint_experts(S.TINY, seed=seed, device="cpu"))
+    cases = [("C1_T64", tiny, S.TINY, 64)] + [(f"C2_T{t}", flash, S.FLASH, t) for t in (1, 8, 64, 256)] + [
+        ("C3_T2048", flash, S.FLASH, 2048)]
+    per = {}
+    total = 0.0
+    for name, experts, shape, t in cases:
+        x = S.make_hidden(t, shape.hidden, seed=9000 + t, device="cpu")
+        logits = S.make_logits(t, shape.experts, seed=9500 + t, device="cpu")
         t0 = time.perf_counter()
-        for lg, xn in data:
-            rr = O.route_topk(lg, K, score_func=O.SCORE_SIGMOID)
-            O.moe_align(rr.ids, 8, E)
-            O.moe_bf16_mirror(xn, rr.ids, rr.weights, src, shared_index=E, workers=cores)
+        ids, weights, _ = TP.gate_route(logits, topk=shape.topk, score_func="sigmoid")
+        TP.dense_moe(x, ids, weights, experts, num_experts=shape.experts,
+                     shared_index=shape.experts if shape.has_shared else None, dtype=torch.bfloat16)
         dt = time.perf_counter() - t0
-    total = tokens * len(data)
-    log(f"[bench] cpu baseline: {len(data)} batches x {tokens} tokens in {dt:.2f} s on {cores} threads")
+        total += dt
+        per[name] = {"tokens": t, "seconds": round(dt, 3), "tokens_per_s": round(t / dt, 2)}
+        log(f"[bench] cpu baseline {name}: {per[name]}")
     return {
-        "value": round(total / dt, 2),
+        "value": per["C2_T64"]["tokens_per_s"],
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{len(data)} decode batches of {tokens} tokens of the same layer (router + alignment + "
-                  "bf16 dequant-then-matmul over every touched expert incl. shared + combine), numpy, "
-                  f"{dt:.2f} s wall",
+        "sample": ("one batch per config (C1 T=64 tiny layer; C2 T=1/8/64/256 and C3 T=2048 on the Flash layer) "
+                   "through the torch restatement of the reference's dense path in bf16, router included; "
+                   f"{total:.1f} s of CPU time on {cores} threads; value = C2 T=64"),
+        "configs": per,
     }
+
+
+def profile_run(pkg, spec: str, seed: int) -> int:
+    """``--profile-run FMT:T:N``: build the Flash layer in format FMT (int4,
+    mxfp4 or w4a8), run one warm-up and N ``TP4MoE.forward_tensor`` calls at T
+    tokens, and exit -- the program the rocprofv3 counter passes wrap."""
+
+    import torch
+
+    fmt, t, n = spec.split(":")
+    t, n = int(t), int(n)
+    S = pkg.synthetic
+    dev = torch.device("cuda:0")
+    shape = S.FLASH
+    E, H, I, K = shape.experts, shape.hidden, shape.inter, shape.topk
+    if fmt == "mxfp4":
+        res = pkg.ResidentMXFP4MoEWeights.from_checkpoint_layout(
+            *S.make_checkpoint_experts_mxfp4(shape, seed=seed, device=dev), experts=E, has_shared=True)
+    elif fmt in ("int4", "w4a8"):
+        res = pkg.ResidentInt4MoEWeights.from_checkpoint_layout(
+            *S.make_checkpoint_experts(shape, seed=seed, device=dev), experts=E, has_shared=True,
+            marlin_input_dtype=torch.float8_e4m3fn if fmt == "w4a8" else None)
+    else:
+        raise SystemExit(f"--profile-run: unknown format {fmt!r} (int4, mxfp4, w4a8)")
+    cfg = pkg.TP4MoEConfig(hidden_size=H, intermediate_size=I, experts=E, topk=K, route_scale=1.0, clamp_limit=0.0,
+                           score_func="sigmoid", shared_experts=1)
+    gate = pkg.ResidentGateWeights(weight=torch.zeros((E, H), dtype=torch.bfloat16, device=dev))
+    layer = pkg.TP4MoE(config=cfg, resident=res, gate=gate, device=dev, global_row_shapes=[t],
+                       marlin_input_dtype=torch.float8_e4m3fn if fmt == "w4a8" else None)
+    x = S.make_hidden(t, H, seed=3000, device=dev).view(1, t, H)
+    logits = S.make_logits(t, E, seed=3001, device=dev)
+    layer.forward_tensor(x, router_logits=logits)
+    torch.cuda.synchronize()
+    for _ in range(n):
+        layer.forward_tensor(x, router_logits=logits)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile_run": spec, "calls": n + 1}), flush=True)
+    return 0
 
 
 if __name__ == "__main__":

@@ -28,11 +28,13 @@ nibble = even K), and MXFP4 (E2M1 codes, one E8M0 scale per 32 K;
 ``moe_forward.py:23-40,115-155``).  A clamp limit of 0 disables the clamp
 (this build's convention; the reference always clamps, Flash uses 10).
 
-Pinned by: ``tests/test_oracle_torch_path.py`` (bf16 mode bit-exact against
-the numpy mirror ``moe_bf16_mirror`` on dyadic inputs built so that every
-rounding point is exercised; fp32 mode against ``moe_fp32``; dequantisers
-against the numpy ones) and the GPU tests of the full layer (fp32 mode on the
-GPU against ``moe_fp32`` on rows covering every alignment block).
+Pinned by: ``tests/test_oracle_torch_path.py`` (bf16 mode against the numpy
+mirror ``moe_bf16_mirror``: >= 99.9% of the outputs bit-identical, the rest
+within 2^-8 of the largest output -- fp32 summation order differs -- while
+dropping any single bf16 cast of the mirror falls below 90%; fp32 mode
+against ``moe_fp32``; dequantisers bit-exact against the numpy ones) and the
+GPU tests of the full layer (fp32 mode on the GPU against ``moe_fp32`` on
+rows covering every alignment block).
 """
 
 from __future__ import annotations
@@ -45,22 +47,26 @@ import torch.nn.functional as F
 FP4_TABLE = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, 0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)
 
 
-def _nibbles(packed: torch.Tensor) -> torch.Tensor:
-    """uint8 [..., N, K/2] -> int64 codes [..., N, K], low nibble first."""
+INT4_TABLE = tuple(range(8)) + tuple(range(-8, 0))
 
-    p = packed.to(torch.int64)
-    return torch.stack((p & 0xF, p >> 4), dim=-1).flatten(-2)
+
+def _byte_pair_table(values, device, dtype) -> torch.Tensor:
+    """[256, 2] table: byte b -> (value of its low nibble, value of its high
+    nibble), the structure of ``_byte_pair_table`` (``ops/dense_moe.py:41-50``)."""
+
+    v = torch.tensor(values, dtype=torch.float32, device=device)
+    b = torch.arange(256, device=device)
+    return torch.stack((v[b & 0xF], v[b >> 4]), dim=-1).to(dtype)
 
 
 def dequant_int4_g128(packed: torch.Tensor, scale: torch.Tensor, *, dtype=torch.float32) -> torch.Tensor:
-    """``W[n, k] = q[n, k] * s[n, k // 128]`` with q the signed nibble.  fp32:
-    exact; bf16: the product rounded once to bf16 (the int4 analogue of
-    ``dequant_mxfp4_bf16``, ``ops/dense_moe.py:53-68``)."""
+    """``W[n, k] = q[n, k] * s[n, k // 128]`` with q the signed nibble (low
+    nibble = even k), by byte-pair table lookup as ``dequant_mxfp4_bf16``
+    (``ops/dense_moe.py:53-68``) does.  fp32: exact; bf16: the product rounded
+    once to bf16."""
 
-    codes = _nibbles(packed)
-    q = torch.where(codes >= 8, codes - 16, codes).to(torch.float32)
-    s = scale.to(torch.float32).repeat_interleave(128, dim=-1)
-    return (q * s).to(dtype)
+    pairs = _byte_pair_table(INT4_TABLE, packed.device, dtype)[packed.long()]
+    return pairs.flatten(-2) * scale.to(dtype).repeat_interleave(128, dim=-1)
 
 
 def decode_e8m0(codes: torch.Tensor) -> torch.Tensor:
@@ -77,11 +83,11 @@ def decode_e8m0(codes: torch.Tensor) -> torch.Tensor:
 
 def dequant_mxfp4(packed: torch.Tensor, scale_codes: torch.Tensor, *, dtype=torch.float32) -> torch.Tensor:
     """E2M1 codes times the E8M0 group scale (32 K): ``dequant_mxfp4``
-    (``moe_forward.py:126-155``); exact in bf16 (``dequant_mxfp4_bf16``)."""
+    (``moe_forward.py:126-155``), by table lookup as ``dequant_mxfp4_bf16``
+    (exact in bf16)."""
 
-    table = torch.tensor(FP4_TABLE, dtype=torch.float32, device=packed.device)
-    vals = table[_nibbles(packed)]
-    return (vals * decode_e8m0(scale_codes).repeat_interleave(32, dim=-1)).to(dtype)
+    pairs = _byte_pair_table(FP4_TABLE, packed.device, dtype)[packed.long()]
+    return pairs.flatten(-2) * decode_e8m0(scale_codes).to(dtype).repeat_interleave(32, dim=-1)
 
 
 @dataclass
