@@ -155,7 +155,6 @@ class _LayerBuffers:
     route_ids: torch.Tensor
     route_weights: torch.Tensor
     margin: torch.Tensor
-    output: torch.Tensor
     alignment: DeterministicMoEAlignment
     block_size_m: int
     ready_event: Any
@@ -365,13 +364,13 @@ class TP4MoE:
                     self._register_shape(int(rows), slot)
         self._validate_provider_storage()
 
-    def _add_shared_fp8(self, flat: torch.Tensor, buffers: "_LayerBuffers") -> None:
+    def _add_shared_fp8(self, flat: torch.Tensor, buffers: "_LayerBuffers", out: torch.Tensor) -> None:
         """output <- bf16(routed + shared(flat)) for an FP8-block shared expert
         (``moe_runtime.py:1860-1873``: shared_bf16_partial, then torch.add)."""
 
         if self._shared_fp8 is not None:
             ops.shared_fp8_add_into(flat, self._shared_fp8, clamp_limit=self.config.clamp_limit,
-                                    out=buffers.output, workspace=buffers.shared_workspace)
+                                    out=out, workspace=buffers.shared_workspace)
 
     # ------------------------------------------------------------ buffers
     def _register_shape(self, rows: int, slot: int) -> None:
@@ -391,7 +390,6 @@ class TP4MoE:
             route_ids=torch.empty(rows, cfg.topk, dtype=torch.int32, device=self.device),
             route_weights=torch.empty(rows, cfg.topk, dtype=torch.float32, device=self.device),
             margin=torch.empty(rows, dtype=torch.float32, device=self.device),
-            output=torch.empty(rows, cfg.hidden_size, dtype=torch.bfloat16, device=self.device),
             alignment=allocate_deterministic_moe_alignment(template, block_size=bs, num_experts=cfg.experts),
             block_size_m=bs,
             ready_event=torch.cuda.Event(blocking=False),
@@ -450,7 +448,7 @@ class TP4MoE:
         tensors = [self.resident.w13_q, self.resident.w13_s, self.resident.w2_q, self.resident.w2_s,
                    self.gate.weight]
         for b in self._buffers.values():
-            tensors += [b.workspace, b.logits, b.route_ids, b.route_weights, b.margin, b.output,
+            tensors += [b.workspace, b.logits, b.route_ids, b.route_weights, b.margin,
                         b.alignment.sorted_token_ids, b.alignment.expert_ids,
                         b.alignment.num_tokens_post_padded]
         for owned in self._route_capture_tensors.values():
@@ -627,7 +625,7 @@ class TP4MoE:
             raise ValueError(f"route capture {key}: its tensors share storage")
         others = [t for k, ts in self._route_capture_tensors.items() if k != key for t in ts]
         for b in self._buffers.values():
-            others += [b.workspace, b.output, b.route_ids, b.route_weights, b.alignment.sorted_token_ids,
+            others += [b.workspace, b.route_ids, b.route_weights, b.alignment.sorted_token_ids,
                        b.alignment.expert_ids, b.alignment.num_tokens_post_padded]
         if mine & {int(t.untyped_storage().data_ptr()) for t in others}:
             raise ValueError(f"route capture {key}: storage aliases another buffer of the layer")
@@ -837,6 +835,10 @@ class TP4MoE:
                 buffers.gathered_input_ids.copy_(local_ids)
             mark("moe_ids_all_gather_done")
 
+            # the call's result: a fresh owning tensor that the combine writes
+            # directly (the reference returns an owning clone of its buffer)
+            output = torch.empty((flat.shape[0], cfg.hidden_size), dtype=torch.bfloat16, device=self.device)
+
             def compute_partial():
                 route_source = "native"
                 margin = None
@@ -865,10 +867,10 @@ class TP4MoE:
                         block_size=buffers.block_size_m, ids=buffers.route_ids,
                         weights=buffers.route_weights, margin=buffers.margin,
                         sorted_token_ids=a.sorted_token_ids, expert_ids=a.expert_ids,
-                        num_tokens_post_padded=a.num_tokens_post_padded, out=buffers.output,
+                        num_tokens_post_padded=a.num_tokens_post_padded, out=output,
                         workspace=buffers.workspace, mxfp4=self._mxfp4,
                     )
-                    self._add_shared_fp8(flat, buffers)
+                    self._add_shared_fp8(flat, buffers, output)
                     return buffers.route_weights, buffers.route_ids, buffers.margin, {}
                 sel_ids = sel_scores = None
                 if self.route_kind == "hash":
@@ -941,19 +943,19 @@ class TP4MoE:
                     route_weights=route_weights, sorted_token_ids=a.sorted_token_ids,
                     expert_ids=a.expert_ids, num_tokens_post_padded=a.num_tokens_post_padded,
                     block_size=buffers.block_size_m, clamp_limit=cfg.clamp_limit,
-                    out=buffers.output, workspace=buffers.workspace,
+                    out=output, workspace=buffers.workspace,
                 )
                 # routed experts, shared expert and the add run in the same fused launch chain
                 # (an FP8-block shared expert as dense linears that add into the routed sum)
                 mark("moe_routed_done")
-                self._add_shared_fp8(flat, buffers)
+                self._add_shared_fp8(flat, buffers, output)
                 mark("moe_shared_done")
                 mark("moe_combine_done")
                 digests = {}
                 if collect_stage_digests:
                     digests = {
                         "gathered_input": _tensor_digest(flat),
-                        "combined_partial": _tensor_digest(buffers.output),
+                        "combined_partial": _tensor_digest(output),
                     }
                 return route_weights, route_ids, margin, digests
 
@@ -961,15 +963,15 @@ class TP4MoE:
             mark("moe_reduce_scatter_done")
 
             def finish():
-                out = buffers.output.reshape(shape).clone()
+                out = output.view(shape)
                 trace = None
                 if collect_trace:
                     if collect_stage_digests:
-                        digests["reduce_scatter_output"] = _tensor_digest(buffers.output)
+                        digests["reduce_scatter_output"] = _tensor_digest(output)
                     trace = MoETrace(
                         local_input_shape=shape,
                         gathered_shape=tuple(flat.shape),
-                        partial_shape=tuple(buffers.output.shape),
+                        partial_shape=tuple(output.shape),
                         local_output_shape=tuple(out.shape),
                         route_ids_row_zero=tuple(int(v) for v in route_ids[0].cpu()),
                         route_weights_row_zero=tuple(float(v) for v in route_weights[0].cpu()),
