@@ -27,8 +27,9 @@ restatement of the reference's dense path on this host's cores, one batch per
 configuration).  ``env`` records versions, the device and the shader clock
 read right after the headline region.
 
-``--profile-run FMT:T:N`` only builds the layer and runs N calls (the program
-for ``rocprofv3 --pmc`` passes).
+``--profile-run FMT:T:N[:graph]`` only builds the layer and runs N calls (the
+program for ``rocprofv3 --pmc`` passes and kernel traces); ``:graph`` adds N
+replays of the call captured as a HIP graph.
 
 ``--copy-calibration`` instead runs a plain 512 MiB device copy (torch
 ``copy_``) 5 times: the reference kernel for scaling the FETCH_SIZE /
@@ -74,8 +75,9 @@ def parse():
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--profile-run", default=None, metavar="FMT:T:N",
-                    help="only run N layer calls (FMT int4|mxfp4|w4a8, T tokens) for rocprofv3 counter passes")
+    ap.add_argument("--profile-run", default=None, metavar="FMT:T:N[:graph]",
+                    help="only run N layer calls (FMT int4|mxfp4|w4a8, T tokens) for rocprofv3 counter passes; "
+                         ":graph adds N replays of the captured call")
     return ap.parse_args()
 
 
@@ -486,9 +488,16 @@ def main() -> int:
 def bench_graph(layer, S, dev, ts, H, E):
     """The decode layer call captured once as a HIP graph (torch.cuda.graph,
     after resetting the slot's completion event, as the reference's stateful
-    graphs do) and replayed: per step the new activations and logits are
-    copied into the captured inputs, then the graph replays.  Eager = the same
-    steps as separate launches."""
+    graphs do) and replayed, against the same call launched eagerly.
+
+    Two pairs per T.  ``ms_per_step_graph`` / ``ms_per_step_eager``: the call
+    on the captured input tensors with nothing between calls -- the layer as
+    one node of a whole decode-stage graph sees it (its input written by the
+    graph's previous node).  ``*_with_input_copies``: each step first copies a
+    new activation and new logits into the captured inputs (two stream copies)
+    and then replays or launches; the graph's first kernel then waits on the
+    copy's completion signal, which costs about a microsecond more than the
+    same wait between two eager launches."""
 
     import torch
 
@@ -510,24 +519,37 @@ def bench_graph(layer, S, dev, ts, H, E):
             layer.forward_tensor(x_s, router_logits=lg_s)
         torch.cuda.synchronize()
 
-        def replay(i):
+        def copy_in(i):
             x_s.copy_(xs[i % 8])
             lg_s.copy_(lgs[i % 8])
+
+        def replay(i):
             graph.replay()
 
         def eager(i):
-            x_s.copy_(xs[i % 8])
-            lg_s.copy_(lgs[i % 8])
+            layer.forward_tensor(x_s, router_logits=lg_s)
+
+        def replay_copied(i):
+            copy_in(i)
+            graph.replay()
+
+        def eager_copied(i):
+            copy_in(i)
             layer.forward_tensor(x_s, router_logits=lg_s)
 
         n = 200
         for i in range(10):
-            replay(i)
-        ms_g = cuda_timer(replay, n)
-        ms_e = cuda_timer(eager, n)
-        out[str(t)] = {"ms_per_step_graph": round(ms_g, 4), "ms_per_step_eager": round(ms_e, 4),
-                       "tokens_per_s_graph": round(t / (ms_g * 1e-3), 1)}
-        log(f"[bench] decode graph T={t}: {out[str(t)]}")
+            replay_copied(i)
+        rec = {}
+        # alternate the two modes twice so that neither always runs first
+        for rnd in range(2):
+            for name, fn in (("graph", replay), ("eager", eager), ("graph_with_input_copies", replay_copied),
+                             ("eager_with_input_copies", eager_copied)):
+                rec.setdefault(name, []).append(cuda_timer(fn, n))
+        row = {f"ms_per_step_{k}": round(min(v), 4) for k, v in rec.items()}
+        row["tokens_per_s_graph"] = round(t / (row["ms_per_step_graph"] * 1e-3), 1)
+        out[str(t)] = row
+        log(f"[bench] decode graph T={t}: {row}")
         del graph
         torch.cuda.synchronize()
         layer.reset_free_slot_completion_event(t, 0)
@@ -870,14 +892,21 @@ def cpu_baseline(pkg, w13, s13, w2, s2, seed):
 
 
 def profile_run(pkg, spec: str, seed: int) -> int:
-    """``--profile-run FMT:T:N``: build the Flash layer in format FMT (int4,
-    mxfp4 or w4a8), run one warm-up and N ``TP4MoE.forward_tensor`` calls at T
-    tokens, and exit -- the program the rocprofv3 counter passes wrap."""
+    """``--profile-run FMT:T:N[:graph]``: build the Flash layer in format FMT
+    (int4, mxfp4 or w4a8), run one warm-up and N ``TP4MoE.forward_tensor``
+    calls at T tokens, and exit -- the program the rocprofv3 counter passes
+    and kernel traces wrap.  With ``:graph`` the call is then captured once
+    as a HIP graph and replayed N times (eager and replayed kernels in one
+    trace)."""
 
     import torch
 
-    fmt, t, n = spec.split(":")
+    parts = spec.split(":")
+    if len(parts) not in (3, 4) or (len(parts) == 4 and parts[3] != "graph"):
+        raise SystemExit(f"--profile-run: expected FMT:T:N or FMT:T:N:graph, got {spec!r}")
+    fmt, t, n = parts[:3]
     t, n = int(t), int(n)
+    graph_mode = len(parts) == 4
     S = pkg.synthetic
     dev = torch.device("cuda:0")
     shape = S.FLASH
@@ -903,7 +932,27 @@ def profile_run(pkg, spec: str, seed: int) -> int:
     for _ in range(n):
         layer.forward_tensor(x, router_logits=logits)
     torch.cuda.synchronize()
-    print(json.dumps({"profile_run": spec, "calls": n + 1}), flush=True)
+    replays = 0
+    if graph_mode:
+        # then the same call captured once and replayed N times
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            layer.forward_tensor(x, router_logits=logits)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        layer.reset_free_slot_completion_event(t, 0)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            layer.forward_tensor(x, router_logits=logits)
+        torch.cuda.synchronize()
+        for _ in range(n):
+            graph.replay()
+        torch.cuda.synchronize()
+        replays = n
+        del graph
+        torch.cuda.synchronize()
+    print(json.dumps({"profile_run": spec, "calls": n + 2 if graph_mode else n + 1, "replays": replays}), flush=True)
     return 0
 
 

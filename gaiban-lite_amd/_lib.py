@@ -82,6 +82,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _f32, _p, _p, _sz, _p],
     ),
     "dsv4moe_pack_int8": (ctypes.c_int, [_p, _i64, _i64, _p, _p]),
+    "dsv4moe_decode_e8m0": (ctypes.c_int, [_p, _i64, _p, _p]),
+    "dsv4moe_dequant_mxfp4": (ctypes.c_int, [_p, _p, _i64, _i64, _p, _p]),
+    "dsv4moe_dequant_fp8_block": (ctypes.c_int, [_p, _i32, _p, _i64, _i64, _p, _p]),
     "dsv4moe_experts_w4a8_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
     "dsv4moe_experts_w4a8": (
         ctypes.c_int,

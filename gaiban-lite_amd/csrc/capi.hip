@@ -112,6 +112,9 @@ int dsv4_launch_block_fp8_gemm(const uint8_t*, const uint8_t*, int64_t, int64_t,
                                const uint8_t*, int32_t, float*, uint16_t*, hipStream_t, int w_rowmajor);
 size_t dsv4_w8a16_workspace_bytes(int64_t, int64_t, int32_t);
 int dsv4_launch_pack_int8(const int8_t*, int64_t, int64_t, uint8_t*, hipStream_t);
+int dsv4_launch_decode_e8m0(const uint8_t*, int64_t, float*, hipStream_t);
+int dsv4_launch_dequant_mxfp4(const uint8_t*, const float*, int64_t, int64_t, float*, hipStream_t);
+int dsv4_launch_dequant_fp8_block(const void*, int32_t, const float*, int64_t, int64_t, float*, hipStream_t);
 int dsv4_launch_w8a16(const uint16_t*, int64_t, int64_t, int64_t, const uint8_t*, const uint16_t*,
                       const uint8_t*, int32_t, float*, uint16_t*, hipStream_t, int accumulate, int w_rowmajor);
 size_t dsv4_shared_fp8_workspace_bytes(int64_t, int, int);
@@ -656,6 +659,43 @@ int dsv4moe_pack_int8(const int8_t* w, int64_t n, int64_t k, uint8_t* packed, vo
   DSV4_REQUIRE(w && packed, "pack_int8: null pointer");
   DSV4_REQUIRE(aligned(w, 16) && aligned(packed, 16), "pack_int8: buffers must be 16-byte aligned");
   return dsv4_launch_pack_int8(w, n, k, packed, static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_decode_e8m0(const uint8_t* codes, int64_t n, float* out, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(n >= 0, "decode_e8m0: negative size");
+  if (n == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(codes && out, "decode_e8m0: null pointer");
+  DSV4_REQUIRE(aligned(out, 4), "decode_e8m0: out must be 4-byte aligned");
+  return dsv4_launch_decode_e8m0(codes, n, out, static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_dequant_mxfp4(const uint8_t* packed, const float* scale, int64_t rows, int64_t k, float* out,
+                          void* stream) {
+  clear_error();
+  DSV4_REQUIRE(rows >= 0, "dequant_mxfp4: negative row count");
+  DSV4_REQUIRE(k > 0 && k % 32 == 0, "dequant_mxfp4: logical k must be a positive multiple of 32, got %lld",
+               (long long)k);
+  if (rows == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(packed && scale && out, "dequant_mxfp4: null pointer");
+  DSV4_REQUIRE(aligned(packed, 16) && aligned(out, 16) && aligned(scale, 4),
+               "dequant_mxfp4: packed and out must be 16-byte aligned, scale 4-byte aligned");
+  return dsv4_launch_dequant_mxfp4(packed, scale, rows, k, out, static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_dequant_fp8_block(const void* w, int32_t w_dtype, const float* scale, int64_t rows, int64_t cols,
+                              float* out, void* stream) {
+  clear_error();
+  DSV4_REQUIRE(w_dtype >= DSV4MOE_DTYPE_BF16 && w_dtype <= DSV4MOE_DTYPE_FP8_E4M3,
+               "dequant_fp8_block: unknown w_dtype %d", (int)w_dtype);
+  DSV4_REQUIRE(rows >= 0 && cols >= 0, "dequant_fp8_block: negative size");
+  if (rows == 0 || cols == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(w && scale && out, "dequant_fp8_block: null pointer");
+  const int elem = w_dtype == DSV4MOE_DTYPE_FP8_E4M3 ? 1 : (w_dtype == DSV4MOE_DTYPE_FP32 ? 4 : 2);
+  DSV4_REQUIRE(aligned(w, elem) && aligned(scale, 4) && aligned(out, cols % 4 == 0 ? 16 : 4),
+               "dequant_fp8_block: misaligned buffer (w to its element size, scale to 4 bytes, out to %d)",
+               cols % 4 == 0 ? 16 : 4);
+  return dsv4_launch_dequant_fp8_block(w, w_dtype, scale, rows, cols, out, static_cast<hipStream_t>(stream));
 }
 
 int32_t dsv4moe_w8a16_split_k(int64_t m, int64_t n, int64_t k) { return dsv4_w8a16_split_k(m, n, k); }

@@ -8,6 +8,11 @@ from the HIP gate-GEMM kernel (bf16 MFMA, fp32 accumulation) and scores,
 top-(k+1) selection, weights and margin from the HIP router kernel.
 ``route_from_logits`` is the same router for callers that already hold fp32
 logits (the synthetic benchmark configurations).
+
+The module's checkpoint dequantisers (``_decoded_e8m0``, ``dequant_mxfp4``,
+``dequant_fp8_block``; reference ``moe_forward.py:115-176``) keep their
+signatures and exception classes and run as HIP streaming kernels; they give
+the dense fp32 weights a dense executor or a check needs.
 """
 
 from __future__ import annotations
@@ -179,6 +184,65 @@ def hash_gate_forward(
     return HashGateForwardTensors(routing_weights=weights, routing_ids=ids, selected_scores=selected)
 
 
+E8M0 = torch.float8_e8m0fnu
+
+
+def _decoded_e8m0(scale: torch.Tensor) -> torch.Tensor:
+    """A scale tensor as fp32 (``moe_forward.py:115-123``): E8M0 or uint8
+    codes are decoded by the HIP kernel (2^(c - 127); byte 0 -> 2^-127,
+    byte 255 -> NaN, as torch's E8M0 conversion); a floating tensor is taken
+    as already decoded and only widened to fp32."""
+
+    C.tensor("scale", scale)
+    if scale.dtype in (torch.uint8, E8M0):
+        if scale.device.type != "cuda":
+            raise ValueError("scale: E8M0 codes are decoded on the GPU; got a CPU tensor")
+        return ops.decode_e8m0(scale.contiguous().view(torch.uint8))
+    if scale.is_floating_point():
+        return scale.contiguous().float()
+    raise TypeError(f"scale: expected E8M0 or uint8 codes or an already decoded float tensor, not {scale.dtype}")
+
+
+def _on_gpu(name: str, t: torch.Tensor) -> None:
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: the dequantiser runs on the GPU; got a {t.device.type} tensor")
+
+
+def dequant_mxfp4(packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """Checkpoint MXFP4 weight -> fp32 [rows, 2 * packed.shape[1]]
+    (``moe_forward.py:126-155``): byte b of a row holds logical K 2b in its
+    low nibble and 2b+1 in its high nibble (E2M1 codes, values
+    ``FP4_VALUES``), one E8M0 (or decoded) scale per 32 K.  Computed by the
+    HIP kernel as one fp32 product per weight, bit-identical to the table
+    lookup times the repeated scale."""
+
+    C.tensor("packed", packed, ndim=2)
+    C.tensor("scale", scale, ndim=2)
+    C.tensor("packed", packed, dtype=(torch.int8, torch.uint8))
+    rows, logical_k = packed.shape[0], 2 * packed.shape[1]
+    if logical_k % 32:
+        raise ValueError(f"packed: logical K = {logical_k} is not a multiple of the 32-wide scale group")
+    C.tensor("scale", scale, shape=(rows, logical_k // 32))
+    _on_gpu("packed", packed)
+    codes = packed.contiguous().view(torch.uint8)
+    return ops.dequant_mxfp4(codes, _decoded_e8m0(scale))
+
+
+def dequant_fp8_block(weight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """128 x 128 block-scaled weight -> fp32 (``moe_forward.py:158-176``):
+    ``weight[r, c] * scale[r // 128, c // 128]`` with the scale E8M0 codes or
+    already decoded; rows and columns need not be multiples of 128.  The
+    weight may be FP8 E4M3FN (the checkpoint's), bf16, fp16 or fp32."""
+
+    C.tensor("weight", weight, ndim=2)
+    C.tensor("scale", scale, ndim=2)
+    rows, cols = weight.shape
+    C.tensor("scale", scale, shape=(-(-rows // 128), -(-cols // 128)))
+    C.tensor("weight", weight, dtype=tuple(ops.DTYPE_CODES))
+    _on_gpu("weight", weight)
+    return ops.dequant_fp8_block(weight, _decoded_e8m0(scale))
+
+
 def error_metrics(observed: torch.Tensor, reference: torch.Tensor) -> dict[str, Any]:
     """JSON-safe max-absolute and relative-RMS error (``moe_forward.py:234-268``)."""
 
@@ -203,9 +267,12 @@ def error_metrics(observed: torch.Tensor, reference: torch.Tensor) -> dict[str, 
 
 
 __all__ = [
+    "E8M0",
     "FP4_VALUES",
     "GateForwardTensors",
     "HashGateForwardTensors",
+    "dequant_fp8_block",
+    "dequant_mxfp4",
     "error_metrics",
     "gate_forward",
     "gate_forward_with_boundary",

@@ -393,6 +393,60 @@ def pack_fp8(weight: torch.Tensor) -> torch.Tensor:
     return pack_int8(weight.view(torch.int8))
 
 
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2, torch.float8_e4m3fn: 3}
+
+
+def _aligned(t: torch.Tensor, align: int) -> torch.Tensor:
+    """``t`` contiguous and starting at an ``align``-byte boundary (a fresh
+    copy when a view starts elsewhere)."""
+
+    t = t.contiguous()
+    return t if t.data_ptr() % align == 0 else t.clone()
+
+
+def decode_e8m0(codes: torch.Tensor) -> torch.Tensor:
+    """E8M0 bytes (uint8, any shape) -> fp32 of the same shape: 2^(c - 127),
+    byte 0 -> 2^-127, byte 255 -> NaN."""
+
+    _check("codes", codes.contiguous(), dtype=torch.uint8)
+    out = torch.empty(codes.shape, dtype=torch.float32, device=codes.device)
+    call("dsv4moe_decode_e8m0", ptr(codes.contiguous()), codes.numel(), ptr(out), _lib.current_stream(codes.device))
+    return out
+
+
+def dequant_mxfp4(packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """E2M1 codes uint8 [rows, k/2] (low nibble = even K) times decoded fp32
+    scales [rows, k/32] -> fp32 [rows, k]."""
+
+    rows, half_k = packed.shape
+    packed = _aligned(packed, 16)
+    scale = _aligned(scale, 4)
+    _check("packed", packed, dtype=torch.uint8)
+    _check("scale", scale, dtype=torch.float32, shape=(rows, 2 * half_k // 32), device=packed.device)
+    out = torch.empty((rows, 2 * half_k), dtype=torch.float32, device=packed.device)
+    call("dsv4moe_dequant_mxfp4", ptr(packed), ptr(scale), rows, 2 * half_k, ptr(out),
+         _lib.current_stream(packed.device))
+    return out
+
+
+def dequant_fp8_block(weight: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """A [rows, cols] weight (E4M3FN, bf16, fp16 or fp32) times decoded fp32
+    scales [ceil(rows/128), ceil(cols/128)] per 128 x 128 block -> fp32."""
+
+    rows, cols = weight.shape
+    if weight.dtype not in DTYPE_CODES:
+        raise TypeError(f"weight must be one of {sorted(map(str, DTYPE_CODES))}, got {weight.dtype}")
+    weight = _aligned(weight, weight.element_size())
+    _check("weight", weight, dtype=weight.dtype)
+    scale = _aligned(scale, 4)
+    _check("scale", scale, dtype=torch.float32, shape=(-(-rows // 128), -(-cols // 128)), device=weight.device)
+    out = torch.empty((rows, cols), dtype=torch.float32, device=weight.device)
+    code = DTYPE_CODES[weight.dtype]
+    call("dsv4moe_dequant_fp8_block", ptr(weight), code, ptr(scale), rows, cols, ptr(out),
+         _lib.current_stream(weight.device))
+    return out
+
+
 def w8a16_split_k(m: int, n: int, k: int) -> int:
     split = int(_lib.load().dsv4moe_w8a16_split_k(m, n, k))
     if split < 1:

@@ -36,6 +36,12 @@ extern "C" {
 
 #define DSV4MOE_GROUP 128  /* int4 quantisation group along K */
 
+/* Element-type codes of the `*_dtype` arguments. */
+#define DSV4MOE_DTYPE_BF16 0
+#define DSV4MOE_DTYPE_FP16 1
+#define DSV4MOE_DTYPE_FP32 2
+#define DSV4MOE_DTYPE_FP8_E4M3 3  /* OCP E4M3FN (torch.float8_e4m3fn) */
+
 /* Message of the last failing call on this thread ("" if none). */
 const char* dsv4moe_last_error(void);
 
@@ -447,6 +453,29 @@ int dsv4moe_experts_w4a8(const uint16_t* x, int64_t tokens, int32_t hidden, int3
  */
 int dsv4moe_act_quant_fp8(const uint16_t* x, int64_t rows, int32_t k, uint8_t* q, float* scale,
                           float* group_sums, void* stream);
+
+/*
+ * Checkpoint-format dequantisers to dense fp32 [rows, k] / [rows, cols]
+ * (HBM-bound streaming kernels off the layer's hot path).  Replace the host
+ * helpers _decoded_e8m0, dequant_mxfp4 and dequant_fp8_block
+ * (runtime/dsv4_direct/moe_forward.py:115-176); the products are the same
+ * fp32 multiplications, so the outputs are bit-identical to those helpers'.
+ *
+ * dsv4moe_decode_e8m0: codes[n] E8M0 bytes -> out[n] fp32 2^(c-127); byte 0
+ *   gives 2^-127, byte 255 NaN (torch float8_e8m0fnu -> float).
+ * dsv4moe_dequant_mxfp4: packed [rows, k/2] E2M1 codes (low nibble = even
+ *   K), scale fp32 [rows, k/32] (decoded) -> out fp32 [rows, k] = value *
+ *   scale; k a positive multiple of 32; packed and out 16-byte aligned.
+ * dsv4moe_dequant_fp8_block: w [rows, cols] of w_dtype (a DSV4MOE_DTYPE_*),
+ *   scale fp32 [ceil(rows/128), ceil(cols/128)] (decoded) -> out fp32
+ *   [rows, cols] = w * scale of the 128 x 128 block; out 16-byte aligned
+ *   when cols % 4 == 0.
+ */
+int dsv4moe_decode_e8m0(const uint8_t* codes, int64_t n, float* out, void* stream);
+int dsv4moe_dequant_mxfp4(const uint8_t* packed, const float* scale, int64_t rows, int64_t k, float* out,
+                          void* stream);
+int dsv4moe_dequant_fp8_block(const void* w, int32_t w_dtype, const float* scale, int64_t rows, int64_t cols,
+                              float* out, void* stream);
 
 #ifdef __cplusplus
 }

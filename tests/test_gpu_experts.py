@@ -110,6 +110,49 @@ def test_topk_above_one_combine_batch(shared):
     check_layer(shape, 40, seed=13)
 
 
+@pytest.mark.parametrize("shared", [False, True])
+def test_topk_above_one_combine_batch_sums_in_slot_order(shared):
+    """The combine's adds, bit for bit: slot 0, then slots 1..k-1 in order,
+    then the shared row, in fp32, one bf16 rounding.  The fp32 contributions
+    are read back from the end of the workspace (the last region, 256-byte
+    aligned, one row of H fp32 per (token, slot) and per shared token)."""
+
+    shape = S.LayerShape(experts=16, hidden=1024, inter=512, topk=10, has_shared=shared)
+    res, _ = layer(shape)
+    t, k, h = 40, shape.topk, shape.hidden
+    print(f"[experts] combine slot order k={k} shared={shared}", flush=True)
+    x = S.make_hidden(t, h, seed=19, device=DEV)
+    r = route_from_logits(S.make_logits(t, shape.experts, seed=20, device=DEV), topk=k)
+    ids, weights = r.routing_ids, r.routing_weights
+    bs = ops.block_size_m(t, k, shape.experts)
+    align = deterministic_moe_align_block_size(ids, block_size=bs, num_experts=shape.experts)
+    out = torch.empty((t, h), dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(ops.experts_workspace_bytes(t, k, h, shape.inter, shared), dtype=torch.uint8, device=DEV)
+    ops.experts_w4a16_into(
+        x, w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, experts=shape.experts,
+        inter=shape.inter, has_shared=shared, route_weights=weights,
+        sorted_token_ids=align.sorted_token_ids, expert_ids=align.expert_ids,
+        num_tokens_post_padded=align.num_tokens_post_padded, block_size=bs, clamp_limit=0.0,
+        out=out, workspace=ws)
+    torch.cuda.synchronize()
+    rows = t * k + (t if shared else 0)
+    contrib = ws[ws.numel() - rows * h * 4:].view(torch.float32).view(rows, h)
+    slots = contrib[: t * k].view(t, k, h)
+
+    def in_order(order):
+        s = slots[:, order[0]].clone()
+        for j in order[1:]:
+            s = s + slots[:, j]
+        if shared:
+            s = s + contrib[t * k:]
+        return s.to(torch.bfloat16)
+
+    want = in_order(list(range(k)))
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    # the check can tell orders apart: the reversed sum rounds differently somewhere
+    assert not torch.equal(want.view(torch.int16), in_order(list(range(k))[::-1]).view(torch.int16))
+
+
 @pytest.mark.parametrize("t", [1, 8, 64, 256])
 def test_flash_decode(t):
     rows = np.unique(np.r_[np.arange(min(t, 6)), t - 1])
