@@ -31,6 +31,9 @@ _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
 
+# the C ABI revision these signatures describe (dsv4moe_abi_version)
+ABI_VERSION = 3
+
 # name -> (restype, argtypes)
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_last_error": (ctypes.c_char_p, []),
@@ -55,19 +58,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dsv4moe_align_ws": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _sz, _p]),
     "dsv4moe_pack_int4_g128": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p]),
     "dsv4moe_experts_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32, _i32]),
+    "dsv4moe_pack_int4_ratios": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _p]),
     "dsv4moe_experts_w4a16": (
         ctypes.c_int,
-        [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _p, _p, _i64, _p, _p, _i32,
+        [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _i64, _p, _p, _i32,
          _f32, _p, _p, _sz, _p],
     ),
     "dsv4moe_layer_w4a16": (
         ctypes.c_int,
-        [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _i32, _f32,
+        [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p, _p, _i32, _f32,
          _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _sz, _p],
     ),
     "dsv4moe_layer_w4a16_noalloc": (
         ctypes.c_int,
-        [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _i32, _f32,
+        [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p, _p, _i32, _f32,
          _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p],
     ),
     "dsv4moe_pack_mxfp4_g32": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p]),
@@ -123,6 +127,10 @@ def load() -> ctypes.CDLL:
                     "run __graft_entry__.build() first"
                 )
             lib = ctypes.CDLL(str(LIB_PATH))
+            lib.dsv4moe_abi_version.restype = _i32
+            found = int(lib.dsv4moe_abi_version())
+            if found != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH} has C ABI {found}, this binding needs {ABI_VERSION}: rebuild it")
             for name, (restype, argtypes) in SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.restype = restype

@@ -72,12 +72,13 @@ int dsv4_launch_gate_logits(const uint16_t*, const uint16_t*, int64_t, int, int,
                             hipStream_t);
 int dsv4_launch_align(const int32_t*, int64_t, int32_t, int32_t, int32_t*, int64_t, int32_t*,
                       int64_t, int32_t*, hipStream_t);
+int dsv4_launch_pack_ratios(const uint16_t*, int64_t, int64_t, int64_t, float*, hipStream_t);
 int dsv4_launch_pack(const uint8_t*, const uint16_t*, int64_t, int64_t, int64_t, int, uint8_t*,
                      uint16_t*, hipStream_t);
 size_t dsv4_experts_workspace_bytes(int64_t, int, int, int, int);
 int dsv4_launch_experts_w4a16(const uint16_t*, int64_t, int, int, int, int, const uint8_t*,
-                              const uint16_t*, const uint8_t*, const uint16_t*, int, const float*,
-                              const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
+                              const uint16_t*, const uint8_t*, const uint16_t*, const float*, const float*, int,
+                              const float*, const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
                               uint16_t*, void*, hipStream_t, bool rowsums_ready = false);
 float* dsv4_experts_xsum(void*, int64_t, int, int, int, int);
 int dsv4_launch_prologue(int32_t, const float*, const float*, int64_t, int32_t, int32_t, int32_t, float, int32_t*,
@@ -144,7 +145,7 @@ extern "C" {
 
 const char* dsv4moe_last_error(void) { return dsv4host::g_error; }
 
-int32_t dsv4moe_abi_version(void) { return 2; }
+int32_t dsv4moe_abi_version(void) { return 3; }
 
 int dsv4moe_profile_begin(int32_t max_calls) {
   return dsv4moe_profile_begin_stamps(max_calls, (1u << dsv4host::kNumStamps) - 1u);
@@ -348,10 +349,30 @@ int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, i
                           static_cast<hipStream_t>(stream));
 }
 
+int dsv4moe_pack_int4_ratios(const uint16_t* packed_scales, int64_t batch, int64_t n, int64_t k, float* ratios,
+                             void* stream) {
+  clear_error();
+  DSV4_REQUIRE(batch >= 0 && n >= 0 && k >= 0, "pack_ratios: negative size");
+  DSV4_REQUIRE(n % 32 == 0, "pack_ratios: n=%lld must be a multiple of 32", (long long)n);
+  DSV4_REQUIRE(k % DSV4MOE_GROUP == 0, "pack_ratios: k=%lld must be a multiple of 128", (long long)k);
+  if (batch == 0 || n == 0 || k == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(packed_scales && ratios, "pack_ratios: null pointer");
+  DSV4_REQUIRE(aligned(packed_scales, 2) && aligned(ratios, 16),
+               "pack_ratios: scales 2-byte / ratios 16-byte alignment required");
+  return dsv4_launch_pack_ratios(packed_scales, batch, n, k, ratios, static_cast<hipStream_t>(stream));
+}
+
 size_t dsv4moe_experts_workspace_bytes(int64_t tokens, int32_t topk, int32_t hidden,
                                        int32_t inter, int32_t has_shared) {
   if (tokens < 0 || topk <= 0 || hidden <= 0 || inter <= 0) return 0;
   return dsv4_experts_workspace_bytes(tokens, topk, hidden, inter, has_shared ? 1 : 0);
+}
+
+// The W4A16 prefill kernels' group-scale ratios (dsv4moe_pack_int4_ratios).
+static int validate_ratios(const char* who, const float* w13r, const float* w2r) {
+  DSV4_REQUIRE(w13r && w2r, "%s: null scale-ratio pointer (dsv4moe_pack_int4_ratios)", who);
+  DSV4_REQUIRE(aligned(w13r, 16) && aligned(w2r, 16), "%s: scale ratios must be 16-byte aligned", who);
+  return DSV4MOE_OK;
 }
 
 static int validate_experts(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
@@ -393,7 +414,7 @@ static int validate_experts(const uint16_t* x, int64_t tokens, int32_t hidden, i
 int dsv4moe_experts_w4a16(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
                           int32_t experts, int32_t topk, const uint8_t* w13q,
                           const uint16_t* w13s, const uint8_t* w2q, const uint16_t* w2s,
-                          int32_t has_shared, const float* weights,
+                          const float* w13r, const float* w2r, int32_t has_shared, const float* weights,
                           const int32_t* sorted_token_ids, int64_t capacity,
                           const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
                           int32_t block_size, float clamp_limit, uint16_t* out,
@@ -403,6 +424,8 @@ int dsv4moe_experts_w4a16(const uint16_t* x, int64_t tokens, int32_t hidden, int
                             capacity, block_size, out, workspace, workspace_bytes, has_shared,
                             "experts_w4a16");
   if (rc != DSV4MOE_OK || tokens == 0) return rc;
+  rc = validate_ratios("experts_w4a16", w13r, w2r);
+  if (rc != DSV4MOE_OK) return rc;
   DSV4_REQUIRE(weights && sorted_token_ids && expert_ids && num_tokens_post_padded,
                "experts_w4a16: null route/alignment pointer");
   DSV4_REQUIRE(!(clamp_limit < 0.0f) && clamp_limit < 3.0e38f, "experts_w4a16: clamp_limit must be >= 0 and finite");
@@ -410,7 +433,7 @@ int dsv4moe_experts_w4a16(const uint16_t* x, int64_t tokens, int32_t hidden, int
   dsv4host::prof_stamp(dsv4host::kStampBegin, s);
   dsv4host::prof_stamp(dsv4host::kStampRoute, s);
   dsv4host::prof_stamp(dsv4host::kStampAlign, s);
-  return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+  return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s, w13r, w2r,
                                    has_shared ? 1 : 0, weights, sorted_token_ids, capacity,
                                    expert_ids, num_tokens_post_padded, block_size, clamp_limit,
                                    out, workspace, static_cast<hipStream_t>(stream));
@@ -518,7 +541,8 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                         int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
                         int32_t topk, int32_t score_func, float route_scale,
                         const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
-                        const uint16_t* w2s, int32_t has_shared, float clamp_limit,
+                        const uint16_t* w2s, const float* w13r, const float* w2r, int32_t has_shared,
+                        float clamp_limit,
                         int32_t block_size, int32_t* ids, float* weights, float* margin,
                         int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
                         int32_t* num_tokens_post_padded, uint16_t* out, void* workspace,
@@ -528,6 +552,8 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                             capacity, block_size, out, workspace, workspace_bytes, has_shared,
                             "layer_w4a16");
   if (rc != DSV4MOE_OK || tokens == 0) return rc;
+  rc = validate_ratios("layer_w4a16", w13r, w2r);
+  if (rc != DSV4MOE_OK) return rc;
   rc = validate_layer_route("layer_w4a16", logits, topk, score_func, route_scale, clamp_limit, ids, weights,
                             sorted_token_ids, expert_ids, num_tokens_post_padded);
   if (rc != DSV4MOE_OK) return rc;
@@ -537,7 +563,7 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
                          route_scale, has_shared, block_size, ids, weights, margin, sorted_token_ids, capacity,
                          expert_ids, num_tokens_post_padded, workspace, s);
   if (rc != DSV4MOE_OK) return rc;
-  return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+  return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s, w13r, w2r,
                                    has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
                                    num_tokens_post_padded, block_size, clamp_limit, out, workspace, s,
                                    /*rowsums_ready=*/true);
@@ -629,9 +655,9 @@ int dsv4moe_layer_w4a16_noalloc(const uint16_t* x, const float* logits, const fl
                                 int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
                                 int32_t topk, int32_t score_func, float route_scale,
                                 const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
-                                const uint16_t* w2s, int32_t has_shared, float clamp_limit,
-                                int32_t block_size, int32_t* ids, float* weights, float* margin,
-                                int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                                const uint16_t* w2s, const float* w13r, const float* w2r, int32_t has_shared,
+                                float clamp_limit, int32_t block_size, int32_t* ids, float* weights,
+                                float* margin, int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
                                 int32_t* num_tokens_post_padded, uint16_t* out, void* stream) {
   clear_error();
   if (tokens == 0) return DSV4MOE_OK;
@@ -646,7 +672,7 @@ int dsv4moe_layer_w4a16_noalloc(const uint16_t* x, const float* logits, const fl
   const int rc = noalloc_scratch_address(static_cast<hipStream_t>(stream), &ws);
   if (rc != DSV4MOE_OK) return rc;
   return dsv4moe_layer_w4a16(x, logits, bias, tokens, hidden, inter, experts, topk, score_func, route_scale, w13q,
-                             w13s, w2q, w2s, has_shared, clamp_limit, block_size, ids, weights, margin,
+                             w13s, w2q, w2s, w13r, w2r, has_shared, clamp_limit, block_size, ids, weights, margin,
                              sorted_token_ids, capacity, expert_ids, num_tokens_post_padded, out, ws,
                              (size_t)DSV4MOE_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -14,8 +14,9 @@
 // Arithmetic per quantisation group g (128 K values) of weight row n and
 // token column t:  the MFMA chain starts from -136 * sum_g(x) (from the
 // precomputed 64-wide row sums, added in a fixed order) and sums
-// (q + 136) * x (dequant_biased), which leaves sum_g(q * x); the kernel
-// accumulates s[n, g] times it in fp32.
+// (q + 136) * x (dequant_biased), which leaves sum_g(q * x); the decode
+// kernel accumulates s[n, g] times it in fp32, the prefill kernel keeps a
+// running sum divided by the current group's scale (see there).
 //
 // Two kernels share this arithmetic:
 //  * expert_decode_kernel (alignment blocks of <= 16 token slots): one
@@ -254,12 +255,13 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   //  * token tile: 64 slots x 256 B, 16-byte part p of slot s stored at part
   //    p ^ (s & 15) (conflict-free ds_read_b128 of the B fragments);
   //  * the 64 slots' two 64-wide activation sums;
-  //  * each wavefront's 4 weight tiles (4 KiB) and their 16-row scales (128 B).
+  //  * each wavefront's 4 weight tiles (4 KiB) and their 16-row scale ratios
+  //    (fp32, 256 B).
   // Padded slots read zeros (out-of-range buffer offsets).
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kPfSlots * 256];
   __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * kTileBytes];
-  // 64 lanes x 4 B per scale DMA: lanes 0..31 carry the two pairs' 64-byte
-  // blocks, lanes 32..63 write zeros into the upper half of the 256-byte slot.
+  // 64 lanes x 4 B per ratio DMA: lanes 0..31 carry pair p0's 128-byte block,
+  // lanes 32..63 pair p0 + 1's.
   __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];
   __shared__ float xsum[2][2][kPfSlots];
   const int lane = threadIdx.x & 63;
@@ -288,6 +290,8 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
       (void*)(p.wq + (int64_t)b.expert * p.wq_stride), (short)0, (int)p.wq_stride, kRsrcFlags);
   const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.ws + (int64_t)b.expert * p.ws_stride), (short)0, (int)(p.ws_stride * 2), kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t r_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.wr + (int64_t)b.expert * p.ws_stride), (short)0, (int)(p.ws_stride * 4), kRsrcFlags);
 
   // token tile: DMA q (0..3) of wave w fills LDS rows 16w + 4q + lane/16
   uint32_t dma_off[4];
@@ -306,8 +310,8 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   // weight tiles: pair p, group g, member m at byte ((p*groups + g)*2 + m) * 1 KiB
   const uint32_t w_off0 = (uint32_t)(p0 * groups) * 2048 + lane * 16;
   const uint32_t w_off1 = (uint32_t)((p0 + 1) * groups) * 2048 + lane * 16;
-  // scales: 64 bytes per (pair, group); lanes 0..31 copy 4 bytes each of both pairs
-  const uint32_t s_off = lane < 32 ? (uint32_t)((p0 + (lane >> 4)) * groups) * 64 + (lane & 15) * 4 : kOobOffset;
+  // ratios: 128 bytes per (pair, group), 32 lanes x 4 bytes per pair
+  const uint32_t r_off = (uint32_t)((p0 + (lane >> 5)) * groups) * 128 + (lane & 31) * 4;
 
   auto issue = [&](int g, int buf) {
 #pragma unroll
@@ -317,13 +321,22 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
     lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][kTileBytes]), w_off0 + kTileBytes, g * 2048);
     lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][2 * kTileBytes]), w_off1, g * 2048);
     lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][3 * kTileBytes]), w_off1 + kTileBytes, g * 2048);
-    lds_copy4(s_rsrc, lds_addr(&scl[buf][wave][0]), s_off, g * 64);
+    lds_copy4(r_rsrc, lds_addr(&scl[buf][wave][0]), r_off, g * 128);
     if (wave == 0) {
       lds_copy4(sum_rsrc, lds_addr(&xsum[buf][0][0]), sum_off, g * 8);
       lds_copy4(sum_rsrc, lds_addr(&xsum[buf][1][0]), sum_off, g * 8 + 4);
     }
   };
 
+  // Running sum per accumulator element (row n, token column t): after group
+  // g it holds sum_{g' <= g} s[n, g'] * sum_g'(q * x) divided by s[n, g].  At
+  // the start of group g it is multiplied by r = s[n, g-1] / s[n, g] (fp32
+  // ratios precomputed from the packed scales; r is 0 for g = 0, where the
+  // accumulator is 0) and -136 * sum_g(x) is added, one FMA per element; the
+  // MFMA chain then adds sum_g((q + 136) * x), leaving the quotient for group
+  // g.  The last group's scale is applied in the epilogue.  One accumulator
+  // set and no second pass over partial sums: the FMA of a tile waits only for
+  // that tile's previous MFMA, 16 MFMAs earlier.
   f32x4 acc[R][C];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -333,7 +346,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   const int sw = lane & 15;  // swizzle key of this lane's slots (ct*16 + sw)
   const uint32_t magic = dequant_magic();
   // One group: optionally prefetch group g+1 into the other buffers, then
-  // 64 MFMAs and the fp32 group scaling.
+  // the fold and 64 MFMAs.
   auto step = [&](int g, auto u_c, auto prefetch_c) {
     constexpr int u = decltype(u_c)::value;
     if constexpr (decltype(prefetch_c)::value) issue(g + 1, (u + 1) & 1);
@@ -341,14 +354,15 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
 #pragma unroll
     for (int r = 0; r < R; ++r)
       wv[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]);
-    // each MFMA chain starts from -136 * sum_g(x) of its token column
-    f32x4 init[C];
+    float nc[C];
 #pragma unroll
-    for (int ct = 0; ct < C; ++ct) {
-      const float nc = -kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
-      init[ct] = f32x4{nc, nc, nc, nc};
-    }
-    f32x4 tmp[R][C];
+    for (int ct = 0; ct < C; ++ct)
+      nc[ct] = -kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
+    // ratios of strip r = 2j + m: pair j's block, element (quad * 2 + m) * 4 + i
+    f32x4 ratio[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      ratio[r] = *reinterpret_cast<const f32x4*>(&scl[u][wave][(r >> 1) * 128 + ((lane >> 4) * 2 + (r & 1)) * 16]);
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       const int part = ((4 * d + (lane >> 4)) ^ sw) * 16;
@@ -361,19 +375,14 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
       for (int r = 0; r < R; ++r) {
         const bf16x8 a = dequant_biased(wv[r][d], magic);
 #pragma unroll
-        for (int ct = 0; ct < C; ++ct)
-          tmp[r][ct] = mfma_bf16(a, bfr[ct], d == 0 ? init[ct] : tmp[r][ct]);
+        for (int ct = 0; ct < C; ++ct) {
+          if (d == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[r][ct][i] = __builtin_fmaf(acc[r][ct][i], ratio[r][i], nc[ct]);
+          }
+          acc[r][ct] = mfma_bf16(a, bfr[ct], acc[r][ct]);
+        }
       }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const u32x2 sv = *reinterpret_cast<const u32x2*>(&scl[u][wave][(r >> 1) * 64 + 16 * (lane >> 4) + 8 * (r & 1)]);
-      float sc[4];
-      scale4(sv, sc);
-#pragma unroll
-      for (int ct = 0; ct < C; ++ct)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * tmp[r][ct][i];
     }
     lds_dma_wait_all();
     __syncthreads();
@@ -394,6 +403,19 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   }
   step(groups - 2, U0{}, PF{});
   step(groups - 1, U1{}, NOPF{});
+  // the last group's scales (bf16, 4 rows of strip r per lane)
+  float slast[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t off = (uint32_t)((p0 + (r >> 1)) * groups + groups - 1) * 64 + 16 * (lane >> 4) + 8 * (r & 1);
+    scale4(__builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(s_rsrc, off, 0, 0)), slast[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int ct = 0; ct < C; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[r][ct][i] *= slast[r][i];
 
   if constexpr (STAGE == 1) {
     __shared__ float red[4][C * 16];
@@ -590,7 +612,8 @@ int32_t* dsv4_experts_align_scratch(void* workspace, int64_t tokens, int topk, i
 
 int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int inter,
                               int experts, int topk, const uint8_t* w13q, const uint16_t* w13s,
-                              const uint8_t* w2q, const uint16_t* w2s, int has_shared,
+                              const uint8_t* w2q, const uint16_t* w2s, const float* w13r, const float* w2r,
+                              int has_shared,
                               const float* weights, const int32_t* sorted, int64_t capacity,
                               const int32_t* expert_ids, const int32_t* ntpp, int block_size,
                               float clamp_limit, uint16_t* out, void* workspace,
@@ -630,6 +653,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   // stage 1: W13 [2I, H]
   p.wq = w13q;
   p.ws = w13s;
+  p.wr = w13r;
   p.wq_stride = (int64_t)2 * inter * hidden / 2;
   p.ws_stride = (int64_t)2 * inter * (hidden / kGroup);
   p.k_dim = hidden;
@@ -652,6 +676,7 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   // stage 2: W2 [H, I]
   p.wq = w2q;
   p.ws = w2s;
+  p.wr = w2r;
   p.wq_stride = (int64_t)hidden * inter / 2;
   p.ws_stride = (int64_t)hidden * (inter / kGroup);
   p.k_dim = inter;

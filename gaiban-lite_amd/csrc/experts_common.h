@@ -14,6 +14,7 @@ constexpr int kXcds = 8;                  // XCDs; workgroup id i runs on XCD i 
 struct ExpertGemmParams {
   const uint8_t* wq;     // tiled int4, expert-major
   const uint16_t* ws;    // tiled scales
+  const float* wr;       // int4 prefill: fp32 ratios of consecutive group scales, same order (ws_stride per expert)
   int64_t wq_stride;     // bytes per expert
   int64_t ws_stride;     // scale elements per expert
   int k_dim;             // K of the weight matrix

@@ -109,6 +109,25 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const uint16_t* __rest
   }
 }
 
+// Group-scale ratios of the int4 prefill kernels, over the packed scales in
+// their element order (mat, p, g, quad, m, i): r = s[g-1] / s[g] of the same
+// row (32 elements back), correctly rounded in fp32, and 0 for g = 0.  The
+// prefill kernels keep each accumulator divided by the current group's scale
+// (a <- a * r + the next group's partial sums) and multiply by the last
+// group's scale at the end; packed scales are never zero (see above), so
+// every ratio is finite.
+__global__ __launch_bounds__(256) void pack_ratio_kernel(const uint16_t* __restrict__ packed_s,
+                                                         float* __restrict__ ratios, int64_t groups,
+                                                         int64_t total) {
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t g = (idx >> 5) % groups;
+    float r = 0.0f;
+    if (g > 0) r = bf16_bits_to_float(packed_s[idx - 32]) / bf16_bits_to_float(packed_s[idx]);
+    ratios[idx] = r;
+  }
+}
+
 // MXFP4 (E2M1 codes, one E8M0 scale per 32 K; the reference checkpoint
 // format, runtime/dsv4_direct/moe_forward.py:126-155).  Same tile geometry
 // and pair interleave as the int4 layout; inside a tile lane L's dword d is
@@ -184,6 +203,19 @@ int dsv4_launch_pack_mxfp4(const uint8_t* canon, const uint8_t* canon_scales, in
     hipLaunchKernelGGL(pack_e8m0_kernel, dim3(sgrid), dim3(256), 0, stream, canon_scales, packed_scales, n, k,
                        batch, pairing);
     DSV4_CHECK_LAUNCH("pack_e8m0_kernel");
+  }
+  return DSV4MOE_OK;
+}
+
+int dsv4_launch_pack_ratios(const uint16_t* packed_scales, int64_t batch, int64_t n, int64_t k, float* ratios,
+                            hipStream_t stream) {
+  const int64_t total = batch * n * (k / kGroup);
+  const int64_t blocks = (total + 255) / 256;
+  const unsigned grid = (unsigned)(blocks < 65535 * 16 ? blocks : 65535 * 16);
+  if (total > 0) {
+    hipLaunchKernelGGL(pack_ratio_kernel, dim3(grid), dim3(256), 0, stream, packed_scales, ratios, k / kGroup,
+                       total);
+    DSV4_CHECK_LAUNCH("pack_ratio_kernel");
   }
   return DSV4MOE_OK;
 }

@@ -315,6 +315,12 @@ class TP4MoE:
         self.group = group
         self._marlin_input_dtype = marlin_input_dtype
         self._mxfp4 = isinstance(resident, ResidentMXFP4MoEWeights)
+        # the W4A16 entries' scale ratios, computed once here (never inside a call,
+        # which may be under graph capture); other formats take none
+        self._ratio_kwargs: dict[str, torch.Tensor] = {}
+        if not self._mxfp4 and marlin_input_dtype is None and device.type == "cuda":
+            w13r, w2r = resident.scale_ratios()
+            self._ratio_kwargs = {"w13r": w13r, "w2r": w2r}
         # shared expert: inside the grouped kernels (expert index E of the routed
         # stack) or, in the checkpoint FP8 format, as dense linears after them
         self._shared_fp8 = getattr(resident, "shared_fp8", None)
@@ -446,7 +452,7 @@ class TP4MoE:
 
     def _runtime_tensors(self) -> list[torch.Tensor]:
         tensors = [self.resident.w13_q, self.resident.w13_s, self.resident.w2_q, self.resident.w2_s,
-                   self.gate.weight]
+                   self.gate.weight, *self._ratio_kwargs.values()]
         for b in self._buffers.values():
             tensors += [b.workspace, b.logits, b.route_ids, b.route_weights, b.margin,
                         b.alignment.sorted_token_ids, b.alignment.expert_ids,
@@ -862,7 +868,7 @@ class TP4MoE:
                         flat, logits, self._gate_bias, topk=cfg.topk, score_func=cfg.score_func,
                         route_scale=cfg.route_scale, w13q=self.resident.w13_q,
                         w13s=self.resident.w13_s, w2q=self.resident.w2_q, w2s=self.resident.w2_s,
-                        experts=cfg.experts, inter=cfg.intermediate_size,
+                        **self._ratio_kwargs, experts=cfg.experts, inter=cfg.intermediate_size,
                         has_shared=self._grouped_shared, clamp_limit=cfg.clamp_limit,
                         block_size=buffers.block_size_m, ids=buffers.route_ids,
                         weights=buffers.route_weights, margin=buffers.margin,
@@ -938,7 +944,7 @@ class TP4MoE:
                     experts_into = ops.experts_w4a16_into
                 experts_into(
                     flat, w13q=self.resident.w13_q, w13s=self.resident.w13_s,
-                    w2q=self.resident.w2_q, w2s=self.resident.w2_s, experts=cfg.experts,
+                    w2q=self.resident.w2_q, w2s=self.resident.w2_s, **self._ratio_kwargs, experts=cfg.experts,
                     inter=cfg.intermediate_size, has_shared=self._grouped_shared,
                     route_weights=route_weights, sorted_token_ids=a.sorted_token_ids,
                     expert_ids=a.expert_ids, num_tokens_post_padded=a.num_tokens_post_padded,

@@ -221,6 +221,22 @@ def pack_int4_g128(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = F
     return packed, packed_scales
 
 
+def pack_int4_ratios(packed_scales: torch.Tensor, *, n: int, k: int) -> torch.Tensor:
+    """fp32 ratios of consecutive group scales of ``pack_int4_g128`` scales
+    (``dsv4moe_pack_int4_ratios``): same shape and element order, element =
+    the row's scale of group g-1 over its scale of group g (0 for g = 0).
+    The W4A16 prefill kernels read them."""
+
+    dev = packed_scales.device
+    _check("packed_scales", packed_scales, dtype=torch.bfloat16, device=dev)
+    if packed_scales.shape[-1] != n * (k // GROUP):
+        raise ValueError(f"packed_scales: last dimension {packed_scales.shape[-1]} != n*k/128 = {n * (k // GROUP)}")
+    batch = packed_scales.numel() // packed_scales.shape[-1] if packed_scales.ndim > 1 else 1
+    ratios = torch.empty(packed_scales.shape, dtype=torch.float32, device=dev)
+    call("dsv4moe_pack_int4_ratios", ptr(packed_scales), batch, n, k, ptr(ratios), _lib.current_stream(dev))
+    return ratios
+
+
 def pack_mxfp4_g32(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = False
                    ) -> tuple[torch.Tensor, torch.Tensor]:
     """Checkpoint-layout MXFP4 [.., n, k/2] u8 (E2M1, low nibble = even k) +
@@ -293,6 +309,7 @@ def _experts_into(
     x: torch.Tensor,
     *,
     w13q, w13s, w2q, w2s,
+    w13r=None, w2r=None,
     experts: int,
     inter: int,
     has_shared: bool,
@@ -312,13 +329,29 @@ def _experts_into(
     _check("out", out, dtype=torch.bfloat16, shape=(tokens, hidden), device=dev)
     _check("route_weights", route_weights, dtype=torch.float32, shape=(tokens, topk), device=dev)
     _check("workspace", workspace, dtype=torch.uint8, device=dev)
+    ratios = _scale_ratio_args(entry == "dsv4moe_experts_w4a16", w13r, w2r, w13s, w2s, dev)
     call(
         entry, ptr(x), tokens, hidden, inter, experts, topk, ptr(w13q),
-        ptr(w13s), ptr(w2q), ptr(w2s), int(bool(has_shared)), ptr(route_weights),
+        ptr(w13s), ptr(w2q), ptr(w2s), *ratios, int(bool(has_shared)), ptr(route_weights),
         ptr(sorted_token_ids), sorted_token_ids.numel(), ptr(expert_ids),
         ptr(num_tokens_post_padded), block_size, float(clamp_limit), ptr(out), ptr(workspace),
         workspace.numel(), _lib.current_stream(dev),
     )
+
+
+def _scale_ratio_args(takes_ratios: bool, w13r, w2r, w13s, w2s, dev) -> list:
+    """The (w13r, w2r) pointer arguments of the W4A16 entries (fp32, shaped
+    as their scales); the other formats take none."""
+
+    if not takes_ratios:
+        if w13r is not None or w2r is not None:
+            raise ValueError("only the W4A16 entries take scale ratios")
+        return []
+    if w13r is None or w2r is None:
+        raise TypeError("the W4A16 entries need w13r and w2r (pack_int4_ratios of the scales)")
+    _check("w13r", w13r, dtype=torch.float32, shape=tuple(w13s.shape), device=dev)
+    _check("w2r", w2r, dtype=torch.float32, shape=tuple(w2s.shape), device=dev)
+    return [ptr(w13r), ptr(w2r)]
 
 
 def layer_w4a16_into(
@@ -330,6 +363,7 @@ def layer_w4a16_into(
     score_func: str | int,
     route_scale: float,
     w13q, w13s, w2q, w2s,
+    w13r=None, w2r=None,
     experts: int,
     inter: int,
     has_shared: bool,
@@ -358,11 +392,12 @@ def layer_w4a16_into(
     _check("workspace", workspace, dtype=torch.uint8, device=dev)
     if bias is not None:
         _check("bias", bias, dtype=torch.float32, shape=(experts,), device=dev)
+    ratios = _scale_ratio_args(not mxfp4, w13r, w2r, w13s, w2s, dev)
     call(
         "dsv4moe_layer_mxfp4" if mxfp4 else "dsv4moe_layer_w4a16", ptr(x), ptr(logits), ptr(bias), tokens,
         hidden, inter, experts,
         topk, score_func_id(score_func), float(route_scale), ptr(w13q), ptr(w13s), ptr(w2q),
-        ptr(w2s), int(bool(has_shared)), float(clamp_limit), block_size, ptr(ids), ptr(weights),
+        ptr(w2s), *ratios, int(bool(has_shared)), float(clamp_limit), block_size, ptr(ids), ptr(weights),
         ptr(margin), ptr(sorted_token_ids), sorted_token_ids.numel(), ptr(expert_ids),
         ptr(num_tokens_post_padded), ptr(out), ptr(workspace), workspace.numel(),
         _lib.current_stream(dev),

@@ -145,6 +145,10 @@ class ResidentInt4MoEWeights:
     marlin_input_dtype: torch.dtype | None = None
     weight_format: str = "int4_g128"
     shared_fp8: ResidentFP8SharedExpert | None = None  # shared expert in the checkpoint FP8 format
+    # fp32 ratios of consecutive group scales (ops.pack_int4_ratios), shaped as
+    # w13_s / w2_s: the W4A16 prefill kernels' running-sum scaling reads them
+    w13_r: torch.Tensor | None = None
+    w2_r: torch.Tensor | None = None
 
     @property
     def device(self) -> torch.device:
@@ -152,7 +156,21 @@ class ResidentInt4MoEWeights:
 
     @property
     def resident_bytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in (self.w13_q, self.w13_s, self.w2_q, self.w2_s))
+        tensors = [self.w13_q, self.w13_s, self.w2_q, self.w2_s]
+        tensors += [t for t in (self.w13_r, self.w2_r) if t is not None]
+        return sum(t.numel() * t.element_size() for t in tensors)
+
+    def scale_ratios(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(w13_r, w2_r), computed on the device from the packed scales the
+        first time (one pass over them) and kept."""
+
+        if self.w13_r is None or self.w2_r is None:
+            if self.device.type != "cuda":
+                raise ValueError("scale ratios are computed on the GPU; these weights live on the CPU")
+            h, i = self.hidden_size, self.intermediate_size
+            self.w13_r = ops.pack_int4_ratios(self.w13_s, n=2 * i, k=h)
+            self.w2_r = ops.pack_int4_ratios(self.w2_s, n=h, k=i)
+        return self.w13_r, self.w2_r
 
     @property
     def bytes_per_expert(self) -> int:
@@ -169,6 +187,9 @@ class ResidentInt4MoEWeights:
             "w2_q": ((e_tot, h * i // 2), torch.uint8),
             "w2_s": ((e_tot, h * (i // GROUP)), torch.bfloat16),
         }
+        for name in ("w13_r", "w2_r"):
+            if getattr(self, name) is not None:
+                expected[name] = (expected[name.replace("_r", "_s")][0], torch.float32)
         for name, (shape, dtype) in expected.items():
             t = getattr(self, name)
             if tuple(t.shape) != shape or t.dtype != dtype:
@@ -209,6 +230,8 @@ class ResidentInt4MoEWeights:
         q2, s2 = ops.pack_int4_g128(w2_packed.contiguous(), w2_scale.contiguous(), gated=False)
         out = cls(q13, s13, q2, s2, experts, hidden, inter, has_shared, layer_id, checkpoint_id,
                   marlin_input_dtype, shared_fp8=shared_fp8)
+        if marlin_input_dtype is None:  # the W4A16 kernels' running-sum ratios
+            out.scale_ratios()
         out.validate()
         return out
 

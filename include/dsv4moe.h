@@ -182,6 +182,20 @@ int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, i
                            uint16_t* packed_scales, void* stream);
 
 /*
+ * Group-scale ratios of the W4A16 prefill kernels, from packed scales
+ * (dsv4moe_pack_int4_g128's packed_scales [batch, n*k/128] bf16) into
+ * ratios fp32 [batch, n*k/128] in the same element order: the ratio of a
+ * row's scale of group g-1 to its scale of group g (fp32, correctly rounded;
+ * 0 for g = 0).  The prefill kernels keep each accumulator divided by the
+ * current group's scale: a <- a * ratio + (next group's partial sums), and
+ * multiply by the last group's scale at the end.  Computed once per packed
+ * weight set; no counterpart in the reference (its Marlin kernels scale each
+ * dequantised weight).  n a multiple of 32, k of 128.
+ */
+int dsv4moe_pack_int4_ratios(const uint16_t* packed_scales, int64_t batch, int64_t n, int64_t k, float* ratios,
+                             void* stream);
+
+/*
  * Workspace needed by dsv4moe_experts_w4a16 / _w4a8 (bytes).
  */
 size_t dsv4moe_experts_workspace_bytes(int64_t tokens, int32_t topk, int32_t hidden,
@@ -195,6 +209,8 @@ size_t dsv4moe_experts_workspace_bytes(int64_t tokens, int32_t topk, int32_t hid
  *   w13q/w13s  tiled int4 + scales (DSV4MOE_PAIR_GATED), experts(+1 shared) x
  *              [2*inter, hidden] (rows [0,inter) = gate w1, [inter,2*inter) = up w3)
  *   w2q/w2s    tiled int4 + scales (DSV4MOE_PAIR_PLAIN), experts(+1 shared) x [hidden, inter]
+ *   w13r/w2r   fp32 scale ratios of w13s / w2s (dsv4moe_pack_int4_ratios), read by
+ *              the prefill kernels (block_size >= 32); required, 16-byte aligned
  *   has_shared 1: expert index `experts` is the always-on shared expert
  *   weights  fp32 [tokens, topk]  (route weights, applied to the w2 output)
  *   sorted_token_ids / expert_ids / num_tokens_post_padded: dsv4moe_align output
@@ -205,7 +221,7 @@ size_t dsv4moe_experts_workspace_bytes(int64_t tokens, int32_t topk, int32_t hid
 int dsv4moe_experts_w4a16(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
                           int32_t experts, int32_t topk, const uint8_t* w13q,
                           const uint16_t* w13s, const uint8_t* w2q, const uint16_t* w2s,
-                          int32_t has_shared, const float* weights,
+                          const float* w13r, const float* w2r, int32_t has_shared, const float* weights,
                           const int32_t* sorted_token_ids, int64_t capacity,
                           const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
                           int32_t block_size, float clamp_limit, uint16_t* out,
@@ -215,13 +231,15 @@ int dsv4moe_experts_w4a16(const uint16_t* x, int64_t tokens, int32_t hidden, int
  * Whole MoE layer, W4A16: route (from logits) -> align -> experts -> combine.
  * Replaces TP4MoE.compute_partial (runtime/dsv4_direct/moe_runtime.py:1714-1888)
  * at world size 1.  Route and alignment outputs are caller-owned and written.
- * bias may be NULL; margin may be NULL.
+ * bias may be NULL; margin may be NULL.  Weights, scales and scale ratios as
+ * in dsv4moe_experts_w4a16.
  */
 int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bias,
                         int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
                         int32_t topk, int32_t score_func, float route_scale,
                         const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
-                        const uint16_t* w2s, int32_t has_shared, float clamp_limit,
+                        const uint16_t* w2s, const float* w13r, const float* w2r, int32_t has_shared,
+                        float clamp_limit,
                         int32_t block_size, int32_t* ids, float* weights, float* margin,
                         int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
                         int32_t* num_tokens_post_padded, uint16_t* out, void* workspace,
@@ -244,9 +262,9 @@ int dsv4moe_layer_w4a16_noalloc(const uint16_t* x, const float* logits, const fl
                                 int64_t tokens, int32_t hidden, int32_t inter, int32_t experts,
                                 int32_t topk, int32_t score_func, float route_scale,
                                 const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
-                                const uint16_t* w2s, int32_t has_shared, float clamp_limit,
-                                int32_t block_size, int32_t* ids, float* weights, float* margin,
-                                int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                                const uint16_t* w2s, const float* w13r, const float* w2r, int32_t has_shared,
+                                float clamp_limit, int32_t block_size, int32_t* ids, float* weights,
+                                float* margin, int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
                                 int32_t* num_tokens_post_padded, uint16_t* out, void* stream);
 
 /*

@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in dsv4moe.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.dsv4moe_abi_version() == 2
+    assert lib.dsv4moe_abi_version() == 3
 
 
 def test_host_policy_functions_match_oracle():
@@ -62,13 +62,20 @@ def test_validation_rejects_before_launch():
     assert "multiple of 32" in _einval("dsv4moe_pack_int4_g128", fake, fake, 1, 48, 128, 0, fake, fake, None)
     assert "pairing" in _einval("dsv4moe_pack_int4_g128", fake, fake, 1, 64, 128, 2, fake, fake, None)
     assert "block_size" in _einval("dsv4moe_experts_w4a16", fake, 4, 4096, 2048, 256, 6, fake, fake, fake, fake,
-                                   1, fake, fake, 192, fake, fake, 12, 0.0, fake, fake, 1 << 30, None)
+                                   fake, fake, 1, fake, fake, 192, fake, fake, 12, 0.0, fake, fake, 1 << 30, None)
     assert "hidden" in _einval("dsv4moe_experts_w4a16", fake, 4, 4000, 2048, 256, 6, fake, fake, fake, fake,
-                               1, fake, fake, 192, fake, fake, 8, 0.0, fake, fake, 1 << 30, None)
+                               fake, fake, 1, fake, fake, 192, fake, fake, 8, 0.0, fake, fake, 1 << 30, None)
     ws = ops.experts_workspace_bytes(4, 6, 4096, 2048, True)
     assert "workspace" in _einval("dsv4moe_experts_w4a16", fake, 4, 4096, 2048, 256, 6, fake, fake, fake, fake,
-                                  1, fake, fake, 192, fake, fake, 8, 0.0, fake, ctypes.c_void_p(0x100000),
-                                  ws - 1, None)
+                                  fake, fake, 1, fake, fake, 192, fake, fake, 8, 0.0, fake,
+                                  ctypes.c_void_p(0x100000), ws - 1, None)
+    # the scale ratios of the prefill kernels are required
+    good_ws = ctypes.c_void_p(0x100000)
+    assert "scale-ratio" in _einval("dsv4moe_experts_w4a16", fake, 4, 4096, 2048, 256, 6, fake, fake, fake, fake,
+                                    None, fake, 1, fake, fake, 192, fake, fake, 8, 0.0, fake, good_ws, ws, None)
+    assert "multiple of 32" in _einval("dsv4moe_pack_int4_ratios", fake, 1, 48, 128, fake, None)
+    assert "multiple of 128" in _einval("dsv4moe_pack_int4_ratios", fake, 1, 64, 100, fake, None)
+    assert "null" in _einval("dsv4moe_pack_int4_ratios", None, 1, 64, 128, fake, None)
 
 
 def test_align_workspace_policy_and_validation():

@@ -55,7 +55,9 @@ def run(fmt, x, weights, align, bs):
     ws = torch.empty(ws_fn(t, k, SHAPE.hidden, SHAPE.inter, True), dtype=torch.uint8, device=DEV)
     out = torch.empty((t, SHAPE.hidden), dtype=torch.bfloat16, device=DEV)
     fn = {"w4a16": ops.experts_w4a16_into, "w4a8": ops.experts_w4a8_into, "mxfp4": ops.experts_mxfp4_into}[fmt]
-    fn(x, w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, experts=SHAPE.experts, inter=SHAPE.inter,
+    ratios = dict(w13r=res.w13_r, w2r=res.w2_r) if fmt == "w4a16" else {}
+    fn(x, w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, **ratios, experts=SHAPE.experts,
+       inter=SHAPE.inter,
        has_shared=True, route_weights=weights, sorted_token_ids=align.sorted_token_ids, expert_ids=align.expert_ids,
        num_tokens_post_padded=align.num_tokens_post_padded, block_size=bs, clamp_limit=0.0, out=out, workspace=ws)
     torch.cuda.synchronize()

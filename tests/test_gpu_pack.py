@@ -52,3 +52,28 @@ def test_pack_rejects_bad_shapes():
     scales = torch.zeros((1, 48, 1), dtype=torch.bfloat16, device=DEV)
     with pytest.raises(ValueError):
         ops.pack_int4_g128(canon, scales)
+
+
+@pytest.mark.parametrize("n,k,batch", [(64, 1024, 2), (4096, 2048, 1), (32, 128, 3)])
+def test_scale_ratios(n, k, batch):
+    """Ratios of consecutive group scales over the packed scales: element e
+    of group g is s(e of g-1) / s(e of g), fp32 correctly rounded (the same
+    IEEE division on the CPU), 0 in group 0; zero-scale groups were replaced
+    by the packer, so every ratio is finite.  Scales span 2^-20 .. 2^20."""
+
+    g = torch.Generator(DEV).manual_seed(n + k)
+    canon = torch.randint(0, 256, (batch, n, k // 2), dtype=torch.uint8, device=DEV, generator=g)
+    expo = torch.randint(-20, 21, (batch, n, k // 128), device=DEV, generator=g).float()
+    scales = ((torch.rand((batch, n, k // 128), device=DEV, generator=g) + 0.5) * torch.exp2(expo)).to(torch.bfloat16)
+    scales[0, 3, 1:3] = 0.0
+    _, ps = ops.pack_int4_g128(canon, scales, gated=n % 64 == 0)
+    ratios = ops.pack_int4_ratios(ps, n=n, k=k)
+    torch.cuda.synchronize()
+    groups = k // 128
+    sv = ps.float().cpu().view(batch, n // 32, groups, 32)
+    want = torch.zeros_like(sv)
+    want[:, :, 1:] = sv[:, :, :-1] / sv[:, :, 1:]
+    got = ratios.cpu().view(batch, n // 32, groups, 32)
+    assert ratios.dtype == torch.float32 and ratios.shape == ps.shape
+    assert torch.isfinite(got).all()
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))

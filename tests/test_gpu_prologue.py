@@ -59,7 +59,8 @@ def run_layer(shape, tokens, score, seed, route_scale=1.5, clamp=0.0):
             out=torch.empty((tokens, H), dtype=torch.bfloat16, device=DEV),
         )
 
-    common = dict(w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, experts=E, inter=I,
+    common = dict(w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, w13r=res.w13_r, w2r=res.w2_r,
+                  experts=E, inter=I,
                   has_shared=True, clamp_limit=clamp, block_size=bs)
     f = bufs()
     ops.layer_w4a16_into(x, logits, bias, topk=k, score_func=score, route_scale=route_scale, ids=f["ids"],

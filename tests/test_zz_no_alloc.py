@@ -40,7 +40,7 @@ def _args(res, x, logits, b):
     p = _lib.ptr
     t = x.shape[0]
     return [p(x), p(logits), None, t, H, I, E, K, _lib.SCORE_FUNCS["sigmoid"], 1.0, p(res.w13_q), p(res.w13_s),
-            p(res.w2_q), p(res.w2_s), 1, 0.0, b["bs"], p(b["ids"]), p(b["w"]), p(b["margin"]), p(b["sorted"]),
+            p(res.w2_q), p(res.w2_s), p(res.w13_r), p(res.w2_r), 1, 0.0, b["bs"], p(b["ids"]), p(b["w"]), p(b["margin"]), p(b["sorted"]),
             b["cap"], p(b["eids"]), p(b["ntpp"]), p(b["out"])]
 
 
@@ -77,7 +77,7 @@ def test_noalloc_layer_rejects_a_workspace_above_the_scratch():
     fake = torch.empty(16, dtype=torch.uint8, device=DEV)
 
     class _Res:  # weight pointers are never dereferenced: the call fails before any launch
-        w13_q = w13_s = w2_q = w2_s = fake
+        w13_q = w13_s = w2_q = w2_s = w13_r = w2_r = fake
 
     with pytest.raises(ValueError, match="static scratch"):
         _lib.call("dsv4moe_layer_w4a16_noalloc", *_args(_Res, x, logits, b), _lib.current_stream(DEV))
