@@ -250,7 +250,6 @@ constexpr int kPfSlots = 64;
 template <int STAGE>
 __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams p, int total_blocks) {
   constexpr int R = 4;
-  constexpr int C = 4;
   // Per group, copied into LDS by buffer_load ... lds (double buffered):
   //  * token tile: 64 slots x 256 B, 16-byte part p of slot s stored at part
   //    p ^ (s & 15) (conflict-free ds_read_b128 of the B fragments);
@@ -264,6 +263,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   // lanes 32..63 pair p0 + 1's.
   __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];
   __shared__ float xsum[2][2][kPfSlots];
+  __shared__ float red[4][kPfSlots];  // stage-1 epilogue: per-wavefront column sums
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
@@ -328,152 +328,166 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
     }
   };
 
-  // Running sum per accumulator element (row n, token column t): after group
-  // g it holds sum_{g' <= g} s[n, g'] * sum_g'(q * x) divided by s[n, g].  At
-  // the start of group g it is multiplied by r = s[n, g-1] / s[n, g] (fp32
-  // ratios precomputed from the packed scales; r is 0 for g = 0, where the
-  // accumulator is 0) and -136 * sum_g(x) is added, one FMA per element; the
-  // MFMA chain then adds sum_g((q + 136) * x), leaving the quotient for group
-  // g.  The last group's scale is applied in the epilogue.  One accumulator
-  // set and no second pass over partial sums: the FMA of a tile waits only for
-  // that tile's previous MFMA, 16 MFMAs earlier.
-  f32x4 acc[R][C];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int ct = 0; ct < C; ++ct) acc[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Token columns that hold a valid slot: the alignment pads each expert's
+  // run at its end, so a block's valid slots come first.  A block with at
+  // most 32 of them runs the loop over two 16-slot column tiles instead of
+  // four (the MFMAs and scale FMAs of the empty tiles are skipped).
+  const uint64_t valid = __ballot(slot_rowid(p, b, lane, tk) >= 0);
+  const int used = valid ? 64 - __builtin_clzll(valid) : 0;
 
-  const int sw = lane & 15;  // swizzle key of this lane's slots (ct*16 + sw)
-  const uint32_t magic = dequant_magic();
-  // One group: optionally prefetch group g+1 into the other buffers, then
-  // the fold and 64 MFMAs.
-  auto step = [&](int g, auto u_c, auto prefetch_c) {
-    constexpr int u = decltype(u_c)::value;
-    if constexpr (decltype(prefetch_c)::value) issue(g + 1, (u + 1) & 1);
-    u32x4 wv[R];
+  auto body = [&](auto c_c) {
+    constexpr int C = decltype(c_c)::value;
+    // Running sum per accumulator element (row n, token column t): after group
+    // g it holds sum_{g' <= g} s[n, g'] * sum_g'(q * x) divided by s[n, g].  At
+    // the start of group g it is multiplied by r = s[n, g-1] / s[n, g] (fp32
+    // ratios precomputed from the packed scales; r is 0 for g = 0, where the
+    // accumulator is 0) and -136 * sum_g(x) is added, one FMA per element; the
+    // MFMA chain then adds sum_g((q + 136) * x), leaving the quotient for group
+    // g.  The last group's scale is applied in the epilogue.  One accumulator
+    // set and no second pass over partial sums: the FMA of a tile waits only for
+    // that tile's previous MFMA, 16 MFMAs earlier.
+    f32x4 acc[R][C];
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      wv[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]);
-    float nc[C];
 #pragma unroll
-    for (int ct = 0; ct < C; ++ct)
-      nc[ct] = -kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
-    // ratios of strip r = 2j + m: pair j's block, element (quad * 2 + m) * 4 + i
-    f32x4 ratio[R];
+      for (int ct = 0; ct < C; ++ct) acc[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int sw = lane & 15;  // swizzle key of this lane's slots (ct*16 + sw)
+    const uint32_t magic = dequant_magic();
+    // One group: optionally prefetch group g+1 into the other buffers, then
+    // the fold and 64 MFMAs.
+    auto step = [&](int g, auto u_c, auto prefetch_c) {
+      constexpr int u = decltype(u_c)::value;
+      if constexpr (decltype(prefetch_c)::value) issue(g + 1, (u + 1) & 1);
+      u32x4 wv[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      ratio[r] = *reinterpret_cast<const f32x4*>(&scl[u][wave][(r >> 1) * 128 + ((lane >> 4) * 2 + (r & 1)) * 16]);
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const int part = ((4 * d + (lane >> 4)) ^ sw) * 16;
-      bf16x8 bfr[C];
+      for (int r = 0; r < R; ++r)
+        wv[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]);
+      float nc[C];
 #pragma unroll
       for (int ct = 0; ct < C; ++ct)
-        bfr[ct] = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][(ct * 16 + sw) * 256 + part]));
+        nc[ct] = -kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
+      // ratios of strip r = 2j + m: pair j's block, element (quad * 2 + m) * 4 + i
+      f32x4 ratio[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const bf16x8 a = dequant_biased(wv[r][d], magic);
+      for (int r = 0; r < R; ++r)
+        ratio[r] = *reinterpret_cast<const f32x4*>(&scl[u][wave][(r >> 1) * 128 + ((lane >> 4) * 2 + (r & 1)) * 16]);
 #pragma unroll
-        for (int ct = 0; ct < C; ++ct) {
-          if (d == 0) {
+      for (int d = 0; d < 4; ++d) {
+        const int part = ((4 * d + (lane >> 4)) ^ sw) * 16;
+        bf16x8 bfr[C];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[r][ct][i] = __builtin_fmaf(acc[r][ct][i], ratio[r][i], nc[ct]);
+        for (int ct = 0; ct < C; ++ct)
+          bfr[ct] = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][(ct * 16 + sw) * 256 + part]));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const bf16x8 a = dequant_biased(wv[r][d], magic);
+#pragma unroll
+          for (int ct = 0; ct < C; ++ct) {
+            if (d == 0) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[r][ct][i] = __builtin_fmaf(acc[r][ct][i], ratio[r][i], nc[ct]);
+            }
+            acc[r][ct] = mfma_bf16(a, bfr[ct], acc[r][ct]);
           }
-          acc[r][ct] = mfma_bf16(a, bfr[ct], acc[r][ct]);
         }
       }
-    }
+      lds_dma_wait_all();
+      __syncthreads();
+    };
+    using U0 = std::integral_constant<int, 0>;
+    using U1 = std::integral_constant<int, 1>;
+    using PF = std::true_type;
+    using NOPF = std::false_type;
+
+    issue(0, 0);
     lds_dma_wait_all();
     __syncthreads();
-  };
-  using U0 = std::integral_constant<int, 0>;
-  using U1 = std::integral_constant<int, 1>;
-  using PF = std::true_type;
-  using NOPF = std::false_type;
+    // groups is even (checked on the host); the last group issues no prefetch,
+    // so no LDS DMA is in flight when the workgroup leaves the loop.
+    for (int g0 = 0; g0 + 2 < groups; g0 += 2) {
+      step(g0, U0{}, PF{});
+      step(g0 + 1, U1{}, PF{});
+    }
+    step(groups - 2, U0{}, PF{});
+    step(groups - 1, U1{}, NOPF{});
+    // the last group's scales (bf16, 4 rows of strip r per lane)
+    float slast[R][4];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t off = (uint32_t)((p0 + (r >> 1)) * groups + groups - 1) * 64 + 16 * (lane >> 4) + 8 * (r & 1);
+      scale4(__builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(s_rsrc, off, 0, 0)), slast[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int ct = 0; ct < C; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][ct][i] *= slast[r][i];
 
-  issue(0, 0);
-  lds_dma_wait_all();
-  __syncthreads();
-  // groups is even (checked on the host); the last group issues no prefetch,
-  // so no LDS DMA is in flight when the workgroup leaves the loop.
-  for (int g0 = 0; g0 + 2 < groups; g0 += 2) {
-    step(g0, U0{}, PF{});
-    step(g0 + 1, U1{}, PF{});
-  }
-  step(groups - 2, U0{}, PF{});
-  step(groups - 1, U1{}, NOPF{});
-  // the last group's scales (bf16, 4 rows of strip r per lane)
-  float slast[R][4];
+    if constexpr (STAGE == 1) {
+      const float lim = p.clamp_limit;
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint32_t off = (uint32_t)((p0 + (r >> 1)) * groups + groups - 1) * 64 + 16 * (lane >> 4) + 8 * (r & 1);
-    scale4(__builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(s_rsrc, off, 0, 0)), slast[r]);
-  }
+      for (int ct = 0; ct < C; ++ct) {
+        const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
+        float part = 0.0f;
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+        for (int s = 0; s < 2; ++s) {
+          uint32_t bits[4];
 #pragma unroll
-    for (int ct = 0; ct < C; ++ct)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[r][ct][i] *= slast[r][i];
-
-  if constexpr (STAGE == 1) {
-    __shared__ float red[4][C * 16];
-    const float lim = p.clamp_limit;
-#pragma unroll
-    for (int ct = 0; ct < C; ++ct) {
-      const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
-      float part = 0.0f;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        uint32_t bits[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float gt = acc[2 * s][ct][i];
-          float up = acc[2 * s + 1][ct][i];
-          if (lim > 0.0f) {
-            gt = fminf(gt, lim);
-            up = fminf(fmaxf(up, -lim), lim);
+          for (int i = 0; i < 4; ++i) {
+            float gt = acc[2 * s][ct][i];
+            float up = acc[2 * s + 1][ct][i];
+            if (lim > 0.0f) {
+              gt = fminf(gt, lim);
+              up = fminf(fmaxf(up, -lim), lim);
+            }
+            bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+            part += __uint_as_float(bits[i] << 16);
           }
-          bits[i] = float_to_bf16_bits(silu_f(gt) * up);
-          part += __uint_as_float(bits[i] << 16);
+          if (rowid >= 0) {
+            const int n = n0 + 32 * wave + 16 * s + 4 * (lane >> 4);
+            u32x2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+            *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) = packed;
+          }
         }
-        if (rowid >= 0) {
-          const int n = n0 + 32 * wave + 16 * s + 4 * (lane >> 4);
-          u32x2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
-          *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) = packed;
+        part += __shfl_xor(part, 16, 64);
+        part += __shfl_xor(part, 32, 64);
+        if (lane < 16) red[wave][ct * 16 + lane] = part;
+      }
+      __syncthreads();
+      if (threadIdx.x < C * 16) {
+        const int col = threadIdx.x;
+        const int64_t rid = slot_rowid(p, b, col, tk);
+        if (rid >= 0) {
+          float* dst = p.hsum_out + rid * (p.inter / kSumChunk) + n0 / kSumChunk;
+          dst[0] = red[0][col] + red[1][col];
+          dst[1] = red[2][col] + red[3][col];
         }
       }
-      part += __shfl_xor(part, 16, 64);
-      part += __shfl_xor(part, 32, 64);
-      if (lane < 16) red[wave][ct * 16 + lane] = part;
-    }
-    __syncthreads();
-    if (threadIdx.x < C * 16) {
-      const int col = threadIdx.x;
-      const int64_t rid = slot_rowid(p, b, col, tk);
-      if (rid >= 0) {
-        float* dst = p.hsum_out + rid * (p.inter / kSumChunk) + n0 / kSumChunk;
-        dst[0] = red[0][col] + red[1][col];
-        dst[1] = red[2][col] + red[3][col];
+    } else {
+#pragma unroll
+      for (int ct = 0; ct < C; ++ct) {
+        const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
+        if (rowid < 0) continue;
+        const float wr = contrib_weight(p, b, rowid, tk);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int n = n0 + 64 * wave + 16 * r + 4 * (lane >> 4);
+          f32x4 v = acc[r][ct];
+          v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
+          *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+        }
       }
     }
-  } else {
-#pragma unroll
-    for (int ct = 0; ct < C; ++ct) {
-      const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
-      if (rowid < 0) continue;
-      const float wr = contrib_weight(p, b, rowid, tk);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int n = n0 + 64 * wave + 16 * r + 4 * (lane >> 4);
-        f32x4 v = acc[r][ct];
-        v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
-        *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
-      }
-    }
-  }
+  };
+  if (used > 32)
+    body(std::integral_constant<int, 4>{});
+  else
+    body(std::integral_constant<int, 2>{});
 }
+
 
 // Per-row fp32 sums of bf16 activations over each 64-wide K chunk, summed in
 // ascending k order.
