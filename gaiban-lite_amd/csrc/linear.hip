@@ -286,6 +286,184 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
   }
 }
 
+// Up to 64 tokens with a K split: the split runs inside the workgroup.
+// Workgroup tile: 16*R output channels x 16*C tokens; wavefront w of the
+// `split` wavefronts computes split w's partial -- windows [w * wps,
+// min(wins, (w + 1) * wps)), the same MFMA chain per (channel, token) as a
+// split workgroup of w8a16_kernel -- scales it, and leaves it in LDS; the
+// workgroup then sums the partials in split order (fp32, split 0 first) and
+// rounds once, the additions of split_reduce_kernel, so the bits equal the
+// two-launch result for the same split.  No workspace and no second launch.
+// Operands go straight to registers (the lane's 16 weight bytes and 32
+// activation bytes of a window are what its MFMAs use), D windows in flight
+// per wavefront; windows past a split's end load out of range (zeros) and
+// add exact zeros.  WPS > 0: the window count per split is WPS (checked on
+// the host) and the window sequence is straight-line code, so each window
+// waits only for its own loads; WPS = 0: a loop over groups of D windows.
+template <int R, int C, int D, int WPS, bool FP8>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void w8a16_wsplit_kernel(
+    LinearParams p) {
+  __shared__ __attribute__((aligned(16))) f32x4 red[8][R * C][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = split index (wavefront-uniform)
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int per_xcd = (tiles + kLinXcds - 1) / kLinXcds;
+  const int item = (blockIdx.x % kLinXcds) * per_xcd + blockIdx.x / kLinXcds;
+  if (item >= tiles) return;
+  const int tn = item % p.tiles_n;
+  const int tm = item / p.tiles_n;
+
+  const int wins = p.k / kWin;
+  const int w_begin = wave * p.win_per_split;
+  const int w_end = min(wins, w_begin + p.win_per_split);
+  const int strips = p.n >> 4;
+  const int strip0 = tn * R;
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+
+  // int8 format: the lane's 4 channel scales, loaded ahead of the weight stream
+  u32x2 sv[R];
+  if constexpr (!FP8) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      sv[r] = *reinterpret_cast<const u32x2*>(p.ws + min(strip0 + r, strips - 1) * 16 + 4 * j);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  uint32_t srow[4] = {0, 0, 0, 0};
+  if constexpr (FP8) {
+    const uint8_t* row = p.ws8 + (int64_t)(min(strip0, strips - 1) >> 3) * p.kblocks;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (64 * q + lane < p.kblocks) srow[q] = row[64 * q + lane];
+  }
+
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.a, (short)0, (int)(p.m * p.k * 2), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wq, (short)0, (int)((int64_t)p.n * p.k), kLinRsrcFlags);
+  const int wstep = weight_window_step(p.w_rowmajor);
+  uint32_t w_off[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    w_off[r] = strip0 + r < strips ? weight_lane_offset(p.w_rowmajor, strip0 + r, lane, p.k, wins) : kLinOob;
+  // lane's 32 activation bytes of a window: token tm*16C + 16c + n16, K 16j .. 16j+15
+  uint32_t a_off[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int64_t tok = (int64_t)tm * 16 * C + c * 16 + n16;
+    a_off[c] = tok < p.m ? (uint32_t)(tok * p.k * 2 + j * 32) : kLinOob;
+  }
+
+  u32x4 wr[D][R];
+  u32x4 ar[D][C][2];
+  // a window past the split's end reads at kLinOob + (small) soffset: out of range, zeros
+  auto load = [&](int win, int t) {
+    const bool in = win < w_end;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      wr[t][r] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, in ? w_off[r] : kLinOob, win * wstep, 0));
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const uint32_t off = in ? a_off[c] : kLinOob;
+      ar[t][c][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, win * 128, 0));
+      ar[t][c][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, win * 128 + 16, 0));
+    }
+  };
+
+  f32x4 acc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto consume = [&](int win, int t) {
+    float bscale = 0.0f;
+    if constexpr (FP8) {
+      const int kb = min(win, wins - 1) >> 1;
+      const uint32_t word = kb < 64 ? srow[0] : (kb < 128 ? srow[1] : (kb < 192 ? srow[2] : srow[3]));
+      bscale = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)word, kb & 63) << 23);
+    }
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      bf16x8 a[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if constexpr (FP8)
+          a[r] = dequant_fp8x8(wr[t][r][2 * d], wr[t][r][2 * d + 1], bscale);
+        else
+          a[r] = dequant_i8x8(wr[t][r][2 * d], wr[t][r][2 * d + 1]);
+      }
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const bf16x8 b = __builtin_bit_cast(bf16x8, ar[t][c][d]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][c] = mfma_bf16(a[r], b, acc[r][c]);
+      }
+    }
+  };
+
+  // sched_barrier keeps each group of loads where it stands: the scheduler
+  // would otherwise sink loads toward their uses and shrink the ring
+  if constexpr (WPS > 0) {
+    constexpr int kDepth = D < WPS ? D : WPS;
+#pragma unroll
+    for (int t = 0; t < kDepth; ++t) load(w_begin + t, t);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < WPS; ++i) {
+      consume(w_begin + i, i % kDepth);
+      if (i + kDepth < WPS) load(w_begin + i + kDepth, i % kDepth);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < D; ++t) load(w_begin + t, t);
+    for (int i = 0; i < p.win_per_split; i += D) {
+#pragma unroll
+      for (int t = 0; t < D; ++t) {
+        consume(w_begin + i + t, t);
+        load(w_begin + i + t + D, t);
+      }
+    }
+  }
+
+  // this split's scaled partial: lane holds channels 16*strip + 4*j + (0..3) of token c*16 + n16
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float sc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if constexpr (!FP8) {
+      sc[0] = __uint_as_float(sv[r][0] << 16);
+      sc[1] = __uint_as_float(sv[r][0] & 0xFFFF0000u);
+      sc[2] = __uint_as_float(sv[r][1] << 16);
+      sc[3] = __uint_as_float(sv[r][1] & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      red[wave][r * C + c][lane] = f32x4{acc[r][c][0] * sc[0], acc[r][c][1] * sc[1], acc[r][c][2] * sc[2],
+                                         acc[r][c][3] * sc[3]};
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < R * C * 64; q += blockDim.x) {
+    const int rc = q >> 6, l = q & 63;
+    const int r = rc / C, c = rc % C;
+    const int strip = strip0 + r;
+    const int64_t tok = (int64_t)tm * 16 * C + c * 16 + (l & 15);
+    if (strip >= strips || tok >= p.m) continue;
+    f32x4 sum = red[0][rc][l];
+    for (int w = 1; w < p.split; ++w) {
+      const f32x4 v = red[w][rc][l];
+      sum[0] += v[0];
+      sum[1] += v[1];
+      sum[2] += v[2];
+      sum[3] += v[3];
+    }
+    const float v[4] = {sum[0], sum[1], sum[2], sum[3]};
+    uint16_t* dst = p.out + tok * p.n + strip * 16 + 4 * (l >> 4);
+    *reinterpret_cast<u32x2*>(dst) = finish_bf16x4(v, dst, p.accumulate != 0);
+  }
+}
+
 // The same tile for 64 or more tokens (C >= 4), with the copies as inline
 // asm into a three-buffer ring two windows ahead and one explicit wait per
 // window (the compiler-visible copies of w8a16_kernel make every ds_read
@@ -1154,6 +1332,35 @@ static void launch_w8a8_block_kernel(const BlockFp8Params& p, int r, int c, hipS
   else hipLaunchKernelGGL((w8a8_block_kernel<2, 4>), grid, dim3(256), 0, stream, p);
 }
 
+// The in-workgroup split (w8a16_wsplit_kernel) for up to 16 tokens and 2..8
+// splits, 16 channels per workgroup.  (17..64 tokens keep the split
+// workgroups and the reduce launch: there the in-workgroup split measured
+// 40-60% slower -- each wavefront re-reads its activations, no LDS sharing.)
+static bool wsplit_geometry(int64_t m, int split, int* r, int* c) {
+  if (m > 16 || split < 2 || split > 8) return false;
+  *c = m <= 16 ? 1 : (m <= 32 ? 2 : 4);
+  *r = m <= 16 ? 1 : 2;
+  return true;
+}
+
+template <bool FP8>
+static void launch_w8a16_wsplit(const LinearParams& p, int r, int c, hipStream_t stream) {
+  const int tiles = p.tiles_m * p.tiles_n;
+  const dim3 grid((unsigned)(((tiles + kLinXcds - 1) / kLinXcds) * kLinXcds));
+  const dim3 block((unsigned)(64 * p.split));
+  const int wps = p.win_per_split;
+  if (c == 1) {
+    if (wps == 8) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 8, FP8>), grid, block, 0, stream, p);
+    else if (wps == 16) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 16, FP8>), grid, block, 0, stream, p);
+    else if (wps == 32) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 32, FP8>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 0, FP8>), grid, block, 0, stream, p);
+  } else if (c == 2) {
+    hipLaunchKernelGGL((w8a16_wsplit_kernel<2, 2, 4, 0, FP8>), grid, block, 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((w8a16_wsplit_kernel<2, 4, 2, 0, FP8>), grid, block, 0, stream, p);
+  }
+}
+
 template <bool FP8>
 static void launch_w8a16_kernel(const LinearParams& p, int r, int c, hipStream_t stream) {
   const int items = p.split * p.tiles_m * p.tiles_n;
@@ -1213,7 +1420,8 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
                       const uint16_t* ws, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
                       hipStream_t stream, int accumulate, int w_rowmajor) {
   int r, c;
-  w8a16_geometry(m, n, &r, &c);
+  const bool wsplit = wsplit_geometry(m, split, &r, &c);
+  if (!wsplit) w8a16_geometry(m, n, &r, &c);
   LinearParams p;
   p.a = a;
   p.m = m;
@@ -1226,12 +1434,21 @@ int dsv4_launch_w8a16(const uint16_t* a, int64_t m, int64_t n, int64_t k, const 
   p.split = split;
   const int wins = (int)(k / kWin);
   p.win_per_split = (wins + split - 1) / split;
-  p.tiles_n = (int)((n + 64 * r - 1) / (64 * r));
+  const int tile_n = wsplit ? 16 * r : 64 * r;
+  p.tiles_n = (int)((n + tile_n - 1) / tile_n);
   p.tiles_m = (int)((m + 16 * c - 1) / (16 * c));
   p.out = out;
   p.partial = workspace;
   p.accumulate = accumulate;
   p.w_rowmajor = w_rowmajor;
+  if (wsplit) {
+    if (ws8 != nullptr)
+      launch_w8a16_wsplit<true>(p, r, c, stream);
+    else
+      launch_w8a16_wsplit<false>(p, r, c, stream);
+    DSV4_CHECK_LAUNCH("w8a16_wsplit_kernel");
+    return DSV4MOE_OK;
+  }
   if (ws8 != nullptr)
     launch_w8a16_kernel<true>(p, r, c, stream);
   else

@@ -119,3 +119,35 @@ def test_prefill_tile_with_explicit_split():
 
     rows = np.sort(np.random.default_rng(7).choice(8192, 64, replace=False))
     run(8192, 4096, 4096, split=2, rows=rows)
+
+
+@pytest.mark.parametrize("m,n,k,split", [(1, 4096, 4096, 8), (5, 1024, 4096, 4), (16, 4096, 4096, 2),
+                                         (24, 1024, 4096, 8), (33, 4096, 4096, 4), (64, 1024, 4096, 8),
+                                         (64, 16384, 4096, 4), (3, 208, 640, 4), (40, 208, 640, 4)])
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_in_workgroup_split_matches_two_launch_reduction(m, n, k, split, fmt):
+    """Up to 64 tokens a K split runs inside one workgroup (each wavefront
+    one split's partial, summed through LDS in split order); above 64 the
+    partials go through the workspace and a reduce launch.  A row of C
+    depends only on its row of A, and the split boundaries are the same, so
+    the first m rows of a 128-token call with the same split must carry the
+    same bits -- which pins the in-workgroup order of the additions.  Ragged
+    N and a last split shorter than the others included (K=640: 10 windows
+    over 4 splits of 3)."""
+
+    print(f"[w8a16 {fmt}] in-workgroup split M={m} N={n} K={k} split={split}", flush=True)
+    gen = torch.Generator(DEV).manual_seed(m * 7 + split)
+    a = torch.randn((128, k), device=DEV, generator=gen).to(torch.bfloat16)
+    if fmt == "fp8":
+        codes, scales = S.make_fp8_block_linear(n, k, seed=31, device=DEV)
+        w, w_s = codes.view(torch.float8_e4m3fn), scales.view(torch.float8_e8m0fnu)
+        prep = L.prepare_fp8_block_weight(codes, scales)
+    else:
+        w, w_s = S.make_int8_linear(n, k, seed=31, device=DEV)
+        prep = L.prepare_int8_weight(w, w_s)
+    small = L.w8a16_linear(a[:m].contiguous(), w, w_s, split_k=split)
+    small_tiled = L.w8a16_linear(a[:m].contiguous(), prep, split_k=split)
+    big = L.w8a16_linear(a, w, w_s, split_k=split)
+    torch.cuda.synchronize()
+    assert torch.equal(small.view(torch.int16), small_tiled.view(torch.int16))
+    assert torch.equal(small.view(torch.int16), big[:m].view(torch.int16))
