@@ -408,8 +408,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   if constexpr (WPS > 0) {
     constexpr int kDepth = D < WPS ? D : WPS;
 #pragma unroll
-    for (int t = 0; t < kDepth; ++t) load(w_begin + t, t);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int t = 0; t < kDepth; ++t) {
+      load(w_begin + t, t);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int i = 0; i < WPS; ++i) {
       consume(w_begin + i, i % kDepth);
@@ -1147,6 +1149,129 @@ __global__ __launch_bounds__(256, 2) void w8a8_block_kernel(BlockFp8Params p) {
   }
 }
 
+// Up to 16 tokens with a K split: the split runs inside the workgroup, as in
+// w8a16_wsplit_kernel.  Workgroup tile: one 16-channel strip x 16 tokens;
+// wavefront w of the `split` wavefronts runs split w's K blocks [w * kbps,
+// min(kblocks, (w + 1) * kbps)) -- the MFMA chain of a split workgroup of
+// w8a8_block_kernel -- and the workgroup sums the partials through LDS in
+// split order, the additions of split_reduce_kernel: the same bits as the
+// two-launch path for the same split.  Per K block a lane loads its two
+// 16-byte weight parts, its token's two 16-byte parts and its token's E8M0
+// byte straight to registers, D blocks in flight; blocks past a split's end
+// load out of range (zeros, and a zero scale byte, 2^-127, times zero).
+// KPS > 0: KPS blocks per split (checked on the host), straight-line code.
+template <int D, int KPS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void w8a8_wsplit_kernel(
+    BlockFp8Params p) {
+  __shared__ __attribute__((aligned(16))) f32x4 red[8][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = split index
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int per_xcd = (tiles + kLinXcds - 1) / kLinXcds;
+  const int item = (blockIdx.x % kLinXcds) * per_xcd + blockIdx.x / kLinXcds;
+  if (item >= tiles) return;
+  const int strip = item % p.tiles_n;
+  const int tm = item / p.tiles_n;
+
+  const int kb_begin = wave * p.kb_per_split;
+  const int kb_end = min(p.kblocks, kb_begin + p.kb_per_split);
+  const int wins = p.k / kWin;
+  const int strips = p.n >> 4;
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+
+  // the strip's 128-row scale block: lane i holds the E8M0 bytes of K blocks i, 64 + i, 128 + i, 192 + i
+  uint32_t srow[4] = {0, 0, 0, 0};
+  {
+    const uint8_t* row = p.ws8 + (int64_t)(strip >> 3) * p.kblocks;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (64 * q + lane < p.kblocks) srow[q] = row[64 * q + lane];
+  }
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.a, (short)0, (int)(p.m * p.k), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.as, (short)0, (int)(p.m * p.kblocks), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wq, (short)0, (int)((int64_t)p.n * p.k), kLinRsrcFlags);
+  const int wstep = weight_window_step(p.w_rowmajor);
+  const uint32_t w_off = weight_lane_offset(p.w_rowmajor, strip, lane, p.k, wins);
+  const int64_t tok = (int64_t)tm * 16 + n16;
+  const uint32_t a_off = tok < p.m ? (uint32_t)(tok * p.k + j * 16) : kLinOob;
+  const uint32_t s_off = tok < p.m ? (uint32_t)(tok * p.kblocks) : kLinOob;
+
+  u32x4 wr[D][2];
+  u32x4 ar[D][2];
+  int st[D];
+  // a block past the split's end reads at kLinOob + (small) soffset: out of range, zeros
+  auto load = [&](int kb, int t) {
+    const bool in = kb < kb_end;
+    const uint32_t wo = in ? w_off : kLinOob;
+    const uint32_t ao = in ? a_off : kLinOob;
+    wr[t][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, wo, (2 * kb) * wstep, 0));
+    wr[t][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, wo, (2 * kb + 1) * wstep, 0));
+    ar[t][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ao, kb * 128, 0));
+    ar[t][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ao, kb * 128 + 64, 0));
+    st[t] = (int)__builtin_amdgcn_raw_buffer_load_b8(s_rsrc, in ? s_off : kLinOob, kb, 0);
+  };
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int kb, int t) {
+    const int kbc = min(kb, p.kblocks - 1);
+    const uint32_t word = kbc < 64 ? srow[0] : (kbc < 128 ? srow[1] : (kbc < 192 ? srow[2] : srow[3]));
+    const int sw = __builtin_amdgcn_readlane((int)word, kbc & 63);
+    const i32x8 wv = {(int)wr[t][0][0], (int)wr[t][0][1], (int)wr[t][0][2], (int)wr[t][0][3],
+                      (int)wr[t][1][0], (int)wr[t][1][1], (int)wr[t][1][2], (int)wr[t][1][3]};
+    const i32x8 tv = {(int)ar[t][0][0], (int)ar[t][0][1], (int)ar[t][0][2], (int)ar[t][0][3],
+                      (int)ar[t][1][0], (int)ar[t][1][1], (int)ar[t][1][2], (int)ar[t][1][3]};
+    acc = mfma_fp8_block(wv, tv, acc, sw, st[t]);
+  };
+
+  // sched_barrier keeps each group of loads where it stands (see w8a16_wsplit_kernel)
+  if constexpr (KPS > 0) {
+    constexpr int kDepth = D < KPS ? D : KPS;
+#pragma unroll
+    for (int t = 0; t < kDepth; ++t) {
+      load(kb_begin + t, t);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = 0; i < KPS; ++i) {
+      consume(kb_begin + i, i % kDepth);
+      if (i + kDepth < KPS) load(kb_begin + i + kDepth, i % kDepth);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < D; ++t) load(kb_begin + t, t);
+    for (int i = 0; i < p.kb_per_split; i += D) {
+#pragma unroll
+      for (int t = 0; t < D; ++t) {
+        consume(kb_begin + i + t, t);
+        load(kb_begin + i + t + D, t);
+      }
+    }
+  }
+
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int64_t t = (int64_t)tm * 16 + n16;
+    if (t < p.m && strip < strips) {
+      f32x4 sum = red[0][lane];
+      for (int w = 1; w < p.split; ++w) {
+        const f32x4 v = red[w][lane];
+        sum[0] += v[0];
+        sum[1] += v[1];
+        sum[2] += v[2];
+        sum[3] += v[3];
+      }
+      const float v[4] = {sum[0], sum[1], sum[2], sum[3]};
+      uint16_t* dst = p.out + t * p.n + strip * 16 + 4 * j;
+      *reinterpret_cast<u32x2*>(dst) = finish_bf16x4(v, dst, false);
+    }
+  }
+}
+
 // Many tokens: a three-stage pipeline through LDS.  Per K block, inline-asm
 // buffer_load ... lds copies the token tile (16C rows x 128 B, part q of row t
 // at q ^ swz128(t)), each wavefront's R weight strips (2 KiB each) and the
@@ -1508,6 +1633,7 @@ int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, i
                                const uint8_t* wq, const uint8_t* ws8, int32_t split, float* workspace, uint16_t* out,
                                hipStream_t stream, int w_rowmajor) {
   int r, c;
+  const bool wsplit = m <= 16 && split >= 2 && split <= 8;
   w8a8_geometry(m, n, k, &r, &c);
   BlockFp8Params p;
   p.a = a;
@@ -1525,6 +1651,18 @@ int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, i
   p.out = out;
   p.partial = workspace;
   p.w_rowmajor = w_rowmajor;
+  if (wsplit) {  // one strip x 16 tokens per workgroup, the split inside it
+    p.tiles_n = (int)((n + 15) / 16);
+    p.tiles_m = (int)((m + 15) / 16);
+    const dim3 grid((unsigned)(((p.tiles_n * p.tiles_m + kLinXcds - 1) / kLinXcds) * kLinXcds));
+    const dim3 block((unsigned)(64 * split));
+    if (p.kb_per_split == 4) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 4>), grid, block, 0, stream, p);
+    else if (p.kb_per_split == 8) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 8>), grid, block, 0, stream, p);
+    else if (p.kb_per_split == 16) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 16>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((w8a8_wsplit_kernel<4, 0>), grid, block, 0, stream, p);
+    DSV4_CHECK_LAUNCH("w8a8_wsplit_kernel");
+    return DSV4MOE_OK;
+  }
   launch_w8a8_block_kernel(p, r, c, stream);
   DSV4_CHECK_LAUNCH("w8a8_block_kernel");
   if (split > 1) {

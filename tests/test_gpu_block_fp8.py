@@ -172,3 +172,28 @@ def test_prefill_kernel_with_explicit_split(split):
 
     rows = np.sort(np.random.default_rng(split).choice(8192, 64, replace=False))
     run(8192, 4096, 4096, split=split, rows=rows)
+
+
+@pytest.mark.parametrize("m,n,k,split", [(1, 4096, 4096, 8), (7, 1024, 4096, 8), (16, 16384, 4096, 4),
+                                         (3, 4096, 4096, 2), (5, 208, 640, 2), (9, 208, 1024, 4)])
+def test_in_workgroup_split_matches_two_launch_reduction(m, n, k, split):
+    """Up to 16 tokens a K split runs inside one workgroup (each wavefront
+    one split's K blocks, the partials summed through LDS in split order);
+    from 17 tokens the split workgroups write partials that a reduce launch
+    sums.  Rows of C depend only on their row of A and the split boundaries
+    are the same, so the first m rows of a 40-token call with the same split
+    must carry the same bits.  Ragged N (N=208: the last 128-row scale
+    block partial) and a last split with fewer blocks (K=640: 5 blocks over
+    2 splits of 3) included."""
+
+    print(f"[block fp8] in-workgroup split M={m} N={n} K={k} split={split}", flush=True)
+    codes, scales = S.make_fp8_block_linear(n, k, seed=41, device=DEV)
+    prep = L.prepare_fp8_block_weight(codes, scales)
+    x = torch.randn((40, k), device=DEV, generator=torch.Generator(DEV).manual_seed(m + 100 * split))
+    q, s = quant(x.to(torch.bfloat16))
+    small = gemm(q[:m].contiguous(), s[:m].contiguous(), prep, split)
+    small_raw = gemm(q[:m].contiguous(), s[:m].contiguous(), prep, split, raw=codes)
+    big = gemm(q, s, prep, split)
+    torch.cuda.synchronize()
+    assert torch.equal(small.view(torch.int16), small_raw.view(torch.int16))
+    assert torch.equal(small.view(torch.int16), big[:m].view(torch.int16))
