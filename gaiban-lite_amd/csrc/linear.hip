@@ -300,10 +300,17 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
 // add exact zeros.  WPS > 0: the window count per split is WPS (checked on
 // the host) and the window sequence is straight-line code, so each window
 // waits only for its own loads; WPS = 0: a loop over groups of D windows.
-template <int R, int C, int D, int WPS, bool FP8>
+// LDS_ACT (C = 1, WPS > 0, splits covering K exactly, M*K*2 <= 32 KiB):
+// each wavefront first copies its split's activation rows (the M valid
+// tokens, WPS*128 bytes each) into LDS with 1 KiB DMAs, every lane useful,
+// and the MFMA operands come from there -- lanes of padding tokens read 32
+// zero bytes -- instead of two 16-byte loads per window in which only the
+// lanes of valid tokens fetch anything.
+template <int R, int C, int D, int WPS, bool FP8, bool LDS_ACT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void w8a16_wsplit_kernel(
     LinearParams p) {
   __shared__ __attribute__((aligned(16))) f32x4 red[8][R * C][64];
+  extern __shared__ __attribute__((aligned(16))) uint8_t act_lds[];  // LDS_ACT: [split][M][WPS*128], [split][32] zeros
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = split index (wavefront-uniform)
   const int tiles = p.tiles_m * p.tiles_n;
@@ -354,6 +361,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     a_off[c] = tok < p.m ? (uint32_t)(tok * p.k * 2 + j * 32) : kLinOob;
   }
 
+  // LDS_ACT: this wavefront's rows, and the lane's read address for window w_begin
+  constexpr int kRowBytes = WPS * 128;
+  const uint8_t* act_row = nullptr;
+  if constexpr (LDS_ACT) {
+    static_assert(C == 1 && WPS > 0 && kRowBytes % 1024 == 0, "LDS activations: one token tile, whole KiB rows");
+    const int m = (int)p.m;
+    uint8_t* mine = act_lds + wave * m * kRowBytes;
+    uint8_t* zeros = act_lds + p.split * m * kRowBytes + wave * 32;  // this wavefront's own: no barrier needed
+    if (lane < 2) *reinterpret_cast<u32x4*>(zeros + 16 * lane) = u32x4{0, 0, 0, 0};
+    for (int row = 0; row < m; ++row)
+#pragma unroll
+      for (int q = 0; q < kRowBytes / 1024; ++q)
+        lds_dma16(a_rsrc, (lds_void_ptr)(mine + row * kRowBytes + q * 1024),
+                  (uint32_t)(row * p.k * 2 + w_begin * 128 + lane * 16), q * 1024);
+    act_row = n16 < m ? mine + n16 * kRowBytes + 32 * j : zeros;
+  }
+
   u32x4 wr[D][R];
   u32x4 ar[D][C][2];
   // a window past the split's end reads at kLinOob + (small) soffset: out of range, zeros
@@ -363,11 +387,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     for (int r = 0; r < R; ++r)
       wr[t][r] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, in ? w_off[r] : kLinOob, win * wstep, 0));
+    if constexpr (!LDS_ACT) {
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const uint32_t off = in ? a_off[c] : kLinOob;
-      ar[t][c][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, win * 128, 0));
-      ar[t][c][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, win * 128 + 16, 0));
+      for (int c = 0; c < C; ++c) {
+        const uint32_t off = in ? a_off[c] : kLinOob;
+        ar[t][c][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, win * 128, 0));
+        ar[t][c][1] =
+            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, win * 128 + 16, 0));
+      }
     }
   };
 
@@ -396,7 +423,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       }
 #pragma unroll
       for (int c = 0; c < C; ++c) {
-        const bf16x8 b = __builtin_bit_cast(bf16x8, ar[t][c][d]);
+        bf16x8 b;
+        if constexpr (LDS_ACT) {
+          // padding lanes all read the zero block (one address: a broadcast)
+          const int step = n16 < (int)p.m ? (win - w_begin) * 128 : 0;
+          b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(act_row + step + 16 * d));
+        } else {
+          b = __builtin_bit_cast(bf16x8, ar[t][c][d]);
+        }
 #pragma unroll
         for (int r = 0; r < R; ++r) acc[r][c] = mfma_bf16(a[r], b, acc[r][c]);
       }
@@ -1160,10 +1194,15 @@ __global__ __launch_bounds__(256, 2) void w8a8_block_kernel(BlockFp8Params p) {
 // byte straight to registers, D blocks in flight; blocks past a split's end
 // load out of range (zeros, and a zero scale byte, 2^-127, times zero).
 // KPS > 0: KPS blocks per split (checked on the host), straight-line code.
-template <int D, int KPS>
+// LDS_ACT (KPS > 0, splits covering K exactly, up to 4 tokens): the split's
+// activation rows (KPS*128 bytes each, rows padded to whole KiB) are copied
+// into LDS with 1 KiB DMAs first and the MFMA operands read from there, as in
+// w8a16_wsplit_kernel.
+template <int D, int KPS, bool LDS_ACT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void w8a8_wsplit_kernel(
     BlockFp8Params p) {
   __shared__ __attribute__((aligned(16))) f32x4 red[8][64];
+  extern __shared__ __attribute__((aligned(16))) uint8_t act_lds[];  // LDS_ACT: [split][M][stride], [split][32] zeros
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // = split index
   const int tiles = p.tiles_m * p.tiles_n;
@@ -1200,6 +1239,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   const uint32_t a_off = tok < p.m ? (uint32_t)(tok * p.k + j * 16) : kLinOob;
   const uint32_t s_off = tok < p.m ? (uint32_t)(tok * p.kblocks) : kLinOob;
 
+  constexpr int kRowBytes = KPS * 128;
+  constexpr int kRowStride = (kRowBytes + 1023) / 1024 * 1024;
+  const uint8_t* act_row = nullptr;
+  if constexpr (LDS_ACT) {
+    static_assert(KPS > 0, "LDS activations need a fixed block count per split");
+    const int m = (int)p.m;
+    uint8_t* mine = act_lds + wave * m * kRowStride;
+    uint8_t* zeros = act_lds + p.split * m * kRowStride + wave * 32;  // this wavefront's own: no barrier needed
+    if (lane < 2) *reinterpret_cast<u32x4*>(zeros + 16 * lane) = u32x4{0, 0, 0, 0};
+    for (int row = 0; row < m; ++row)
+#pragma unroll
+      for (int q = 0; q < kRowStride / 1024; ++q) {
+        const int byte = q * 1024 + lane * 16;  // padding past the row copies zeros
+        lds_dma16(a_rsrc, (lds_void_ptr)(mine + row * kRowStride + q * 1024),
+                  byte < kRowBytes ? (uint32_t)(row * p.k + kb_begin * 128 + byte) : kLinOob, 0);
+      }
+    act_row = n16 < m ? mine + n16 * kRowStride + 16 * j : zeros;
+  }
+
   u32x4 wr[D][2];
   u32x4 ar[D][2];
   int st[D];
@@ -1210,8 +1268,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const uint32_t ao = in ? a_off : kLinOob;
     wr[t][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, wo, (2 * kb) * wstep, 0));
     wr[t][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, wo, (2 * kb + 1) * wstep, 0));
-    ar[t][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ao, kb * 128, 0));
-    ar[t][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ao, kb * 128 + 64, 0));
+    if constexpr (!LDS_ACT) {
+      ar[t][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ao, kb * 128, 0));
+      ar[t][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, ao, kb * 128 + 64, 0));
+    }
     st[t] = (int)__builtin_amdgcn_raw_buffer_load_b8(s_rsrc, in ? s_off : kLinOob, kb, 0);
   };
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1221,8 +1281,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int sw = __builtin_amdgcn_readlane((int)word, kbc & 63);
     const i32x8 wv = {(int)wr[t][0][0], (int)wr[t][0][1], (int)wr[t][0][2], (int)wr[t][0][3],
                       (int)wr[t][1][0], (int)wr[t][1][1], (int)wr[t][1][2], (int)wr[t][1][3]};
-    const i32x8 tv = {(int)ar[t][0][0], (int)ar[t][0][1], (int)ar[t][0][2], (int)ar[t][0][3],
-                      (int)ar[t][1][0], (int)ar[t][1][1], (int)ar[t][1][2], (int)ar[t][1][3]};
+    u32x4 lo, hi;
+    if constexpr (LDS_ACT) {
+      // padding lanes all read the zero block (one address: a broadcast)
+      const int step = n16 < (int)p.m ? (kb - kb_begin) * 128 : 0;
+      lo = *reinterpret_cast<const u32x4*>(act_row + step);
+      hi = *reinterpret_cast<const u32x4*>(act_row + step + (n16 < (int)p.m ? 64 : 16));
+    } else {
+      lo = ar[t][0];
+      hi = ar[t][1];
+    }
+    const i32x8 tv = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     acc = mfma_fp8_block(wv, tv, acc, sw, st[t]);
   };
 
@@ -1474,15 +1543,25 @@ static void launch_w8a16_wsplit(const LinearParams& p, int r, int c, hipStream_t
   const dim3 grid((unsigned)(((tiles + kLinXcds - 1) / kLinXcds) * kLinXcds));
   const dim3 block((unsigned)(64 * p.split));
   const int wps = p.win_per_split;
-  if (c == 1) {
-    if (wps == 8) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 8, FP8>), grid, block, 0, stream, p);
-    else if (wps == 16) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 16, FP8>), grid, block, 0, stream, p);
-    else if (wps == 32) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 32, FP8>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 0, FP8>), grid, block, 0, stream, p);
+  // activation rows through LDS: up to 4 tokens, splits covering K exactly, at most 32 KiB
+  const bool lds = p.m <= 4 && wps * p.split == p.k / kWin && p.m * p.k * 2 <= 32768;
+  const size_t lds_bytes = lds ? (size_t)(p.m * p.k * 2 + 32 * p.split) : 0;
+  if (c == 1 && lds) {
+    if (wps == 8) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 8, FP8, true>), grid, block, lds_bytes, stream, p);
+    else if (wps == 16)
+      hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 16, FP8, true>), grid, block, lds_bytes, stream, p);
+    else if (wps == 32)
+      hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 32, FP8, true>), grid, block, lds_bytes, stream, p);
+    else hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 0, FP8, false>), grid, block, 0, stream, p);
+  } else if (c == 1) {
+    if (wps == 8) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 8, FP8, false>), grid, block, 0, stream, p);
+    else if (wps == 16) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 16, FP8, false>), grid, block, 0, stream, p);
+    else if (wps == 32) hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 32, FP8, false>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((w8a16_wsplit_kernel<1, 1, 8, 0, FP8, false>), grid, block, 0, stream, p);
   } else if (c == 2) {
-    hipLaunchKernelGGL((w8a16_wsplit_kernel<2, 2, 4, 0, FP8>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((w8a16_wsplit_kernel<2, 2, 4, 0, FP8, false>), grid, block, 0, stream, p);
   } else {
-    hipLaunchKernelGGL((w8a16_wsplit_kernel<2, 4, 2, 0, FP8>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((w8a16_wsplit_kernel<2, 4, 2, 0, FP8, false>), grid, block, 0, stream, p);
   }
 }
 
@@ -1519,6 +1598,15 @@ int32_t dsv4_w8a16_split_k(int64_t m, int64_t n, int64_t k) {
   w8a16_geometry(m, n, &r, &c);
   const int64_t tiles = ((n + 64 * r - 1) / (64 * r)) * ((m + 16 * c - 1) / (16 * c));
   const int64_t wins = k / kWin;
+  if (m <= 16) {
+    // the in-workgroup split: 4 wavefronts, 8 from N = 8192 (K = 4096, M = 1..16:
+    // N = 1024/4096 fastest at 4, N = 16384 at 8 -- the tiled weights 14.4 -> 11.7 us),
+    // at least 4 windows each
+    if (wins < 2) return 1;
+    int split = n >= 8192 ? 8 : 4;
+    while (split > 2 && wins / split < 4) split /= 2;
+    return split;
+  }
   int split = 1;
   // widen over K until about two workgroups per CU, keeping >= 4 windows per
   // split, at most 8 splits (16 measured slower at M = 1..64: the partial sums
@@ -1610,6 +1698,14 @@ int32_t dsv4_block_fp8_split_k(int64_t m, int64_t n, int64_t k) {
   w8a8_geometry(m, n, k, &r, &c);
   const int64_t tiles = ((n + 64 * r - 1) / (64 * r)) * ((m + 16 * c - 1) / (16 * c));
   const int64_t kblocks = k / 128;
+  if (m <= 16) {
+    // the in-workgroup split, as for W8A16: 4 wavefronts, 8 from N = 8192 (K = 4096:
+    // N = 16384 tiled 13.9 -> 11.1 us at 8), at least 2 K blocks each
+    if (kblocks < 2) return 1;
+    int split = n >= 8192 ? 8 : 4;
+    while (split > 2 && kblocks / split < 2) split /= 2;
+    return split;
+  }
   int split = 1;
   while (split < 8 && tiles * split < 512 && kblocks / (split * 2) >= 2) split *= 2;
   return split;
@@ -1656,10 +1752,19 @@ int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, i
     p.tiles_m = (int)((m + 15) / 16);
     const dim3 grid((unsigned)(((p.tiles_n * p.tiles_m + kLinXcds - 1) / kLinXcds) * kLinXcds));
     const dim3 block((unsigned)(64 * split));
-    if (p.kb_per_split == 4) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 4>), grid, block, 0, stream, p);
-    else if (p.kb_per_split == 8) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 8>), grid, block, 0, stream, p);
-    else if (p.kb_per_split == 16) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 16>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((w8a8_wsplit_kernel<4, 0>), grid, block, 0, stream, p);
+    const int kbps = p.kb_per_split;
+    const int stride = (kbps * 128 + 1023) / 1024 * 1024;
+    // activation rows through LDS: up to 4 tokens, splits covering K exactly, at most 32 KiB
+    const bool lds = m <= 4 && kbps * split == p.kblocks && split * m * stride <= 32768;
+    const size_t lds_bytes = lds ? (size_t)(split * m * stride + 32 * split) : 0;
+    if (lds && kbps == 4) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 4, true>), grid, block, lds_bytes, stream, p);
+    else if (lds && kbps == 8) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 8, true>), grid, block, lds_bytes, stream, p);
+    else if (lds && kbps == 16)
+      hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 16, true>), grid, block, lds_bytes, stream, p);
+    else if (kbps == 4) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 4, false>), grid, block, 0, stream, p);
+    else if (kbps == 8) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 8, false>), grid, block, 0, stream, p);
+    else if (kbps == 16) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 16, false>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((w8a8_wsplit_kernel<4, 0, false>), grid, block, 0, stream, p);
     DSV4_CHECK_LAUNCH("w8a8_wsplit_kernel");
     return DSV4MOE_OK;
   }

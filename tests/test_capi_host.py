@@ -121,15 +121,18 @@ def test_w8a16_validation_and_split_policy():
     for layout in (_lib.WEIGHT_TILED, _lib.WEIGHT_ROWMAJOR):
         assert lib.dsv4moe_w8a16_linear(fake, 0, 64, 4096, fake, layout, fake, 1, None, 0, fake,
                                         None) == _lib.DSV4MOE_OK
-    # this library's policy: a power of two in [1, 8] leaving >= 4 windows of 64 K per split,
-    # raised only while the grid is below 512 workgroups
+    # this library's policy: a power of two in [1, 8] leaving >= 4 windows of 64 K per split;
+    # up to 16 tokens (the split inside the workgroup) 4, or 8 from N = 8192; above, raised only
+    # while the grid is below 512 workgroups
     for m in (1, 16, 17, 64, 65, 8192):
         for n in (1024, 4096, 16384):
             split = lib.dsv4moe_w8a16_split_k(m, n, 4096)
             assert split in (1, 2, 4, 8)
             assert 4096 // 64 // split >= 4
+            if m <= 16:
+                assert split == (8 if n >= 8192 else 4)
+    assert lib.dsv4moe_w8a16_split_k(1, 4096, 512) == 2  # 8 windows: 2 splits of 4
     assert lib.dsv4moe_w8a16_split_k(8192, 4096, 4096) == 1
-    assert lib.dsv4moe_w8a16_split_k(1, 4096, 4096) > 1
     assert lib.dsv4moe_w8a16_split_k(0, 4096, 4096) == -1
 
 
@@ -148,14 +151,16 @@ def test_block_fp8_validation_and_split_policy():
     assert "x_dtype" in _einval("dsv4moe_act_quant_block_fp8", fake, 3, 4, 128, fake, fake, None)
     assert "multiple of 128" in _einval("dsv4moe_act_quant_block_fp8", fake, 0, 4, 100, fake, fake, None)
     assert lib.dsv4moe_block_fp8_gemm(*g(0, 64, 4096, 1, 0)) == _lib.DSV4MOE_OK
-    # this library's split: a power of two in [1, 8] leaving >= 2 K blocks per split,
-    # raised only while the grid is below 512 workgroups
+    # this library's split: a power of two in [1, 8] leaving >= 2 K blocks per split; up to 16
+    # tokens 4, or 8 from N = 8192; above, raised only while the grid is below 512 workgroups
     for m in (1, 16, 17, 64, 65, 8192):
         for n in (1024, 4096, 16384):
             split = lib.dsv4moe_block_fp8_split_k(m, n, 4096)
             assert split in (1, 2, 4, 8) and 32 // split >= 2
+            if m <= 16:
+                assert split == (8 if n >= 8192 else 4)
+    assert lib.dsv4moe_block_fp8_split_k(1, 16384, 512) == 2  # 4 K blocks: 2 splits of 2
     assert lib.dsv4moe_block_fp8_split_k(8192, 4096, 4096) == 1
-    assert lib.dsv4moe_block_fp8_split_k(1, 4096, 4096) == 8
     assert lib.dsv4moe_block_fp8_split_k(0, 4096, 4096) == -1
 
 

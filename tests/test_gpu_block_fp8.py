@@ -174,17 +174,20 @@ def test_prefill_kernel_with_explicit_split(split):
     run(8192, 4096, 4096, split=split, rows=rows)
 
 
-@pytest.mark.parametrize("m,n,k,split", [(1, 4096, 4096, 8), (7, 1024, 4096, 8), (16, 16384, 4096, 4),
-                                         (3, 4096, 4096, 2), (5, 208, 640, 2), (9, 208, 1024, 4)])
+@pytest.mark.parametrize("m,n,k,split", [(1, 4096, 4096, 8), (2, 1024, 4096, 4), (4, 16384, 1024, 2),
+                                         (7, 1024, 4096, 8), (16, 16384, 4096, 4), (3, 4096, 4096, 2),
+                                         (5, 208, 640, 2), (9, 208, 1024, 4)])
 def test_in_workgroup_split_matches_two_launch_reduction(m, n, k, split):
     """Up to 16 tokens a K split runs inside one workgroup (each wavefront
     one split's K blocks, the partials summed through LDS in split order);
     from 17 tokens the split workgroups write partials that a reduce launch
     sums.  Rows of C depend only on their row of A and the split boundaries
     are the same, so the first m rows of a 40-token call with the same split
-    must carry the same bits.  Ragged N (N=208: the last 128-row scale
-    block partial) and a last split with fewer blocks (K=640: 5 blocks over
-    2 splits of 3) included."""
+    must carry the same bits.  Up to 4 tokens with splits covering K
+    exactly the activation rows go through LDS (M=1..4 here, rows of 4, 8
+    and 16 blocks); ragged N (N=208: the last 128-row scale block partial)
+    and a last split with fewer blocks (K=640: 5 blocks over 2 splits of 3)
+    included."""
 
     print(f"[block fp8] in-workgroup split M={m} N={n} K={k} split={split}", flush=True)
     codes, scales = S.make_fp8_block_linear(n, k, seed=41, device=DEV)

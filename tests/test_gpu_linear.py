@@ -121,7 +121,8 @@ def test_prefill_tile_with_explicit_split():
     run(8192, 4096, 4096, split=2, rows=rows)
 
 
-@pytest.mark.parametrize("m,n,k,split", [(1, 4096, 4096, 8), (5, 1024, 4096, 4), (16, 4096, 4096, 2),
+@pytest.mark.parametrize("m,n,k,split", [(1, 4096, 4096, 8), (2, 1024, 4096, 2), (3, 16384, 4096, 4),
+                                         (4, 4096, 1024, 8), (5, 1024, 4096, 4), (16, 4096, 4096, 2),
                                          (24, 1024, 4096, 8), (33, 4096, 4096, 4), (64, 1024, 4096, 8),
                                          (64, 16384, 4096, 4), (3, 208, 640, 4), (40, 208, 640, 4)])
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])
@@ -131,9 +132,10 @@ def test_in_workgroup_split_matches_two_launch_reduction(m, n, k, split, fmt):
     partials go through the workspace and a reduce launch.  A row of C
     depends only on its row of A, and the split boundaries are the same, so
     the first m rows of a 128-token call with the same split must carry the
-    same bits -- which pins the in-workgroup order of the additions.  Ragged
-    N and a last split shorter than the others included (K=640: 10 windows
-    over 4 splits of 3)."""
+    same bits -- which pins the in-workgroup order of the additions.  Up to
+    4 tokens with splits covering K exactly the activation rows go through
+    LDS (M=1..4 here); ragged N and a last split shorter than the others
+    included (K=640: 10 windows over 4 splits of 3)."""
 
     print(f"[w8a16 {fmt}] in-workgroup split M={m} N={n} K={k} split={split}", flush=True)
     gen = torch.Generator(DEV).manual_seed(m * 7 + split)
