@@ -77,7 +77,8 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--profile-run", default=None, metavar="FMT:T:N[:graph]",
                     help="only run N layer calls (FMT int4|mxfp4|w4a8, T tokens) for rocprofv3 counter passes; "
-                         ":graph adds N replays of the captured call")
+                         ":graph adds N replays of the captured call; FMT linear-w8a8|linear-w8a16: N calls of "
+                         "the dense linear at M=T, K=4096, N in {4096, 16384} (tiled weights)")
     return ap.parse_args()
 
 
@@ -891,6 +892,44 @@ def cpu_baseline(pkg, w13, s13, w2, s2, seed):
     }
 
 
+def profile_run_linear(pkg, fmt: str, m: int, n: int, dev) -> int:
+    """The dense-linear programs of ``--profile-run``: N calls each at M=m,
+    K=4096, N in {4096, 16384}, on the load-time tiled weights (W8A8: the
+    block-FP8 GEMM after one activation quantisation; W8A16: int8 weights)."""
+
+    import torch
+
+    F, L, S = pkg.fp8_linear, pkg.weight_only_linear, pkg.synthetic
+    k = 4096
+    for cols in (4096, 16384):
+        if fmt == "linear-w8a8":
+            q, s = S.make_fp8_block_linear(cols, k, device=dev)
+            prep = L.prepare_fp8_block_weight(q, s)
+            x = S.make_hidden(m, k, seed=7000 + m, device=dev)
+            qp = F.make_quantization_plan(m, k)
+            aq = torch.empty(qp.quantized_shape, dtype=F.FP8_DTYPE, device=dev)
+            a_s = torch.empty(qp.scale_shape, dtype=F.E8M0_DTYPE, device=dev)
+            F.activation_quant_into(x, aq, a_s, plan=qp)
+            plan = F.make_gemm_plan(m, cols, k)
+            o = torch.empty(plan.output_shape, dtype=torch.bfloat16, device=dev)
+            ws = torch.empty(plan.workspace_shape, dtype=torch.float32, device=dev)
+            for _ in range(n):
+                F.block_fp8_gemm_into(aq, a_s, prep, None, o, ws, plan=plan)
+        else:
+            q, s = S.make_int8_linear(cols, k, device=dev)
+            prep = L.prepare_int8_weight(q, s)
+            a = S.make_hidden(m, k, seed=6000 + m, device=dev)
+            plan = L.make_gemm_plan(m, cols, k)
+            o = torch.empty(plan.output_shape, dtype=torch.bfloat16, device=dev)
+            ws = L.allocate_workspace(plan, dev)
+            for _ in range(n):
+                L.w8a16_prepared_gemm_into(a, prep, o, ws, plan=plan)
+        torch.cuda.synchronize()
+    print(json.dumps({"profile_run": f"{fmt}:{m}:{n}", "calls_per_shape": n, "shapes": ["N=4096", "N=16384"]}),
+          flush=True)
+    return 0
+
+
 def profile_run(pkg, spec: str, seed: int) -> int:
     """``--profile-run FMT:T:N[:graph]``: build the Flash layer in format FMT
     (int4, mxfp4 or w4a8), run one warm-up and N ``TP4MoE.forward_tensor``
@@ -909,6 +948,10 @@ def profile_run(pkg, spec: str, seed: int) -> int:
     graph_mode = len(parts) == 4
     S = pkg.synthetic
     dev = torch.device("cuda:0")
+    if fmt in ("linear-w8a8", "linear-w8a16"):
+        if graph_mode:
+            raise SystemExit("--profile-run: the dense linears run eager only")
+        return profile_run_linear(pkg, fmt, t, n, dev)
     shape = S.FLASH
     E, H, I, K = shape.experts, shape.hidden, shape.inter, shape.topk
     if fmt == "mxfp4":

@@ -387,9 +387,15 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
       const u32x4 b1 = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((2 * jg + 1) ^ swz128(row)) * 16]);
       bfr[ct] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
     }
-    float corr[C];
+    // the MFMA starts from -sum_g(xq) / 64 of the lane's token (its four
+    // outputs are four weight rows of one token), so one FMA per output
+    // applies the group scale: acc += s * (2^-9 sum(u * xq) - sum_g(xq) / 64)
+    f32x4 negcorr[C];
 #pragma unroll
-    for (int ct = 0; ct < C; ++ct) corr[ct] = xsum[u][ct * 16 + sw] * kInvSum;
+    for (int ct = 0; ct < C; ++ct) {
+      const float c = -xsum[u][ct * 16 + sw] * kInvSum;
+      negcorr[ct] = f32x4{c, c, c, c};
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const i32x8 a = spread_nibbles(*reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]));
@@ -398,11 +404,11 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
       scale4(sv, sc);
       f32x4 tmp[C];
 #pragma unroll
-      for (int ct = 0; ct < C; ++ct) tmp[ct] = mfma_fp8(a, bfr[ct], f32x4{0.f, 0.f, 0.f, 0.f});
+      for (int ct = 0; ct < C; ++ct) tmp[ct] = mfma_fp8(a, bfr[ct], negcorr[ct]);
 #pragma unroll
       for (int ct = 0; ct < C; ++ct)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[r][ct][i] += sc[i] * (tmp[ct][i] - corr[ct]);
+        for (int i = 0; i < 4; ++i) acc[r][ct][i] = __builtin_fmaf(sc[i], tmp[ct][i], acc[r][ct][i]);
     }
     if (issue2) wait_step();  // this wavefront's copies of group g + 1 have landed
     else lds_dma_wait_all();
