@@ -286,7 +286,170 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
   }
 }
 
-// Up to 64 tokens with a K split: the split runs inside the workgroup.
+// 17..64 tokens: the tile of w8a16_kernel (64*R channels x 16*C tokens over
+// one K split, the same partials, so the same bits), with each wavefront's
+// weights straight to registers, D windows in flight, and the workgroup's
+// token rows for the whole split copied into LDS first (DMAs issued before
+// any weight load, so the waits for them are exact) -- the LDS copies of the
+// weights, one or two windows deep, were what w8a16_kernel waited on.
+// WPS > 0: WPS windows per split, straight-line code; WPS*16*C*128 bytes of
+// LDS (<= 64 KiB, checked on the host).
+template <int R, int C, int D, int WPS, bool FP8>
+__global__ __launch_bounds__(256, 2) __attribute__((amdgpu_waves_per_eu(1, 2))) void w8a16_regw_kernel(
+    LinearParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t xs_all[];  // [WPS][16C rows][128 B]
+  constexpr int kRows = 16 * C;
+  constexpr int kWinBytes = kRows * 128;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int items = p.split * p.tiles_m * p.tiles_n;
+  const int per_xcd = (items + kLinXcds - 1) / kLinXcds;
+  const int item = (blockIdx.x % kLinXcds) * per_xcd + blockIdx.x / kLinXcds;
+  if (item >= items) return;
+  const int tn = item % p.tiles_n;
+  const int tm = (item / p.tiles_n) % p.tiles_m;
+  const int sp = item / (p.tiles_n * p.tiles_m);
+
+  const int wins = p.k / kWin;
+  const int w_begin = sp * WPS;
+  const int w_end = min(wins, w_begin + WPS);
+  const int strips = p.n >> 4;
+  const int strip0 = tn * 4 * R + wave * R;
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+
+  u32x2 sv[R];
+  if constexpr (!FP8) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      sv[r] = *reinterpret_cast<const u32x2*>(p.ws + min(strip0 + r, strips - 1) * 16 + 4 * j);
+  }
+  uint32_t srow[4] = {0, 0, 0, 0};
+  if constexpr (FP8) {
+    const uint8_t* row = p.ws8 + (int64_t)(min(strip0, strips - 1) >> 3) * p.kblocks;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (64 * q + lane < p.kblocks) srow[q] = row[64 * q + lane];
+  }
+
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.a, (short)0, (int)(p.m * p.k * 2), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wq, (short)0, (int)((int64_t)p.n * p.k), kLinRsrcFlags);
+
+  // token rows of every window of the split: 2C DMAs of 1 KiB (8 rows x 128 B)
+  // per window, DMA q = wave + 4i; part q of row t at q ^ swz128(t); rows past
+  // M and windows past the split's end copy zeros
+  constexpr int kActDma = 2 * C;
+  static_assert(kActDma % 4 == 0, "every wavefront issues the same number of copies");
+#pragma unroll
+  for (int i = 0; i < kActDma / 4; ++i) {
+    const int q = wave + 4 * i;
+    const int row = q * 8 + (lane >> 3);
+    const int64_t tok = (int64_t)tm * kRows + row;
+    const int part = (lane & 7) ^ swz128(row);
+    const uint32_t base = tok < p.m ? (uint32_t)(tok * p.k * 2 + part * 16) : kLinOob;
+#pragma unroll
+    for (int w = 0; w < WPS; ++w) {
+      const int win = w_begin + w;
+      lds_dma16(a_rsrc, (lds_void_ptr)&xs_all[w * kWinBytes + q * 1024], win < w_end ? base : kLinOob, win * 128);
+    }
+  }
+
+  const int wstep = weight_window_step(p.w_rowmajor);
+  uint32_t w_off[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    w_off[r] = strip0 + r < strips ? weight_lane_offset(p.w_rowmajor, strip0 + r, lane, p.k, wins) : kLinOob;
+  u32x4 wr[D][R];
+  auto load = [&](int win, int t) {
+    const bool in = win < w_end;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      wr[t][r] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, in ? w_off[r] : kLinOob, win * wstep, 0));
+  };
+  constexpr int kDepth = D < WPS ? D : WPS;
+#pragma unroll
+  for (int t = 0; t < kDepth; ++t) {
+    load(w_begin + t, t);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // this wavefront's token copies have landed (only weight loads may remain), then everyone's
+  lds_dma_wait_keep<kDepth * R>();
+  __syncthreads();
+
+  f32x4 acc[R][C];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < WPS; ++i) {
+    const int win = w_begin + i;
+    const int t = i % kDepth;
+    float bscale = 0.0f;
+    if constexpr (FP8) {
+      const int kb = min(win, wins - 1) >> 1;
+      const uint32_t word = kb < 64 ? srow[0] : (kb < 128 ? srow[1] : (kb < 192 ? srow[2] : srow[3]));
+      bscale = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)word, kb & 63) << 23);
+    }
+    const uint8_t* xw = &xs_all[i * kWinBytes];
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      bf16x8 a[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if constexpr (FP8)
+          a[r] = dequant_fp8x8(wr[t][r][2 * d], wr[t][r][2 * d + 1], bscale);
+        else
+          a[r] = dequant_i8x8(wr[t][r][2 * d], wr[t][r][2 * d + 1]);
+      }
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int row = c * 16 + n16;
+        const int part = (2 * j + d) ^ swz128(row);
+        const bf16x8 b = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xw[row * 128 + part * 16]));
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][c] = mfma_bf16(a[r], b, acc[r][c]);
+      }
+    }
+    if (i + kDepth < WPS) load(w_begin + i + kDepth, t);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // epilogue as w8a16_kernel: lane holds channels 16*strip + 4*j + (0..3) of token c*16 + n16
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int strip = strip0 + r;
+    if (strip >= strips) continue;
+    const int n = strip * 16 + 4 * j;
+    float sc[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if constexpr (!FP8) {
+      sc[0] = __uint_as_float(sv[r][0] << 16);
+      sc[1] = __uint_as_float(sv[r][0] & 0xFFFF0000u);
+      sc[2] = __uint_as_float(sv[r][1] << 16);
+      sc[3] = __uint_as_float(sv[r][1] & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int64_t tok = (int64_t)tm * kRows + c * 16 + n16;
+      if (tok >= p.m) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[r][c][e] * sc[e];
+      if (p.split == 1) {
+        uint16_t* dst = p.out + tok * p.n + n;
+        *reinterpret_cast<u32x2*>(dst) = finish_bf16x4(v, dst, p.accumulate != 0);
+      } else {
+        float* dst = p.partial + ((int64_t)sp * p.m + tok) * p.n + n;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+      }
+    }
+  }
+}
+
+// Up to 16 tokens with a K split: the split runs inside the workgroup.
 // Workgroup tile: 16*R output channels x 16*C tokens; wavefront w of the
 // `split` wavefronts computes split w's partial -- windows [w * wps,
 // min(wins, (w + 1) * wps)), the same MFMA chain per (channel, token) as a
@@ -1573,6 +1736,18 @@ static void launch_w8a16_kernel(const LinearParams& p, int r, int c, hipStream_t
   else if (r == 4 && c == 4) hipLaunchKernelGGL((w8a16_kernel3<4, 4, FP8>), grid, dim3(256), 0, stream, p);
   else if (r == 2 && c == 8) hipLaunchKernelGGL((w8a16_kernel<2, 8, FP8>), grid, dim3(256), 0, stream, p);
   else if (c == 1) hipLaunchKernelGGL((w8a16_kernel<2, 1, FP8>), grid, dim3(256), 0, stream, p);
+  else if ((c == 2 || c == 4) && (p.win_per_split == 8 || p.win_per_split == 4)) {
+    // weights straight to registers, the split's token rows in LDS
+    const size_t lds = (size_t)p.win_per_split * 16 * c * 128;
+    if (c == 2 && p.win_per_split == 8)
+      hipLaunchKernelGGL((w8a16_regw_kernel<2, 2, 8, 8, FP8>), grid, dim3(256), lds, stream, p);
+    else if (c == 2)
+      hipLaunchKernelGGL((w8a16_regw_kernel<2, 2, 8, 4, FP8>), grid, dim3(256), lds, stream, p);
+    else if (p.win_per_split == 8)
+      hipLaunchKernelGGL((w8a16_regw_kernel<2, 4, 8, 8, FP8>), grid, dim3(256), lds, stream, p);
+    else
+      hipLaunchKernelGGL((w8a16_regw_kernel<2, 4, 8, 4, FP8>), grid, dim3(256), lds, stream, p);
+  }
   else if (c == 2) hipLaunchKernelGGL((w8a16_kernel<2, 2, FP8>), grid, dim3(256), 0, stream, p);
   else hipLaunchKernelGGL((w8a16_kernel<2, 4, FP8>), grid, dim3(256), 0, stream, p);
 }

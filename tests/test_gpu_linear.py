@@ -124,12 +124,15 @@ def test_prefill_tile_with_explicit_split():
 @pytest.mark.parametrize("m,n,k,split", [(1, 4096, 4096, 8), (2, 1024, 4096, 2), (3, 16384, 4096, 4),
                                          (4, 4096, 1024, 8), (5, 1024, 4096, 4), (16, 4096, 4096, 2),
                                          (24, 1024, 4096, 8), (33, 4096, 4096, 4), (64, 1024, 4096, 8),
-                                         (64, 16384, 4096, 4), (3, 208, 640, 4), (40, 208, 640, 4)])
+                                         (64, 16384, 4096, 4), (3, 208, 640, 4), (40, 208, 640, 4),
+                                         (48, 4096, 4096, 8), (20, 208, 2048, 8)])
 @pytest.mark.parametrize("fmt", ["int8", "fp8"])
 def test_in_workgroup_split_matches_two_launch_reduction(m, n, k, split, fmt):
     """Up to 64 tokens a K split runs inside one workgroup (each wavefront
     one split's partial, summed through LDS in split order); above 64 the
-    partials go through the workspace and a reduce launch.  A row of C
+    partials go through the workspace and a reduce launch (17..64 tokens with
+    4 or 8 windows per split: weights straight to registers, the split's
+    token rows in LDS).  A row of C
     depends only on its row of A, and the split boundaries are the same, so
     the first m rows of a 128-token call with the same split must carry the
     same bits -- which pins the in-workgroup order of the additions.  Up to
