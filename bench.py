@@ -34,6 +34,14 @@ replays of the call captured as a HIP graph.
 ``--copy-calibration`` instead runs a plain 512 MiB device copy (torch
 ``copy_``) 5 times: the reference kernel for scaling the FETCH_SIZE /
 WRITE_SIZE counters of a ``rocprofv3 --pmc`` run to bytes.
+
+``roofline.traffic`` (HBM bytes per stage-1 launch) is measured in the run:
+after the timed work the bench starts two child processes, ``rocprofv3 --pmc
+FETCH_SIZE`` and ``rocprofv3 --pmc WRITE_SIZE`` over ``bench.py
+--traffic-run`` (the headline layer, one call per pooled batch, then two
+512 MiB device copies), and scales each counter by what it reads for the
+copy.  ``--traffic-pmc 0``, or passes that fail, fall back to the figure of
+the committed counter summary, and ``traffic_source`` says which was used.
 """
 
 from __future__ import annotations
@@ -75,6 +83,10 @@ def parse():
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--traffic-pmc", type=int, default=1,
+                    help="1 measures roofline.traffic with two rocprofv3 --pmc child passes; 0 uses the committed figure")
+    ap.add_argument("--traffic-run", action="store_true",
+                    help="child program of the traffic passes: one decode call per pooled batch, then two copies")
     ap.add_argument("--profile-run", default=None, metavar="FMT:T:N[:graph]",
                     help="only run N layer calls (FMT int4|mxfp4|w4a8, T tokens) for rocprofv3 counter passes; "
                          ":graph adds N replays of the captured call; FMT linear-w8a8|linear-w8a16: N calls of "
@@ -85,16 +97,108 @@ def parse():
 def copy_calibration() -> int:
     import torch
 
-    n = 512 << 20
+    copy_pair(torch, reps=5)
+    print(json.dumps({"copy_calibration_bytes_per_launch": COPY_CAL_BYTES, "launches": 5}), flush=True)
+    return 0
+
+
+COPY_CAL_BYTES = 512 << 20
+
+
+def copy_pair(torch, n=COPY_CAL_BYTES, reps=5):
+    """``reps`` plain device copies of ``n`` bytes (one copy kernel each)."""
+
     a = torch.empty(n, dtype=torch.uint8, device="cuda")
     a.fill_(1)
     b = torch.empty_like(a)
     torch.cuda.synchronize()
-    for _ in range(5):
+    for _ in range(reps):
         b.copy_(a)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes_per_launch": n, "launches": 5}), flush=True)
-    return 0
+    del a, b
+
+
+def read_counter_csv(out_dir: Path):
+    """Per-kernel lists of counter values (one entry per dispatch) from the
+    ``*counter_collection.csv`` files a rocprofv3 --pmc pass wrote."""
+
+    import csv
+
+    per = {}
+    for f in sorted(out_dir.rglob("*counter_collection.csv")):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                per.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return per
+
+
+def measure_traffic(args, stage1_alg_bytes):
+    """HBM bytes per stage-1 decode launch from two rocprofv3 --pmc child
+    passes (FETCH_SIZE, then WRITE_SIZE) over ``bench.py --traffic-run``, each
+    counter scaled by its reading for a plain 512 MiB device copy in the same
+    pass.  Returns a dict, or None when rocprofv3 is absent or a pass fails.
+
+    The child runs one decode call per pooled batch of the headline (the same
+    seeds as the timed steps), so the counters cover the same routing mix;
+    ``stage1_alg_bytes`` maps a distinct-expert count to that launch's
+    algorithmic bytes, for the ratio of measured to algorithmic traffic."""
+
+    import shutil
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if not exe or not shutil.which("timeout"):
+        return None
+    read = {}
+    distinct = None
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = Path(tempfile.mkdtemp(prefix=f"bench_pmc_{ctr.lower()}_", dir="/tmp"))
+        cmd = ["timeout", "-k", "10", "240", exe, "--pmc", ctr, "--output-format", "csv", "-d", str(out),
+               "-o", "run", "--", sys.executable, str(Path(__file__).resolve()), "--traffic-run",
+               "--tokens", str(args.tokens), "--pool", str(args.pool), "--seed", str(args.seed),
+               "--prefill-tokens", "0", "--secondary", "0", "--cpu-baseline", "0"]
+        log(f"[bench] traffic pass {ctr}: {' '.join(cmd)}")
+        try:
+            proc = subprocess.run(cmd, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, stdout=subprocess.PIPE,
+                                  text=True, timeout=300)
+            info = None
+            for ln in proc.stdout.splitlines():
+                if ln.startswith('{"traffic_run"'):
+                    info = json.loads(ln)
+            per = read_counter_csv(out)
+        except (OSError, subprocess.SubprocessError, ValueError, KeyError) as e:
+            log(f"[bench] traffic pass {ctr} failed: {e!r}")
+            return None
+        finally:
+            shutil.rmtree(out, ignore_errors=True)
+        # rocprofv3 may end nonzero after the program finished and its files
+        # are whole; the child's closing line and the dispatch counts decide
+        st1 = [v for k, v in per.items() if "expert_decode_kernel<1" in k]
+        # the 512 MiB copies are the largest copy dispatches (the layer's own
+        # device copies are far smaller)
+        cpy = sorted((x for k, v in per.items() if "copyBuffer" in k for x in v), reverse=True)
+        if info is None or len(st1) != 1 or len(st1[0]) != info["stage1_launches"] or len(cpy) < info["copies"]:
+            log(f"[bench] traffic pass {ctr}: rc={proc.returncode}, closing line {info is not None}, "
+                f"stage-1 kernels {[len(v) for v in st1]}, copy dispatches {len(cpy)}: not used")
+            return None
+        distinct = info["distinct_per_launch"]
+        read[ctr] = (sum(st1[0]) / len(st1[0]), sum(cpy[:info["copies"]]) / info["copies"])
+        log(f"[bench] traffic pass {ctr}: rc={proc.returncode}, stage-1 mean {read[ctr][0]:.1f} KiB over "
+            f"{len(st1[0])} launches, copy {read[ctr][1]:.1f} KiB")
+    scale = {c: COPY_CAL_BYTES / (read[c][1] * 1024.0) for c in read}
+    traffic = sum(read[c][0] * 1024.0 * scale[c] for c in read)
+    alg = sum(stage1_alg_bytes(d) for d in distinct) / len(distinct)
+    return {
+        "bytes": int(round(traffic)),
+        "fetch_kib": round(read["FETCH_SIZE"][0], 1),
+        "write_kib": round(read["WRITE_SIZE"][0], 1),
+        "fetch_scale": round(scale["FETCH_SIZE"], 4),
+        "write_scale": round(scale["WRITE_SIZE"], 4),
+        "launches": len(distinct),
+        "algorithmic_bytes_same_launches": int(alg),
+        "over_algorithmic": round(traffic / alg, 4),
+    }
 
 
 def traffic_from_profile():
@@ -249,6 +353,8 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration()
+    if args.traffic_run:
+        args.prefill_tokens, args.secondary = 0, 0
     import numpy as np
     import torch
 
@@ -288,6 +394,25 @@ def main() -> int:
         d = [int(torch.unique(pkg.route_from_logits(lg, topk=K, score_func="sigmoid").routing_ids).numel())
              for lg in lgs]
         return xs, lgs, d
+
+    def stage1_alg_bytes(d):
+        # stage-1 (w13 + SwiGLU) bytes of one decode launch with d distinct
+        # routed experts: their w13 and scales plus the shared expert's, x
+        # read, h written for the T k routed and T shared rows
+        return (d + 1) * b13 + T * H * 2 + (T * K + T) * I * 2
+
+    if args.traffic_run:
+        # the program the traffic passes wrap: one warm-up call on batch 0,
+        # one call per pooled batch (the headline's seeds), then the copies
+        xs, lgs, distinct = pools(T, args.pool, 1000)
+        order = [0] + list(range(args.pool))
+        for i in order:
+            layer.forward_tensor(xs[i], router_logits=lgs[i])
+        torch.cuda.synchronize()
+        copy_pair(torch, reps=2)
+        print(json.dumps({"traffic_run": True, "stage1_launches": len(order), "copies": 2,
+                          "distinct_per_launch": [distinct[i] for i in order]}), flush=True)
+        return 0
 
     # ------------------------------------------------------------- prefill
     # Timed before the decode headline: a GPU that has just been idle (fresh
@@ -385,7 +510,7 @@ def main() -> int:
     ms_fixed = cuda_timer(lambda i: layer.forward_tensor(xs[0], router_logits=lgs[0]), args.steps,
                           sync_before=False)
     d_mean = float(np.mean([distinct[i % args.pool] for i in range(args.steps)]))
-    stage1_bytes = (d_mean + 1) * b13 + T * H * 2 + (T * K + T) * I * 2
+    stage1_bytes = stage1_alg_bytes(d_mean)
     st1_ms = roof["stage1_w13"]
     achieved = stage1_bytes / (st1_ms * 1e-3) / 1e9
     log(f"[bench] decode T={T}: {ms:.4f} ms/step (stage-1 events), {ms_all:.4f} with all kernel events, "
@@ -431,7 +556,16 @@ def main() -> int:
     if args.cpu_baseline:
         cpu = cpu_baseline(pkg, w13, s13, w2, s2, args.seed)
 
-    traffic = traffic_from_profile()
+    traffic_pmc = measure_traffic(args, stage1_alg_bytes) if args.traffic_pmc else None
+    if traffic_pmc is not None:
+        traffic = traffic_pmc["bytes"]
+        traffic_source = ("measured in this run: rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE child passes "
+                          "over bench.py --traffic-run, each scaled by its reading for a 512 MiB device copy")
+    else:
+        traffic = traffic_from_profile()
+        traffic_source = (f"committed counter summary {TRAFFIC_PROFILE.relative_to(ROOT)}"
+                          + (" (the passes of this run failed)" if args.traffic_pmc else "")
+                          if traffic is not None else None)
     line = {
         "metric": METRIC,
         "value": round(T / (ms * 1e-3), 1),
@@ -470,6 +604,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
+            "traffic_counters": traffic_pmc,
             "algorithmic_bytes_per_launch": int(stage1_bytes),
             "launch_ms": round(st1_ms, 5),
             "launches_timed": ncalls,
