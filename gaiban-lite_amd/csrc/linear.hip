@@ -1679,6 +1679,210 @@ __global__ __launch_bounds__(256 * H, 1) void w8a8_block_prefill_kernel(BlockFp8
   }
 }
 
+// Large grids without a K split: 256 tokens x 256 channels per workgroup,
+// two stages through LDS.  Wavefront (wm, wn) = (wave / 2, wave % 2) owns the
+// TM token tiles wm*TM .. (16 tokens each) and the 8 strips 8 wn .. 8 wn + 7
+// of the tile (128 channels: one E8M0 row block, so its weight scale is one
+// byte per K block).  Per K block the wavefront issues 8 TM MFMAs between two
+// barriers (4x the prefill kernel above), so the barrier and the LDS read
+// latency at the top of each block weigh a quarter as much.  buffer_load ...
+// lds copies block kb + 1 (256 token rows of 128 B, part q of row t at
+// q ^ swz128(t); the 16 strips' two 1 KiB weight tiles, or with row-major
+// weights (RM) their 256 rows like the token rows; the tokens' E8M0 dwords)
+// while block kb is computed.  The work items go to the XCDs in
+// contiguous runs, and inside a run groups of kGemmGroupM token tiles walk the
+// channel tiles together, so one XCD's L2 serves each token tile and each
+// weight tile to several workgroups.  The accumulation per output is the same
+// chain of scaled MFMAs in K-block order as in the kernels above: same bits.
+constexpr int kGemmGroupM = 4;
+// wavefront rows over the tokens: 2 (4 wavefronts, 128 x 128 each) or 4 (8
+// wavefronts, two per SIMD, 64 tokens x 128 channels each)
+#ifndef DSV4_GEMM256_WM
+#define DSV4_GEMM256_WM 2
+#endif
+constexpr int kGemm256Wm = DSV4_GEMM256_WM;
+
+template <int WM, int TM, bool RM>
+__global__ __launch_bounds__(128 * WM, 1) void w8a8_gemm256_kernel(BlockFp8Params p) {
+  constexpr int kWaves = 2 * WM;
+  constexpr int kTok = 256;
+  constexpr int TN = 8;
+  static_assert(16 * TM * WM == kTok, "256 token rows per workgroup");
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kTok * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[2][16 * 2048];
+  __shared__ __attribute__((aligned(16))) uint32_t scs[2][kTok];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+
+  const int items = p.tiles_m * p.tiles_n;
+  const int per_xcd = (items + kLinXcds - 1) / kLinXcds;
+  const int item = (blockIdx.x % kLinXcds) * per_xcd + blockIdx.x / kLinXcds;
+  if (item >= items) return;
+  const int group = item / (kGemmGroupM * p.tiles_n);
+  const int first_m = group * kGemmGroupM;
+  const int gm = min(kGemmGroupM, p.tiles_m - first_m);
+  const int in_group = item - group * kGemmGroupM * p.tiles_n;
+  const int tm = first_m + in_group % gm;
+  const int tn = in_group / gm;
+
+  const int wins = p.k / kWin;
+  const int strips = p.n >> 4;
+  const int64_t tok0 = (int64_t)tm * kTok;
+
+  const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.a, (short)0, (int)(p.m * p.k), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t as_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.as, (short)0, (int)(p.m * p.kblocks), kLinRsrcFlags);
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.wq, (short)0, (int)((int64_t)p.n * p.k), kLinRsrcFlags);
+
+  // token copies: copy q (0..31) fills rows 8q .. 8q + 7; wavefront w issues
+  // q = w, w + kWaves, ...
+  constexpr int kActPerWave = 32 / kWaves;
+  uint32_t a_off[kActPerWave];
+#pragma unroll
+  for (int i = 0; i < kActPerWave; ++i) {
+    const int row = (wave + kWaves * i) * 8 + (lane >> 3);
+    const int64_t tok = tok0 + row;
+    const int part = (lane & 7) ^ swz128(row);
+    a_off[i] = tok < p.m ? (uint32_t)(tok * p.k + part * 16) : kLinOob;
+  }
+  // weight copies.  Tiled (RM = false): wavefront w copies strips w*kSpw ..
+  // of the tile, both 1 KiB windows of the block each.  Row-major (RM): the
+  // 256 rows like the token rows, 8 whole 128-byte rows per copy (part q of
+  // row t at q ^ swz128(t)), read back like the token fragments.
+  constexpr int kSpw = 16 / kWaves;
+  const int wstep = weight_window_step(p.w_rowmajor);
+  uint32_t w_off[kSpw];
+#pragma unroll
+  for (int s = 0; s < kSpw; ++s) {
+    if constexpr (RM) {
+      const int row = (wave + kWaves * s) * 8 + (lane >> 3);
+      const int part = (lane & 7) ^ swz128(row);
+      w_off[s] = (uint32_t)((int64_t)(tn * 256 + row) * p.k + part * 16);
+    } else {
+      const int strip = tn * 16 + wave * kSpw + s;
+      w_off[s] = strip < strips ? weight_lane_offset(p.w_rowmajor, strip, lane, p.k, wins) : kLinOob;
+    }
+  }
+  // scale dwords: wavefront w copies tokens 64 (w % 4) .. + 63 (with 8
+  // wavefronts two copy the same bytes to the same place: no branch in the
+  // loop body)
+  const int64_t stok = tok0 + 64 * (wave & 3) + lane;
+  const uint32_t s_off = stok < p.m ? (uint32_t)(stok * p.kblocks) : kLinOob;
+  // this wavefront's weight scale row (host: N % 256 == 0, so it exists;
+  // K <= 8192, so lane kb holds block kb's byte)
+  uint32_t srow = 0;
+  if (lane < p.kblocks) srow = p.ws8[(int64_t)(tn * 2 + wn) * p.kblocks + lane];
+  // A wait the compiler sees: its own wait before the first use of srow
+  // would otherwise sit inside the K loop (the waits of the copies are
+  // inline asm, which it does not count), where it also waits for the copies
+  // issued just before it.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  const int n16 = lane & 15;
+  const int j = lane >> 4;
+
+  auto issue = [&](int kb, int buf) {
+#pragma unroll
+    for (int i = 0; i < kActPerWave; ++i)
+      lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + kWaves * i) * 1024]), a_off[i], kb * 128);
+#pragma unroll
+    for (int s = 0; s < kSpw; ++s) {
+      if constexpr (RM) {
+        // two copies of 8 rows each: rows 8 (w + kWaves s) .. and the same + 128
+        lds_copy16(w_rsrc, lds_addr(&wts[buf][(wave + kWaves * s) * 1024]), w_off[s], kb * 128);
+        lds_copy16(w_rsrc, lds_addr(&wts[buf][(wave + kWaves * s) * 1024 + 16384]), w_off[s] + 128 * p.k,
+                   kb * 128);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          lds_copy16(w_rsrc, lds_addr(&wts[buf][(wave * kSpw + s) * 2048 + t * 1024]), w_off[s],
+                     (2 * kb + t) * wstep);
+      }
+    }
+    lds_copy4(as_rsrc, lds_addr(&scs[buf][64 * (wave & 3)]), s_off, kb & ~3);
+  };
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int r = 0; r < TN; ++r)
+#pragma unroll
+    for (int c = 0; c < TM; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Step kb: issue block kb + 1 into the other buffer (released by step
+  // kb - 1's barrier), compute block kb, wait for block kb + 1.
+  auto step = [&](int kb, auto u_c) {
+    constexpr int u = decltype(u_c)::value;
+    // the last block re-copies itself into the idle buffer (no branch in the
+    // loop body; nothing reads that buffer again)
+    issue(min(kb + 1, p.kblocks - 1), u ^ 1);
+    const int sw = __builtin_amdgcn_readlane((int)srow, kb);
+    i32x8 tv[TM];
+    int st[TM];
+#pragma unroll
+    for (int c = 0; c < TM; ++c) {
+      const int row = (wm * TM + c) * 16 + n16;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((j ^ swz128(row)) * 16)]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + (((4 + j) ^ swz128(row)) * 16)]);
+      tv[c] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      st[c] = (int)((scs[u][row] >> (8 * (kb & 3))) & 0xFF);
+    }
+#pragma unroll
+    for (int r = 0; r < TN; ++r) {
+      u32x4 lo, hi;
+      if constexpr (RM) {
+        const int row = (wn * TN + r) * 16 + n16;
+        lo = *reinterpret_cast<const u32x4*>(&wts[u][row * 128 + ((j ^ swz128(row)) * 16)]);
+        hi = *reinterpret_cast<const u32x4*>(&wts[u][row * 128 + (((4 + j) ^ swz128(row)) * 16)]);
+      } else {
+        const uint8_t* wp = &wts[u][(wn * TN + r) * 2048 + lane * 16];
+        lo = *reinterpret_cast<const u32x4*>(wp);
+        hi = *reinterpret_cast<const u32x4*>(wp + 1024);
+      }
+      const i32x8 wv = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+#pragma unroll
+      for (int c = 0; c < TM; ++c) acc[r][c] = mfma_fp8_block(wv, tv[c], acc[r][c], sw, st[c]);
+    }
+    // the block's MFMAs stay ahead of the wait (the scheduler would otherwise
+    // sink them past the barrier, leaving the wait right behind the copies)
+    __builtin_amdgcn_sched_barrier(0);
+    lds_dma_wait_all();  // this wavefront's copies of block kb + 1 have landed
+    __syncthreads();     // ... and everyone's; buffer u is free again
+  };
+  using U0 = std::integral_constant<int, 0>;
+  using U1 = std::integral_constant<int, 1>;
+
+  issue(0, 0);
+  lds_dma_wait_all();
+  __syncthreads();
+  // kblocks is a multiple of 4 (host check); the last step issues nothing
+  for (int kb = 0; kb < p.kblocks; kb += 2) {
+    step(kb, U0{});
+    step(kb + 1, U1{});
+  }
+
+#pragma unroll
+  for (int r = 0; r < TN; ++r) {
+    const int n = (tn * 16 + wn * TN + r) * 16 + 4 * j;
+#pragma unroll
+    for (int c = 0; c < TM; ++c) {
+      const int64_t tok = tok0 + (wm * TM + c) * 16 + n16;
+      if (tok >= p.m) continue;
+      const float v[4] = {acc[r][c][0], acc[r][c][1], acc[r][c][2], acc[r][c][3]};
+      uint16_t* dst = p.out + tok * p.n + n;
+      *reinterpret_cast<u32x2*>(dst) = finish_bf16x4(v, dst, false);
+    }
+  }
+}
+
+// The 256 x 256 kernel's domain: no K split, K % 512 == 0, K <= 8192, N % 256 == 0, and
+// at least one workgroup per CU.
+static bool gemm256_fits(int64_t m, int64_t n, int64_t k, int split) {
+  return split == 1 && k % 512 == 0 && k <= 8192 && n % 256 == 0 && ((m + 255) / 256) * (n / 256) >= 256;
+}
+
 static void launch_w8a8_block_kernel(const BlockFp8Params& p, int r, int c, hipStream_t stream) {
   const int items = p.split * p.tiles_m * p.tiles_n;
   const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
@@ -1941,6 +2145,20 @@ int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, i
     else if (kbps == 16) hipLaunchKernelGGL((w8a8_wsplit_kernel<8, 16, false>), grid, block, 0, stream, p);
     else hipLaunchKernelGGL((w8a8_wsplit_kernel<4, 0, false>), grid, block, 0, stream, p);
     DSV4_CHECK_LAUNCH("w8a8_wsplit_kernel");
+    return DSV4MOE_OK;
+  }
+  if (gemm256_fits(m, n, k, split)) {
+    p.tiles_m = (int)((m + 255) / 256);
+    p.tiles_n = (int)(n / 256);
+    const int items = p.tiles_m * p.tiles_n;
+    const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
+    if (w_rowmajor)
+      hipLaunchKernelGGL((w8a8_gemm256_kernel<kGemm256Wm, 16 / kGemm256Wm, true>), grid, dim3(128 * kGemm256Wm), 0,
+                         stream, p);
+    else
+      hipLaunchKernelGGL((w8a8_gemm256_kernel<kGemm256Wm, 16 / kGemm256Wm, false>), grid, dim3(128 * kGemm256Wm), 0,
+                         stream, p);
+    DSV4_CHECK_LAUNCH("w8a8_gemm256_kernel");
     return DSV4MOE_OK;
   }
   launch_w8a8_block_kernel(p, r, c, stream);
