@@ -1695,26 +1695,32 @@ __global__ __launch_bounds__(256 * H, 1) void w8a8_block_prefill_kernel(BlockFp8
 // weight tile to several workgroups.  The accumulation per output is the same
 // chain of scaled MFMAs in K-block order as in the kernels above: same bits.
 constexpr int kGemmGroupM = 4;
-// wavefront rows over the tokens: 2 (4 wavefronts, 128 x 128 each) or 4 (8
-// wavefronts, two per SIMD, 64 tokens x 128 channels each)
+// The wavefront grid: WM x WN wavefronts (wave = wm * WN + wn), each TM =
+// 16 / WM token tiles x TN = 16 / WN strips: 2 x 2 of 128 x 128 (one
+// wavefront per SIMD) or 2 x 4 of 128 tokens x 64 channels (two per SIMD).
 #ifndef DSV4_GEMM256_WM
-#define DSV4_GEMM256_WM 2
+#define DSV4_GEMM256_WM 4
+#endif
+#ifndef DSV4_GEMM256_WN
+#define DSV4_GEMM256_WN 2
 #endif
 constexpr int kGemm256Wm = DSV4_GEMM256_WM;
+constexpr int kGemm256Wn = DSV4_GEMM256_WN;
 
-template <int WM, int TM, bool RM>
-__global__ __launch_bounds__(128 * WM, 1) void w8a8_gemm256_kernel(BlockFp8Params p) {
-  constexpr int kWaves = 2 * WM;
+template <int WM, int WN, bool RM>
+__global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8Params p) {
+  constexpr int kWaves = WM * WN;
   constexpr int kTok = 256;
-  constexpr int TN = 8;
-  static_assert(16 * TM * WM == kTok, "256 token rows per workgroup");
+  constexpr int TM = 16 / WM;
+  constexpr int TN = 16 / WN;
+  static_assert(kWaves == 4 || kWaves == 8, "4 or 8 wavefronts");
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kTok * 128];
   __shared__ __attribute__((aligned(16))) uint8_t wts[2][16 * 2048];
   __shared__ __attribute__((aligned(16))) uint32_t scs[2][kTok];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
 
   const int items = p.tiles_m * p.tiles_n;
   const int per_xcd = (items + kLinXcds - 1) / kLinXcds;
@@ -1775,7 +1781,7 @@ __global__ __launch_bounds__(128 * WM, 1) void w8a8_gemm256_kernel(BlockFp8Param
   // this wavefront's weight scale row (host: N % 256 == 0, so it exists;
   // K <= 8192, so lane kb holds block kb's byte)
   uint32_t srow = 0;
-  if (lane < p.kblocks) srow = p.ws8[(int64_t)(tn * 2 + wn) * p.kblocks + lane];
+  if (lane < p.kblocks) srow = p.ws8[(int64_t)((tn * 256 + wn * TN * 16) >> 7) * p.kblocks + lane];
   // A wait the compiler sees: its own wait before the first use of srow
   // would otherwise sit inside the K loop (the waits of the copies are
   // inline asm, which it does not count), where it also waits for the copies
@@ -1819,16 +1825,9 @@ __global__ __launch_bounds__(128 * WM, 1) void w8a8_gemm256_kernel(BlockFp8Param
     // loop body; nothing reads that buffer again)
     issue(min(kb + 1, p.kblocks - 1), u ^ 1);
     const int sw = __builtin_amdgcn_readlane((int)srow, kb);
-    i32x8 tv[TM];
-    int st[TM];
-#pragma unroll
-    for (int c = 0; c < TM; ++c) {
-      const int row = (wm * TM + c) * 16 + n16;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((j ^ swz128(row)) * 16)]);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + (((4 + j) ^ swz128(row)) * 16)]);
-      tv[c] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      st[c] = (int)((scs[u][row] >> (8 * (kb & 3))) & 0xFF);
-    }
+    // the wavefront's TN weight fragments, kept for the block; the token
+    // fragments stream through, one per TN MFMAs
+    i32x8 wv[TN];
 #pragma unroll
     for (int r = 0; r < TN; ++r) {
       u32x4 lo, hi;
@@ -1841,9 +1840,17 @@ __global__ __launch_bounds__(128 * WM, 1) void w8a8_gemm256_kernel(BlockFp8Param
         lo = *reinterpret_cast<const u32x4*>(wp);
         hi = *reinterpret_cast<const u32x4*>(wp + 1024);
       }
-      const i32x8 wv = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      wv[r] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
 #pragma unroll
-      for (int c = 0; c < TM; ++c) acc[r][c] = mfma_fp8_block(wv, tv[c], acc[r][c], sw, st[c]);
+    for (int c = 0; c < TM; ++c) {
+      const int row = (wm * TM + c) * 16 + n16;
+      const u32x4 lo = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + ((j ^ swz128(row)) * 16)]);
+      const u32x4 hi = *reinterpret_cast<const u32x4*>(&xs[u][row * 128 + (((4 + j) ^ swz128(row)) * 16)]);
+      const i32x8 tv = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      const int st = (int)((scs[u][row] >> (8 * (kb & 3))) & 0xFF);
+#pragma unroll
+      for (int r = 0; r < TN; ++r) acc[r][c] = mfma_fp8_block(wv[r], tv, acc[r][c], sw, st);
     }
     // the block's MFMAs stay ahead of the wait (the scheduler would otherwise
     // sink them past the barrier, leaving the wait right behind the copies)
@@ -2153,11 +2160,11 @@ int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, i
     const int items = p.tiles_m * p.tiles_n;
     const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
     if (w_rowmajor)
-      hipLaunchKernelGGL((w8a8_gemm256_kernel<kGemm256Wm, 16 / kGemm256Wm, true>), grid, dim3(128 * kGemm256Wm), 0,
-                         stream, p);
+      hipLaunchKernelGGL((w8a8_gemm256_kernel<kGemm256Wm, kGemm256Wn, true>), grid, dim3(64 * kGemm256Wm * kGemm256Wn),
+                         0, stream, p);
     else
-      hipLaunchKernelGGL((w8a8_gemm256_kernel<kGemm256Wm, 16 / kGemm256Wm, false>), grid, dim3(128 * kGemm256Wm), 0,
-                         stream, p);
+      hipLaunchKernelGGL((w8a8_gemm256_kernel<kGemm256Wm, kGemm256Wn, false>), grid, dim3(64 * kGemm256Wm * kGemm256Wn),
+                         0, stream, p);
     DSV4_CHECK_LAUNCH("w8a8_gemm256_kernel");
     return DSV4MOE_OK;
   }

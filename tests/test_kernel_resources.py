@@ -127,3 +127,67 @@ def test_mxfp4_prefill_reads_no_register_in_flight(tmp_path):
     assert len(names) == 2
     for name in names:
         assert inflight_register_reads(asm, name) == [], name
+
+
+def _device_asm(src: Path, tmp_path: Path) -> str:
+    from gaiban_lite_amd import build_ext
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path / (src.stem + ".s")
+    subprocess.run([hipcc, *build_ext.HIPCC_FLAGS, f"-I{ROOT / 'include'}", f"-I{CSRC}", "--cuda-device-only",
+                    "-S", str(src), "-o", str(out)], check=True, capture_output=True)
+    return out.read_text()
+
+
+def k_loop_bodies(asm: str, kernel: str) -> list[list[tuple[str, bool]]]:
+    """The loops of `kernel` (loop header label to the last branch back to
+    it) as (instruction, inside inline asm) pairs."""
+
+    start = asm.index(kernel + ":")
+    lines = asm[start:asm.index(".Lfunc_end", start)].split("\n")
+    rows, inasm = [], False
+    for line in lines:
+        s = line.strip()
+        if s.startswith(";;#ASMSTART"):
+            inasm = True
+        elif s.startswith(";;#ASMEND"):
+            inasm = False
+        rows.append((s, inasm))
+    loops = []
+    for i, (s, _) in enumerate(rows):
+        if "Loop Header" not in s:
+            continue
+        label = s.split(":")[0]
+        back = [k for k, (t, _) in enumerate(rows) if re.search(r"s_c?branch\w*\s+" + re.escape(label) + r"\b", t)]
+        if back:
+            loops.append(rows[i:max(back) + 1])
+    return loops
+
+
+def test_w8a8_gemm256_k_loop_is_one_block_with_only_its_own_copy_waits(tmp_path):
+    """The 256 x 256 block-FP8 kernel's K loop: no spills, LDS within a CU,
+    no branch inside the loop body, and no vmcnt wait of the compiler's in
+    it -- the copies' waits are inline asm, which the compiler does not
+    count, so a wait of its own there (for a prologue load it still thinks
+    outstanding) would also wait for the copies just issued and expose
+    their whole latency every block; a branch lets the MFMAs of a block
+    sink past that block's wait."""
+
+    meta = kernel_metadata(CSRC / "linear.hip", tmp_path)
+    gemm = {k: v for k, v in meta.items() if "w8a8_gemm256_kernel" in k}
+    assert len(gemm) == 2
+    for name, m in gemm.items():
+        assert m["vgpr_spill_count"] == 0, name
+        assert m["group_segment_fixed_size"] <= 160 * 1024, name
+    asm = _device_asm(CSRC / "linear.hip", tmp_path)
+    for name in gemm:
+        loops = k_loop_bodies(asm, name)
+        dma_loops = [lp for lp in loops if any(a and "buffer_load" in s and " lds" in s for s, a in lp)]
+        assert len(dma_loops) == 1, name
+        body = dma_loops[0]
+        assert sum(1 for s, _ in body if s.startswith("v_mfma")) > 0, name
+        assert [s for s, a in body if not a and s.startswith("s_waitcnt") and "vmcnt" in s] == [], name
+        branches = [s for s, _ in body if s.startswith(("s_cbranch", "s_branch"))]
+        assert len(branches) == 1, (name, branches)  # the back edge only
