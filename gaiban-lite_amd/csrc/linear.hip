@@ -1679,25 +1679,27 @@ __global__ __launch_bounds__(256 * H, 1) void w8a8_block_prefill_kernel(BlockFp8
   }
 }
 
-// Large grids without a K split: 256 tokens x 256 channels per workgroup,
-// two stages through LDS.  Wavefront (wm, wn) = (wave / 2, wave % 2) owns the
-// TM token tiles wm*TM .. (16 tokens each) and the 8 strips 8 wn .. 8 wn + 7
-// of the tile (128 channels: one E8M0 row block, so its weight scale is one
-// byte per K block).  Per K block the wavefront issues 8 TM MFMAs between two
-// barriers (4x the prefill kernel above), so the barrier and the LDS read
-// latency at the top of each block weigh a quarter as much.  buffer_load ...
-// lds copies block kb + 1 (256 token rows of 128 B, part q of row t at
-// q ^ swz128(t); the 16 strips' two 1 KiB weight tiles, or with row-major
-// weights (RM) their 256 rows like the token rows; the tokens' E8M0 dwords)
-// while block kb is computed.  The work items go to the XCDs in
+// Large grids without a K split: 256 tokens x CH (256 or 128) channels per
+// workgroup, two stages through LDS.  Wavefront (wm, wn) owns the TM token
+// tiles wm*TM .. (16 tokens each) and the TN strips wn*TN .. of the tile (at
+// most 128 channels: inside one E8M0 row block, so its weight scale is one
+// byte per K block); it keeps its TN weight fragments in registers for the
+// block and streams its token fragments through.  With 256 x 256 a K block
+// is 256 MFMAs per SIMD between two barriers (4x the 128 x 256 kernel above),
+// so the barrier and the LDS read latency at the top of each block weigh
+// less.  buffer_load ... lds copies block kb + 1 (256 token rows of 128 B,
+// part q of row t at q ^ swz128(t); the strips' two 1 KiB weight tiles, or
+// with row-major weights (RM) their CH rows like the token rows; the tokens'
+// E8M0 dwords) while block kb is computed.  The work items go to the XCDs in
 // contiguous runs, and inside a run groups of kGemmGroupM token tiles walk the
 // channel tiles together, so one XCD's L2 serves each token tile and each
 // weight tile to several workgroups.  The accumulation per output is the same
 // chain of scaled MFMAs in K-block order as in the kernels above: same bits.
 constexpr int kGemmGroupM = 4;
 // The wavefront grid: WM x WN wavefronts (wave = wm * WN + wn), each TM =
-// 16 / WM token tiles x TN = 16 / WN strips: 2 x 2 of 128 x 128 (one
-// wavefront per SIMD) or 2 x 4 of 128 tokens x 64 channels (two per SIMD).
+// 16 / WM token tiles x TN = CH / 16 / WN strips.  4 x 2: 8 wavefronts, two
+// per SIMD (each 64 tokens x 128 or 64 channels); 2 x 2: one per SIMD, 128 x
+// 128 at 256 channels (456 registers, more of them copied around the MFMAs).
 #ifndef DSV4_GEMM256_WM
 #define DSV4_GEMM256_WM 4
 #endif
@@ -1707,15 +1709,17 @@ constexpr int kGemmGroupM = 4;
 constexpr int kGemm256Wm = DSV4_GEMM256_WM;
 constexpr int kGemm256Wn = DSV4_GEMM256_WN;
 
-template <int WM, int WN, bool RM>
+template <int WM, int WN, int CH, bool RM>
 __global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8Params p) {
   constexpr int kWaves = WM * WN;
   constexpr int kTok = 256;
+  constexpr int kStrips = CH / 16;
   constexpr int TM = 16 / WM;
-  constexpr int TN = 16 / WN;
+  constexpr int TN = kStrips / WN;
   static_assert(kWaves == 4 || kWaves == 8, "4 or 8 wavefronts");
+  static_assert(CH == 128 || CH == 256, "128 or 256 channels per workgroup");
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kTok * 128];
-  __shared__ __attribute__((aligned(16))) uint8_t wts[2][16 * 2048];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[2][CH * 128];
   __shared__ __attribute__((aligned(16))) uint32_t scs[2][kTok];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1757,19 +1761,21 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8P
   }
   // weight copies.  Tiled (RM = false): wavefront w copies strips w*kSpw ..
   // of the tile, both 1 KiB windows of the block each.  Row-major (RM): the
-  // 256 rows like the token rows, 8 whole 128-byte rows per copy (part q of
-  // row t at q ^ swz128(t)), read back like the token fragments.
-  constexpr int kSpw = 16 / kWaves;
+  // CH rows like the token rows, copy q = w, w + kWaves, .. filling rows
+  // 8q .. 8q + 7 (part q of row t at q ^ swz128(t)), read back like the token
+  // fragments.
+  constexpr int kSpw = kStrips / kWaves;
+  constexpr int kWCopies = RM ? CH / 8 / kWaves : 2 * kSpw;
   const int wstep = weight_window_step(p.w_rowmajor);
-  uint32_t w_off[kSpw];
+  uint32_t w_off[RM ? kWCopies : kSpw];
 #pragma unroll
-  for (int s = 0; s < kSpw; ++s) {
+  for (int s = 0; s < (RM ? kWCopies : kSpw); ++s) {
     if constexpr (RM) {
       const int row = (wave + kWaves * s) * 8 + (lane >> 3);
       const int part = (lane & 7) ^ swz128(row);
-      w_off[s] = (uint32_t)((int64_t)(tn * 256 + row) * p.k + part * 16);
+      w_off[s] = (uint32_t)((int64_t)(tn * CH + row) * p.k + part * 16);
     } else {
-      const int strip = tn * 16 + wave * kSpw + s;
+      const int strip = tn * kStrips + wave * kSpw + s;
       w_off[s] = strip < strips ? weight_lane_offset(p.w_rowmajor, strip, lane, p.k, wins) : kLinOob;
     }
   }
@@ -1778,10 +1784,10 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8P
   // loop body)
   const int64_t stok = tok0 + 64 * (wave & 3) + lane;
   const uint32_t s_off = stok < p.m ? (uint32_t)(stok * p.kblocks) : kLinOob;
-  // this wavefront's weight scale row (host: N % 256 == 0, so it exists;
+  // this wavefront's weight scale row (host: N % CH == 0, so it exists;
   // K <= 8192, so lane kb holds block kb's byte)
   uint32_t srow = 0;
-  if (lane < p.kblocks) srow = p.ws8[(int64_t)((tn * 256 + wn * TN * 16) >> 7) * p.kblocks + lane];
+  if (lane < p.kblocks) srow = p.ws8[(int64_t)((tn * CH + wn * TN * 16) >> 7) * p.kblocks + lane];
   // A wait the compiler sees: its own wait before the first use of srow
   // would otherwise sit inside the K loop (the waits of the copies are
   // inline asm, which it does not count), where it also waits for the copies
@@ -1795,12 +1801,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8P
     for (int i = 0; i < kActPerWave; ++i)
       lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + kWaves * i) * 1024]), a_off[i], kb * 128);
 #pragma unroll
-    for (int s = 0; s < kSpw; ++s) {
+    for (int s = 0; s < (RM ? kWCopies : kSpw); ++s) {
       if constexpr (RM) {
-        // two copies of 8 rows each: rows 8 (w + kWaves s) .. and the same + 128
         lds_copy16(w_rsrc, lds_addr(&wts[buf][(wave + kWaves * s) * 1024]), w_off[s], kb * 128);
-        lds_copy16(w_rsrc, lds_addr(&wts[buf][(wave + kWaves * s) * 1024 + 16384]), w_off[s] + 128 * p.k,
-                   kb * 128);
       } else {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -1872,7 +1875,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8P
 
 #pragma unroll
   for (int r = 0; r < TN; ++r) {
-    const int n = (tn * 16 + wn * TN + r) * 16 + 4 * j;
+    const int n = (tn * kStrips + wn * TN + r) * 16 + 4 * j;
 #pragma unroll
     for (int c = 0; c < TM; ++c) {
       const int64_t tok = tok0 + (wm * TM + c) * 16 + n16;
@@ -1884,10 +1887,16 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8P
   }
 }
 
-// The 256 x 256 kernel's domain: no K split, K % 512 == 0, K <= 8192, N % 256 == 0, and
-// at least one workgroup per CU.
-static bool gemm256_fits(int64_t m, int64_t n, int64_t k, int split) {
-  return split == 1 && k % 512 == 0 && k <= 8192 && n % 256 == 0 && ((m + 255) / 256) * (n / 256) >= 256;
+// The channels per workgroup of the 256-token kernel (0: another kernel):
+// no K split, K % 512 == 0, K <= 8192, N a multiple of the channel tile, and
+// at least one workgroup per CU -- 256 channels where that fills the GPU,
+// else 128.
+static int gemm256_channels(int64_t m, int64_t n, int64_t k, int split) {
+  if (split != 1 || k % 512 != 0 || k > 8192) return 0;
+  const int64_t tiles_m = (m + 255) / 256;
+  if (n % 256 == 0 && tiles_m * (n / 256) >= 256) return 256;
+  if (n % 128 == 0 && tiles_m * (n / 128) >= 256) return 128;
+  return 0;
 }
 
 static void launch_w8a8_block_kernel(const BlockFp8Params& p, int r, int c, hipStream_t stream) {
@@ -2154,17 +2163,17 @@ int dsv4_launch_block_fp8_gemm(const uint8_t* a, const uint8_t* as, int64_t m, i
     DSV4_CHECK_LAUNCH("w8a8_wsplit_kernel");
     return DSV4MOE_OK;
   }
-  if (gemm256_fits(m, n, k, split)) {
+  if (const int ch = gemm256_channels(m, n, k, split)) {
     p.tiles_m = (int)((m + 255) / 256);
-    p.tiles_n = (int)(n / 256);
+    p.tiles_n = (int)(n / ch);
     const int items = p.tiles_m * p.tiles_n;
     const dim3 grid((unsigned)(((items + kLinXcds - 1) / kLinXcds) * kLinXcds));
-    if (w_rowmajor)
-      hipLaunchKernelGGL((w8a8_gemm256_kernel<kGemm256Wm, kGemm256Wn, true>), grid, dim3(64 * kGemm256Wm * kGemm256Wn),
-                         0, stream, p);
-    else
-      hipLaunchKernelGGL((w8a8_gemm256_kernel<kGemm256Wm, kGemm256Wn, false>), grid, dim3(64 * kGemm256Wm * kGemm256Wn),
-                         0, stream, p);
+    const dim3 block(64 * kGemm256Wm * kGemm256Wn);
+    constexpr int WM = kGemm256Wm, WN = kGemm256Wn;
+    if (ch == 256 && w_rowmajor) hipLaunchKernelGGL((w8a8_gemm256_kernel<WM, WN, 256, true>), grid, block, 0, stream, p);
+    else if (ch == 256) hipLaunchKernelGGL((w8a8_gemm256_kernel<WM, WN, 256, false>), grid, block, 0, stream, p);
+    else if (w_rowmajor) hipLaunchKernelGGL((w8a8_gemm256_kernel<WM, WN, 128, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((w8a8_gemm256_kernel<WM, WN, 128, false>), grid, block, 0, stream, p);
     DSV4_CHECK_LAUNCH("w8a8_gemm256_kernel");
     return DSV4MOE_OK;
   }

@@ -202,17 +202,20 @@ def test_in_workgroup_split_matches_two_launch_reduction(m, n, k, split):
     assert torch.equal(small.view(torch.int16), big[:m].view(torch.int16))
 
 
-def test_gemm256_kernel_matches_three_stage_kernel_bits():
-    """Grids of at least 256 workgroups of 256 x 256 without a K split run the
-    256 x 256 two-stage kernel (here M=4196, N=4096: 17 x 16 tiles, the last
-    token tile ragged); below that the 128 x 256 three-stage kernel runs.  A
-    row of C depends only on its row of A, and both kernels add the same
-    scaled MFMAs in K-block order, so rows 0..2047 and 4096..4195 equal a
-    2048-token and a 100-token call (split 1) bit for bit, for tiled and
-    row-major weights; a row subset against the closed form as well."""
+@pytest.mark.parametrize("m,n", [(4196, 4096), (8192, 1024)])
+def test_gemm256_kernel_matches_three_stage_kernel_bits(m, n):
+    """Grids of at least 256 workgroups of 256 tokens without a K split run
+    the 256-token two-stage kernel: 256 channels per workgroup where that
+    fills the GPU (M=4196, N=4096: 17 x 16 tiles, the last token tile
+    ragged), else 128 (M=8192, N=1024: 32 x 8); smaller grids run the
+    128 x 256 three-stage kernel.  A row of C depends only on its row of A,
+    and both kernels add the same scaled MFMAs in K-block order, so the
+    first 2048 rows and the last 100 equal a 2048-token and a 100-token
+    call (split 1) bit for bit, for tiled and row-major weights; a row
+    subset against the closed form as well."""
 
-    m, n, k = 4196, 4096, 4096
-    print(f"[block fp8] 256 x 256 kernel M={m} N={n} K={k}", flush=True)
+    k = 4096
+    print(f"[block fp8] 256-token kernel M={m} N={n} K={k}", flush=True)
     codes, scales = S.make_fp8_block_linear(n, k, seed=51, device=DEV)
     prep = L.prepare_fp8_block_weight(codes, scales)
     x = torch.randn((m, k), device=DEV, generator=torch.Generator(DEV).manual_seed(52)).to(torch.bfloat16)
@@ -220,12 +223,12 @@ def test_gemm256_kernel_matches_three_stage_kernel_bits():
     big = gemm(q, s, prep, 1)
     big_raw = gemm(q, s, prep, 1, raw=codes)
     head = gemm(q[:2048].contiguous(), s[:2048].contiguous(), prep, 1)
-    tail = gemm(q[4096:].contiguous(), s[4096:].contiguous(), prep, 1)
+    tail = gemm(q[m - 100:].contiguous(), s[m - 100:].contiguous(), prep, 1)
     torch.cuda.synchronize()
     assert torch.equal(big.view(torch.int16), big_raw.view(torch.int16))
     assert torch.equal(big[:2048].view(torch.int16), head.view(torch.int16))
-    assert torch.equal(big[4096:].view(torch.int16), tail.view(torch.int16))
-    rows = np.r_[0, 255, 256, 2047, 3000, 4095, 4096, 4195]
+    assert torch.equal(big[m - 100:].view(torch.int16), tail.view(torch.int16))
+    rows = np.r_[0, 255, 256, 2047, 3000, 4095, m - 100, m - 1]
     ref = O.block_fp8_gemm_f32(q.cpu().numpy()[rows], s.cpu().numpy()[rows], codes.cpu().numpy(),
                                scales.cpu().numpy())
-    assert_moe_close(to_np_f32(big)[rows], ref, what="256 x 256 kernel")
+    assert_moe_close(to_np_f32(big)[rows], ref, what=f"256-token kernel N={n}")
