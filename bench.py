@@ -90,7 +90,7 @@ def parse():
     ap.add_argument("--profile-run", default=None, metavar="FMT:T:N[:graph]",
                     help="only run N layer calls (FMT int4|mxfp4|w4a8, T tokens) for rocprofv3 counter passes; "
                          ":graph adds N replays of the captured call; FMT linear-w8a8|linear-w8a16: N calls of "
-                         "the dense linear at M=T, K=4096, N in {4096, 16384} (tiled weights)")
+                         "the dense linear at M=T, K=4096, N in {1024, 4096, 16384} (tiled weights)")
     return ap.parse_args()
 
 
@@ -1030,14 +1030,15 @@ def cpu_baseline(pkg, w13, s13, w2, s2, seed):
 
 def profile_run_linear(pkg, fmt: str, m: int, n: int, dev) -> int:
     """The dense-linear programs of ``--profile-run``: N calls each at M=m,
-    K=4096, N in {4096, 16384}, on the load-time tiled weights (W8A8: the
-    block-FP8 GEMM after one activation quantisation; W8A16: int8 weights)."""
+    K=4096, N in {1024, 4096, 16384}, on the load-time tiled weights (W8A8:
+    the block-FP8 GEMM after one activation quantisation; W8A16: int8
+    weights)."""
 
     import torch
 
     F, L, S = pkg.fp8_linear, pkg.weight_only_linear, pkg.synthetic
     k = 4096
-    for cols in (4096, 16384):
+    for cols in (1024, 4096, 16384):
         if fmt == "linear-w8a8":
             q, s = S.make_fp8_block_linear(cols, k, device=dev)
             prep = L.prepare_fp8_block_weight(q, s)
@@ -1061,7 +1062,7 @@ def profile_run_linear(pkg, fmt: str, m: int, n: int, dev) -> int:
             for _ in range(n):
                 L.w8a16_prepared_gemm_into(a, prep, o, ws, plan=plan)
         torch.cuda.synchronize()
-    print(json.dumps({"profile_run": f"{fmt}:{m}:{n}", "calls_per_shape": n, "shapes": ["N=4096", "N=16384"]}),
+    print(json.dumps({"profile_run": f"{fmt}:{m}:{n}", "calls_per_shape": n, "shapes": ["N=1024", "N=4096", "N=16384"]}),
           flush=True)
     return 0
 
