@@ -556,6 +556,7 @@ def main() -> int:
     if args.cpu_baseline:
         cpu = cpu_baseline(pkg, w13, s13, w2, s2, args.seed)
 
+    sclk_end = read_sclk()  # before the counter passes below
     traffic_pmc = measure_traffic(args, stage1_alg_bytes) if args.traffic_pmc else None
     if traffic_pmc is not None:
         traffic = traffic_pmc["bytes"]
@@ -616,7 +617,7 @@ def main() -> int:
         "per_step_ms": [round(v, 4) for v in step_ms],
         **secondary,
         "cpu_baseline": cpu,
-        "env": environment(torch, sclk_busy=sclk_busy, sclk_end=read_sclk()),
+        "env": environment(torch, sclk_busy=sclk_busy, sclk_end=sclk_end),
     }
     print(json.dumps(line), flush=True)
     return 0
