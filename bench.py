@@ -154,14 +154,15 @@ def measure_traffic(args, stage1_alg_bytes):
     distinct = None
     for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
         out = Path(tempfile.mkdtemp(prefix=f"bench_pmc_{ctr.lower()}_", dir="/tmp"))
-        cmd = ["timeout", "-k", "10", "240", exe, "--pmc", ctr, "--output-format", "csv", "-d", str(out),
+        # a pass takes a few seconds; a stuck one costs at most ~1.5 minutes
+        cmd = ["timeout", "-k", "10", "80", exe, "--pmc", ctr, "--output-format", "csv", "-d", str(out),
                "-o", "run", "--", sys.executable, str(Path(__file__).resolve()), "--traffic-run",
                "--tokens", str(args.tokens), "--pool", str(args.pool), "--seed", str(args.seed),
                "--prefill-tokens", "0", "--secondary", "0", "--cpu-baseline", "0"]
         log(f"[bench] traffic pass {ctr}: {' '.join(cmd)}")
         try:
             proc = subprocess.run(cmd, cwd="/tmp", env={**os.environ, "TMPDIR": "/tmp"}, stdout=subprocess.PIPE,
-                                  text=True, timeout=300)
+                                  text=True, timeout=100)
             info = None
             for ln in proc.stdout.splitlines():
                 if ln.startswith('{"traffic_run"'):
