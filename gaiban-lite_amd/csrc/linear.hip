@@ -1718,6 +1718,8 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8P
   constexpr int TN = kStrips / WN;
   static_assert(kWaves == 4 || kWaves == 8, "4 or 8 wavefronts");
   static_assert(CH == 128 || CH == 256, "128 or 256 channels per workgroup");
+  static_assert(16 % WM == 0 && kStrips % WN == 0 && TN * 16 <= 128, "a wavefront's strips lie in one scale block");
+  static_assert(kStrips % kWaves == 0 && (CH / 8) % kWaves == 0, "every wavefront issues the same copies");
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kTok * 128];
   __shared__ __attribute__((aligned(16))) uint8_t wts[2][CH * 128];
   __shared__ __attribute__((aligned(16))) uint32_t scs[2][kTok];
