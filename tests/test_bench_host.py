@@ -47,3 +47,17 @@ def test_more_than_one_gpu_is_refused():
                        timeout=60)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_traffic_passes_fall_back_without_the_profiler(monkeypatch):
+    """No rocprofv3 on the host: the in-run counter passes return None, and
+    the bench then reports the committed figure (`traffic_from_profile`)."""
+
+    import shutil
+    import types
+
+    bench = _bench()
+    monkeypatch.setattr(shutil, "which", lambda name: None)
+    args = types.SimpleNamespace(tokens=64, pool=16, seed=0)
+    assert bench.measure_traffic(args, lambda d: 1.0) is None
+    assert bench.traffic_from_profile() == 1796098888
