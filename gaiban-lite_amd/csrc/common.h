@@ -136,6 +136,13 @@ __device__ __forceinline__ uint32_t lds_addr(T* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)p;
 }
 
+// SiLU with the hardware reciprocal (v_rcp_f32, within an ulp) instead of
+// the IEEE division: the prefill epilogues (32 per lane per work item, about
+// 8 instructions less each; stage 1 1-1.5% faster).  The h it feeds is
+// rounded to bf16; the decode kernels and the shared expert keep silu_f.
+__device__ __forceinline__ float silu_rcp(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
 __device__ __forceinline__ float silu_f(float g) {
   return g / (1.0f + __expf(-g));
 }

@@ -443,7 +443,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
               gt = fminf(gt, lim);
               up = fminf(fmaxf(up, -lim), lim);
             }
-            bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+            bits[i] = float_to_bf16_bits(silu_rcp(gt) * up);
             part += __uint_as_float(bits[i] << 16);
           }
           if (rowid >= 0) {

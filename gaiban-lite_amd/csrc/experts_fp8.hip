@@ -453,7 +453,7 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
             gt = fminf(gt, lim);
             up = fminf(fmaxf(up, -lim), lim);
           }
-          bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+          bits[i] = float_to_bf16_bits(silu_rcp(gt) * up);
         }
         const int n = n0 + 32 * wave + 16 * s + 4 * jg;
         *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) =

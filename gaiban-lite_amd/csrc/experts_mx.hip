@@ -355,7 +355,7 @@ __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, 
             gt = fminf(gt, lim);
             up = fminf(fmaxf(up, -lim), lim);
           }
-          bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+          bits[i] = float_to_bf16_bits(silu_rcp(gt) * up);
         }
         const int n = n0 + 32 * wave + 16 * s + 4 * (lane >> 4);
         u32x2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
