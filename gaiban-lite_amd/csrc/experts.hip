@@ -86,10 +86,12 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
   return it;
 }
 
-// RING = 4: weights two groups ahead, four workgroups per CU (many items).
-// RING = 8: weights six groups ahead, for launches with fewer items than
-// resident workgroups (T ~ 1), where the bytes in flight per workgroup, not the
-// workgroup count, bound the stream; K must be a multiple of 8 groups.
+// RING = 4: weights two groups ahead, four workgroups per CU.
+// RING = 8: weights six groups ahead, two workgroups per CU; K must be a
+// multiple of 8 groups.  Stage 1 (w13, 256 KiB per item) streams faster with
+// the deeper ring at every T measured; stage 2 (128 KiB items) keeps RING = 4
+// unless its items fit one wave of resident workgroups (T ~ 1), where the
+// bytes in flight per workgroup, not the workgroup count, bound the stream.
 template <int STAGE, int RING>
 __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(ExpertGemmParams p) {
   constexpr int R = 2;
@@ -588,15 +590,17 @@ static int decode_resident_grid() {
   return cache[dev];
 }
 
-// The decode launch of one stage: the deep-ring kernel when every item fits
-// in one wave of resident workgroups (few blocks, T ~ 1) and K allows it,
-// else the four-workgroups-per-CU kernel.  `blocks` bounds the active blocks
+// The decode launch of one stage: the deep-ring kernel for stage 1, and for
+// stage 2 when every item fits in one wave of resident workgroups (few
+// blocks, T ~ 1), when K allows it; else the four-workgroups-per-CU kernel.
+// Either grid is at most one wave of resident workgroups (persistent items).  `blocks` bounds the active blocks
 // (the kernel reads the real count from the alignment on the device).
 template <int STAGE>
 static void launch_decode(const ExpertGemmParams& p, int blocks, hipStream_t stream) {
   const int items = p.n_tiles * blocks;
-  if ((p.k_dim / kGroup) % 8 == 0 && items <= decode_resident_grid<STAGE, 8>()) {
-    hipLaunchKernelGGL((expert_decode_kernel<STAGE, 8>), dim3((unsigned)items), dim3(256), 0, stream, p);
+  if ((p.k_dim / kGroup) % 8 == 0 && (STAGE == 1 || items <= decode_resident_grid<STAGE, 8>())) {
+    const int grid = std::min(items, decode_resident_grid<STAGE, 8>());
+    hipLaunchKernelGGL((expert_decode_kernel<STAGE, 8>), dim3((unsigned)grid), dim3(256), 0, stream, p);
   } else {
     const int grid = std::min(items, decode_resident_grid<STAGE, 4>());
     hipLaunchKernelGGL((expert_decode_kernel<STAGE, 4>), dim3((unsigned)grid), dim3(256), 0, stream, p);
