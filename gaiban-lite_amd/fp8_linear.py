@@ -168,9 +168,15 @@ def block_fp8_gemm_into(activation: torch.Tensor, activation_scale: torch.Tensor
         if (weight.n, weight.k) != plan.weight_shape:
             raise ValueError(f"prepared weight is {(weight.n, weight.k)}, the plan needs {plan.weight_shape}")
         w_bytes, w_scale = weight.packed, weight.scale
-        if weight_scale is not None and not torch.equal(_e8m0("weight_scale", weight_scale,
-                                                               plan.weight_scale_shape, device), w_scale):
-            raise ValueError("weight_scale differs from the prepared weight's scales")
+        # A prepared weight carries its scales.  A weight_scale given beside it
+        # must be the tensor it was prepared from (same storage and shape):
+        # comparing values would read device memory back, a synchronisation
+        # inside a call that may be captured.
+        if weight_scale is not None:
+            given = _e8m0("weight_scale", weight_scale, plan.weight_scale_shape, device)
+            if given.data_ptr() != w_scale.data_ptr() or given.shape != w_scale.shape:
+                raise ValueError("weight_scale is not the scale tensor the weight was prepared with; "
+                                 "pass None with a prepared weight")
     else:
         w_bytes = C.tensor("weight", weight, shape=plan.weight_shape, dtype=FP8_DTYPE, device=device,
                            contiguous=True)

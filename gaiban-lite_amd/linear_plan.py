@@ -91,6 +91,36 @@ class GemmPlan:
         return self.output_grid + ((self.split_k,) if self.split_k > 1 else ())
 
 
+# Values the reference's Triton launcher accepts for each tuning field
+# (``weight_only_linear.py:147-165``; ``fp8_linear.py`` checks the same set).
+TUNING_CHOICES: Final = {
+    "block_m": (16, 32, 64),
+    "block_n": (32, 64, 128),
+    "num_warps": (4, 8),
+    "num_stages": (2, 3, 4),
+}
+# Output channels per MFMA strip: every linear kernel here writes whole
+# 16-channel strips, so N must be a multiple of this.
+N_MULTIPLE: Final = 16
+
+
+def validate_tuning(tuning: GemmTuning) -> None:
+    """TypeError unless ``tuning`` is a GemmTuning; ValueError for a field that
+    is not an int or not one of the reference's supported values, or a
+    block_n that does not divide the 128-channel weight scale block."""
+
+    if not isinstance(tuning, GemmTuning):
+        raise TypeError(f"tuning: expected GemmTuning, got {type(tuning).__name__}")
+    for field, allowed in TUNING_CHOICES.items():
+        value = getattr(tuning, field)
+        if isinstance(value, bool) or not isinstance(value, int):
+            raise ValueError(f"tuning.{field} must be an int, got {value!r}")
+        if value not in allowed:
+            raise ValueError(f"tuning.{field}={value} is not one of {allowed}")
+    if WEIGHT_BLOCK_N % tuning.block_n:
+        raise ValueError(f"tuning.block_n={tuning.block_n} does not divide the {WEIGHT_BLOCK_N}-channel scale block")
+
+
 def build_plan(m: int, n: int, k: int, *, split_k: int | None, tuning: GemmTuning,
                policy: Callable[[int, int, int], int]) -> GemmPlan:
     """A validated plan; ``policy`` picks the split when ``split_k`` is None.
@@ -98,12 +128,11 @@ def build_plan(m: int, n: int, k: int, *, split_k: int | None, tuning: GemmTunin
     tuning record of the wrong type (TypeError)."""
 
     dims = [C.positive_int(name, v) for name, v in (("m", m), ("n", n), ("k", k))]
-    if not isinstance(tuning, GemmTuning):
-        raise TypeError(f"tuning: expected GemmTuning, got {type(tuning).__name__}")
-    for field in ("block_m", "block_n", "num_warps", "num_stages"):
-        C.positive_int(f"tuning.{field}", getattr(tuning, field))
+    validate_tuning(tuning)
     if dims[2] % BLOCK_K:
         raise ValueError(f"k={k} is not a multiple of {BLOCK_K}")
+    if dims[1] % N_MULTIPLE:
+        raise ValueError(f"n={n} is not a multiple of {N_MULTIPLE}: the kernels store 16-channel strips")
     chosen = policy(*dims) if split_k is None else split_k
     if isinstance(chosen, bool) or chosen not in SUPPORTED_SPLIT_K:
         raise ValueError(f"split_k={chosen!r} is not one of {SUPPORTED_SPLIT_K}")
@@ -112,5 +141,5 @@ def build_plan(m: int, n: int, k: int, *, split_k: int | None, tuning: GemmTunin
     return GemmPlan(*dims, split_k=chosen, tuning=tuning)
 
 
-__all__ = ["BLOCK_K", "DEFAULT_GEMM_TUNING", "GemmPlan", "GemmTuning", "SUPPORTED_SPLIT_K", "WEIGHT_BLOCK_N",
-           "build_plan"]
+__all__ = ["BLOCK_K", "DEFAULT_GEMM_TUNING", "GemmPlan", "GemmTuning", "N_MULTIPLE", "SUPPORTED_SPLIT_K",
+           "TUNING_CHOICES", "WEIGHT_BLOCK_N", "build_plan", "validate_tuning"]

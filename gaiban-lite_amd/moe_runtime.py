@@ -310,6 +310,11 @@ class TP4MoE:
         self.gate = gate
         self.layer_id = resident.layer_id
         self.route_kind = gate.route_kind
+        # Hash layers: when True, every eager call reads the token ids' range
+        # back to the host and raises ValueError for an id outside the table
+        # (a synchronisation per call).  When False (the default, as the
+        # reference's forward), such an id makes the call's output NaN.
+        self.check_hash_token_ids = False
         self.rank = 0
         self.device = device
         self.group = group
@@ -449,6 +454,17 @@ class TP4MoE:
             C.owns_whole_storage(name, t)
         C.distinct_storages(named, what="alignment provider storage")
         return owned
+
+    def _current_ratios(self) -> dict[str, torch.Tensor]:
+        """The W4A16 prefill kernels' scale ratios, recomputed in place first
+        if the resident scales changed since they were derived (a host-side
+        check of the scales' storage and version; no device read)."""
+
+        if self._ratio_kwargs:
+            w13r, w2r = self.resident.scale_ratios()
+            if w13r is not self._ratio_kwargs["w13r"] or w2r is not self._ratio_kwargs["w2r"]:
+                self._ratio_kwargs = {"w13r": w13r, "w2r": w2r}
+        return self._ratio_kwargs
 
     def _runtime_tensors(self) -> list[torch.Tensor]:
         tensors = [self.resident.w13_q, self.resident.w13_s, self.resident.w2_q, self.resident.w2_s,
@@ -795,10 +811,13 @@ class TP4MoE:
                 if not input_ids_local.is_contiguous():
                     raise ValueError("input_ids_local must be contiguous")
                 local_ids = input_ids_local.view(-1)
-                # an id outside the table would route to expert -1; the kernels
-                # would then poison the output with NaN, but an eager call fails
-                # here first (one host read; skipped while a graph is captured)
-                if local_ids.device.type != "cuda" or not torch.cuda.is_current_stream_capturing():
+                # A token id outside the table routes to expert -1 on the device:
+                # the alignment then reports a negative padded count and every
+                # output of the call is NaN.  The host-side range check costs a
+                # device-to-host read per call, so it runs only when the caller
+                # asks for it (check_hash_token_ids), and never under capture.
+                if self.check_hash_token_ids and (
+                        local_ids.device.type != "cuda" or not torch.cuda.is_current_stream_capturing()):
                     C.ids_below("input_ids_local", local_ids, int(self.gate.tid2eid.shape[0]))
             shape = tuple(hidden_local.shape)
             flat = hidden_local.reshape(-1, cfg.hidden_size).contiguous()
@@ -868,7 +887,7 @@ class TP4MoE:
                         flat, logits, self._gate_bias, topk=cfg.topk, score_func=cfg.score_func,
                         route_scale=cfg.route_scale, w13q=self.resident.w13_q,
                         w13s=self.resident.w13_s, w2q=self.resident.w2_q, w2s=self.resident.w2_s,
-                        **self._ratio_kwargs, experts=cfg.experts, inter=cfg.intermediate_size,
+                        **self._current_ratios(), experts=cfg.experts, inter=cfg.intermediate_size,
                         has_shared=self._grouped_shared, clamp_limit=cfg.clamp_limit,
                         block_size=buffers.block_size_m, ids=buffers.route_ids,
                         weights=buffers.route_weights, margin=buffers.margin,
@@ -944,7 +963,7 @@ class TP4MoE:
                     experts_into = ops.experts_w4a16_into
                 experts_into(
                     flat, w13q=self.resident.w13_q, w13s=self.resident.w13_s,
-                    w2q=self.resident.w2_q, w2s=self.resident.w2_s, **self._ratio_kwargs, experts=cfg.experts,
+                    w2q=self.resident.w2_q, w2s=self.resident.w2_s, **self._current_ratios(), experts=cfg.experts,
                     inter=cfg.intermediate_size, has_shared=self._grouped_shared,
                     route_weights=route_weights, sorted_token_ids=a.sorted_token_ids,
                     expert_ids=a.expert_ids, num_tokens_post_padded=a.num_tokens_post_padded,

@@ -221,18 +221,24 @@ def pack_int4_g128(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = F
     return packed, packed_scales
 
 
-def pack_int4_ratios(packed_scales: torch.Tensor, *, n: int, k: int) -> torch.Tensor:
+def pack_int4_ratios(packed_scales: torch.Tensor, *, n: int, k: int,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 ratios of consecutive group scales of ``pack_int4_g128`` scales
     (``dsv4moe_pack_int4_ratios``): same shape and element order, element =
     the row's scale of group g-1 over its scale of group g (0 for g = 0).
-    The W4A16 prefill kernels read them."""
+    The W4A16 prefill kernels read them.  With ``out`` (fp32, the scales'
+    shape) the ratios are written there and nothing is allocated."""
 
     dev = packed_scales.device
     _check("packed_scales", packed_scales, dtype=torch.bfloat16, device=dev)
     if packed_scales.shape[-1] != n * (k // GROUP):
         raise ValueError(f"packed_scales: last dimension {packed_scales.shape[-1]} != n*k/128 = {n * (k // GROUP)}")
     batch = packed_scales.numel() // packed_scales.shape[-1] if packed_scales.ndim > 1 else 1
-    ratios = torch.empty(packed_scales.shape, dtype=torch.float32, device=dev)
+    if out is None:
+        ratios = torch.empty(packed_scales.shape, dtype=torch.float32, device=dev)
+    else:
+        _check("out", out, dtype=torch.float32, device=dev, shape=tuple(packed_scales.shape))
+        ratios = out
     call("dsv4moe_pack_int4_ratios", ptr(packed_scales), batch, n, k, ptr(ratios), _lib.current_stream(dev))
     return ratios
 

@@ -19,7 +19,7 @@ with E' = experts + (1 if shared).
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -146,9 +146,13 @@ class ResidentInt4MoEWeights:
     weight_format: str = "int4_g128"
     shared_fp8: ResidentFP8SharedExpert | None = None  # shared expert in the checkpoint FP8 format
     # fp32 ratios of consecutive group scales (ops.pack_int4_ratios), shaped as
-    # w13_s / w2_s: the W4A16 prefill kernels' running-sum scaling reads them
+    # w13_s / w2_s: the W4A16 prefill kernels' running-sum scaling reads them.
+    # They are derived state: scale_ratios() recomputes them (in place, a
+    # kernel launch, no allocation) whenever w13_s or w2_s was replaced or
+    # written in place since, keyed on the scales' storage and version counter.
     w13_r: torch.Tensor | None = None
     w2_r: torch.Tensor | None = None
+    _ratio_key: tuple | None = field(default=None, repr=False, compare=False)
 
     @property
     def device(self) -> torch.device:
@@ -160,16 +164,29 @@ class ResidentInt4MoEWeights:
         tensors += [t for t in (self.w13_r, self.w2_r) if t is not None]
         return sum(t.numel() * t.element_size() for t in tensors)
 
-    def scale_ratios(self) -> tuple[torch.Tensor, torch.Tensor]:
-        """(w13_r, w2_r), computed on the device from the packed scales the
-        first time (one pass over them) and kept."""
+    def _scales_key(self) -> tuple:
+        return tuple((t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape), t._version)
+                     for t in (self.w13_s, self.w2_s))
 
-        if self.w13_r is None or self.w2_r is None:
-            if self.device.type != "cuda":
-                raise ValueError("scale ratios are computed on the GPU; these weights live on the CPU")
-            h, i = self.hidden_size, self.intermediate_size
-            self.w13_r = ops.pack_int4_ratios(self.w13_s, n=2 * i, k=h)
-            self.w2_r = ops.pack_int4_ratios(self.w2_s, n=h, k=i)
+    def scale_ratios(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """(w13_r, w2_r), computed on the device from the packed scales: the
+        first time into new tensors, later again into the same tensors when
+        the scales changed since (new tensors, or an in-place write, which
+        bumps their version counter).  Checking costs no device access; a
+        recomputation is one kernel launch on the current stream, ordered
+        before the work that follows it there."""
+
+        key = self._scales_key()
+        if self.w13_r is not None and self.w2_r is not None and key == self._ratio_key:
+            return self.w13_r, self.w2_r
+        if self.device.type != "cuda":
+            raise ValueError("scale ratios are computed on the GPU; these weights live on the CPU")
+        h, i = self.hidden_size, self.intermediate_size
+        same_shape = (self.w13_r is not None and self.w2_r is not None
+                      and self.w13_r.shape == self.w13_s.shape and self.w2_r.shape == self.w2_s.shape)
+        self.w13_r = ops.pack_int4_ratios(self.w13_s, n=2 * i, k=h, out=self.w13_r if same_shape else None)
+        self.w2_r = ops.pack_int4_ratios(self.w2_s, n=h, k=i, out=self.w2_r if same_shape else None)
+        self._ratio_key = key
         return self.w13_r, self.w2_r
 
     @property

@@ -39,7 +39,14 @@ What pins each function (checked in ``tests/test_oracle_*.py``):
   scaled, clamped values; ``moe_w4a8_f32`` -- a float64 pipeline built on that
   torch cast (quantised x, bf16 SwiGLU, quantised h, weight on the w2 output,
   shared expert) on tiny shapes.
-* ``hash_route`` -- its closed form (table gather, renormalised sqrt-softplus).
+* ``hash_route`` -- torch's own ``F.softplus(x).sqrt()`` -> ``index_select`` ->
+  ``gather`` -> ``sum`` -> div -> ``* route_scale`` sequence
+  (``moe_forward.py:218-223``) on seeded Flash-shape logits and random tables:
+  ids equal, weights within 8 ulp (``tests/test_oracle_metrics.py``).
+* ``error_metrics`` / ``rel_fro`` -- hand-computed known answers (an
+  asymmetric pair that fixes which argument is the reference, the eps floor
+  of the denominator, the non-finite, shape-mismatch and empty cases) and
+  scale invariance (``tests/test_oracle_metrics.py``).
 * ``moe_bf16_mirror`` -- against a torch restatement of the reference's bf16
   op order (torch's own bf16 matmuls, fp32 clamp / SiLU and casts): at least
   99.9% of the outputs bit-identical, the rest within 2^-8 of the largest
@@ -947,6 +954,8 @@ def error_metrics(observed, reference) -> dict:
     r = np.asarray(reference, dtype=np.float64)
     if o.shape != r.shape:
         raise ValueError("shape mismatch")
+    if o.size == 0:
+        raise ValueError("cannot compare empty tensors")
     if not (np.isfinite(o).all() and np.isfinite(r).all()):
         return {"finite": False, "max_abs": None, "rms_rel": None, "reference_rms": None}
     d = o - r

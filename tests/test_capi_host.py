@@ -183,6 +183,33 @@ def test_block_fp8_plans_mirror_reference_contract():
     assert F.primitive_contract()["supported_split_k"] == [1, 2, 4, 8]
 
 
+@pytest.mark.parametrize("module", ["fp8_linear", "weight_only_linear"])
+def test_gemm_plans_reject_unsupported_tuning_and_n(module):
+    """The reference's tuning checks (``weight_only_linear.py:147-165``): each
+    field must be one of its supported values and block_n must divide the
+    128-channel scale block; N values the HIP kernels cannot run (not a
+    multiple of 16) are refused when the plan is built, not at launch."""
+
+    import importlib
+
+    M = importlib.import_module(f"gaiban_lite_amd.{module}")
+    from gaiban_lite_amd.linear_plan import GemmTuning
+
+    for ok in (GemmTuning(), GemmTuning(16, 128, 8, 2), GemmTuning(64, 32, 4, 4)):
+        assert M.make_gemm_plan(64, 1024, 4096, tuning=ok).tuning == ok
+    for bad in (GemmTuning(block_m=48), GemmTuning(block_m=128), GemmTuning(block_n=256), GemmTuning(block_n=16),
+                GemmTuning(num_warps=2), GemmTuning(num_warps=16), GemmTuning(num_stages=1),
+                GemmTuning(num_stages=5), GemmTuning(block_m=True), GemmTuning(block_n=64.0)):
+        with pytest.raises(ValueError, match="tuning"):
+            M.make_gemm_plan(64, 1024, 4096, tuning=bad)
+    with pytest.raises(TypeError):
+        M.make_gemm_plan(64, 1024, 4096, tuning=(32, 64, 4, 3))
+    for n in (1000, 24, 1):
+        with pytest.raises(ValueError, match="multiple of 16"):
+            M.make_gemm_plan(64, n, 4096)
+    assert M.make_gemm_plan(64, 48, 4096).n == 48
+
+
 def test_workspace_formula():
     # x row sums (per 64 columns) + h + h row sums + fp32 contributions, each 256-byte aligned
     t, k, h, i = 64, 6, 4096, 2048

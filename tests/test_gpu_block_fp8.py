@@ -160,6 +160,9 @@ def test_reference_api_round_trip():
             outs.append(out)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[2], outs[3])
+    # beside a prepared weight only its own scale tensor is accepted (no value compare)
+    with pytest.raises(ValueError, match="prepared"):
+        F.block_fp8_gemm_into(aq, a_s, L.prepare_fp8_block_weight(w, w_s), w_s.clone(), outs[3], ws, plan=gp)
     ref = O.block_fp8_gemm_f32(aq.view(torch.uint8).cpu().numpy(), a_s.view(torch.uint8).cpu().numpy(),
                                codes.cpu().numpy(), scales.cpu().numpy())
     for out in (outs[0], outs[2]):

@@ -204,6 +204,20 @@ def test_hash_gate():
     assert_moe_close(to_np_f32(out.view(48, -1)), oracle_out(layer, x, ref.ids, ref.weights), what="hash")
     with pytest.raises(ValueError):
         layer(x)  # hash routing needs input ids
+    # a token id outside the table: by default no host read, the output is NaN
+    bad_ids = input_ids.clone()
+    bad_ids[0, 5] = vocab
+    poisoned, _ = layer(x, input_ids_local=bad_ids)
+    torch.cuda.synchronize()
+    assert torch.isnan(poisoned.float()).all()
+    # opted in, the eager call is refused before any launch
+    layer.check_hash_token_ids = True
+    with pytest.raises(ValueError, match="outside"):
+        layer(x, input_ids_local=bad_ids)
+    layer.check_hash_token_ids = False
+    again, _ = layer(x, input_ids_local=input_ids)
+    torch.cuda.synchronize()
+    assert torch.equal(again, out)
 
 
 def test_slots_shapes_and_buffer_donor():

@@ -77,3 +77,36 @@ def test_scale_ratios(n, k, batch):
     assert ratios.dtype == torch.float32 and ratios.shape == ps.shape
     assert torch.isfinite(got).all()
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+def test_scale_ratios_follow_in_place_scale_updates():
+    """The resident ratios are derived from the scales: after an in-place
+    write to w13_s / w2_s (or new scale tensors) ``scale_ratios()`` recomputes
+    them into the same tensors, equal to a fresh computation; with the scales
+    unchanged it launches nothing and returns the same tensors."""
+
+    from gaiban_lite_amd.synthetic import LayerShape, make_checkpoint_experts
+    from gaiban_lite_amd.weights import ResidentInt4MoEWeights
+
+    shape = LayerShape(experts=3, hidden=512, inter=256, topk=2, has_shared=True)
+    print("[pack] ratio refresh", flush=True)
+    res = ResidentInt4MoEWeights.from_checkpoint_layout(*make_checkpoint_experts(shape, seed=5, device=DEV),
+                                                        experts=3, has_shared=True)
+    r13, r2 = res.scale_ratios()
+    key = res._ratio_key
+    assert res.scale_ratios() == (r13, r2) and res._ratio_key == key
+    before13, before2 = r13.clone(), r2.clone()
+    res.w13_s[1, :4096].mul_(2.5)   # in place: bumps the version counter
+    res.w2_s[2].mul_(0.75)
+    a13, a2 = res.scale_ratios()
+    assert a13 is r13 and a2 is r2
+    torch.cuda.synchronize()
+    want13 = ops.pack_int4_ratios(res.w13_s, n=2 * shape.inter, k=shape.hidden)
+    want2 = ops.pack_int4_ratios(res.w2_s, n=shape.hidden, k=shape.inter)
+    assert torch.equal(a13, want13) and torch.equal(a2, want2)
+    assert not torch.equal(a13, before13) and not torch.equal(a2, before2)
+    # replacing the scale tensor is seen as well
+    res.w2_s = res.w2_s.clone() * 2.0
+    b13, b2 = res.scale_ratios()
+    torch.cuda.synchronize()
+    assert b2 is r2 and torch.equal(b2, ops.pack_int4_ratios(res.w2_s, n=shape.hidden, k=shape.inter))

@@ -167,6 +167,8 @@ def test_cpu_layer_refuses_to_compute():
 def test_hash_token_ids_outside_the_table_are_rejected():
     table = torch.stack([torch.arange(K) + i % (E - K) for i in range(100)]).to(torch.int64)
     layer = _layer(tid2eid=table)
+    assert layer.check_hash_token_ids is False  # opt-in: one host read per call
+    layer.check_hash_token_ids = True
     x = torch.zeros((1, 4, H), dtype=torch.bfloat16)
     for bad in ([[0, 1, 100, 2]], [[-1, 0, 0, 0]]):
         with pytest.raises(ValueError, match=r"input_ids_local: values span .* outside \[0, 100\)"):
