@@ -17,7 +17,8 @@ from __future__ import annotations
 import sys
 
 from . import _lib, build_ext, contracts, linear_plan, ops, synthetic, weights  # noqa: F401
-from . import checkpoint, deterministic_moe_align, fp8_linear, moe_forward, moe_runtime, weight_only_linear  # noqa: F401
+from . import checkpoint, deterministic_moe_align, fixed_moe_align, fp8_linear, moe_forward, moe_runtime  # noqa: F401
+from . import weight_only_linear  # noqa: F401
 from .deterministic_moe_align import (  # noqa: F401
     DeterministicMoEAlignment,
     allocate_deterministic_moe_alignment,

@@ -135,3 +135,70 @@ def test_route_capture_inside_a_bound_graph(rows):
         assert torch.equal(out_s, eager), f"replay {i} differs from the eager call"
     del graph
     torch.cuda.synchronize()
+
+
+def test_fixed_b240_provider_layout_eager_and_captured():
+    """The fixed B240 provider (``fixed_moe_align.py:67-155,407-421``): its
+    layout equals the oracle's brute force for uniform and skewed [240, 6]
+    routes (an expert with more than one block, unused experts); a layer
+    that aligns through it gives the same bits as the built-in alignment;
+    captured inside ``bind_alignment_provider_for_capture(provider, ...)``
+    and replayed with new inputs it equals eager calls."""
+
+    import numpy as np
+
+    import oracle as O
+    from gaiban_lite_amd import fixed_moe_align as FA
+
+    print("[graph] fixed B240 provider", flush=True)
+    g = torch.Generator(DEV).manual_seed(240)
+    prov = FA.FixedB240MoEAlignmentProvider(device=DEV, global_row_shapes=(240,), slots_per_shape=2,
+                                            route_kind="learned")
+    uniform = torch.argsort(torch.rand((240, 256), device=DEV, generator=g), dim=1)[:, :6].to(torch.int32)
+    skewed = uniform.clone()
+    skewed[:, 0] = 7  # expert 7 in every row: 240 routes = 30 blocks
+    skewed[:40, 1] = 3
+    skewed = torch.where((skewed == 7) & (torch.arange(6, device=DEV) > 0), torch.full_like(skewed, 11), skewed)
+    for ids in (uniform, skewed):
+        out, _ = FA.allocate_fixed_b240_alignment(ids)
+        got = prov(ids, block_size=8, num_experts=256, output=out, slot=0)
+        assert got is out
+        torch.cuda.synchronize()
+        ref = O.moe_align_bruteforce(ids.cpu().numpy(), 8, 256)
+        np.testing.assert_array_equal(out.sorted_token_ids.cpu().numpy(), ref.sorted_token_ids)
+        np.testing.assert_array_equal(out.expert_ids.cpu().numpy(), ref.expert_ids)
+        assert int(out.num_tokens_post_padded.item()) == ref.num_tokens_post_padded
+
+    shape = S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True)
+    base = build(shape, [240])
+    layer = TP4MoE(config=base.config, resident=base.resident, gate=base.gate, device=DEV,
+                   global_row_shapes=[240], slots_per_shape=2, alignment_provider=prov)
+    xs = [S.make_hidden(240, shape.hidden, seed=300 + i, device=DEV).view(1, 240, shape.hidden) for i in range(4)]
+    for x in xs[:2]:
+        a = layer.forward_tensor(x, slot=1)
+        b = base.forward_tensor(x, slot=1)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+    x_s = xs[0].clone()
+    side = torch.cuda.Stream(DEV)
+    side.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            layer.forward_tensor(x_s, slot=0)
+    torch.cuda.current_stream(DEV).wait_stream(side)
+    torch.cuda.synchronize()
+    layer.reset_free_slot_completion_event(240, 0)
+    graph = torch.cuda.CUDAGraph()
+    with layer.bind_alignment_provider_for_capture(prov, buffer_keys=[(240, 0)]):
+        with torch.cuda.graph(graph):
+            out_s = layer.forward_tensor(x_s, slot=0)
+    torch.cuda.synchronize()
+    for i in (1, 2, 3, 0):
+        x_s.copy_(xs[i])
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = base.forward_tensor(xs[i], slot=1)
+        torch.cuda.synchronize()
+        assert torch.equal(out_s, eager), f"replay of input {i} differs from the eager call"
+    del graph
+    torch.cuda.synchronize()
