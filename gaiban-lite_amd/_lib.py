@@ -75,6 +75,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p],
     ),
     "dsv4moe_pack_mxfp4_g32": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p]),
+    "dsv4moe_pack_mxfp4_g32_w4a8": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _i32, _p, _p, _p]),
+    "dsv4moe_experts_w4a8_mxfp4": (
+        ctypes.c_int,
+        [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _p, _p, _i64, _p, _p, _i32,
+         _f32, _p, _p, _sz, _p],
+    ),
     "dsv4moe_layer_mxfp4": (
         ctypes.c_int,
         [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _i32, _f32,

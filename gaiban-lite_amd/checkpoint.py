@@ -156,11 +156,14 @@ def load_resident_mxfp4_layer(
     checkpoint_id: str | None = None,
     progress: Callable[[str], None] | None = None,
     progress_every: int = 32,
+    marlin_input_dtype: torch.dtype | None = None,
 ) -> ResidentMXFP4MoEWeights:
     """Routed experts (MXFP4) and the FP8 shared expert of one layer, this
     rank's intermediate slice (``load_resident_moe_layer``,
     ``marlin_moe.py:270-401``).  ``key_prefix`` overrides
-    ``layers.{layer_id}.ffn`` (the MTP block uses ``mtp.0.ffn``)."""
+    ``layers.{layer_id}.ffn`` (the MTP block uses ``mtp.0.ffn``);
+    ``marlin_input_dtype=torch.float8_e4m3fn`` packs the routed experts for
+    the W4A8 kernels."""
 
     start, end = tp_slice(intermediate_size, rank, world_size)
     local = end - start
@@ -195,12 +198,58 @@ def load_resident_mxfp4_layer(
         shared = load_shared_fp8(reader, prefix, h, start, end, device)
     resident = ResidentMXFP4MoEWeights.from_checkpoint_layout(
         w13, s13, w2, s2, experts=n_experts, has_shared=False, layer_id=layer_id, checkpoint_id=checkpoint_id,
-        shared_fp8=shared,
+        shared_fp8=shared, marlin_input_dtype=marlin_input_dtype,
     )
     del w13, s13, w2, s2
     torch.cuda.synchronize(device)
     resident.load_seconds = time.perf_counter() - started
+    resident.rank, resident.world_size = rank, world_size
+    resident.intermediate_start, resident.intermediate_end = start, end
     return resident
+
+
+def _require_checkpoint_sha256(checkpoint_id) -> str:
+    if (not isinstance(checkpoint_id, str) or len(checkpoint_id) != 64
+            or any(c not in "0123456789abcdef" for c in checkpoint_id)):
+        raise ValueError("resident MoE loads require a lowercase SHA-256 checkpoint_id (64 hex digits)")
+    return checkpoint_id
+
+
+def load_resident_moe_layer(
+    *,
+    stage_root: Path,
+    layer_id: int,
+    rank: int,
+    world_size: int,
+    hidden_size: int,
+    intermediate_size: int,
+    n_experts: int,
+    device: torch.device,
+    progress_every: int = 32,
+    progress: Callable[[str], None] | None = None,
+    checkpoint_id: str | None = None,
+    key_prefix: str | None = None,
+    marlin_input_dtype: torch.dtype | None = None,
+) -> ResidentMXFP4MoEWeights:
+    """The reference's loader entry under its own name and keywords
+    (``runtime/dsv4_direct/ops/marlin_moe.py:270-300``): every routed expert of
+    one layer (MXFP4) and the FP8 shared expert, this rank's intermediate
+    slice, as resident tiles for this library's kernels.  ``checkpoint_id``
+    must be the checkpoint's lowercase SHA-256 (ValueError otherwise, before
+    anything is read); ``marlin_input_dtype`` None gives the W4A16 kernels'
+    packing, ``torch.float8_e4m3fn`` the W4A8 kernels'.  The result carries
+    ``layer_id``, ``rank``, ``world_size``, ``intermediate_start``,
+    ``intermediate_end``, ``checkpoint_id``, ``marlin_input_dtype`` and
+    ``load_seconds`` as the reference's resident record does."""
+
+    _require_checkpoint_sha256(checkpoint_id)
+    if marlin_input_dtype not in (None, torch.float8_e4m3fn):
+        raise ValueError(f"marlin_input_dtype must be None or torch.float8_e4m3fn, not {marlin_input_dtype!r}")
+    return load_resident_mxfp4_layer(
+        stage_root=stage_root, layer_id=layer_id, hidden_size=hidden_size, intermediate_size=intermediate_size,
+        n_experts=n_experts, device=device, rank=rank, world_size=world_size, key_prefix=key_prefix,
+        checkpoint_id=checkpoint_id, progress=progress, progress_every=progress_every,
+        marlin_input_dtype=marlin_input_dtype)
 
 
 def load_shared_fp8(reader: ShardReader, prefix: str, hidden_size: int, start: int, end: int,
@@ -256,6 +305,7 @@ __all__ = [
     "INDEX_NAME",
     "ShardReader",
     "load_gate",
+    "load_resident_moe_layer",
     "load_resident_mxfp4_layer",
     "load_shared_fp8",
     "load_weight_map",

@@ -100,6 +100,11 @@ int dsv4_launch_pack_mxfp4(const uint8_t*, const uint8_t*, int64_t, int64_t, int
 int dsv4_launch_experts_mxfp4(const uint16_t*, int64_t, int, int, int, int, const uint8_t*, const uint8_t*,
                               const uint8_t*, const uint8_t*, int, const float*, const int32_t*, int64_t,
                               const int32_t*, const int32_t*, int, float, uint16_t*, void*, hipStream_t);
+int dsv4_launch_pack_mxfp4_a8(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, int, uint8_t*,
+                              uint8_t*, hipStream_t);
+int dsv4_launch_experts_w4a8_mxfp4(const uint16_t*, int64_t, int, int, int, int, const uint8_t*, const uint8_t*,
+                                   const uint8_t*, const uint8_t*, int, const float*, const int32_t*, int64_t,
+                                   const int32_t*, const int32_t*, int, float, uint16_t*, void*, hipStream_t);
 size_t dsv4_experts_w4a8_workspace_bytes(int64_t, int, int, int, int);
 int dsv4_launch_act_quant_fp8(const uint16_t*, int64_t, int, uint8_t*, float*, float*, hipStream_t);
 int dsv4_launch_experts_w4a8(const uint16_t*, int64_t, int, int, int, int, const uint8_t*,
@@ -452,6 +457,48 @@ int dsv4moe_pack_mxfp4_g32(const uint8_t* canon, const uint8_t* canon_scales, in
   DSV4_REQUIRE(aligned(canon, 4) && aligned(packed, 16), "pack_mxfp4: canon 4-byte / packed 16-byte alignment required");
   return dsv4_launch_pack_mxfp4(canon, canon_scales, batch, n, k, pairing, packed, packed_scales,
                                 static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_pack_mxfp4_g32_w4a8(const uint8_t* canon, const uint8_t* canon_scales, int64_t batch, int64_t n,
+                                int64_t k, int32_t pairing, uint8_t* packed, uint8_t* packed_scales,
+                                void* stream) {
+  clear_error();
+  DSV4_REQUIRE(batch >= 0 && n >= 0 && k >= 0, "pack_mxfp4_w4a8: negative size");
+  DSV4_REQUIRE(n % 32 == 0, "pack_mxfp4_w4a8: n=%lld must be a multiple of 32", (long long)n);
+  DSV4_REQUIRE(pairing == DSV4MOE_PAIR_PLAIN || pairing == DSV4MOE_PAIR_GATED,
+               "pack_mxfp4_w4a8: unknown pairing %d", pairing);
+  DSV4_REQUIRE(k % DSV4MOE_GROUP == 0, "pack_mxfp4_w4a8: k=%lld must be a multiple of 128", (long long)k);
+  if (batch == 0 || n == 0 || k == 0) return DSV4MOE_OK;
+  DSV4_REQUIRE(canon && canon_scales && packed && packed_scales, "pack_mxfp4_w4a8: null pointer");
+  DSV4_REQUIRE(aligned(canon, 4) && aligned(packed, 16),
+               "pack_mxfp4_w4a8: canon 4-byte / packed 16-byte alignment required");
+  return dsv4_launch_pack_mxfp4_a8(canon, canon_scales, batch, n, k, pairing, packed, packed_scales,
+                                   static_cast<hipStream_t>(stream));
+}
+
+int dsv4moe_experts_w4a8_mxfp4(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
+                               int32_t experts, int32_t topk, const uint8_t* w13q, const uint8_t* w13s,
+                               const uint8_t* w2q, const uint8_t* w2s, int32_t has_shared, const float* weights,
+                               const int32_t* sorted_token_ids, int64_t capacity, const int32_t* expert_ids,
+                               const int32_t* num_tokens_post_padded, int32_t block_size, float clamp_limit,
+                               uint16_t* out, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = validate_experts(x, tokens, hidden, inter, experts, topk, w13q,
+                            reinterpret_cast<const uint16_t*>(w13s), w2q, reinterpret_cast<const uint16_t*>(w2s),
+                            capacity, block_size, out, workspace, workspace_bytes, has_shared,
+                            "experts_w4a8_mxfp4", true);
+  if (rc != DSV4MOE_OK || tokens == 0) return rc;
+  DSV4_REQUIRE(weights && sorted_token_ids && expert_ids && num_tokens_post_padded,
+               "experts_w4a8_mxfp4: null route/alignment pointer");
+  DSV4_REQUIRE(!(clamp_limit < 0.0f) && clamp_limit < 3.0e38f,
+               "experts_w4a8_mxfp4: clamp_limit must be >= 0 and finite");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dsv4host::prof_stamp(dsv4host::kStampBegin, s);
+  dsv4host::prof_stamp(dsv4host::kStampRoute, s);
+  dsv4host::prof_stamp(dsv4host::kStampAlign, s);
+  return dsv4_launch_experts_w4a8_mxfp4(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
+                                        has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
+                                        num_tokens_post_padded, block_size, clamp_limit, out, workspace, s);
 }
 
 int dsv4moe_experts_mxfp4(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,

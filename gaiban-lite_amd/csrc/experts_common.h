@@ -188,6 +188,47 @@ inline ExpertWorkspace carve_workspace(void* base, int64_t tokens, int topk, int
   return w;
 }
 
+// Workspace of the W4A8 launchers (caller-owned, 256-byte aligned pieces):
+// e4m3 x and its per-row scales and per-128-K sums, h bf16, e4m3 h with its
+// scales and sums, fp32 contributions.  The MXFP4 W4A8 path carves the same
+// pieces and leaves the sums unused.
+struct Fp8Workspace {
+  uint8_t* xq;
+  float* xscale;
+  float* xsum;
+  uint16_t* h;
+  uint8_t* hq;
+  float* hscale;
+  float* hsum;
+  float* contrib;
+  size_t bytes;
+};
+
+inline Fp8Workspace carve_fp8(void* base, int64_t tokens, int topk, int hidden, int inter, int has_shared) {
+  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
+  char* b = static_cast<char*>(base);
+  size_t off = 0;
+  Fp8Workspace w;
+  w.xq = reinterpret_cast<uint8_t*>(b + off);
+  off += align256((size_t)tokens * hidden);
+  w.xscale = reinterpret_cast<float*>(b + off);
+  off += align256(sizeof(float) * (size_t)tokens);
+  w.xsum = reinterpret_cast<float*>(b + off);
+  off += align256(sizeof(float) * (size_t)tokens * (hidden / dsv4::kGroup));
+  w.h = reinterpret_cast<uint16_t*>(b + off);
+  off += align256(sizeof(uint16_t) * (size_t)rows * inter);
+  w.hq = reinterpret_cast<uint8_t*>(b + off);
+  off += align256((size_t)rows * inter);
+  w.hscale = reinterpret_cast<float*>(b + off);
+  off += align256(sizeof(float) * (size_t)rows);
+  w.hsum = reinterpret_cast<float*>(b + off);
+  off += align256(sizeof(float) * (size_t)rows * (inter / dsv4::kGroup));
+  w.contrib = reinterpret_cast<float*>(b + off);
+  off += align256(sizeof(float) * (size_t)rows * hidden);
+  w.bytes = off;
+  return w;
+}
+
 // Host launchers shared by the expert paths (experts.hip).
 int dsv4_launch_combine(const float* contrib, const int32_t* ntpp, int64_t tokens, int topk, int hidden,
                         int has_shared, uint16_t* out, hipStream_t stream);

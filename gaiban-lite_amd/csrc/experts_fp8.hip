@@ -58,6 +58,9 @@ constexpr float kUnScale = 512.0f;       // 2^9
 // One wavefront per row (K % 512 == 0).  Writes q (e4m3, MFMA order), the
 // row scale and, per 128-K group, the fp32 sum of the 128 e4m3 values (each
 // lane adds its 8 values in K order, then a fixed xor tree over 16 lanes).
+// NATURAL: q in K order and no group sums (the MXFP4 W4A8 kernels' operand,
+// whose K order is the checkpoint's).
+template <bool NATURAL>
 __global__ __launch_bounds__(256) void act_quant_fp8_kernel(const uint16_t* __restrict__ x, int64_t rows,
                                                             int k, uint8_t* __restrict__ q,
                                                             float* __restrict__ scale,
@@ -93,6 +96,15 @@ __global__ __launch_bounds__(256) void act_quant_fp8_kernel(const uint16_t* __re
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / s, -448.0f), 448.0f);
+    if constexpr (NATURAL) {
+      int lo = 0, hi = 0;
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], lo, false);
+      lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], lo, true);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4], f[5], hi, false);
+      hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6], f[7], hi, true);
+      *reinterpret_cast<u32x2*>(q + row * k + o * 8) = u32x2{(uint32_t)lo, (uint32_t)hi};
+      continue;
+    }
     // output byte b holds K offset {0,4,1,5,2,6,3,7}[b]
     int lo = 0, hi = 0;
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[4], lo, false);
@@ -473,8 +485,8 @@ __global__ __launch_bounds__(256, 2) void expert_fp8_prefill_kernel(ExpertGemmPa
 
 static void launch_act_quant(const uint16_t* x, int64_t rows, int k, uint8_t* q, float* scale, float* gsum,
                              hipStream_t stream) {
-  hipLaunchKernelGGL(act_quant_fp8_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, x, rows, k,
-                     q, scale, gsum);
+  hipLaunchKernelGGL(act_quant_fp8_kernel<false>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, x, rows,
+                     k, q, scale, gsum);
 }
 
 template <int STAGE>
@@ -513,47 +525,19 @@ static void launch_fp8_stage(const ExpertGemmParams& p, bool decode, int stage, 
 
 using namespace dsv4;
 
-struct Fp8Workspace {
-  uint8_t* xq;
-  float* xscale;
-  float* xsum;
-  uint16_t* h;
-  uint8_t* hq;
-  float* hscale;
-  float* hsum;
-  float* contrib;
-  size_t bytes;
-};
-
-static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
-
-static Fp8Workspace carve_fp8(void* base, int64_t tokens, int topk, int hidden, int inter, int has_shared) {
-  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
-  char* b = static_cast<char*>(base);
-  size_t off = 0;
-  Fp8Workspace w;
-  w.xq = reinterpret_cast<uint8_t*>(b + off);
-  off += al256((size_t)tokens * hidden);
-  w.xscale = reinterpret_cast<float*>(b + off);
-  off += al256(sizeof(float) * (size_t)tokens);
-  w.xsum = reinterpret_cast<float*>(b + off);
-  off += al256(sizeof(float) * (size_t)tokens * (hidden / kGroup));
-  w.h = reinterpret_cast<uint16_t*>(b + off);
-  off += al256(sizeof(uint16_t) * (size_t)rows * inter);
-  w.hq = reinterpret_cast<uint8_t*>(b + off);
-  off += al256((size_t)rows * inter);
-  w.hscale = reinterpret_cast<float*>(b + off);
-  off += al256(sizeof(float) * (size_t)rows);
-  w.hsum = reinterpret_cast<float*>(b + off);
-  off += al256(sizeof(float) * (size_t)rows * (inter / kGroup));
-  w.contrib = reinterpret_cast<float*>(b + off);
-  off += al256(sizeof(float) * (size_t)rows * hidden);
-  w.bytes = off;
-  return w;
-}
-
 size_t dsv4_experts_w4a8_workspace_bytes(int64_t tokens, int topk, int hidden, int inter, int has_shared) {
   return carve_fp8(nullptr, tokens, topk, hidden, inter, has_shared).bytes;
+}
+
+// Per-row e4m3 quantisation in K order (no group sums): the activation
+// operand of the MXFP4 W4A8 kernels.
+int dsv4_launch_act_quant_fp8_rows(const uint16_t* x, int64_t rows, int k, uint8_t* q, float* scale,
+                                   hipStream_t stream) {
+  if (rows == 0) return DSV4MOE_OK;
+  hipLaunchKernelGGL(act_quant_fp8_kernel<true>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, x, rows,
+                     k, q, scale, nullptr);
+  DSV4_CHECK_LAUNCH("act_quant_fp8_kernel (K order)");
+  return DSV4MOE_OK;
 }
 
 int dsv4_launch_act_quant_fp8(const uint16_t* x, int64_t rows, int k, uint8_t* q, float* scale, float* gsum,

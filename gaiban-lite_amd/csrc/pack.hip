@@ -161,6 +161,33 @@ __global__ __launch_bounds__(256) void pack_mxfp4_kernel(const uint8_t* __restri
   }
 }
 
+// MXFP4 weights for the W4A8 kernels (block-scaled fp8 x fp4 MFMA): the same
+// tile geometry, pair interleave and scale layout, but inside a tile lane L
+// holds the 16 checkpoint bytes of row L%16 for k = 128g + 32*(L/16) .. +31:
+// 32 E2M1 codes of one scale group, the MFMA's fp4 A operand as is.
+__global__ __launch_bounds__(256) void pack_mxfp4_a8_kernel(const uint8_t* __restrict__ canon,
+                                                            uint8_t* __restrict__ packed, int64_t n,
+                                                            int64_t k, int64_t batch, int pairing) {
+  const int64_t groups = k / kGroup;
+  const int64_t tiles_per_mat = (n / 16) * groups;
+  const int64_t total = batch * tiles_per_mat * 64;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(idx & 63);
+    const int64_t tile = idx >> 6;  // destination tile order: (mat, p, g, m)
+    const int64_t mat = tile / tiles_per_mat;
+    const int64_t tin = tile % tiles_per_mat;
+    const int m = (int)(tin & 1);
+    const int64_t g = (tin >> 1) % groups;
+    const int64_t p = (tin >> 1) / groups;
+    const int64_t row = member_row0(p, m, n, pairing) + (lane & 15);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(canon + mat * n * (k / 2) + row * (k / 2) +
+                                                            (g * kGroup + 32 * (lane >> 4)) / 2);
+    const u32x4 out = {src[0], src[1], src[2], src[3]};
+    *reinterpret_cast<u32x4*>(packed + mat * n * (k / 2) + tin * kTileBytes + lane * 16) = out;
+  }
+}
+
 __global__ __launch_bounds__(256) void pack_e8m0_kernel(const uint8_t* __restrict__ canon_s,
                                                         uint8_t* __restrict__ packed_s, int64_t n,
                                                         int64_t k, int64_t batch, int pairing) {
@@ -195,6 +222,28 @@ int dsv4_launch_pack_mxfp4(const uint8_t* canon, const uint8_t* canon_scales, in
   if (work > 0) {
     hipLaunchKernelGGL(pack_mxfp4_kernel, dim3(grid), dim3(256), 0, stream, canon, packed, n, k, batch, pairing);
     DSV4_CHECK_LAUNCH("pack_mxfp4_kernel");
+  }
+  const int64_t swork = batch * n * (k / 32);
+  const int64_t sblocks = (swork + 255) / 256;
+  const unsigned sgrid = (unsigned)(sblocks < 65535 * 16 ? sblocks : 65535 * 16);
+  if (swork > 0) {
+    hipLaunchKernelGGL(pack_e8m0_kernel, dim3(sgrid), dim3(256), 0, stream, canon_scales, packed_scales, n, k,
+                       batch, pairing);
+    DSV4_CHECK_LAUNCH("pack_e8m0_kernel");
+  }
+  return DSV4MOE_OK;
+}
+
+int dsv4_launch_pack_mxfp4_a8(const uint8_t* canon, const uint8_t* canon_scales, int64_t batch, int64_t n,
+                              int64_t k, int pairing, uint8_t* packed, uint8_t* packed_scales,
+                              hipStream_t stream) {
+  const int64_t work = batch * (n / 16) * (k / kGroup) * 64;
+  const int64_t blocks = (work + 255) / 256;
+  const unsigned grid = (unsigned)(blocks < 65535 * 16 ? blocks : 65535 * 16);
+  if (work > 0) {
+    hipLaunchKernelGGL(pack_mxfp4_a8_kernel, dim3(grid), dim3(256), 0, stream, canon, packed, n, k, batch,
+                       pairing);
+    DSV4_CHECK_LAUNCH("pack_mxfp4_a8_kernel");
   }
   const int64_t swork = batch * n * (k / 32);
   const int64_t sblocks = (swork + 255) / 256;

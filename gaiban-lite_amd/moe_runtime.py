@@ -956,7 +956,7 @@ class TP4MoE:
                         self._poison_alignment_runtime()
                         raise RuntimeError("alignment provider must return the caller-owned output")
                 if self._mxfp4:
-                    experts_into = ops.experts_mxfp4_into
+                    experts_into = ops.experts_w4a8_mxfp4_into if self._marlin_input_dtype else ops.experts_mxfp4_into
                 elif self._marlin_input_dtype:
                     experts_into = ops.experts_w4a8_into
                 else:

@@ -243,11 +243,13 @@ def pack_int4_ratios(packed_scales: torch.Tensor, *, n: int, k: int,
     return ratios
 
 
-def pack_mxfp4_g32(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = False
+def pack_mxfp4_g32(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = False, w4a8: bool = False
                    ) -> tuple[torch.Tensor, torch.Tensor]:
     """Checkpoint-layout MXFP4 [.., n, k/2] u8 (E2M1, low nibble = even k) +
     E8M0 scales [.., n, k/32] u8 -> tiles (packed u8 [.., n*k/2], scales u8
-    [.., n*k/32]) in the tile geometry and pairing of ``pack_int4_g128``."""
+    [.., n*k/32]) in the tile geometry and pairing of ``pack_int4_g128``.
+    ``w4a8`` selects the lane layout of the W4A8 kernels
+    (``dsv4moe_pack_mxfp4_g32_w4a8``: one 32-K scale group per lane)."""
 
     if canon.ndim == 2:
         canon = canon.unsqueeze(0)
@@ -262,7 +264,7 @@ def pack_mxfp4_g32(canon: torch.Tensor, scales: torch.Tensor, *, gated: bool = F
     _check("scales", scales, dtype=torch.uint8, shape=(batch, n, k // 32), device=dev)
     packed = torch.empty((batch, n * half_k), dtype=torch.uint8, device=dev)
     packed_scales = torch.empty((batch, n * (k // 32)), dtype=torch.uint8, device=dev)
-    call("dsv4moe_pack_mxfp4_g32", ptr(canon), ptr(scales), batch, n, k,
+    call("dsv4moe_pack_mxfp4_g32_w4a8" if w4a8 else "dsv4moe_pack_mxfp4_g32", ptr(canon), ptr(scales), batch, n, k,
          _lib.PAIR_GATED if gated else _lib.PAIR_PLAIN, ptr(packed), ptr(packed_scales),
          _lib.current_stream(dev))
     if squeeze:
@@ -277,6 +279,32 @@ def experts_workspace_bytes(tokens: int, topk: int, hidden: int, inter: int, has
 def experts_w4a8_workspace_bytes(tokens: int, topk: int, hidden: int, inter: int, has_shared: bool) -> int:
     return int(_lib.load().dsv4moe_experts_w4a8_workspace_bytes(tokens, topk, hidden, inter,
                                                                   int(bool(has_shared))))
+
+
+def w4a8_workspace_views(workspace: torch.Tensor, tokens: int, topk: int, hidden: int, inter: int,
+                         has_shared: bool) -> dict[str, torch.Tensor]:
+    """Views of the pieces of a W4A8 entry's workspace after a call (the
+    layout of ``dsv4moe_experts_w4a8_workspace_bytes``: 256-byte aligned e4m3
+    x [T, H], its fp32 row scales [T] and per-128 sums [T, H/128], bf16 h
+    [R, I], e4m3 h [R, I], its scales [R] and sums [R, I/128], fp32
+    contributions [R, H]; R = T*k (+ T with the shared expert, whose rows
+    follow the routed ones)).  For inspection; nothing is copied."""
+
+    rows = tokens * topk + (tokens if has_shared else 0)
+    pieces = [("xq", torch.uint8, (tokens, hidden)), ("xscale", torch.float32, (tokens,)),
+              ("xsum", torch.float32, (tokens, hidden // GROUP)), ("h", torch.bfloat16, (rows, inter)),
+              ("hq", torch.uint8, (rows, inter)), ("hscale", torch.float32, (rows,)),
+              ("hsum", torch.float32, (rows, inter // GROUP)), ("contrib", torch.float32, (rows, hidden))]
+    views, off = {}, 0
+    for name, dtype, shape in pieces:
+        n = dtype.itemsize
+        for d in shape:
+            n *= d
+        views[name] = workspace[off:off + n].view(dtype).view(shape)
+        off += -(-n // 256) * 256
+    if off > workspace.numel():
+        raise ValueError(f"workspace of {workspace.numel()} bytes is below the {off} the layout needs")
+    return views
 
 
 def act_quant_fp8_into(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor, group_sums: torch.Tensor) -> None:
@@ -297,6 +325,14 @@ def experts_w4a8_into(x: torch.Tensor, **kw) -> None:
     """W4A8 counterpart of ``experts_w4a16_into`` (same keywords)."""
 
     _experts_into("dsv4moe_experts_w4a8", x, **kw)
+
+
+def experts_w4a8_mxfp4_into(x: torch.Tensor, **kw) -> None:
+    """W4A8 over MXFP4 experts (``dsv4moe_experts_w4a8_mxfp4``): same
+    keywords as ``experts_w4a16_into`` with ``pack_mxfp4_g32(w4a8=True)``
+    weights and E8M0 scales; workspace of ``experts_w4a8_workspace_bytes``."""
+
+    _experts_into("dsv4moe_experts_w4a8_mxfp4", x, **kw)
 
 
 def experts_w4a16_into(x: torch.Tensor, **kw) -> None:

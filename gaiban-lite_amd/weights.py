@@ -286,6 +286,24 @@ class ResidentMXFP4MoEWeights:
     weight_format: str = "mxfp4_g32"
     shared_fp8: ResidentFP8SharedExpert | None = None  # shared expert in the checkpoint FP8 format
     load_seconds: float | None = None  # set by the checkpoint loader
+    # the tensor-parallel slice the loader took (world size 1: the whole layer)
+    rank: int = 0
+    world_size: int = 1
+    intermediate_start: int | None = None
+    intermediate_end: int | None = None
+
+    @property
+    def routed(self) -> "ResidentMXFP4MoEWeights":
+        """The routed experts (this container), as the reference's resident
+        record names them."""
+
+        return self
+
+    @property
+    def shared(self) -> ResidentFP8SharedExpert | None:
+        """The FP8 shared expert, as the reference's resident record names it."""
+
+        return self.shared_fp8
 
     @property
     def device(self) -> torch.device:
@@ -304,8 +322,8 @@ class ResidentMXFP4MoEWeights:
         h, i = self.hidden_size, self.intermediate_size
         if h % 512 or i % 512:
             raise ValueError("MXFP4 experts need hidden and intermediate sizes that are multiples of 512")
-        if self.marlin_input_dtype is not None:
-            raise ValueError("MXFP4 experts run with bf16 activations (W4A16)")
+        if self.marlin_input_dtype not in (None, torch.float8_e4m3fn):
+            raise ValueError(f"MXFP4 experts run with bf16 or float8_e4m3fn activations, not {self.marlin_input_dtype}")
         expected = {
             "w13_q": ((e_tot, i * h), torch.uint8),
             "w13_s": ((e_tot, 2 * i * h // 32), torch.uint8),
@@ -333,6 +351,7 @@ class ResidentMXFP4MoEWeights:
         layer_id: int | None = None,
         checkpoint_id: str | None = None,
         shared_fp8: ResidentFP8SharedExpert | None = None,
+        marlin_input_dtype: torch.dtype | None = None,
     ) -> "ResidentMXFP4MoEWeights":
         """Repack stacked checkpoint-layout experts on the device.
 
@@ -341,6 +360,9 @@ class ResidentMXFP4MoEWeights:
         bytes), ``w2_packed`` [E', H, I/2] u8, ``w2_scale`` [E', H, I/32] u8.
         The reserved scale byte 255 (NaN in the reference's decode) is
         rejected with ValueError; the check reads the device (load time).
+        ``marlin_input_dtype=torch.float8_e4m3fn`` packs for the W4A8 kernels
+        (per-token e4m3 activations; the reference's ``is_a_8bit`` repack,
+        ``ops/marlin_moe.py:197-222``): same bytes, another lane layout.
         """
 
         def as_u8(t):
@@ -354,10 +376,15 @@ class ResidentMXFP4MoEWeights:
             raise ValueError("expert count does not match the stacked tensors")
         C.no_reserved_e8m0("w13_scale", w13_scale)
         C.no_reserved_e8m0("w2_scale", w2_scale)
-        q13, s13 = ops.pack_mxfp4_g32(as_u8(w13_packed).contiguous(), as_u8(w13_scale).contiguous(), gated=True)
-        q2, s2 = ops.pack_mxfp4_g32(as_u8(w2_packed).contiguous(), as_u8(w2_scale).contiguous(), gated=False)
+        if marlin_input_dtype not in (None, torch.float8_e4m3fn):
+            raise ValueError(f"unsupported marlin_input_dtype {marlin_input_dtype!r}")
+        a8 = marlin_input_dtype is not None
+        q13, s13 = ops.pack_mxfp4_g32(as_u8(w13_packed).contiguous(), as_u8(w13_scale).contiguous(), gated=True,
+                                      w4a8=a8)
+        q2, s2 = ops.pack_mxfp4_g32(as_u8(w2_packed).contiguous(), as_u8(w2_scale).contiguous(), gated=False,
+                                    w4a8=a8)
         out = cls(q13, s13, q2, s2, experts, hidden, inter, has_shared, layer_id, checkpoint_id,
-                  shared_fp8=shared_fp8)
+                  marlin_input_dtype=marlin_input_dtype, shared_fp8=shared_fp8)
         out.validate()
         return out
 

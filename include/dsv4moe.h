@@ -300,6 +300,34 @@ int dsv4moe_experts_mxfp4(const uint16_t* x, int64_t tokens, int32_t hidden, int
                           size_t workspace_bytes, void* stream);
 
 /*
+ * W4A8 over MXFP4 experts: the reference's W4A8 mode on its checkpoint
+ * format, _fused_marlin_moe(input_dtype=float8_e4m3fn) over MXFP4 weights
+ * with the is_a_8bit repack (runtime/dsv4_direct/ops/marlin_moe.py:197-222,
+ * moe_runtime.py:207-235,1829-1856).
+ *
+ * dsv4moe_pack_mxfp4_g32_w4a8 repacks checkpoint-layout weights as
+ * dsv4moe_pack_mxfp4_g32 (same arguments, tile geometry, pairing and
+ * packed_scales), except inside a tile: lane L holds the 16 checkpoint bytes
+ * of row L%16 for k = 128g + 32*(L/16) .. +31, i.e. one 32-K scale group.
+ * dsv4moe_experts_w4a8_mxfp4: as dsv4moe_experts_w4a8 (workspace from
+ * dsv4moe_experts_w4a8_workspace_bytes) with those weights: x and the
+ * SwiGLU output h are quantised per row to e4m3 (s = max(amax, 1e-12) / 448),
+ * each 32-K product of E2M1 codes and e4m3 codes is scaled by the group's
+ * E8M0 byte inside the block-scaled fp8 x fp4 MFMA, fp32 accumulation, the
+ * row scale applied to the result.  hidden % 512 == 0, inter % 512 == 0.
+ */
+int dsv4moe_pack_mxfp4_g32_w4a8(const uint8_t* canon, const uint8_t* canon_scales, int64_t batch,
+                                int64_t n, int64_t k, int32_t pairing, uint8_t* packed,
+                                uint8_t* packed_scales, void* stream);
+int dsv4moe_experts_w4a8_mxfp4(const uint16_t* x, int64_t tokens, int32_t hidden, int32_t inter,
+                               int32_t experts, int32_t topk, const uint8_t* w13q, const uint8_t* w13s,
+                               const uint8_t* w2q, const uint8_t* w2s, int32_t has_shared,
+                               const float* weights, const int32_t* sorted_token_ids, int64_t capacity,
+                               const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                               int32_t block_size, float clamp_limit, uint16_t* out, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/*
  * Whole MoE layer over MXFP4 experts: route (from logits) -> align ->
  * experts (dsv4moe_experts_mxfp4) -> combine, as dsv4moe_layer_w4a16 (same
  * arguments; w13s / w2s are the packed E8M0 bytes).  Replaces

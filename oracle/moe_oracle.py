@@ -47,6 +47,10 @@ What pins each function (checked in ``tests/test_oracle_*.py``):
   asymmetric pair that fixes which argument is the reference, the eps floor
   of the denominator, the non-finite, shape-mismatch and empty cases) and
   scale invariance (``tests/test_oracle_metrics.py``).
+* ``moe_w4a8_mxfp4_f32`` -- the same float64 pipeline over torch's
+  ``float8_e4m3fn`` cast and ``torch_path.dequant_mxfp4`` (itself bit-exact
+  with the reference's dequantiser), with E8M0 scales spread over 2^-30 ..
+  2^10 per 32-K group (``tests/test_oracle_ffn.py``).
 * ``moe_bf16_mirror`` -- against a torch restatement of the reference's bf16
   op order (torch's own bf16 matmuls, fp32 clamp / SiLU and casts): at least
   99.9% of the outputs bit-identical, the rest within 2^-8 of the largest
@@ -99,12 +103,14 @@ __all__ = [
     "moe_bf16_mirror",
     "moe_fp32",
     "moe_w4a8_f32",
+    "moe_w4a8_mxfp4_f32",
     "pack_int4_rows",
     "rel_fro",
     "route_scores",
     "route_topk",
     "sigmoid_f32",
     "softmax_f32",
+    "swiglu_f32",
     "sqrtsoftplus_f32",
     "unpack_int4_rows",
     "shared_fp8_bf16",
@@ -590,6 +596,13 @@ def _swiglu(g: np.ndarray, u: np.ndarray, clamp_limit: float) -> np.ndarray:
     return (_silu(g) * u).astype(F32)
 
 
+def swiglu_f32(g, u, clamp_limit: float) -> np.ndarray:
+    """The expert activation in fp32 (``model.py:598-603``), as ``moe_fp32``
+    applies it: clamp (when ``clamp_limit`` > 0), then SiLU(gate) * up."""
+
+    return _swiglu(np.asarray(g, dtype=F32), np.asarray(u, dtype=F32), clamp_limit)
+
+
 class ExpertSource:
     """Accessor for int4-g128 experts in the canonical layout.
 
@@ -830,6 +843,28 @@ def moe_w4a8_f32(
     if shared_index is not None:
         y += ffn(xd, shared_index, F32(1.0))
     return y.astype(F32)
+
+
+def moe_w4a8_mxfp4_f32(
+    x,
+    ids,
+    weights,
+    experts: MXFP4ExpertSource,
+    *,
+    shared_index: int | None = None,
+    clamp_limit: float = 0.0,
+    rows=None,
+) -> np.ndarray:
+    """W4A8 over the checkpoint's MXFP4 experts (the reference's W4A8 mode on
+    its routed-expert format: ``_fused_marlin_moe(input_dtype=fp8)`` over
+    MXFP4 weights with the ``is_a_8bit`` repack, ``ops/marlin_moe.py:197-222``,
+    ``moe_runtime.py:207-235``): the ``moe_w4a8_f32`` pipeline -- per-token
+    e4m3 x and h, bf16 SwiGLU output, weight on the w2 output -- over the
+    exactly dequantised E2M1 * 2^(e-127) weights."""
+
+    if not isinstance(experts, MXFP4ExpertSource):
+        raise TypeError("moe_w4a8_mxfp4_f32 takes an MXFP4ExpertSource")
+    return moe_w4a8_f32(x, ids, weights, experts, shared_index=shared_index, clamp_limit=clamp_limit, rows=rows)
 
 
 def automatic_split_k(m: int, n: int, k: int, block_m: int = 32, block_n: int = 64,

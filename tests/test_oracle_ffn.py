@@ -173,6 +173,53 @@ def test_moe_w4a8_oracle_against_torch_fp8_pipeline():
     assert O.rel_fro(got, O.moe_fp32(x, ids, w, src, shared_index=e, clamp_limit=0.4)) > 1e-3
 
 
+def test_moe_w4a8_mxfp4_oracle_against_torch_fp8_pipeline():
+    """MXFP4 W4A8 oracle vs an independent float64 pipeline: torch's
+    float8_e4m3fn cast for x and h, the MXFP4 weights dequantised by the
+    torch restatement of the reference's table lookup (``torch_path.
+    dequant_mxfp4``), E8M0 scales spread over 2^-30 .. 2^10 per 32-K group."""
+
+    import torch
+
+    from oracle import torch_path as TP
+
+    rng = np.random.default_rng(19)
+    e, h, i, t, k = 3, 256, 128, 5, 2
+    w13 = rng.integers(0, 256, size=(e + 1, 2 * i, h // 2), dtype=np.uint8)
+    s13 = rng.integers(97, 138, size=(e + 1, 2 * i, h // 32), dtype=np.uint8)
+    w2 = rng.integers(0, 256, size=(e + 1, h, i // 2), dtype=np.uint8)
+    s2 = rng.integers(97, 138, size=(e + 1, h, i // 32), dtype=np.uint8)
+    src = O.MXFP4ExpertSource(w13, s13, w2, s2)
+    x = O.bf16_round((rng.standard_normal((t, h)) * 3).astype(np.float32))
+    ids = np.array([[0, 2], [1, 0], [2, 1], [0, 1], [2, 0]])
+    w = rng.uniform(0.1, 1.0, size=(t, k)).astype(np.float32)
+    got = O.moe_w4a8_mxfp4_f32(x, ids, w, src, shared_index=e, clamp_limit=0.0)
+
+    def quant(v):
+        v = torch.from_numpy(np.asarray(v, dtype=np.float32))
+        s = v.abs().amax(-1, keepdim=True).clamp_min(1e-12) / 448.0
+        q = (v / s).clamp(-448, 448).to(torch.float8_e4m3fn).to(torch.float64)
+        return (q * s.double()).numpy()
+
+    def deq(codes, scales):
+        return TP.dequant_mxfp4(torch.from_numpy(codes), torch.from_numpy(scales)).double().numpy()
+
+    xd = quant(x)
+    ref = np.zeros((t, h))
+    for tok in range(t):
+        pairs = [(ids[tok, j], float(w[tok, j])) for j in range(k)] + [(e, 1.0)]
+        for ex, weight in pairs:
+            m13 = deq(w13[ex], s13[ex])
+            g = xd[tok] @ m13[:i].T
+            u = xd[tok] @ m13[i:].T
+            act = torch.from_numpy((g / (1 + np.exp(-g)) * u).astype(np.float32)).to(torch.bfloat16).float().numpy()
+            ref[tok] += (quant(act[None])[0] @ deq(w2[ex], s2[ex]).T) * weight
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    assert O.rel_fro(got, O.moe_fp32(x, ids, w, src, shared_index=e)) > 1e-3
+    with pytest.raises(TypeError):
+        O.moe_w4a8_mxfp4_f32(x, ids, w, _tiny_source(rng, e + 1, 128, 128))
+
+
 def test_e8m0_decode_matches_torch_float8_e8m0fnu():
     """The reference decodes scales with scale.view(torch.float8_e8m0fnu).float()
     (moe_forward.py:115-123); the oracle's decode equals it for every byte but
