@@ -88,7 +88,7 @@ def parse():
     ap.add_argument("--traffic-run", action="store_true",
                     help="child program of the traffic passes: one decode call per pooled batch, then two copies")
     ap.add_argument("--profile-run", default=None, metavar="FMT:T:N[:graph]",
-                    help="only run N layer calls (FMT int4|mxfp4|w4a8, T tokens) for rocprofv3 counter passes; "
+                    help="only run N layer calls (FMT int4|mxfp4|w4a8|w4a8-mxfp4, T tokens) for rocprofv3 counter passes; "
                          ":graph adds N replays of the captured call; FMT linear-w8a8|linear-w8a16: N calls of "
                          "the dense linear at M=T, K=4096, N in {1024, 4096, 16384} (tiled weights)")
     return ap.parse_args()
@@ -547,6 +547,7 @@ def main() -> int:
         secondary["decode_graph"] = bench_graph(layer, S, dev, [1, 8, T], H, E)
         secondary["w4a8"] = bench_w4a8(pkg, resident, gate, cfg, dev, T, args)
         secondary["mxfp4"] = bench_mxfp4(pkg, gate, cfg, dev, T, args)
+        secondary["w4a8_mxfp4"] = bench_w4a8_mxfp4(pkg, gate, cfg, dev, T, args)
         secondary["fp8_shared"] = bench_shared_fp8(pkg, gate, cfg, dev, T, args)
         secondary["w8a16_linear"] = bench_w8a16(pkg, dev)
         secondary["w8a16_fp8_block_linear"] = bench_w8a16(pkg, dev, fmt="fp8")
@@ -695,7 +696,26 @@ def bench_graph(layer, S, dev, ts, H, E):
     return out
 
 
-def bench_w4a8(pkg, resident, gate, cfg, dev, T, args):
+def bench_w4a8_mxfp4(pkg, gate, cfg, dev, T, args):
+    """W4A8 over the checkpoint's MXFP4 experts (E2M1 codes with E8M0 per-32
+    scales against per-token e4m3 activations on the block-scaled fp8 x fp4
+    MFMA): the lines of ``bench_w4a8`` with those weights."""
+
+    import torch
+
+    S = pkg.synthetic
+    w13, s13, w2, s2 = S.make_checkpoint_experts_mxfp4(S.FLASH, seed=args.seed, device=dev)
+    res = pkg.ResidentMXFP4MoEWeights.from_checkpoint_layout(w13, s13, w2, s2, experts=cfg.experts, has_shared=True,
+                                                              marlin_input_dtype=torch.float8_e4m3fn)
+    del w13, s13, w2, s2
+    out = bench_w4a8(pkg, res, gate, cfg, dev, T, args, experts_into=pkg.ops.experts_w4a8_mxfp4_into,
+                     label="w4a8 mxfp4")
+    del res
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_w4a8(pkg, resident, gate, cfg, dev, T, args, experts_into=None, label="w4a8"):
     """W4A8 experts (fp8 activations, the same resident int4 weights) at the
     decode T and the prefill size, uniform routing (router from logits) and
     Zipf(1.1) routing (fixed ids); a step is route (uniform only) + alignment +
@@ -704,6 +724,7 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args):
     import torch
 
     S, ops = pkg.synthetic, pkg.ops
+    experts_into = experts_into or ops.experts_w4a8_into
     E, H, I, K = cfg.experts, cfg.hidden_size, cfg.intermediate_size, cfg.topk
     ts = [T] + ([args.prefill_tokens] if args.prefill_tokens else [])
     out = {}
@@ -729,11 +750,11 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args):
                     ids.copy_(zipf_ids)
                 ops.align_into(ids, block_size=bs, num_experts=E, sorted_token_ids=sorted_ids,
                                expert_ids=expert_ids, num_tokens_post_padded=ntpp, workspace=ws)
-                ops.experts_w4a8_into(x, w13q=resident.w13_q, w13s=resident.w13_s, w2q=resident.w2_q,
-                                      w2s=resident.w2_s, experts=E, inter=I, has_shared=True, route_weights=w,
-                                      sorted_token_ids=sorted_ids, expert_ids=expert_ids,
-                                      num_tokens_post_padded=ntpp, block_size=bs, clamp_limit=0.0, out=o,
-                                      workspace=ws)
+                experts_into(x, w13q=resident.w13_q, w13s=resident.w13_s, w2q=resident.w2_q,
+                             w2s=resident.w2_s, experts=E, inter=I, has_shared=True, route_weights=w,
+                             sorted_token_ids=sorted_ids, expert_ids=expert_ids,
+                             num_tokens_post_padded=ntpp, block_size=bs, clamp_limit=0.0, out=o,
+                             workspace=ws)
             ops.route_topk_into(lg, None, topk=K, score_func="sigmoid", route_scale=1.0, ids=ids, weights=w)
             for i in range(3):
                 step(i)
@@ -750,7 +771,7 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args):
             if routing == "zipf":
                 entry["hottest_over_mean_load"] = round(float(counts.max() / counts.mean()), 1)
             out[f"T{t}_{routing}"] = entry
-            log(f"[bench] w4a8 T={t} {routing}: {entry}")
+            log(f"[bench] {label} T={t} {routing}: {entry}")
         del x, lg, o, ws
     return out
 
@@ -1071,7 +1092,7 @@ def profile_run_linear(pkg, fmt: str, m: int, n: int, dev) -> int:
 
 def profile_run(pkg, spec: str, seed: int) -> int:
     """``--profile-run FMT:T:N[:graph]``: build the Flash layer in format FMT
-    (int4, mxfp4 or w4a8), run one warm-up and N ``TP4MoE.forward_tensor``
+    (int4, mxfp4, w4a8 or w4a8-mxfp4), run one warm-up and N ``TP4MoE.forward_tensor``
     calls at T tokens, and exit -- the program the rocprofv3 counter passes
     and kernel traces wrap.  With ``:graph`` the call is then captured once
     as a HIP graph and replayed N times (eager and replayed kernels in one
@@ -1093,20 +1114,22 @@ def profile_run(pkg, spec: str, seed: int) -> int:
         return profile_run_linear(pkg, fmt, t, n, dev)
     shape = S.FLASH
     E, H, I, K = shape.experts, shape.hidden, shape.inter, shape.topk
-    if fmt == "mxfp4":
+    fp8_act = fmt in ("w4a8", "w4a8-mxfp4")
+    if fmt in ("mxfp4", "w4a8-mxfp4"):
         res = pkg.ResidentMXFP4MoEWeights.from_checkpoint_layout(
-            *S.make_checkpoint_experts_mxfp4(shape, seed=seed, device=dev), experts=E, has_shared=True)
+            *S.make_checkpoint_experts_mxfp4(shape, seed=seed, device=dev), experts=E, has_shared=True,
+            marlin_input_dtype=torch.float8_e4m3fn if fp8_act else None)
     elif fmt in ("int4", "w4a8"):
         res = pkg.ResidentInt4MoEWeights.from_checkpoint_layout(
             *S.make_checkpoint_experts(shape, seed=seed, device=dev), experts=E, has_shared=True,
             marlin_input_dtype=torch.float8_e4m3fn if fmt == "w4a8" else None)
     else:
-        raise SystemExit(f"--profile-run: unknown format {fmt!r} (int4, mxfp4, w4a8)")
+        raise SystemExit(f"--profile-run: unknown format {fmt!r} (int4, mxfp4, w4a8, w4a8-mxfp4)")
     cfg = pkg.TP4MoEConfig(hidden_size=H, intermediate_size=I, experts=E, topk=K, route_scale=1.0, clamp_limit=0.0,
                            score_func="sigmoid", shared_experts=1)
     gate = pkg.ResidentGateWeights(weight=torch.zeros((E, H), dtype=torch.bfloat16, device=dev))
     layer = pkg.TP4MoE(config=cfg, resident=res, gate=gate, device=dev, global_row_shapes=[t],
-                       marlin_input_dtype=torch.float8_e4m3fn if fmt == "w4a8" else None)
+                       marlin_input_dtype=torch.float8_e4m3fn if fp8_act else None)
     x = S.make_hidden(t, H, seed=3000, device=dev).view(1, t, H)
     logits = S.make_logits(t, E, seed=3001, device=dev)
     layer.forward_tensor(x, router_logits=logits)
