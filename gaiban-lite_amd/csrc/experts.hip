@@ -241,12 +241,15 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(E
 //   STAGE 1: gate strips (n0 + 32w)/16 + {0,1} and the matching up strips,
 //            n0 = tile * 128 (the workgroup covers h columns [n0, n0+128));
 //   STAGE 2: strips (n0 + 64w)/16 + {0..3}, n0 = tile * 256.
-// Per group the 64 x 128 token tile and its 64 group sums are copied into LDS
-// by buffer_load ... lds (double buffered, one group ahead); each wavefront
-// reads 4 B fragments per K step and issues 16 MFMAs.  Work items (block,
-// tile) follow prefill_item: groups of consecutive blocks run tile by tile on
-// one XCD, so a weight tile is fetched once for the group and a block's token
-// rows stay in that XCD's L2 across its tiles.
+// Per group the 64 x 128 token tile, its 64 group sums and each wavefront's
+// scale ratios are copied into LDS by buffer_load ... lds (double buffered,
+// one group ahead); each wavefront's weight tiles are private to it and go
+// straight into registers, one group ahead, so LDS carries only the shared
+// operand.  Each wavefront reads 4 B fragments per K step and issues 16
+// MFMAs.  Work items (block, tile) follow prefill_item: groups of
+// consecutive blocks run tile by tile on one XCD, so a weight tile is
+// fetched once for the group and a block's token rows stay in that XCD's L2
+// across its tiles.
 constexpr int kPfSlots = 64;
 
 template <int STAGE>
@@ -256,11 +259,9 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   //  * token tile: 64 slots x 256 B, 16-byte part p of slot s stored at part
   //    p ^ (s & 15) (conflict-free ds_read_b128 of the B fragments);
   //  * the 64 slots' two 64-wide activation sums;
-  //  * each wavefront's 4 weight tiles (4 KiB) and their 16-row scale ratios
-  //    (fp32, 256 B).
+  //  * each wavefront's 16-row scale ratios (fp32, 256 B).
   // Padded slots read zeros (out-of-range buffer offsets).
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kPfSlots * 256];
-  __shared__ __attribute__((aligned(16))) uint8_t wts[2][4][R * kTileBytes];
   // 64 lanes x 4 B per ratio DMA: lanes 0..31 carry pair p0's 128-byte block,
   // lanes 32..63 pair p0 + 1's.
   __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];
@@ -319,15 +320,35 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
 #pragma unroll
     for (int q = 0; q < 4; ++q)
       lds_copy16(act_rsrc, lds_addr(&xs[buf][(16 * wave + 4 * q) * 256]), dma_off[q], g * 256);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][0]), w_off0, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][kTileBytes]), w_off0 + kTileBytes, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][2 * kTileBytes]), w_off1, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][3 * kTileBytes]), w_off1 + kTileBytes, g * 2048);
     lds_copy4(r_rsrc, lds_addr(&scl[buf][wave][0]), r_off, g * 128);
     if (wave == 0) {
       lds_copy4(sum_rsrc, lds_addr(&xsum[buf][0][0]), sum_off, g * 8);
       lds_copy4(sum_rsrc, lds_addr(&xsum[buf][1][0]), sum_off, g * 8 + 4);
     }
+  };
+  // The weight tiles are private to the wavefront: loaded straight into
+  // registers, one group ahead, as inline asm -- the compiler neither counts
+  // them in its own vmcnt waits nor lets their uses move above wait_weights,
+  // which takes the registers as in/out operands.  The registers in flight
+  // must not be touched in between: the kernel must compile without spills
+  // (tests/test_kernel_resources.py checks the compiled code object).
+  struct WRegs {
+    u32x4 w[R];
+  };
+  auto load_weights = [&](int g, WRegs& o) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t gw = __builtin_amdgcn_readfirstlane((uint32_t)g * 2048u);
+    const uint32_t w0b = w_off0 + kTileBytes, w1b = w_off1 + kTileBytes;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(o.w[0]) : "v"(w_off0), "s"(w_rsrc), "s"(gw));
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(o.w[1]) : "v"(w0b), "s"(w_rsrc), "s"(gw));
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(o.w[2]) : "v"(w_off1), "s"(w_rsrc), "s"(gw));
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(o.w[3]) : "v"(w1b), "s"(w_rsrc), "s"(gw));
+#endif
+  };
+  auto wait_weights = [&](WRegs& o) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(o.w[0]), "+v"(o.w[1]), "+v"(o.w[2]), "+v"(o.w[3]) : : "memory");
+#endif
   };
 
   // Token columns that hold a valid slot: the alignment pads each expert's
@@ -356,15 +377,14 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
 
     const int sw = lane & 15;  // swizzle key of this lane's slots (ct*16 + sw)
     const uint32_t magic = dequant_magic();
-    // One group: optionally prefetch group g+1 into the other buffers, then
-    // the fold and 64 MFMAs.
-    auto step = [&](int g, auto u_c, auto prefetch_c) {
+    // One group: optionally prefetch group g+1 into the other buffers and
+    // registers, then the fold and 64 MFMAs.
+    auto step = [&](int g, auto u_c, auto prefetch_c, const WRegs& cur, WRegs& nxt) {
       constexpr int u = decltype(u_c)::value;
-      if constexpr (decltype(prefetch_c)::value) issue(g + 1, (u + 1) & 1);
-      u32x4 wv[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        wv[r] = *reinterpret_cast<const u32x4*>(&wts[u][wave][r * kTileBytes + lane * 16]);
+      if constexpr (decltype(prefetch_c)::value) {
+        issue(g + 1, (u + 1) & 1);
+        load_weights(g + 1, nxt);
+      }
       float nc[C];
 #pragma unroll
       for (int ct = 0; ct < C; ++ct)
@@ -384,7 +404,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
               bf16x8, *reinterpret_cast<const u32x4*>(&xs[u][(ct * 16 + sw) * 256 + part]));
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const bf16x8 a = dequant_biased(wv[r][d], magic);
+          const bf16x8 a = dequant_biased(cur.w[r][d], magic);
 #pragma unroll
           for (int ct = 0; ct < C; ++ct) {
             if (d == 0) {
@@ -395,25 +415,30 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
           }
         }
       }
-      lds_dma_wait_all();
-      __syncthreads();
+      if constexpr (decltype(prefetch_c)::value)
+        wait_weights(nxt);  // this wavefront's copies and loads of group g + 1 have landed
+      else
+        lds_dma_wait_all();
+      __syncthreads();     // ... and everyone's; buffer u is free again
     };
     using U0 = std::integral_constant<int, 0>;
     using U1 = std::integral_constant<int, 1>;
     using PF = std::true_type;
     using NOPF = std::false_type;
 
+    WRegs wa, wb;
     issue(0, 0);
-    lds_dma_wait_all();
+    load_weights(0, wa);
+    wait_weights(wa);
     __syncthreads();
     // groups is even (checked on the host); the last group issues no prefetch,
-    // so no LDS DMA is in flight when the workgroup leaves the loop.
+    // so no copy or load is in flight when the workgroup leaves the loop.
     for (int g0 = 0; g0 + 2 < groups; g0 += 2) {
-      step(g0, U0{}, PF{});
-      step(g0 + 1, U1{}, PF{});
+      step(g0, U0{}, PF{}, wa, wb);
+      step(g0 + 1, U1{}, PF{}, wb, wa);
     }
-    step(groups - 2, U0{}, PF{});
-    step(groups - 1, U1{}, NOPF{});
+    step(groups - 2, U0{}, PF{}, wa, wb);
+    step(groups - 1, U1{}, NOPF{}, wb, wa);
     // the last group's scales (bf16, 4 rows of strip r per lane)
     float slast[R][4];
 #pragma unroll

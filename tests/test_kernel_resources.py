@@ -129,6 +129,22 @@ def test_mxfp4_prefill_reads_no_register_in_flight(tmp_path):
         assert inflight_register_reads(asm, name) == [], name
 
 
+def test_int4_prefill_kernel_register_weights(tmp_path):
+    """The int4 (W4A16) prefill kernel keeps its next weight group in
+    registers loaded by inline assembly as well: no spills, and nothing reads
+    those registers before the explicit wait."""
+
+    meta = kernel_metadata(CSRC / "experts.hip", tmp_path)
+    prefill = {k: v for k, v in meta.items() if "expert_prefill_kernel" in k}
+    assert len(prefill) == 2
+    for name, m in prefill.items():
+        assert m["vgpr_spill_count"] == 0, name
+        assert m["sgpr_spill_count"] == 0, name
+    asm = _device_asm(CSRC / "experts.hip", tmp_path)
+    for name in prefill:
+        assert inflight_register_reads(asm, name) == [], name
+
+
 def _device_asm(src: Path, tmp_path: Path) -> str:
     from gaiban_lite_amd import build_ext
 
