@@ -548,6 +548,7 @@ def main() -> int:
         secondary["w4a8"] = bench_w4a8(pkg, resident, gate, cfg, dev, T, args)
         secondary["mxfp4"] = bench_mxfp4(pkg, gate, cfg, dev, T, args)
         secondary["w4a8_mxfp4"] = bench_w4a8_mxfp4(pkg, gate, cfg, dev, T, args)
+        secondary["vendor_bf16_gemm"] = bench_vendor_bf16_gemm(dev)
         secondary["fp8_shared"] = bench_shared_fp8(pkg, gate, cfg, dev, T, args)
         secondary["w8a16_linear"] = bench_w8a16(pkg, dev)
         secondary["w8a16_fp8_block_linear"] = bench_w8a16(pkg, dev, fmt="fp8")
@@ -693,6 +694,33 @@ def bench_graph(layer, S, dev, ts, H, E):
         del graph
         torch.cuda.synchronize()
         layer.reset_free_slot_completion_event(t, 0)
+    return out
+
+
+def bench_vendor_bf16_gemm(dev):
+    """The vendor library's dense bf16 GEMM (torch.bmm, hipBLASLt / rocBLAS)
+    on plain bf16 operands at this layer's per-expert shapes -- 256 experts x
+    192 tokens (the uniform T=8192 load) through w13 [4096 x 4096] and w2
+    [4096 x 2048] -- and on a large square GEMM: what a tuned dense GEMM
+    sustains on this GPU at its load-time clocks, with no dequantisation, as
+    context for the prefill fractions of the nominal 2.5 PFLOP/s peak."""
+
+    import torch
+
+    out = {}
+    for name, (batch, m, n, k, reps) in {"experts_w13_256x192x4096x4096": (256, 192, 4096, 4096, 10),
+                                         "experts_w2_256x192x4096x2048": (256, 192, 4096, 2048, 10),
+                                         "square_8192": (1, 8192, 8192, 8192, 5)}.items():
+        a = torch.randn(batch, m, k, device=dev, dtype=torch.bfloat16)
+        b = torch.randn(batch, k, n, device=dev, dtype=torch.bfloat16)  # contiguous right operand
+        for _ in range(3):
+            torch.bmm(a, b)
+        ms = cuda_timer(lambda i: torch.bmm(a, b), reps)
+        tf = 2.0 * batch * m * n * k / (ms * 1e-3) / 1e12
+        out[name] = {"ms": round(ms, 4), "tflops": round(tf, 1), "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+        log(f"[bench] vendor bf16 GEMM {name}: {out[name]}")
+        del a, b
+    torch.cuda.empty_cache()
     return out
 
 

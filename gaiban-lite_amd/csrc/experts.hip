@@ -252,6 +252,13 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(E
 // across its tiles.
 constexpr int kPfSlots = 64;
 
+// An expert whose group scales spread too widely for the running-sum scaling
+// (marked by dsv4moe_pack_int4_ratios: 1.0 in its ratio element 0, which is
+// otherwise 0) is computed by expert_prefill_exact_kernel instead.
+__device__ __forceinline__ bool expert_needs_exact(const ExpertGemmParams& p, int expert) {
+  return __builtin_nontemporal_load(p.wr + (int64_t)expert * p.ws_stride) != 0.0f;
+}
+
 template <int STAGE>
 __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams p, int total_blocks) {
   constexpr int R = 4;
@@ -275,6 +282,7 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
   const int64_t tk = p.tokens * p.topk;
   const BlockInfo b = block_info(p, blk);
   if (!b.active) return;
+  if (expert_needs_exact(p, b.expert)) return;  // expert_prefill_exact_kernel computes it
 
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
@@ -516,6 +524,175 @@ __global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams
 }
 
 
+// ----------------------------------------------------- exact prefill path
+// The prefill blocks of experts marked for exact scaling (see
+// expert_needs_exact), with each group's partial sums scaled by the group's
+// own bf16 scale, as the decode kernels do: part = -136 * sum_g(x) + the MFMA
+// chain of the group, then acc += s[n, g] * part.  Correctness only (such
+// scale spreads do not occur in the benchmark weights): plain loads, one
+// barrier pair per group, the same tile (64 slots x 256 rows, wavefront w on
+// strip pairs tile*8 + 2w and + 1), the same K assignment and the same
+// epilogue as expert_prefill_kernel.  Persistent over kExactGrid
+// workgroups: each takes 256 blocks at a time, finds the marked ones with
+// one load per thread and computes every N tile of each; with nothing
+// marked every workgroup leaves after one round of loads.
+constexpr int kExactGrid = 64;
+
+template <int STAGE>
+__global__ __launch_bounds__(256, 1) void expert_prefill_exact_kernel(ExpertGemmParams p, int total_blocks) {
+  constexpr int R = 4, C = 4;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[kPfSlots * 256];  // slot s: its 128 K of bf16
+  __shared__ float xsum_s[kPfSlots];
+  __shared__ float red[4][kPfSlots];
+  __shared__ int list[256];
+  __shared__ int count;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sw = lane & 15;
+  const int64_t tk = p.tokens * p.topk;
+  const int groups = p.k_dim / kGroup;
+  const int sums_per_row = p.k_dim / kSumChunk;
+  const uint32_t magic = dequant_magic();
+
+  for (int base = (int)blockIdx.x * 256; base < total_blocks; base += (int)gridDim.x * 256) {
+    if (threadIdx.x == 0) count = 0;
+    __syncthreads();
+    const int blk0 = base + (int)threadIdx.x;
+    if (blk0 < total_blocks) {
+      const BlockInfo bi = block_info(p, blk0);
+      if (bi.active && expert_needs_exact(p, bi.expert)) list[atomicAdd(&count, 1)] = blk0;
+    }
+    __syncthreads();
+    const int marked = count;
+    for (int li = 0; li < marked; ++li) {
+      const BlockInfo b = block_info(p, list[li]);
+      const uint8_t* wexp = p.wq + (int64_t)b.expert * p.wq_stride;
+      const uint16_t* sexp = p.ws + (int64_t)b.expert * p.ws_stride;
+      // this thread's token-tile share: slot ts, 16-byte parts 4*tq .. 4*tq + 3
+      const int ts = (int)threadIdx.x >> 2, tq = (int)threadIdx.x & 3;
+      const int64_t tar = act_row_of<STAGE>(slot_rowid(p, b, ts, tk), tk, p.topk);
+      for (int tile = 0; tile < p.n_tiles; ++tile) {
+        const int n0 = STAGE == 1 ? tile * 128 : tile * 256;
+        const int p0 = tile * 8 + 2 * wave;
+        f32x4 acc[R][C];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int ct = 0; ct < C; ++ct) acc[r][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int g = 0; g < groups; ++g) {
+          __syncthreads();  // the previous group's tile has been read
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int part = 4 * tq + e;
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (tar >= 0) v = load16(p.act + tar * p.k_dim + g * kGroup + part * 8);
+            *reinterpret_cast<u32x4*>(&xs[ts * 256 + part * 16]) = v;
+          }
+          if (threadIdx.x < kPfSlots) {
+            const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, (int)threadIdx.x, tk), tk, p.topk);
+            xsum_s[threadIdx.x] = ar >= 0 ? p.act_sum[ar * sums_per_row + 2 * g] + p.act_sum[ar * sums_per_row + 2 * g + 1]
+                                          : 0.0f;
+          }
+          __syncthreads();
+          f32x4 part[R][C];
+#pragma unroll
+          for (int ct = 0; ct < C; ++ct) {
+            const float nc = -kDequantBias * xsum_s[ct * 16 + sw];
+#pragma unroll
+            for (int r = 0; r < R; ++r) part[r][ct] = f32x4{nc, nc, nc, nc};
+          }
+          u32x4 wv[R];
+          float sc[R][4];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const int pair = p0 + (r >> 1);
+            wv[r] = load16(wexp + ((int64_t)(pair * groups + g) * 2 + (r & 1)) * kTileBytes + lane * 16);
+            const uint16_t* sp = sexp + (int64_t)(pair * groups + g) * 32 + 8 * (lane >> 4) + 4 * (r & 1);
+            scale4(*reinterpret_cast<const u32x2*>(sp), sc[r]);
+          }
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            bf16x8 bfr[C];
+#pragma unroll
+            for (int ct = 0; ct < C; ++ct)
+              bfr[ct] = __builtin_bit_cast(
+                  bf16x8, *reinterpret_cast<const u32x4*>(&xs[(ct * 16 + sw) * 256 + (4 * d + (lane >> 4)) * 16]));
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              const bf16x8 a = dequant_biased(wv[r][d], magic);
+#pragma unroll
+              for (int ct = 0; ct < C; ++ct) part[r][ct] = mfma_bf16(a, bfr[ct], part[r][ct]);
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int ct = 0; ct < C; ++ct)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[r][ct][i] = __builtin_fmaf(sc[r][i], part[r][ct][i], acc[r][ct][i]);
+        }
+
+        if constexpr (STAGE == 1) {
+          const float lim = p.clamp_limit;
+#pragma unroll
+          for (int ct = 0; ct < C; ++ct) {
+            const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
+            float partsum = 0.0f;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+              uint32_t bits[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                float gt = acc[2 * s2][ct][i];
+                float up = acc[2 * s2 + 1][ct][i];
+                if (lim > 0.0f) {
+                  gt = fminf(gt, lim);
+                  up = fminf(fmaxf(up, -lim), lim);
+                }
+                bits[i] = float_to_bf16_bits(silu_rcp(gt) * up);
+                partsum += __uint_as_float(bits[i] << 16);
+              }
+              if (rowid >= 0) {
+                const int n = n0 + 32 * wave + 16 * s2 + 4 * (lane >> 4);
+                *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) =
+                    u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+              }
+            }
+            partsum += __shfl_xor(partsum, 16, 64);
+            partsum += __shfl_xor(partsum, 32, 64);
+            if (lane < 16) red[wave][ct * 16 + lane] = partsum;
+          }
+          __syncthreads();
+          if (threadIdx.x < C * 16) {
+            const int col = (int)threadIdx.x;
+            const int64_t rid = slot_rowid(p, b, col, tk);
+            if (rid >= 0) {
+              float* dst = p.hsum_out + rid * (p.inter / kSumChunk) + n0 / kSumChunk;
+              dst[0] = red[0][col] + red[1][col];
+              dst[1] = red[2][col] + red[3][col];
+            }
+          }
+        } else {
+#pragma unroll
+          for (int ct = 0; ct < C; ++ct) {
+            const int64_t rowid = slot_rowid(p, b, ct * 16 + sw, tk);
+            if (rowid < 0) continue;
+            const float wr = contrib_weight(p, b, rowid, tk);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              const int n = n0 + 64 * wave + 16 * r + 4 * (lane >> 4);
+              f32x4 v = acc[r][ct];
+              v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
+              *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // everyone is done with `list` and `count`
+  }
+}
+
 // Per-row fp32 sums of bf16 activations over each 64-wide K chunk, summed in
 // ascending k order.
 __global__ __launch_bounds__(256) void row_chunk_sum_kernel(const uint16_t* __restrict__ x,
@@ -712,6 +889,8 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
     p.n_tiles = inter / 128;
     hipLaunchKernelGGL(expert_prefill_kernel<1>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)),
                        dim3(256), 0, stream, p, blocks);
+    hipLaunchKernelGGL(expert_prefill_exact_kernel<1>, dim3((unsigned)kExactGrid), dim3(256), 0, stream, p,
+                       blocks);
   }
   DSV4_CHECK_LAUNCH("expert stage 1");
   dsv4host::prof_stamp(dsv4host::kStampStage1, stream);
@@ -736,6 +915,8 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
     p.n_tiles = hidden / 256;
     hipLaunchKernelGGL(expert_prefill_kernel<2>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)),
                        dim3(256), 0, stream, p, blocks);
+    hipLaunchKernelGGL(expert_prefill_exact_kernel<2>, dim3((unsigned)kExactGrid), dim3(256), 0, stream, p,
+                       blocks);
   }
   DSV4_CHECK_LAUNCH("expert stage 2");
   dsv4host::prof_stamp(dsv4host::kStampStage2, stream);

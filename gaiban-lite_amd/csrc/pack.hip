@@ -114,8 +114,10 @@ __global__ __launch_bounds__(256) void pack_scales_kernel(const uint16_t* __rest
 // row (32 elements back), correctly rounded in fp32, and 0 for g = 0.  The
 // prefill kernels keep each accumulator divided by the current group's scale
 // (a <- a * r + the next group's partial sums) and multiply by the last
-// group's scale at the end; packed scales are never zero (see above), so
-// every ratio is finite.
+// group's scale at the end.  Packed scales are never zero (see above), but a
+// ratio, or the running sum it multiplies, can still leave the fp32 range
+// when a row's scales spread widely (a group of 2^-100 after one of 2^100):
+// pack_exact_flag_kernel marks such matrices for the exact-scaling path.
 __global__ __launch_bounds__(256) void pack_ratio_kernel(const uint16_t* __restrict__ packed_s,
                                                          float* __restrict__ ratios, int64_t groups,
                                                          int64_t total) {
@@ -256,6 +258,40 @@ int dsv4_launch_pack_mxfp4_a8(const uint8_t* canon, const uint8_t* canon_scales,
   return DSV4MOE_OK;
 }
 
+// A matrix (one expert) needs the exact-scaling prefill path when one of its
+// rows has a running-sum amplification max_g (s[0] + ... + s[g]) / s[g] above
+// 2^64: the running sum after group g holds the scaled partial sums so far
+// divided by s[g], so with the amplification bounded by 2^64 it stays finite
+// while the partial sums stay below ~2^64 (activations up to ~2^50).  One
+// thread per row scans its groups; a marked matrix gets 1.0 in its ratio
+// element 0 (a group-0 ratio, 0 otherwise and multiplied by a zero
+// accumulator, so the mark changes no product).  Written after
+// pack_ratio_kernel on the same stream; several threads may write the same
+// 1.0.
+constexpr float kExactAmplification = 18446744073709551616.0f;  // 2^64
+
+__global__ __launch_bounds__(256) void pack_exact_flag_kernel(const uint16_t* __restrict__ packed_s,
+                                                              float* __restrict__ ratios, int64_t n,
+                                                              int64_t groups, int64_t batch) {
+  const int64_t per_mat = n;  // rows
+  const int64_t total = batch * per_mat;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t mat = idx / per_mat;
+    const int64_t rin = idx % per_mat;
+    const int64_t pair = rin / 32;
+    const int64_t o = rin % 32;  // element of the row inside a (pair, group) block
+    const uint16_t* base = packed_s + mat * n * groups + pair * groups * 32 + o;
+    float sum = 0.0f, amp = 0.0f;
+    for (int64_t g = 0; g < groups; ++g) {
+      const float sg = fabsf(bf16_bits_to_float(base[g * 32]));
+      sum += sg;
+      amp = fmaxf(amp, sum / sg);  // inf or NaN compare as above the bound below
+    }
+    if (!(amp <= kExactAmplification)) ratios[mat * n * groups] = 1.0f;
+  }
+}
+
 int dsv4_launch_pack_ratios(const uint16_t* packed_scales, int64_t batch, int64_t n, int64_t k, float* ratios,
                             hipStream_t stream) {
   const int64_t total = batch * n * (k / kGroup);
@@ -265,6 +301,11 @@ int dsv4_launch_pack_ratios(const uint16_t* packed_scales, int64_t batch, int64_
     hipLaunchKernelGGL(pack_ratio_kernel, dim3(grid), dim3(256), 0, stream, packed_scales, ratios, k / kGroup,
                        total);
     DSV4_CHECK_LAUNCH("pack_ratio_kernel");
+    const int64_t rows = batch * n;
+    const int64_t fblocks = (rows + 255) / 256;
+    hipLaunchKernelGGL(pack_exact_flag_kernel, dim3((unsigned)(fblocks < 65535 * 16 ? fblocks : 65535 * 16)),
+                       dim3(256), 0, stream, packed_scales, ratios, n, k / kGroup, batch);
+    DSV4_CHECK_LAUNCH("pack_exact_flag_kernel");
   }
   return DSV4MOE_OK;
 }

@@ -47,6 +47,10 @@ What pins each function (checked in ``tests/test_oracle_*.py``):
   asymmetric pair that fixes which argument is the reference, the eps floor
   of the denominator, the non-finite, shape-mismatch and empty cases) and
   scale invariance (``tests/test_oracle_metrics.py``).
+* ``running_sum_amplification`` / ``needs_exact_scaling`` -- hand-computed
+  rows (a 2^100 group before a 2^-100 group, equal scales, a descending
+  ramp) and the fp32 overflow they predict in a running-sum restatement
+  (``tests/test_oracle_numerics.py``).
 * ``moe_w4a8_mxfp4_f32`` -- the same float64 pipeline over torch's
   ``float8_e4m3fn`` cast and ``torch_path.dequant_mxfp4`` (itself bit-exact
   with the reference's dequantiser), with E8M0 scales spread over 2^-30 ..
@@ -104,6 +108,8 @@ __all__ = [
     "moe_fp32",
     "moe_w4a8_f32",
     "moe_w4a8_mxfp4_f32",
+    "needs_exact_scaling",
+    "running_sum_amplification",
     "pack_int4_rows",
     "rel_fro",
     "route_scores",
@@ -538,6 +544,30 @@ def unpack_int4_rows(packed) -> np.ndarray:
     out[:, 0::2] = _NIBBLE_VALUES[p & 0xF]
     out[:, 1::2] = _NIBBLE_VALUES[p >> 4]
     return out
+
+
+EXACT_AMPLIFICATION = 2.0 ** 64
+
+
+def running_sum_amplification(scale_bits) -> np.ndarray:
+    """Per row of int4-g128 group scales (bf16 bits [.., n, k/128]): the
+    largest factor max_g (s_0 + ... + s_g) / s_g by which the W4A16 prefill
+    kernels' running sum (each accumulator kept divided by the current
+    group's scale) can exceed the largest partial sum, in float64.  Rows above
+    ``EXACT_AMPLIFICATION`` need exact per-group scaling (the rule of
+    ``pack_exact_flag_kernel``)."""
+
+    s = np.abs(bf16_bits_to_f32(np.asarray(scale_bits)).astype(np.float64))
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        return (np.cumsum(s, axis=-1) / s).max(axis=-1)
+
+
+def needs_exact_scaling(scale_bits) -> np.ndarray:
+    """Per matrix (the leading axes of ``scale_bits`` [.., n, k/128]): does any
+    row's running-sum amplification exceed 2^64 (or is it not finite)?"""
+
+    amp = running_sum_amplification(scale_bits)
+    return ~(amp <= EXACT_AMPLIFICATION).all(axis=-1)
 
 
 def dequant_int4_g128(packed, scale_bits, group: int = 128) -> np.ndarray:

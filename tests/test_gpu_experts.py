@@ -237,3 +237,61 @@ def test_wide_scale_range_prefill():
         return (torch.exp2(e) * (1.0 + torch.rand(s.shape, device=DEV, generator=g))).to(torch.bfloat16)
 
     _custom_layer_check(shape, wide, wide, ts=(64, 200), seed=23)
+
+
+def test_extreme_scale_spread_takes_the_exact_path():
+    """An expert whose gate rows put a 2^100 group scale next to a 2^-100 one
+    (the running-sum ratio alone would be 2^200, beyond fp32) is marked by
+    the ratio packer -- exactly the experts the oracle's rule names -- and its
+    prefill blocks go through the exact-scaling kernel: the prefill output
+    (blocks of 64) equals the decode kernels' (blocks of 16, exact per-group
+    scaling) and the fp32 oracle, on every row, while the other experts keep
+    the running-sum path."""
+
+    shape = S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True)
+    print("[experts] extreme scale spread", flush=True)
+    w13, s13, w2, s2 = S.make_checkpoint_experts(shape, seed=31, device=DEV)
+    # expert 3: gate rows [0, I) alternate 2^100 / 2^-100 per group; the up rows
+    # stay ordinary, so h and the outputs stay within fp32
+    g = torch.arange(s13.shape[-1], device=DEV)
+    wild = torch.where(g % 2 == 0, torch.tensor(2.0 ** 100, device=DEV), torch.tensor(2.0 ** -100, device=DEV))
+    s13[3, :shape.inter] = (wild * 1e-2).to(torch.bfloat16)
+    # expert 5: a spread of 2^40 only, below the bound: stays on the fast path
+    s2[5] = (s2[5].float() * torch.where(torch.arange(s2.shape[-1], device=DEV) % 2 == 0, 2.0 ** 20,
+                                        2.0 ** -20)).to(torch.bfloat16)
+    res = ResidentInt4MoEWeights.from_checkpoint_layout(w13, s13, w2, s2, experts=shape.experts, has_shared=True)
+    torch.cuda.synchronize()
+    marked13 = (res.w13_r[:, 0] != 0).cpu().numpy()
+    marked2 = (res.w2_r[:, 0] != 0).cpu().numpy()
+    bits = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(marked13, O.needs_exact_scaling(bits(s13)))
+    np.testing.assert_array_equal(marked2, O.needs_exact_scaling(bits(s2)))
+    assert marked13.tolist() == [False, False, False, True, False, False, False, False, False]
+    assert not marked2.any()
+    src = DeviceExpertSource(w13, s13, w2, s2)
+    t = 256
+    x = S.make_hidden(t, shape.hidden, seed=32, device=DEV)
+    ids = torch.stack([torch.full((t,), 3, device=DEV), (torch.arange(t, device=DEV) % 7 + 4) % 8], dim=1)
+    ids[::5, 1] = 5
+    ids = ids.to(torch.int32)
+    w = torch.full((t, 2), 0.5, device=DEV, dtype=torch.float32)
+    outs = {}
+    for bs in (16, 64):
+        align = deterministic_moe_align_block_size(ids, block_size=bs, num_experts=shape.experts)
+        out = torch.empty((t, shape.hidden), dtype=torch.bfloat16, device=DEV)
+        ws = torch.empty(ops.experts_workspace_bytes(t, 2, shape.hidden, shape.inter, True), dtype=torch.uint8,
+                         device=DEV)
+        ops.experts_w4a16_into(
+            x, w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, w13r=res.w13_r, w2r=res.w2_r,
+            experts=shape.experts, inter=shape.inter, has_shared=True, route_weights=w,
+            sorted_token_ids=align.sorted_token_ids, expert_ids=align.expert_ids,
+            num_tokens_post_padded=align.num_tokens_post_padded, block_size=bs, clamp_limit=0.0, out=out,
+            workspace=ws)
+        torch.cuda.synchronize()
+        outs[bs] = to_np_f32(out)
+        assert np.isfinite(outs[bs]).all(), bs
+    ref = O.moe_fp32(to_np_f32(x), ids.cpu().numpy(), w.cpu().numpy(), src, shared_index=shape.experts)
+    assert np.abs(ref).max() > 1e25  # the 2^100 groups dominate
+    assert_moe_close(outs[64], outs[16], what="prefill (exact path) vs decode")
+    assert_moe_close(outs[64], ref, what="prefill (exact path) vs oracle")
+    assert_moe_close(outs[16], ref, what="decode vs oracle")

@@ -135,3 +135,54 @@ def test_act_quant_per_token(amax):
     else:
         # amax below the 1e-12 floor: x / s < 2^-10 rounds to zero in e4m3
         assert (q == 0).all()
+
+
+def _bits(values):
+    return O.bf16_to_bits(np.asarray(values, dtype=np.float32))
+
+
+def test_running_sum_amplification_known_answers():
+    """max_g (s_0 + ... + s_g) / s_g per row, by hand: equal scales -> the
+    group count; an ascending row -> at most 2; a 2^100 group followed by a
+    2^-100 group -> 2^200 (and the fp32 ratio of the two overflows)."""
+
+    rows = np.stack([
+        _bits([0.01] * 8),
+        _bits([2.0 ** g for g in range(8)]),
+        _bits([2.0 ** 100, 2.0 ** -100] + [1.0] * 6),
+        _bits([1.0, 2.0 ** -70] + [1.0] * 6),
+        _bits([1.0, 2.0 ** -60] + [1.0] * 6),
+    ])
+    amp = O.running_sum_amplification(rows)
+    assert amp[0] == pytest.approx(8.0, rel=1e-2)          # bf16(0.01) repeated: exactly the group count
+    assert 1.0 <= amp[1] <= 2.0
+    assert amp[2] == pytest.approx(2.0 ** 200, rel=1e-6)
+    assert amp[3] == pytest.approx(2.0 ** 70, rel=1e-6)
+    assert amp[4] == pytest.approx(2.0 ** 60, rel=1e-6)
+    flags = O.needs_exact_scaling(rows[:, None, :])          # five one-row matrices
+    assert flags.tolist() == [False, False, True, True, False]
+    # the whole matrix is marked when any one row is
+    assert O.needs_exact_scaling(rows[None]).tolist() == [True]
+    assert np.float32(2.0 ** 100) / np.float32(2.0 ** -100) == np.inf
+
+
+def test_running_sum_overflow_is_what_the_rule_predicts():
+    """A restatement of the running-sum recurrence in fp32 (a <- a * r + P,
+    r = s[g-1] / s[g], result a * s[last]) against exact per-group scaling:
+    finite and equal where the rule allows it, non-finite on a marked row."""
+
+    def running(scales, partials):
+        a = np.float32(0.0)
+        for g, pg in enumerate(partials):
+            r = np.float32(0.0) if g == 0 else np.float32(scales[g - 1]) / np.float32(scales[g])
+            a = np.float32(a * r + np.float32(pg))
+        return np.float32(a * np.float32(scales[-1]))
+
+    partials = np.full(8, 2.0 ** 20, dtype=np.float32)
+    safe = np.float32([1.0, 2.0 ** -40] + [1.0] * 6)
+    wild = np.float32([2.0 ** 100, 2.0 ** -100] + [1.0] * 6)
+    with np.errstate(over="ignore", invalid="ignore"):
+        assert running(safe, partials) == pytest.approx(float((safe.astype(np.float64) * 2.0 ** 20).sum()), rel=1e-6)
+        assert not np.isfinite(running(wild, partials))
+    assert O.needs_exact_scaling(_bits(safe)[None, None]).tolist() == [False]
+    assert O.needs_exact_scaling(_bits(wild)[None, None]).tolist() == [True]
