@@ -119,12 +119,25 @@ def test_route_hash_matches_oracle():
                                   np.take_along_axis(ref.scores, ref.ids, 1).view(np.uint32))
 
 
-def test_gate_logits_fp32_accumulation():
-    g = torch.Generator(DEV).manual_seed(21)
-    x = torch.randn(100, 4096, device=DEV, generator=g).to(torch.bfloat16)
-    wg = (torch.randn(256, 4096, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
-    logits = torch.empty(100, 256, dtype=torch.float32, device=DEV)
+@pytest.mark.parametrize("tokens,hidden,experts", [(1, 4096, 256), (100, 4096, 256), (1000, 4096, 256),
+                                                    (8192, 4096, 256), (37, 1056, 72), (700, 1056, 256),
+                                                    (600, 512, 200)])
+def test_gate_logits_fp32_accumulation(tokens, hidden, experts):
+    """Both gate kernels (K split over 8 wavefronts up to 512 tokens; 64 x 64
+    LDS tiles above, when K is a multiple of 128) against a float64 product;
+    ragged token / expert tiles and a K that splits unevenly; the same call
+    twice gives the same bits."""
+
+    print(f"[gate] T={tokens} H={hidden} E={experts}", flush=True)
+    g = torch.Generator(DEV).manual_seed(21 + tokens)
+    x = torch.randn(tokens, hidden, device=DEV, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(experts, hidden, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    logits = torch.full((tokens, experts), float("nan"), dtype=torch.float32, device=DEV)
     ops.gate_logits_into(x, wg, logits)
+    again = torch.empty_like(logits)
+    ops.gate_logits_into(x, wg, again)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, again)
     ref = x.double().cpu() @ wg.double().cpu().T
     err = (logits.double().cpu() - ref).abs().max().item()
     assert err <= 1e-5 * ref.abs().max().item() + 1e-6, err
