@@ -79,6 +79,7 @@ def parse():
     ap.add_argument("--pool", type=int, default=16)
     ap.add_argument("--prefill-tokens", type=int, default=8192, help="0 skips the prefill lines")
     ap.add_argument("--prefill-steps", type=int, default=10)
+    ap.add_argument("--prefill-warmup", type=int, default=10, help="untimed prefill calls before each prefill line")
     ap.add_argument("--secondary", type=int, default=1, help="0 skips the extra decode/prefill/W4A8/W8A16 lines")
     ap.add_argument("--cpu-baseline", type=int, default=1, help="0 skips the CPU baseline")
     ap.add_argument("--seed", type=int, default=0)
@@ -424,13 +425,17 @@ def main() -> int:
     prefill = None
     prefill_lines = {}
     if prefill_ts:
-        for tp in prefill_ts:
+        # the smaller sizes first: the headline size is timed on a GPU that has
+        # been running MFMA work for a while, and each line's timed calls queue
+        # behind its own untimed warm-up calls (no idle gap, clocks settled)
+        for tp in sorted(prefill_ts):
             xp = S.make_hidden(tp, H, seed=3000, device=dev).view(1, tp, H)
             lp = S.make_logits(tp, E, seed=3001, device=dev)
-            for _ in range(2):
+            for _ in range(args.prefill_warmup):
                 layer.forward_tensor(xp, router_logits=lp)
             ops.profile_begin(args.prefill_steps)
-            pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps)
+            pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps,
+                             sync_before=False)
             pk, _ = ops.profile_end()
             flops = 6.0 * tp * (K + 1) * H * I
             mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
@@ -544,6 +549,8 @@ def main() -> int:
 
     # -------------------------------------------------------- W4A8 and W8A16
     if args.secondary:
+        secondary["layer_from_hidden_states"] = bench_from_hidden(
+            pkg, layer, gate_w, dev, [T] + ([args.prefill_tokens] if args.prefill_tokens else []), args)
         secondary["decode_graph"] = bench_graph(layer, S, dev, [1, 8, T], H, E)
         secondary["w4a8"] = bench_w4a8(pkg, resident, gate, cfg, dev, T, args)
         secondary["mxfp4"] = bench_mxfp4(pkg, gate, cfg, dev, T, args)
@@ -697,6 +704,39 @@ def bench_graph(layer, S, dev, ts, H, E):
     return out
 
 
+def bench_from_hidden(pkg, layer, gate_w, dev, ts, args):
+    """The reference's timed unit (``a3_moe_bench.py:89-105``): the layer from
+    hidden states, i.e. the fp32 gate GEMM x . Wg^T (``dsv4moe_gate_logits``)
+    then route, align, experts and combine -- ``TP4MoE.forward_tensor``
+    without router logits.  Also the gate GEMM alone and its share of the
+    step, with its bytes (Wg + x + logits) and flops as rates."""
+
+    import torch
+
+    S, ops = pkg.synthetic, pkg.ops
+    E, H = gate_w.shape
+    out = {}
+    for t in ts:
+        xs = [S.make_hidden(t, H, seed=9000 + t + i, device=dev).view(1, t, H) for i in range(4)]
+        lg = torch.empty((t, E), dtype=torch.float32, device=dev)
+        n = 100 if t <= 256 else args.prefill_steps
+        for i in range(3):
+            layer.forward_tensor(xs[i % 4])
+        ms = cuda_timer(lambda i: layer.forward_tensor(xs[i % 4]), n, sync_before=False)
+        for i in range(3):
+            ops.gate_logits_into(xs[0].view(t, H), gate_w, lg)
+        gms = cuda_timer(lambda i: ops.gate_logits_into(xs[i % 4].view(t, H), gate_w, lg), n, sync_before=False)
+        flops = 2.0 * t * E * H
+        byts = E * H * 2 + t * H * 2 + t * E * 4
+        out[f"T{t}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1),
+                        "gate_gemm_us": round(gms * 1e3, 2), "gate_share_of_step": round(gms / ms, 4),
+                        "gate_gemm_tflops": round(flops / (gms * 1e-3) / 1e12, 1),
+                        "gate_gemm_gbs": round(byts / (gms * 1e-3) / 1e9, 1)}
+        log(f"[bench] layer from hidden states T={t}: {out[f'T{t}']}")
+        del xs, lg
+    return out
+
+
 def bench_vendor_bf16_gemm(dev):
     """The vendor library's dense bf16 GEMM (torch.bmm, hipBLASLt / rocBLAS)
     on plain bf16 operands at this layer's per-expert shapes -- 256 experts x
@@ -784,11 +824,11 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args, experts_into=None, label=
                              num_tokens_post_padded=ntpp, block_size=bs, clamp_limit=0.0, out=o,
                              workspace=ws)
             ops.route_topk_into(lg, None, topk=K, score_func="sigmoid", route_scale=1.0, ids=ids, weights=w)
-            for i in range(3):
+            for i in range(10 if t > 256 else 3):
                 step(i)
-            n = 50 if t <= 256 else 5
+            n = 50 if t <= 256 else 10
             ops.profile_begin(n)
-            ms = cuda_timer(step, n)
+            ms = cuda_timer(step, n, sync_before=False)
             pk, _ = ops.profile_end()
             flops = 6.0 * t * (K + 1) * H * I
             entry = {"ms_per_step": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1), "block_size": bs,
@@ -847,10 +887,11 @@ def bench_mxfp4(pkg, gate, cfg, dev, T, args):
         tp = args.prefill_tokens
         xp = S.make_hidden(tp, H, seed=3000, device=dev).view(1, tp, H)
         lp = S.make_logits(tp, E, seed=3001, device=dev)
-        for _ in range(2):
+        for _ in range(args.prefill_warmup):
             layer.forward_tensor(xp, router_logits=lp)
         ops.profile_begin(args.prefill_steps)
-        pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps)
+        pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps,
+                         sync_before=False)
         pk, _ = ops.profile_end()
         flops = 6.0 * tp * (K + 1) * H * I
         mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
@@ -1054,27 +1095,46 @@ def cpu_baseline(pkg, w13, s13, w2, s2, seed):
     tiny = TP.StackedExperts(*S.make_checkpoint_experts(S.TINY, seed=seed, device="cpu"))
     cases = [("C1_T64", tiny, S.TINY, 64)] + [(f"C2_T{t}", flash, S.FLASH, t) for t in (1, 8, 64, 256)] + [
         ("C3_T2048", flash, S.FLASH, 2048)]
+    # the host's own achievable bf16 GEMM rate (torch.matmul on the CPU, the
+    # operation the restated path spends its time in): the CPU roofline the
+    # per-config FLOP rates are compared with
+    a = torch.randn(1024, 4096).to(torch.bfloat16)
+    b = torch.randn(4096, 4096).to(torch.bfloat16)
+    torch.matmul(a, b)
+    t0 = time.perf_counter()
+    for _ in range(3):
+        torch.matmul(a, b)
+    cpu_gemm_gflops = 3 * 2.0 * 1024 * 4096 * 4096 / (time.perf_counter() - t0) / 1e9
+    rounds = 3
     per = {}
     total = 0.0
     for name, experts, shape, t in cases:
         x = S.make_hidden(t, shape.hidden, seed=9000 + t, device="cpu")
         logits = S.make_logits(t, shape.experts, seed=9500 + t, device="cpu")
-        t0 = time.perf_counter()
-        ids, weights, _ = TP.gate_route(logits, topk=shape.topk, score_func="sigmoid")
-        TP.dense_moe(x, ids, weights, experts, num_experts=shape.experts,
-                     shared_index=shape.experts if shape.has_shared else None, dtype=torch.bfloat16)
-        dt = time.perf_counter() - t0
-        total += dt
-        per[name] = {"tokens": t, "seconds": round(dt, 3), "tokens_per_s": round(t / dt, 2)}
+        times = []
+        for _ in range(rounds):
+            t0 = time.perf_counter()
+            ids, weights, _ = TP.gate_route(logits, topk=shape.topk, score_func="sigmoid")
+            TP.dense_moe(x, ids, weights, experts, num_experts=shape.experts,
+                         shared_index=shape.experts if shape.has_shared else None, dtype=torch.bfloat16)
+            times.append(time.perf_counter() - t0)
+        total += sum(times)
+        med = sorted(times)[len(times) // 2]
+        flops = 6.0 * t * (shape.topk + (1 if shape.has_shared else 0)) * shape.hidden * shape.inter
+        per[name] = {"tokens": t, "seconds_median": round(med, 4), "seconds_min": round(min(times), 4),
+                     "seconds_max": round(max(times), 4), "tokens_per_s": round(t / med, 2),
+                     "gflops": round(flops / med / 1e9, 1),
+                     "frac_of_cpu_gemm_rate": round(flops / med / 1e9 / cpu_gemm_gflops, 4)}
         log(f"[bench] cpu baseline {name}: {per[name]}")
     return {
         "value": per["C2_T64"]["tokens_per_s"],
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": ("one batch per config (C1 T=64 tiny layer; C2 T=1/8/64/256 and C3 T=2048 on the Flash layer) "
-                   "through the torch restatement of the reference's dense path in bf16, router included; "
-                   f"{total:.1f} s of CPU time on {cores} threads; value = C2 T=64"),
+        "sample": (f"median of {rounds} rounds per config (C1 T=64 tiny layer; C2 T=1/8/64/256 and C3 T=2048 on "
+                   "the Flash layer) through the torch restatement of the reference's dense path in bf16, router "
+                   f"included; {total:.1f} s of CPU time on {cores} threads; value = C2 T=64"),
+        "cpu_bf16_gemm_gflops": round(cpu_gemm_gflops, 1),
         "configs": per,
     }
 
