@@ -88,7 +88,7 @@ def parse():
                     help="1 measures roofline.traffic with two rocprofv3 --pmc child passes; 0 uses the committed figure")
     ap.add_argument("--traffic-run", action="store_true",
                     help="child program of the traffic passes: one decode call per pooled batch, then two copies")
-    ap.add_argument("--profile-run", default=None, metavar="FMT:T:N[:graph]",
+    ap.add_argument("--profile-run", default=None, metavar="FMT:T:N[:graph|:hidden]",
                     help="only run N layer calls (FMT int4|mxfp4|w4a8|w4a8-mxfp4, T tokens) for rocprofv3 counter passes; "
                          ":graph adds N replays of the captured call; FMT linear-w8a8|linear-w8a16: N calls of "
                          "the dense linear at M=T, K=4096, N in {1024, 4096, 16384} (tiled weights)")
@@ -1179,21 +1179,23 @@ def profile_run_linear(pkg, fmt: str, m: int, n: int, dev) -> int:
 
 
 def profile_run(pkg, spec: str, seed: int) -> int:
-    """``--profile-run FMT:T:N[:graph]``: build the Flash layer in format FMT
-    (int4, mxfp4, w4a8 or w4a8-mxfp4), run one warm-up and N ``TP4MoE.forward_tensor``
-    calls at T tokens, and exit -- the program the rocprofv3 counter passes
-    and kernel traces wrap.  With ``:graph`` the call is then captured once
-    as a HIP graph and replayed N times (eager and replayed kernels in one
-    trace)."""
+    """``--profile-run FMT:T:N[:graph|:hidden]``: build the Flash layer in
+    format FMT (int4, mxfp4, w4a8 or w4a8-mxfp4), run one warm-up and N
+    ``TP4MoE.forward_tensor`` calls at T tokens, and exit -- the program the
+    rocprofv3 counter passes and kernel traces wrap.  With ``:graph`` the call
+    is then captured once as a HIP graph and replayed N times (eager and
+    replayed kernels in one trace); with ``:hidden`` every call routes from
+    the hidden states (the gate GEMM included) instead of given logits."""
 
     import torch
 
     parts = spec.split(":")
-    if len(parts) not in (3, 4) or (len(parts) == 4 and parts[3] != "graph"):
-        raise SystemExit(f"--profile-run: expected FMT:T:N or FMT:T:N:graph, got {spec!r}")
+    if len(parts) not in (3, 4) or (len(parts) == 4 and parts[3] not in ("graph", "hidden")):
+        raise SystemExit(f"--profile-run: expected FMT:T:N, FMT:T:N:graph or FMT:T:N:hidden, got {spec!r}")
     fmt, t, n = parts[:3]
     t, n = int(t), int(n)
-    graph_mode = len(parts) == 4
+    graph_mode = len(parts) == 4 and parts[3] == "graph"
+    from_hidden = len(parts) == 4 and parts[3] == "hidden"
     S = pkg.synthetic
     dev = torch.device("cuda:0")
     if fmt in ("linear-w8a8", "linear-w8a16"):
@@ -1215,11 +1217,13 @@ def profile_run(pkg, spec: str, seed: int) -> int:
         raise SystemExit(f"--profile-run: unknown format {fmt!r} (int4, mxfp4, w4a8, w4a8-mxfp4)")
     cfg = pkg.TP4MoEConfig(hidden_size=H, intermediate_size=I, experts=E, topk=K, route_scale=1.0, clamp_limit=0.0,
                            score_func="sigmoid", shared_experts=1)
-    gate = pkg.ResidentGateWeights(weight=torch.zeros((E, H), dtype=torch.bfloat16, device=dev))
+    gate_w = (torch.randn((E, H), device=dev, generator=torch.Generator(dev).manual_seed(seed + 7)) * 0.02)
+    gate = pkg.ResidentGateWeights(weight=gate_w.to(torch.bfloat16))
     layer = pkg.TP4MoE(config=cfg, resident=res, gate=gate, device=dev, global_row_shapes=[t],
                        marlin_input_dtype=torch.float8_e4m3fn if fp8_act else None)
     x = S.make_hidden(t, H, seed=3000, device=dev).view(1, t, H)
-    logits = S.make_logits(t, E, seed=3001, device=dev)
+    # ":hidden" routes from the hidden states (the gate GEMM runs in every call)
+    logits = None if from_hidden else S.make_logits(t, E, seed=3001, device=dev)
     layer.forward_tensor(x, router_logits=logits)
     torch.cuda.synchronize()
     for _ in range(n):

@@ -553,6 +553,8 @@ __global__ __launch_bounds__(256, 1) void expert_prefill_exact_kernel(ExpertGemm
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
   const uint32_t magic = dequant_magic();
+  // element 1 of the stack's ratios: 1.0 when any expert of it is marked
+  if (__builtin_nontemporal_load(p.wr + 1) == 0.0f) return;
 
   for (int base = (int)blockIdx.x * 256; base < total_blocks; base += (int)gridDim.x * 256) {
     if (threadIdx.x == 0) count = 0;

@@ -265,9 +265,11 @@ int dsv4_launch_pack_mxfp4_a8(const uint8_t* canon, const uint8_t* canon_scales,
 // while the partial sums stay below ~2^64 (activations up to ~2^50).  One
 // thread per row scans its groups; a marked matrix gets 1.0 in its ratio
 // element 0 (a group-0 ratio, 0 otherwise and multiplied by a zero
-// accumulator, so the mark changes no product).  Written after
-// pack_ratio_kernel on the same stream; several threads may write the same
-// 1.0.
+// accumulator, so the mark changes no product), and element 1 of the first
+// matrix of the call (also a group-0 ratio) becomes 1.0 when any matrix of
+// the call is marked, so the exact kernel's workgroups can leave after one
+// load when none is.  Written after pack_ratio_kernel on the same stream;
+// several threads may write the same 1.0.
 constexpr float kExactAmplification = 18446744073709551616.0f;  // 2^64
 
 __global__ __launch_bounds__(256) void pack_exact_flag_kernel(const uint16_t* __restrict__ packed_s,
@@ -288,7 +290,10 @@ __global__ __launch_bounds__(256) void pack_exact_flag_kernel(const uint16_t* __
       sum += sg;
       amp = fmaxf(amp, sum / sg);  // inf or NaN compare as above the bound below
     }
-    if (!(amp <= kExactAmplification)) ratios[mat * n * groups] = 1.0f;
+    if (!(amp <= kExactAmplification)) {
+      ratios[mat * n * groups] = 1.0f;
+      ratios[1] = 1.0f;  // the stack holds a marked matrix (element 1: another group-0 ratio)
+    }
   }
 }
 

@@ -191,6 +191,14 @@ int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, i
  * multiply by the last group's scale at the end.  Computed once per packed
  * weight set; no counterpart in the reference (its Marlin kernels scale each
  * dequantised weight).  n a multiple of 32, k of 128.
+ * Guard: a matrix (one expert) with a row whose running-sum amplification
+ * max_g (s_0 + ... + s_g) / s_g exceeds 2^64 (e.g. a 2^100 group scale
+ * before a 2^-100 one) gets 1.0 in its element 0, and element 1 of the first
+ * matrix of the call gets 1.0 when any matrix is marked (both are group-0
+ * ratios, otherwise 0 and never multiplied into a nonzero sum); the expert
+ * entries then compute the marked experts' prefill blocks with exact
+ * per-group scaling.  One call must cover the whole expert stack passed to
+ * the expert entries as w13r / w2r.
  */
 int dsv4moe_pack_int4_ratios(const uint16_t* packed_scales, int64_t batch, int64_t n, int64_t k, float* ratios,
                              void* stream);

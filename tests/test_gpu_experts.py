@@ -268,6 +268,8 @@ def test_extreme_scale_spread_takes_the_exact_path():
     np.testing.assert_array_equal(marked2, O.needs_exact_scaling(bits(s2)))
     assert marked13.tolist() == [False, False, False, True, False, False, False, False, False]
     assert not marked2.any()
+    # the stack-level mark (element 1 of the first expert's ratios)
+    assert float(res.w13_r[0, 1]) == 1.0 and float(res.w2_r[0, 1]) == 0.0
     src = DeviceExpertSource(w13, s13, w2, s2)
     t = 256
     x = S.make_hidden(t, shape.hidden, seed=32, device=DEV)
