@@ -13,23 +13,28 @@ the shared expert -> owning output clone) with inputs resident in HBM.  Inputs
 rotate through a pool of seeded batches so every step routes differently (a
 fixed-routing figure is reported beside it).
 
-Order of the run: the prefill lines (T = 8192, then 2048 and 4096: TFLOP/s
-and fraction of the bf16 peak, with a ``prefill_roofline`` block for the
-grouped w13 kernel) come first, then the decode headline (W warm-up steps, K
-timed steps with per-step times on stderr and in ``per_step_ms``), then the
-secondary lines: decode at T in {1, 8, 256}, decode as HIP-graph replays, the
-W4A8 layer (uniform and Zipf routing, T = 64 and 8192), the layer with MXFP4
-experts (the reference checkpoint's E2M1 + E8M0 format), the FP8-block shared
-expert, the W8A16 (int8 and FP8-block) and block-FP8 W8A8 dense linears at
+Order of the run: the prefill lines (T = 2048, 4096 and 8192 in ascending
+order, each after its own untimed warm-up calls: TFLOP/s and fraction of the
+bf16 peak, with a ``prefill_roofline`` block for the grouped w13 kernel at
+T = 8192) come first, then the decode headline (W warm-up steps, K timed
+steps with per-step times on stderr and in ``per_step_ms``), then the
+secondary lines: decode at T in {1, 8, 256}, the layer from hidden states
+(the gate GEMM in the call, T = 64 and 8192), decode as HIP-graph replays,
+the W4A8 layer (uniform and Zipf routing, T = 64 and 8192), the layer with
+MXFP4 experts (the reference checkpoint's E2M1 + E8M0 format), W4A8 over
+those MXFP4 experts, the vendor's bf16 GEMM at the expert shapes, the
+FP8-block shared expert, the W8A16 (int8 and FP8-block) and block-FP8 W8A8 dense linears at
 K = 4096 (M <= 64 timed as 50 calls captured in a HIP graph, beside the
 launch-bound Python-loop figure), and last the CPU baseline (the torch
-restatement of the reference's dense path on this host's cores, one batch per
-configuration).  ``env`` records versions, the device and the shader clock
+restatement of the reference's dense path on this host's cores, the median
+of three rounds per configuration, with its spread and the host's own bf16
+GEMM rate).  ``env`` records versions, the device and the shader clock
 read right after the headline region.
 
-``--profile-run FMT:T:N[:graph]`` only builds the layer and runs N calls (the
-program for ``rocprofv3 --pmc`` passes and kernel traces); ``:graph`` adds N
-replays of the call captured as a HIP graph.
+``--profile-run FMT:T:N[:graph|:hidden]`` only builds the layer and runs N
+calls (the program for ``rocprofv3 --pmc`` passes and kernel traces);
+``:graph`` adds N replays of the call captured as a HIP graph, ``:hidden``
+routes from hidden states (the gate GEMM in every call).
 
 ``--copy-calibration`` instead runs a plain 512 MiB device copy (torch
 ``copy_``) 5 times: the reference kernel for scaling the FETCH_SIZE /

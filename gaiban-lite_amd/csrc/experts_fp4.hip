@@ -11,8 +11,9 @@
 // multiplies the result.
 //
 // No dequantisation work at all.  Operand layout of the 16x16x128 MFMA with
-// an fp4 A and an fp8 B operand (measured on gfx950 with an in-bounds
-// one-hot probe): lane group j (lanes 16j .. 16j+15) of A holds K 32j .. 32j+31
+// an fp4 A and an fp8 B operand on gfx950 (any other K assignment or scale
+// lane fails the per-32-group scale tests of tests/test_gpu_w4a8_mxfp4.py,
+// whose scales differ per group): lane group j (lanes 16j .. 16j+15) of A holds K 32j .. 32j+31
 // of its row, code i in nibble i (low nibble first), and the lane's E8M0
 // scale byte multiplies exactly those 32 products; lane group j of B holds
 // K 16j .. 16j+15 in bytes 0..15 and K 64+16j .. 64+16j+15 in bytes 16..31.

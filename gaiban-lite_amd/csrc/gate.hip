@@ -3,7 +3,9 @@
 // (runtime/dsv4_direct/moe_forward.py:80, reference/inference/model.py:565):
 // bf16 x bf16 products are exact in fp32, so only the summation order differs.
 // Every summation order here is fixed, so the logits of a token do not depend
-// on the other tokens of the batch or on the run.
+// on the other tokens of the batch or on the run; they can differ in the last
+// bits between batches of up to kGateSplitMaxTokens tokens and larger ones,
+// which run the other kernel (as a vendor GEMM changes its algorithm by M).
 //
 // Two kernels by batch size (Wg is [experts, hidden], experts = 256 at the
 // Flash shape: 2 MiB of bf16):

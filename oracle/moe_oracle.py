@@ -55,6 +55,24 @@ What pins each function (checked in ``tests/test_oracle_*.py``):
   ``float8_e4m3fn`` cast and ``torch_path.dequant_mxfp4`` (itself bit-exact
   with the reference's dequantiser), with E8M0 scales spread over 2^-30 ..
   2^10 per 32-K group (``tests/test_oracle_ffn.py``).
+* ``swiglu_f32`` -- torch's ``clamp`` / ``F.silu`` / multiply in
+  ``Expert.forward``'s order, with planted clamp mistakes that fail
+  (``tests/test_oracle_ffn.py``).
+* ``route_scores`` -- through ``route_topk``'s brute force and the float64
+  score closed forms (``tests/test_oracle_route_align.py``).
+* ``fp8_e4m3_encode`` / ``fp8_e4m3_decode`` -- every code round trips and
+  decodes as torch's ``float8_e4m3fn`` (``tests/test_oracle_numerics.py``).
+* ``dequant_fp8_block`` -- torch's ``float8_e4m3fn`` times its
+  ``float8_e8m0fnu`` block scale, bit for bit, ragged last block included;
+  ``w8a16_fp8_linear_f32`` -- a scalar loop over the bf16-rounded weights
+  (``tests/test_oracle_ffn.py``).
+* ``act_quant_block_fp8`` -- codes and exponents equal a torch statement of
+  the reference's quantiser (``fp8_linear.py:168-251``) incl. zero blocks and
+  3e38; ``block_fp8_gemm_f32`` -- a float64 matmul of the dequantised operands
+  (``tests/test_oracle_block_fp8.py``).
+* ``shared_fp8_bf16`` -- the reference's torch op sequence
+  (``moe_runtime.py:238-263``) bit for bit on dyadic operands
+  (``tests/test_oracle_ffn.py``).
 * ``moe_bf16_mirror`` -- against a torch restatement of the reference's bf16
   op order (torch's own bf16 matmuls, fp32 clamp / SiLU and casts): at least
   99.9% of the outputs bit-identical, the rest within 2^-8 of the largest

@@ -331,3 +331,37 @@ def test_shared_fp8_oracle_matches_reference_op_order_in_torch():
     act = (F.silu(gate) * up).to(torch.bfloat16)
     ref = F.linear(act, dq(w2, s2)).float().numpy()
     np.testing.assert_allclose(got, ref, rtol=2e-3, atol=0)
+
+
+@pytest.mark.parametrize("limit", [0.0, 10.0])
+def test_swiglu_against_torch_expert_activation(limit):
+    """``swiglu_f32`` vs torch's own ops in ``Expert.forward``'s order
+    (``model.py:598-603``): up clamped to [-limit, limit], gate clamped above
+    only, then ``F.silu(gate) * up`` in fp32.  Inputs reach +-40, so a
+    missing clamp, a gate clamped below as well, or an up clamped on one
+    side only moves outputs far beyond the tolerance (checked below)."""
+
+    import torch
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(23)
+    g = (rng.standard_normal((64, 96)) * 15).astype(np.float32)
+    u = (rng.standard_normal((64, 96)) * 15).astype(np.float32)
+    g[0, :4] = [-40.0, 40.0, 0.0, -0.0]
+    u[0, :4] = [-40.0, 40.0, 1.0, 1.0]
+
+    def torch_ref(gg, uu, lim, gate_min=False, up_max_only=False):
+        gt, ut = torch.from_numpy(gg), torch.from_numpy(uu)
+        if lim > 0:
+            ut = torch.clamp(ut, max=lim) if up_max_only else torch.clamp(ut, min=-lim, max=lim)
+            gt = torch.clamp(gt, min=-lim, max=lim) if gate_min else torch.clamp(gt, max=lim)
+        return (F.silu(gt) * ut).numpy()
+
+    got = O.swiglu_f32(g, u, limit)
+    ref = torch_ref(g, u, limit)
+    assert got.dtype == np.float32
+    np.testing.assert_allclose(got, ref, rtol=2e-6, atol=1e-30)
+    if limit > 0:
+        for wrong in (torch_ref(g, u, 0.0), torch_ref(g, u, limit, gate_min=True),
+                      torch_ref(g, u, limit, up_max_only=True)):
+            assert not np.allclose(got, wrong, rtol=1e-3, atol=1e-6)
