@@ -438,15 +438,20 @@ def main() -> int:
             lp = S.make_logits(tp, E, seed=3001, device=dev)
             for _ in range(args.prefill_warmup):
                 layer.forward_tensor(xp, router_logits=lp)
-            ops.profile_begin(args.prefill_steps)
+            # ms_per_step without per-kernel events, then the same calls with
+            # them for the per-stage times
             pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps,
                              sync_before=False)
+            ops.profile_begin(args.prefill_steps)
+            pms_ev = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps,
+                                sync_before=False)
             pk, _ = ops.profile_end()
             flops = 6.0 * tp * (K + 1) * H * I
             mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
             prefill_lines[tp] = {
                 "tokens": tp,
                 "ms_per_step": round(pms, 4),
+                "ms_per_step_all_kernel_events": round(pms_ev, 4),
                 "tokens_per_s": round(tp / (pms * 1e-3), 1),
                 "tflops": round(flops / (pms * 1e-3) / 1e12, 2),
                 "frac_of_bf16_peak": round(flops / (pms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
@@ -782,17 +787,19 @@ def bench_w4a8_mxfp4(pkg, gate, cfg, dev, T, args):
                                                               marlin_input_dtype=torch.float8_e4m3fn)
     del w13, s13, w2, s2
     out = bench_w4a8(pkg, res, gate, cfg, dev, T, args, experts_into=pkg.ops.experts_w4a8_mxfp4_into,
-                     label="w4a8 mxfp4")
+                     label="w4a8 mxfp4", mxfp4=True)
     del res
     torch.cuda.empty_cache()
     return out
 
 
-def bench_w4a8(pkg, resident, gate, cfg, dev, T, args, experts_into=None, label="w4a8"):
+def bench_w4a8(pkg, resident, gate, cfg, dev, T, args, experts_into=None, label="w4a8", mxfp4=False):
     """W4A8 experts (fp8 activations, the same resident int4 weights) at the
     decode T and the prefill size, uniform routing (router from logits) and
-    Zipf(1.1) routing (fixed ids); a step is route (uniform only) + alignment +
-    experts + combine, all stream-ordered launches."""
+    Zipf(1.1) routing (fixed ids).  A uniform step is the fused layer entry
+    (route -> align with x quantised beside it -> experts -> combine); a Zipf
+    step is the given ids' alignment + the experts entry (which quantises x
+    itself) + combine; all stream-ordered launches."""
 
     import torch
 
@@ -811,6 +818,7 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args, experts_into=None, label=
         ntpp = torch.empty(1, dtype=torch.int32, device=dev)
         ids = torch.empty((t, K), dtype=torch.int32, device=dev)
         w = torch.empty((t, K), dtype=torch.float32, device=dev)
+        margin = torch.empty((t,), dtype=torch.float32, device=dev)
         o = torch.empty((t, H), dtype=torch.bfloat16, device=dev)
         ws = torch.empty(ops.experts_w4a8_workspace_bytes(t, K, H, I, True), dtype=torch.uint8, device=dev)
         zipf_ids = S.zipf_ids(t, E, K, seed=4, device=dev)
@@ -818,9 +826,14 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args, experts_into=None, label=
         for routing in ("uniform", "zipf"):
             def step(i):
                 if routing == "uniform":
-                    ops.route_topk_into(lg, None, topk=K, score_func="sigmoid", route_scale=1.0, ids=ids, weights=w)
-                else:
-                    ids.copy_(zipf_ids)
+                    ops.layer_w4a8_into(x, lg, None, topk=K, score_func="sigmoid", route_scale=1.0,
+                                        w13q=resident.w13_q, w13s=resident.w13_s, w2q=resident.w2_q,
+                                        w2s=resident.w2_s, experts=E, inter=I, has_shared=True, clamp_limit=0.0,
+                                        block_size=bs, ids=ids, weights=w, margin=margin,
+                                        sorted_token_ids=sorted_ids, expert_ids=expert_ids,
+                                        num_tokens_post_padded=ntpp, out=o, workspace=ws, mxfp4=mxfp4)
+                    return
+                ids.copy_(zipf_ids)
                 ops.align_into(ids, block_size=bs, num_experts=E, sorted_token_ids=sorted_ids,
                                expert_ids=expert_ids, num_tokens_post_padded=ntpp, workspace=ws)
                 experts_into(x, w13q=resident.w13_q, w13s=resident.w13_s, w2q=resident.w2_q,
@@ -832,11 +845,16 @@ def bench_w4a8(pkg, resident, gate, cfg, dev, T, args, experts_into=None, label=
             for i in range(10 if t > 256 else 3):
                 step(i)
             n = 50 if t <= 256 else 10
-            ops.profile_begin(n)
+            # ms_per_step without the library's per-kernel events (as the
+            # headline's ms_per_step_unprofiled); kernel_ms from a second pass
+            # with them, which adds a few us per step
             ms = cuda_timer(step, n, sync_before=False)
+            ops.profile_begin(n)
+            ms_ev = cuda_timer(step, n, sync_before=False)
             pk, _ = ops.profile_end()
             flops = 6.0 * t * (K + 1) * H * I
             entry = {"ms_per_step": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1), "block_size": bs,
+                     "ms_per_step_all_kernel_events": round(ms_ev, 4),
                      "kernel_ms": {k: round(v, 4) for k, v in pk.items() if k not in ("route", "align")}}
             if t > 256:
                 entry["layer_tflops"] = round(flops / (ms * 1e-3) / 1e12, 2)
@@ -874,14 +892,19 @@ def bench_mxfp4(pkg, gate, cfg, dev, T, args):
     for i in range(5):
         layer.forward_tensor(xs[i % 8], router_logits=lgs[i % 8])
     n = 100
+    # ms_per_step without per-kernel events; kernel_ms (and the stage-1 rate)
+    # from a second pass with them
+    ms = cuda_timer(lambda i: layer.forward_tensor(xs[i % 8], router_logits=lgs[i % 8]), n, sync_before=False)
     ops.profile_begin(n)
-    ms = cuda_timer(lambda i: layer.forward_tensor(xs[i % 8], router_logits=lgs[i % 8]), n)
+    ms_ev = cuda_timer(lambda i: layer.forward_tensor(xs[i % 8], router_logits=lgs[i % 8]), n,
+                       sync_before=False)
     pk, _ = ops.profile_end()
     d_mean = float(np.mean([distinct[i % 8] for i in range(n)]))
     st1 = (d_mean + 1) * b13 + T * H * 2 + (T * K + T) * I * 2
     layer_b = (d_mean + 1) * out["expert_bytes"] + 2 * T * H * 2 + T * E * 4 + T * K * 8
     out[f"decode_T{T}"] = {
         "ms_per_step": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "ms_per_step_all_kernel_events": round(ms_ev, 4),
         "layer_hbm_gbs": round(layer_b / (ms * 1e-3) / 1e9, 1),
         "stage1_hbm_gbs": round(st1 / (pk["stage1_w13"] * 1e-3) / 1e9, 1),
         "stage1_frac_of_hbm_peak": round(st1 / (pk["stage1_w13"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -894,9 +917,10 @@ def bench_mxfp4(pkg, gate, cfg, dev, T, args):
         lp = S.make_logits(tp, E, seed=3001, device=dev)
         for _ in range(args.prefill_warmup):
             layer.forward_tensor(xp, router_logits=lp)
-        ops.profile_begin(args.prefill_steps)
         pms = cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps,
                          sync_before=False)
+        ops.profile_begin(args.prefill_steps)
+        cuda_timer(lambda i: layer.forward_tensor(xp, router_logits=lp), args.prefill_steps, sync_before=False)
         pk, _ = ops.profile_end()
         flops = 6.0 * tp * (K + 1) * H * I
         mm_ms = pk["stage1_w13"] + pk["stage2_w2"]
@@ -940,7 +964,7 @@ def bench_shared_fp8(pkg, gate, cfg, dev, T, args):
         for _ in range(3):
             layer.forward_tensor(x, router_logits=lg)
         n = 100 if t == T else args.prefill_steps
-        ms = cuda_timer(lambda i: layer.forward_tensor(x, router_logits=lg), n)
+        ms = cuda_timer(lambda i: layer.forward_tensor(x, router_logits=lg), n, sync_before=False)
         out[f"T{t}"] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(t / (ms * 1e-3), 1)}
         log(f"[bench] fp8 shared expert T={t}: {out[f'T{t}']}")
         del x, lg

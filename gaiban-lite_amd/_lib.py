@@ -86,6 +86,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _i32, _f32,
          _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _sz, _p],
     ),
+    "dsv4moe_layer_w4a8": (
+        ctypes.c_int,
+        [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _i32, _f32,
+         _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _sz, _p],
+    ),
+    "dsv4moe_layer_w4a8_mxfp4": (
+        ctypes.c_int,
+        [_p, _p, _p, _i64, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _i32, _f32,
+         _i32, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _sz, _p],
+    ),
     "dsv4moe_experts_mxfp4": (
         ctypes.c_int,
         [_p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _i32, _p, _p, _i64, _p, _p, _i32,

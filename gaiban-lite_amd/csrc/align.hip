@@ -28,8 +28,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_kernel(
 
 __global__ __launch_bounds__(kAlignThreads) void align_count_kernel(
     const int32_t* __restrict__ ids, int64_t assignments, int experts, int64_t chunk, int chunks,
-    int32_t* __restrict__ counts, const uint16_t* __restrict__ x, int64_t tokens, int hidden,
-    float* __restrict__ xsum) {
+    int32_t* __restrict__ counts, ActPrep prep, int64_t tokens) {
   __shared__ int s_count[kAlignMaxExperts];
   __shared__ int s_bad;
   const int c = blockIdx.x;
@@ -40,7 +39,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_count_kernel(
     if (threadIdx.x == 0) counts[(int64_t)chunks * experts + c] = s_bad;
     return;
   }
-  row_sums_part(x, tokens, hidden, xsum, c - chunks, (int)gridDim.x - chunks);
+  act_prep_part(prep, tokens, c - chunks, (int)gridDim.x - chunks);
 }
 
 __global__ __launch_bounds__(kAlignThreads) void align_place_kernel(
@@ -104,18 +103,17 @@ size_t dsv4_align_scratch_bytes(int64_t assignments, int32_t experts) {
   return sizeof(int32_t) * (size_t)chunks * (size_t)(experts + 1);
 }
 
-// Two-launch alignment [+ activation row sums when x is given].
+// Two-launch alignment [+ the activation work of `prep` beside the counting].
 int dsv4_launch_align_multi(const int32_t* ids, int64_t assignments, int32_t experts, int32_t block_size,
                             int32_t* sorted_ids, int64_t capacity, int32_t* expert_ids, int64_t num_blocks,
-                            int32_t* ntpp, int32_t* scratch, const uint16_t* x, int64_t tokens, int32_t hidden,
-                            float* xsum, hipStream_t stream) {
+                            int32_t* ntpp, int32_t* scratch, const ActPrep& prep, int64_t tokens,
+                            hipStream_t stream) {
   int64_t chunk;
   int chunks;
   dsv4_align_chunks(assignments, &chunk, &chunks);
-  const int64_t sums = x != nullptr ? tokens * (hidden / 64) : 0;
-  const int sum_wgs = (int)std::min<int64_t>((sums + kAlignThreads - 1) / kAlignThreads, kAlignSumWorkgroups);
+  const int sum_wgs = (int)act_prep_workgroups(prep, tokens, kAlignSumWorkgroups);
   hipLaunchKernelGGL(align_count_kernel, dim3((unsigned)(chunks + sum_wgs)), dim3(kAlignThreads), 0, stream, ids,
-                     assignments, experts, chunk, chunks, scratch, x, tokens, hidden, xsum);
+                     assignments, experts, chunk, chunks, scratch, prep, tokens);
   DSV4_CHECK_LAUNCH("align_count_kernel");
   hipLaunchKernelGGL(align_place_kernel, dim3((unsigned)chunks), dim3(kAlignThreads), 0, stream, ids, assignments,
                      experts, expert_bits_of(experts), block_size, chunk, chunks, scratch, sorted_ids, capacity,

@@ -19,6 +19,7 @@
 // counts of the ranges before them.
 #pragma once
 
+#include "act_quant.h"
 #include "common.h"
 
 namespace dsv4 {
@@ -28,7 +29,8 @@ constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kAlignMaxExperts = 1024;
 // Two-launch alignment (align.hip): at least kAlignChunk flat ids per
 // workgroup, at most kAlignMaxChunks workgroups (each sums the counts of all
-// of them), and at most kAlignSumWorkgroups more workgroups for row sums.
+// of them), and at most kAlignSumWorkgroups more workgroups for the
+// activation work beside the counting (row sums or W4A8 quantisation).
 constexpr int kAlignChunk = 4096;
 constexpr int kAlignMaxChunks = 64;
 constexpr int kAlignSumWorkgroups = 160;
@@ -217,6 +219,33 @@ __device__ __forceinline__ void row_sums_part(const uint16_t* __restrict__ x, in
     }
     xsum[idx] = sum;
   }
+}
+
+// Share `part` of `parts` workgroups of kAlignThreads threads of the
+// activation work of a prologue launch: the row sums above, or the W4A8
+// quantiser with one wavefront per row (act_quant.h).
+__device__ __forceinline__ void act_prep_part(const ActPrep& a, int64_t tokens, int part, int parts) {
+  if (a.mode == kPrepRowSums) {
+    row_sums_part(a.x, tokens, a.hidden, a.sums, part, parts);
+    return;
+  }
+  if (a.mode != kPrepQuantInt4 && a.mode != kPrepQuantNatural) return;
+  const int wave = threadIdx.x >> 6;
+  for (int64_t r = (int64_t)part * kAlignWaves + wave; r < tokens; r += (int64_t)parts * kAlignWaves) {
+    if (a.mode == kPrepQuantInt4)
+      act_quant_row<false>(a.x, r, a.hidden, a.q, a.qscale, a.sums);
+    else
+      act_quant_row<true>(a.x, r, a.hidden, a.q, a.qscale, nullptr);
+  }
+}
+
+// Workgroups a prologue launch adds for `a` (at most `cap`): 1024 row sums
+// or 16 quantised rows per workgroup and round.
+inline int64_t act_prep_workgroups(const ActPrep& a, int64_t tokens, int64_t cap) {
+  int64_t n = 0;
+  if (a.mode == kPrepRowSums) n = (tokens * (a.hidden / 64) + kAlignThreads - 1) / kAlignThreads;
+  else if (a.mode == kPrepQuantInt4 || a.mode == kPrepQuantNatural) n = (tokens + kAlignWaves - 1) / kAlignWaves;
+  return n < cap ? n : cap;
 }
 
 }  // namespace dsv4

@@ -7,6 +7,7 @@
 #include <mutex>
 #include <vector>
 
+#include "act_quant.h"
 #include "common.h"
 #include "../../include/dsv4moe.h"
 
@@ -82,13 +83,13 @@ int dsv4_launch_experts_w4a16(const uint16_t*, int64_t, int, int, int, int, cons
                               uint16_t*, void*, hipStream_t, bool rowsums_ready = false);
 float* dsv4_experts_xsum(void*, int64_t, int, int, int, int);
 int dsv4_launch_prologue(int32_t, const float*, const float*, int64_t, int32_t, int32_t, int32_t, float, int32_t*,
-                         float*, float*, int32_t, int32_t*, int64_t, int32_t*, int64_t, int32_t*, const uint16_t*,
-                         int32_t, float*, hipStream_t);
+                         float*, float*, int32_t, int32_t*, int64_t, int32_t*, int64_t, int32_t*,
+                         const dsv4::ActPrep&, hipStream_t);
 // Largest token count routed inside the one-workgroup prologue (one token per
 // wavefront); above it the wide route kernel runs first.
 constexpr int64_t kPrologueRouteMaxTokens = 16;
 int dsv4_launch_align_multi(const int32_t*, int64_t, int32_t, int32_t, int32_t*, int64_t, int32_t*, int64_t,
-                            int32_t*, int32_t*, const uint16_t*, int64_t, int32_t, float*, hipStream_t);
+                            int32_t*, int32_t*, const dsv4::ActPrep&, int64_t, hipStream_t);
 size_t dsv4_align_scratch_bytes(int64_t, int32_t);
 int32_t* dsv4_experts_align_scratch(void*, int64_t, int, int, int, int, size_t*);
 // Fewest flat route ids aligned by the two-launch split over chunks; below it
@@ -104,13 +105,15 @@ int dsv4_launch_pack_mxfp4_a8(const uint8_t*, const uint8_t*, int64_t, int64_t, 
                               uint8_t*, hipStream_t);
 int dsv4_launch_experts_w4a8_mxfp4(const uint16_t*, int64_t, int, int, int, int, const uint8_t*, const uint8_t*,
                                    const uint8_t*, const uint8_t*, int, const float*, const int32_t*, int64_t,
-                                   const int32_t*, const int32_t*, int, float, uint16_t*, void*, hipStream_t);
+                                   const int32_t*, const int32_t*, int, float, uint16_t*, void*, hipStream_t,
+                                   bool x_ready = false);
 size_t dsv4_experts_w4a8_workspace_bytes(int64_t, int, int, int, int);
+void dsv4_experts_w4a8_pieces(void*, int64_t, int, int, int, int, uint8_t**, float**, float**, int32_t**, size_t*);
 int dsv4_launch_act_quant_fp8(const uint16_t*, int64_t, int, uint8_t*, float*, float*, hipStream_t);
 int dsv4_launch_experts_w4a8(const uint16_t*, int64_t, int, int, int, int, const uint8_t*,
                              const uint16_t*, const uint8_t*, const uint16_t*, int, const float*,
                              const int32_t*, int64_t, const int32_t*, const int32_t*, int, float,
-                             uint16_t*, void*, hipStream_t);
+                             uint16_t*, void*, hipStream_t, bool x_ready = false);
 int32_t dsv4_w8a16_split_k(int64_t, int64_t, int64_t);
 int32_t dsv4_block_fp8_split_k(int64_t, int64_t, int64_t);
 int dsv4_launch_act_quant_block_fp8(const void*, int32_t, int64_t, int64_t, uint8_t*, uint8_t*, hipStream_t);
@@ -334,8 +337,8 @@ int dsv4moe_align_ws(const int32_t* ids, int64_t tokens, int32_t topk, int32_t e
     return dsv4_launch_align(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
                              num_blocks, num_tokens_post_padded, s);
   return dsv4_launch_align_multi(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
-                                 num_blocks, num_tokens_post_padded, static_cast<int32_t*>(workspace), nullptr,
-                                 tokens, 0, nullptr, s);
+                                 num_blocks, num_tokens_post_padded, static_cast<int32_t*>(workspace),
+                                 dsv4::ActPrep{dsv4::kPrepNone, nullptr, 0, nullptr, nullptr, nullptr}, tokens, s);
 }
 
 int dsv4moe_pack_int4_g128(const uint8_t* canon, const uint16_t* canon_scales, int64_t batch,
@@ -543,17 +546,18 @@ static int validate_layer_route(const char* who, const float* logits, int32_t to
   return DSV4MOE_OK;
 }
 
-// Route and align a fused layer call [and sum the activation rows when
-// x_sums is given], by token count: for T <= 16 one prologue launch routes,
-// aligns and sums; up to 8191 route ids the route kernel, then the prologue
-// (align + sums); from 8192 ids the route kernel, then the workgroup-split
-// alignment with the sums beside its counting, its scratch in the (not yet
-// used) contribution region of the experts workspace.
-static int layer_route_align(const char* who, const uint16_t* x_sums, const float* logits, const float* bias,
-                             int64_t tokens, int32_t hidden, int32_t inter, int32_t experts, int32_t topk,
-                             int32_t score_func, float route_scale, int32_t has_shared, int32_t block_size,
-                             int32_t* ids, float* weights, float* margin, int32_t* sorted_token_ids, int64_t capacity,
-                             int32_t* expert_ids, int32_t* num_tokens_post_padded, void* workspace, hipStream_t s) {
+// Route and align a fused layer call, with the activation work of `prep`
+// (row sums, W4A8 quantisation or none) beside the alignment, by token count:
+// for T <= 16 one prologue launch routes, aligns and does `prep`; up to 8191
+// route ids the route kernel, then the prologue (align + prep); from 8192 ids
+// the route kernel, then the workgroup-split alignment with `prep` beside its
+// counting and its scratch (`room` bytes) in the not yet used contribution
+// region of the experts workspace.
+static int layer_route_align(const char* who, const dsv4::ActPrep& prep, int32_t* scratch, size_t room,
+                             const float* logits, const float* bias, int64_t tokens, int32_t experts, int32_t topk,
+                             int32_t score_func, float route_scale, int32_t block_size, int32_t* ids, float* weights,
+                             float* margin, int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                             int32_t* num_tokens_post_padded, hipStream_t s) {
   int rc = DSV4MOE_OK;
   const int64_t nblocks = (capacity + block_size - 1) / block_size;
   // (with routing in the prologue the route interval of the profile covers
@@ -565,18 +569,14 @@ static int layer_route_align(const char* who, const uint16_t* x_sums, const floa
     if (rc != DSV4MOE_OK) return rc;
     dsv4host::prof_stamp(dsv4host::kStampRoute, s);
   }
-  float* xsum = x_sums != nullptr ? dsv4_experts_xsum(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0)
-                                  : nullptr;
   if (tokens * topk >= kAlignMultiMinAssignments) {
-    size_t room = 0;
-    int32_t* scratch = dsv4_experts_align_scratch(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0, &room);
     DSV4_REQUIRE(room >= dsv4_align_scratch_bytes(tokens * topk, experts), "%s: align scratch too small", who);
     rc = dsv4_launch_align_multi(ids, tokens * topk, experts, block_size, sorted_token_ids, capacity, expert_ids,
-                                 nblocks, num_tokens_post_padded, scratch, x_sums, tokens, hidden, xsum, s);
+                                 nblocks, num_tokens_post_padded, scratch, prep, tokens, s);
   } else {
     rc = dsv4_launch_prologue(route_in_prologue ? 1 : 0, logits, bias, tokens, experts, topk, score_func,
                               route_scale, ids, weights, margin, block_size, sorted_token_ids, capacity, expert_ids,
-                              nblocks, num_tokens_post_padded, x_sums, hidden, xsum, s);
+                              nblocks, num_tokens_post_padded, prep, s);
   }
   if (rc != DSV4MOE_OK) return rc;
   if (route_in_prologue) dsv4host::prof_stamp(dsv4host::kStampRoute, s);
@@ -606,9 +606,14 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
   if (rc != DSV4MOE_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   dsv4host::prof_stamp(dsv4host::kStampBegin, s);
-  rc = layer_route_align("layer_w4a16", x, logits, bias, tokens, hidden, inter, experts, topk, score_func,
-                         route_scale, has_shared, block_size, ids, weights, margin, sorted_token_ids, capacity,
-                         expert_ids, num_tokens_post_padded, workspace, s);
+  size_t room = 0;
+  int32_t* scratch = dsv4_experts_align_scratch(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0, &room);
+  const dsv4::ActPrep prep{dsv4::kPrepRowSums, x, hidden,
+                           dsv4_experts_xsum(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0), nullptr,
+                           nullptr};
+  rc = layer_route_align("layer_w4a16", prep, scratch, room, logits, bias, tokens, experts, topk, score_func,
+                         route_scale, block_size, ids, weights, margin, sorted_token_ids, capacity, expert_ids,
+                         num_tokens_post_padded, s);
   if (rc != DSV4MOE_OK) return rc;
   return dsv4_launch_experts_w4a16(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s, w13r, w2r,
                                    has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
@@ -639,13 +644,86 @@ int dsv4moe_layer_mxfp4(const uint16_t* x, const float* logits, const float* bia
   dsv4host::prof_stamp(dsv4host::kStampBegin, s);
   // the MXFP4 kernels need no activation row sums (the E8M0 scale is exact
   // inside the conversion)
-  rc = layer_route_align("layer_mxfp4", nullptr, logits, bias, tokens, hidden, inter, experts, topk, score_func,
-                         route_scale, has_shared, block_size, ids, weights, margin, sorted_token_ids, capacity,
-                         expert_ids, num_tokens_post_padded, workspace, s);
+  size_t room = 0;
+  int32_t* scratch = dsv4_experts_align_scratch(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0, &room);
+  rc = layer_route_align("layer_mxfp4", dsv4::ActPrep{dsv4::kPrepNone, nullptr, 0, nullptr, nullptr, nullptr},
+                         scratch, room, logits, bias, tokens, experts, topk, score_func, route_scale, block_size,
+                         ids, weights, margin, sorted_token_ids, capacity, expert_ids, num_tokens_post_padded, s);
   if (rc != DSV4MOE_OK) return rc;
   return dsv4_launch_experts_mxfp4(x, tokens, hidden, inter, experts, topk, w13q, w13s, w2q, w2s,
                                    has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
                                    num_tokens_post_padded, block_size, clamp_limit, out, workspace, s);
+}
+
+// The W4A8 fused layer calls: route -> align (with x quantised to e4m3 by the
+// prologue's other workgroups) -> the W4A8 experts chain.  `mxfp4` picks the
+// MXFP4 W4A8 kernels (x in K order) over the int4 ones.
+static int layer_w4a8_common(const char* who, bool mxfp4, const uint16_t* x, const float* logits, const float* bias,
+                             int64_t tokens, int32_t hidden, int32_t inter, int32_t experts, int32_t topk,
+                             int32_t score_func, float route_scale, const uint8_t* w13q, const void* w13s,
+                             const uint8_t* w2q, const void* w2s, int32_t has_shared, float clamp_limit,
+                             int32_t block_size, int32_t* ids, float* weights, float* margin,
+                             int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                             int32_t* num_tokens_post_padded, uint16_t* out, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = validate_experts(x, tokens, hidden, inter, experts, topk, w13q, static_cast<const uint16_t*>(w13s), w2q,
+                            static_cast<const uint16_t*>(w2s), capacity, block_size, out, workspace, workspace_bytes,
+                            has_shared, who, true);
+  if (rc != DSV4MOE_OK || tokens == 0) return rc;
+  rc = validate_layer_route(who, logits, topk, score_func, route_scale, clamp_limit, ids, weights, sorted_token_ids,
+                            expert_ids, num_tokens_post_padded);
+  if (rc != DSV4MOE_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dsv4host::prof_stamp(dsv4host::kStampBegin, s);
+  uint8_t* xq = nullptr;
+  float* xscale = nullptr;
+  float* xsum = nullptr;
+  int32_t* scratch = nullptr;
+  size_t room = 0;
+  dsv4_experts_w4a8_pieces(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0, &xq, &xscale, &xsum,
+                           &scratch, &room);
+  const dsv4::ActPrep prep{mxfp4 ? dsv4::kPrepQuantNatural : dsv4::kPrepQuantInt4, x, hidden, xsum, xq, xscale};
+  rc = layer_route_align(who, prep, scratch, room, logits, bias, tokens, experts, topk, score_func, route_scale,
+                         block_size, ids, weights, margin, sorted_token_ids, capacity, expert_ids,
+                         num_tokens_post_padded, s);
+  if (rc != DSV4MOE_OK) return rc;
+  if (mxfp4)
+    return dsv4_launch_experts_w4a8_mxfp4(x, tokens, hidden, inter, experts, topk, w13q,
+                                          static_cast<const uint8_t*>(w13s), w2q, static_cast<const uint8_t*>(w2s),
+                                          has_shared ? 1 : 0, weights, sorted_token_ids, capacity, expert_ids,
+                                          num_tokens_post_padded, block_size, clamp_limit, out, workspace, s,
+                                          /*x_ready=*/true);
+  return dsv4_launch_experts_w4a8(x, tokens, hidden, inter, experts, topk, w13q, static_cast<const uint16_t*>(w13s),
+                                  w2q, static_cast<const uint16_t*>(w2s), has_shared ? 1 : 0, weights,
+                                  sorted_token_ids, capacity, expert_ids, num_tokens_post_padded, block_size,
+                                  clamp_limit, out, workspace, s, /*x_ready=*/true);
+}
+
+int dsv4moe_layer_w4a8(const uint16_t* x, const float* logits, const float* bias, int64_t tokens, int32_t hidden,
+                       int32_t inter, int32_t experts, int32_t topk, int32_t score_func, float route_scale,
+                       const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q, const uint16_t* w2s,
+                       int32_t has_shared, float clamp_limit, int32_t block_size, int32_t* ids, float* weights,
+                       float* margin, int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                       int32_t* num_tokens_post_padded, uint16_t* out, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  return layer_w4a8_common("layer_w4a8", false, x, logits, bias, tokens, hidden, inter, experts, topk, score_func,
+                           route_scale, w13q, w13s, w2q, w2s, has_shared, clamp_limit, block_size, ids, weights,
+                           margin, sorted_token_ids, capacity, expert_ids, num_tokens_post_padded, out, workspace,
+                           workspace_bytes, stream);
+}
+
+int dsv4moe_layer_w4a8_mxfp4(const uint16_t* x, const float* logits, const float* bias, int64_t tokens,
+                             int32_t hidden, int32_t inter, int32_t experts, int32_t topk, int32_t score_func,
+                             float route_scale, const uint8_t* w13q, const uint8_t* w13s, const uint8_t* w2q,
+                             const uint8_t* w2s, int32_t has_shared, float clamp_limit, int32_t block_size,
+                             int32_t* ids, float* weights, float* margin, int32_t* sorted_token_ids,
+                             int64_t capacity, int32_t* expert_ids, int32_t* num_tokens_post_padded, uint16_t* out,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  return layer_w4a8_common("layer_w4a8_mxfp4", true, x, logits, bias, tokens, hidden, inter, experts, topk,
+                           score_func, route_scale, w13q, w13s, w2q, w2s, has_shared, clamp_limit, block_size, ids,
+                           weights, margin, sorted_token_ids, capacity, expert_ids, num_tokens_post_padded, out,
+                           workspace, workspace_bytes, stream);
 }
 
 // ------------------------------------------------ allocation-free layer entry

@@ -393,7 +393,7 @@ int dsv4_launch_experts_w4a8_mxfp4(const uint16_t* x, int64_t tokens, int hidden
                                    const uint8_t* w2s, int has_shared, const float* weights,
                                    const int32_t* sorted, int64_t capacity, const int32_t* expert_ids,
                                    const int32_t* ntpp, int block_size, float clamp_limit, uint16_t* out,
-                                   void* workspace, hipStream_t stream) {
+                                   void* workspace, hipStream_t stream, bool x_ready) {
   if (tokens == 0) return DSV4MOE_OK;
   Fp8Workspace ws = carve_fp8(workspace, tokens, topk, hidden, inter, has_shared);
   const int max_blocks = (int)((capacity + block_size - 1) / block_size);
@@ -403,8 +403,10 @@ int dsv4_launch_experts_w4a8_mxfp4(const uint16_t* x, int64_t tokens, int hidden
   const int blocks = max_blocks + shared_blocks;
   const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
 
-  int rc = dsv4_launch_act_quant_fp8_rows(x, tokens, hidden, ws.xq, ws.xscale, stream);
-  if (rc != DSV4MOE_OK) return rc;
+  if (!x_ready) {  // else a prologue launch quantised x beside the alignment
+    const int rc = dsv4_launch_act_quant_fp8_rows(x, tokens, hidden, ws.xq, ws.xscale, stream);
+    if (rc != DSV4MOE_OK) return rc;
+  }
   dsv4host::prof_stamp(dsv4host::kStampRowSum, stream);
 
   ExpertGemmParams p{};
@@ -435,7 +437,7 @@ int dsv4_launch_experts_w4a8_mxfp4(const uint16_t* x, int64_t tokens, int hidden
   launch_fp4_stage(p, decode, 1, blocks, stream);
   DSV4_CHECK_LAUNCH("expert fp4 stage 1");
 
-  rc = dsv4_launch_act_quant_fp8_rows(ws.h, rows, inter, ws.hq, ws.hscale, stream);
+  int rc = dsv4_launch_act_quant_fp8_rows(ws.h, rows, inter, ws.hq, ws.hscale, stream);
   if (rc != DSV4MOE_OK) return rc;
   dsv4host::prof_stamp(dsv4host::kStampStage1, stream);
 

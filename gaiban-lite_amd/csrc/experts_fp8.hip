@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "act_quant.h"
 #include "experts_common.h"
 #include "../../include/dsv4moe.h"
 
@@ -55,86 +56,15 @@ constexpr float kInvSum = 1.0f / 64.0f;  // 8 * 2^-9
 constexpr float kUnScale = 512.0f;       // 2^9
 
 // ------------------------------------------------------------ activation quant
-// One wavefront per row (K % 512 == 0).  Writes q (e4m3, MFMA order), the
-// row scale and, per 128-K group, the fp32 sum of the 128 e4m3 values (each
-// lane adds its 8 values in K order, then a fixed xor tree over 16 lanes).
-// NATURAL: q in K order and no group sums (the MXFP4 W4A8 kernels' operand,
-// whose K order is the checkpoint's).
+// One wavefront per row (act_quant_row, act_quant.h), four rows per workgroup.
 template <bool NATURAL>
 __global__ __launch_bounds__(256) void act_quant_fp8_kernel(const uint16_t* __restrict__ x, int64_t rows,
                                                             int k, uint8_t* __restrict__ q,
                                                             float* __restrict__ scale,
                                                             float* __restrict__ gsum) {
-  const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint16_t* src = x + row * k;
-  const int iters = k / 512;
-  float amax = 0.0f;
-  for (int i = 0; i < iters; ++i) {
-    const u32x4 v = load16(src + (lane + 64 * i) * 8);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[e] << 16)));
-      amax = fmaxf(amax, fabsf(__uint_as_float(v[e] & 0xFFFF0000u)));
-    }
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  const float s = fmaxf(amax, 1e-12f) / 448.0f;
-  if (lane == 0) scale[row] = s;
-
-  const int groups = k / 128;
-  for (int i = 0; i < iters; ++i) {
-    const int o = lane + 64 * i;  // octet: K 8o .. 8o+7
-    const u32x4 v = load16(src + o * 8);
-    float f[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      f[2 * e] = __uint_as_float(v[e] << 16);
-      f[2 * e + 1] = __uint_as_float(v[e] & 0xFFFF0000u);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / s, -448.0f), 448.0f);
-    if constexpr (NATURAL) {
-      int lo = 0, hi = 0;
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], lo, false);
-      lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], lo, true);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4], f[5], hi, false);
-      hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6], f[7], hi, true);
-      *reinterpret_cast<u32x2*>(q + row * k + o * 8) = u32x2{(uint32_t)lo, (uint32_t)hi};
-      continue;
-    }
-    // output byte b holds K offset {0,4,1,5,2,6,3,7}[b]
-    int lo = 0, hi = 0;
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[4], lo, false);
-    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[1], f[5], lo, true);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[6], hi, false);
-    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[3], f[7], hi, true);
-    // decoded values in K order for the group sum
-    float dq[8];
-    dq[0] = __builtin_amdgcn_cvt_f32_fp8(lo, 0);
-    dq[4] = __builtin_amdgcn_cvt_f32_fp8(lo, 1);
-    dq[1] = __builtin_amdgcn_cvt_f32_fp8(lo, 2);
-    dq[5] = __builtin_amdgcn_cvt_f32_fp8(lo, 3);
-    dq[2] = __builtin_amdgcn_cvt_f32_fp8(hi, 0);
-    dq[6] = __builtin_amdgcn_cvt_f32_fp8(hi, 1);
-    dq[3] = __builtin_amdgcn_cvt_f32_fp8(hi, 2);
-    dq[7] = __builtin_amdgcn_cvt_f32_fp8(hi, 3);
-    float sum = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sum += dq[e];
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    sum += __shfl_xor(sum, 4, 64);
-    sum += __shfl_xor(sum, 8, 64);
-    const int g = o >> 4;
-    const int lo16 = o & 15;
-    const int d = lo16 >> 2;
-    const int j = lo16 & 3;
-    *reinterpret_cast<u32x2*>(q + row * k + g * 128 + j * 32 + d * 8) = u32x2{(uint32_t)lo, (uint32_t)hi};
-    if ((lane & 15) == 0) gsum[row * groups + g] = sum;
-  }
+  act_quant_row<NATURAL>(x, row, k, q, scale, gsum);
 }
 
 // ------------------------------------------------------------------ decode
@@ -529,6 +459,23 @@ size_t dsv4_experts_w4a8_workspace_bytes(int64_t tokens, int topk, int hidden, i
   return carve_fp8(nullptr, tokens, topk, hidden, inter, has_shared).bytes;
 }
 
+// The pieces of a W4A8 workspace a fused layer call fills before the experts
+// launches: the quantised x (codes, row scales, group sums), written by the
+// prologue beside the alignment, and the contribution region, which the
+// experts path writes only after it has read the alignment (the split
+// alignment's scratch).
+void dsv4_experts_w4a8_pieces(void* workspace, int64_t tokens, int topk, int hidden, int inter, int has_shared,
+                              uint8_t** xq, float** xscale, float** xsum, int32_t** scratch,
+                              size_t* scratch_bytes) {
+  const Fp8Workspace w = carve_fp8(workspace, tokens, topk, hidden, inter, has_shared);
+  const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
+  *xq = w.xq;
+  *xscale = w.xscale;
+  *xsum = w.xsum;
+  *scratch = reinterpret_cast<int32_t*>(w.contrib);
+  *scratch_bytes = sizeof(float) * (size_t)rows * hidden;
+}
+
 // Per-row e4m3 quantisation in K order (no group sums): the activation
 // operand of the MXFP4 W4A8 kernels.
 int dsv4_launch_act_quant_fp8_rows(const uint16_t* x, int64_t rows, int k, uint8_t* q, float* scale,
@@ -552,7 +499,8 @@ int dsv4_launch_experts_w4a8(const uint16_t* x, int64_t tokens, int hidden, int 
                              const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q,
                              const uint16_t* w2s, int has_shared, const float* weights, const int32_t* sorted,
                              int64_t capacity, const int32_t* expert_ids, const int32_t* ntpp, int block_size,
-                             float clamp_limit, uint16_t* out, void* workspace, hipStream_t stream) {
+                             float clamp_limit, uint16_t* out, void* workspace, hipStream_t stream,
+                             bool x_ready) {
   if (tokens == 0) return DSV4MOE_OK;
   Fp8Workspace ws = carve_fp8(workspace, tokens, topk, hidden, inter, has_shared);
   const int max_blocks = (int)((capacity + block_size - 1) / block_size);
@@ -562,8 +510,10 @@ int dsv4_launch_experts_w4a8(const uint16_t* x, int64_t tokens, int hidden, int 
   const int blocks = max_blocks + shared_blocks;
   const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
 
-  launch_act_quant(x, tokens, hidden, ws.xq, ws.xscale, ws.xsum, stream);
-  DSV4_CHECK_LAUNCH("act_quant_fp8_kernel (x)");
+  if (!x_ready) {  // else a prologue launch quantised x beside the alignment
+    launch_act_quant(x, tokens, hidden, ws.xq, ws.xscale, ws.xsum, stream);
+    DSV4_CHECK_LAUNCH("act_quant_fp8_kernel (x)");
+  }
   dsv4host::prof_stamp(dsv4host::kStampRowSum, stream);
 
   ExpertGemmParams p{};

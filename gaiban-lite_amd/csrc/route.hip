@@ -298,9 +298,7 @@ struct PrologueArgs {
   int32_t* expert_ids;
   int64_t num_blocks;
   int32_t* ntpp;
-  const uint16_t* x;   // row sums: x [tokens][hidden] (null: none)
-  int hidden;
-  float* xsum;         // [tokens][hidden / 64]
+  ActPrep prep;        // activation work of workgroups 1..
   int route;           // route in workgroup 0 (else ids are given)
 };
 
@@ -317,7 +315,7 @@ __global__ __launch_bounds__(kAlignThreads) void prologue_kernel(PrologueArgs a)
                 a.expert_ids, a.num_blocks, a.ntpp);
     return;
   }
-  row_sums_part(a.x, a.tokens, a.hidden, a.xsum, blockIdx.x - 1, gridDim.x - 1);
+  act_prep_part(a.prep, a.tokens, blockIdx.x - 1, gridDim.x - 1);
 }
 
 __global__ __launch_bounds__(256) void route_hash_kernel(
@@ -425,18 +423,17 @@ int dsv4_launch_route_hash(const float* logits, const int64_t* tid2eid, int64_t 
   return DSV4MOE_OK;
 }
 
-// [Route +] align [+ row sums when x is given] as one launch.
+// [Route +] align [+ the activation work of `prep`] as one launch.
 int dsv4_launch_prologue(int32_t route, const float* logits, const float* bias, int64_t tokens, int32_t experts,
                          int32_t topk, int32_t score_func, float route_scale, int32_t* ids, float* weights,
                          float* margin, int32_t block_size, int32_t* sorted_ids, int64_t capacity,
-                         int32_t* expert_ids, int64_t num_blocks, int32_t* ntpp, const uint16_t* x, int32_t hidden,
-                         float* xsum, hipStream_t stream) {
+                         int32_t* expert_ids, int64_t num_blocks, int32_t* ntpp, const ActPrep& prep,
+                         hipStream_t stream) {
   if (tokens == 0) return DSV4MOE_OK;
   PrologueArgs a{logits, bias, tokens, experts, topk, route_scale, ids, weights, margin, 0, block_size,
-                 sorted_ids, capacity, expert_ids, num_blocks, ntpp, x, hidden, xsum, route};
+                 sorted_ids, capacity, expert_ids, num_blocks, ntpp, prep, route};
   while ((1 << a.expert_bits) < experts) ++a.expert_bits;
-  const int64_t sums = x != nullptr ? tokens * (hidden / 64) : 0;
-  const unsigned grid = 1u + (unsigned)std::min<int64_t>((sums + kAlignThreads - 1) / kAlignThreads, 64);
+  const unsigned grid = 1u + (unsigned)act_prep_workgroups(prep, tokens, 64);
   const int epl = (experts + 63) / 64;
 #define DSV4_PROLOGUE(S, N) hipLaunchKernelGGL((prologue_kernel<S, N>), dim3(grid), dim3(kAlignThreads), 0, stream, a)
 #define DSV4_PROLOGUE_EPL(S)          \

@@ -871,7 +871,6 @@ class TP4MoE:
                 capture_key = (flat.shape[0], slot)
                 fused = (
                     self.route_kind == "learned"
-                    and self._marlin_input_dtype is None
                     and override is None
                     and self._active_alignment_provider is None
                     and self._route_tensor_observer is None
@@ -881,6 +880,22 @@ class TP4MoE:
                 if self.route_kind == "learned" and router_logits is None:
                     ops.gate_logits_into(flat, self._gate_weight, buffers.logits)
                 logits = router_logits if router_logits is not None else buffers.logits
+                if fused and self._marlin_input_dtype is not None:
+                    # route -> align (x quantised beside it) -> W4A8 experts -> combine
+                    ops.layer_w4a8_into(
+                        flat, logits, self._gate_bias, topk=cfg.topk, score_func=cfg.score_func,
+                        route_scale=cfg.route_scale, w13q=self.resident.w13_q,
+                        w13s=self.resident.w13_s, w2q=self.resident.w2_q, w2s=self.resident.w2_s,
+                        experts=cfg.experts, inter=cfg.intermediate_size,
+                        has_shared=self._grouped_shared, clamp_limit=cfg.clamp_limit,
+                        block_size=buffers.block_size_m, ids=buffers.route_ids,
+                        weights=buffers.route_weights, margin=buffers.margin,
+                        sorted_token_ids=a.sorted_token_ids, expert_ids=a.expert_ids,
+                        num_tokens_post_padded=a.num_tokens_post_padded, out=output,
+                        workspace=buffers.workspace, mxfp4=self._mxfp4,
+                    )
+                    self._add_shared_fp8(flat, buffers, output)
+                    return buffers.route_weights, buffers.route_ids, buffers.margin, {}
                 if fused:
                     # route -> align -> experts -> combine in one C-ABI call
                     ops.layer_w4a16_into(

@@ -446,6 +446,55 @@ def layer_w4a16_into(
     )
 
 
+def layer_w4a8_into(
+    x: torch.Tensor,
+    logits: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    topk: int,
+    score_func: str | int,
+    route_scale: float,
+    w13q, w13s, w2q, w2s,
+    experts: int,
+    inter: int,
+    has_shared: bool,
+    clamp_limit: float,
+    block_size: int,
+    ids: torch.Tensor,
+    weights: torch.Tensor,
+    margin: torch.Tensor | None,
+    sorted_token_ids: torch.Tensor,
+    expert_ids: torch.Tensor,
+    num_tokens_post_padded: torch.Tensor,
+    out: torch.Tensor,
+    workspace: torch.Tensor,
+    mxfp4: bool = False,
+) -> None:
+    """The fused W4A8 layer entry (``dsv4moe_layer_w4a8`` over int4 residents,
+    or with ``mxfp4`` ``dsv4moe_layer_w4a8_mxfp4`` over MXFP4 residents packed
+    for the W4A8 kernels): x is quantised beside the alignment; the workspace
+    is ``experts_w4a8_workspace_bytes``."""
+
+    tokens, hidden = x.shape
+    dev = x.device
+    _check("x", x, dtype=torch.bfloat16, device=dev)
+    _check("logits", logits, dtype=torch.float32, shape=(tokens, experts), device=dev)
+    _check("ids", ids, dtype=torch.int32, shape=(tokens, topk), device=dev)
+    _check("weights", weights, dtype=torch.float32, shape=(tokens, topk), device=dev)
+    _check("out", out, dtype=torch.bfloat16, shape=(tokens, hidden), device=dev)
+    _check("workspace", workspace, dtype=torch.uint8, device=dev)
+    if bias is not None:
+        _check("bias", bias, dtype=torch.float32, shape=(experts,), device=dev)
+    call(
+        "dsv4moe_layer_w4a8_mxfp4" if mxfp4 else "dsv4moe_layer_w4a8", ptr(x), ptr(logits), ptr(bias), tokens,
+        hidden, inter, experts, topk, score_func_id(score_func), float(route_scale), ptr(w13q), ptr(w13s),
+        ptr(w2q), ptr(w2s), int(bool(has_shared)), float(clamp_limit), block_size, ptr(ids), ptr(weights),
+        ptr(margin), ptr(sorted_token_ids), sorted_token_ids.numel(), ptr(expert_ids),
+        ptr(num_tokens_post_padded), ptr(out), ptr(workspace), workspace.numel(),
+        _lib.current_stream(dev),
+    )
+
+
 def pack_int8(weight: torch.Tensor) -> torch.Tensor:
     """Row-major int8 [n, k] -> tiled uint8 [n*k] (16 rows x 64 K per KiB tile)."""
 

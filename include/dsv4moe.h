@@ -353,6 +353,34 @@ int dsv4moe_layer_mxfp4(const uint16_t* x, const float* logits, const float* bia
                         size_t workspace_bytes, void* stream);
 
 /*
+ * Whole MoE layer in the W4A8 mode (marlin_input_dtype = float8_e4m3fn):
+ * route (from logits) -> align -> W4A8 experts -> combine, with the per-row
+ * e4m3 quantisation of x done by the alignment launch's other workgroups.
+ * Arguments as dsv4moe_layer_w4a16 without the ratios; the workspace size is
+ * dsv4moe_experts_w4a8_workspace_bytes.  dsv4moe_layer_w4a8 takes the int4
+ * weights of dsv4moe_experts_w4a8, dsv4moe_layer_w4a8_mxfp4 the MXFP4 weights
+ * of dsv4moe_experts_w4a8_mxfp4 (w13s / w2s the packed E8M0 bytes); the
+ * results are bit-identical to route, align and that experts entry called in
+ * turn.  Replaces TP4MoE.compute_partial
+ * (runtime/dsv4_direct/moe_runtime.py:1714-1888) with
+ * _preset_w4a8_activation_quant (moe_runtime.py:207-235) at world size 1.
+ */
+int dsv4moe_layer_w4a8(const uint16_t* x, const float* logits, const float* bias, int64_t tokens, int32_t hidden,
+                       int32_t inter, int32_t experts, int32_t topk, int32_t score_func, float route_scale,
+                       const uint8_t* w13q, const uint16_t* w13s, const uint8_t* w2q, const uint16_t* w2s,
+                       int32_t has_shared, float clamp_limit, int32_t block_size, int32_t* ids, float* weights,
+                       float* margin, int32_t* sorted_token_ids, int64_t capacity, int32_t* expert_ids,
+                       int32_t* num_tokens_post_padded, uint16_t* out, void* workspace, size_t workspace_bytes,
+                       void* stream);
+int dsv4moe_layer_w4a8_mxfp4(const uint16_t* x, const float* logits, const float* bias, int64_t tokens,
+                             int32_t hidden, int32_t inter, int32_t experts, int32_t topk, int32_t score_func,
+                             float route_scale, const uint8_t* w13q, const uint8_t* w13s, const uint8_t* w2q,
+                             const uint8_t* w2s, int32_t has_shared, float clamp_limit, int32_t block_size,
+                             int32_t* ids, float* weights, float* margin, int32_t* sorted_token_ids,
+                             int64_t capacity, int32_t* expert_ids, int32_t* num_tokens_post_padded, uint16_t* out,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Weight layouts of the dense linears (argument weight_layout):
  *   DSV4MOE_WEIGHT_ROWMAJOR  the checkpoint's bytes as stored, row-major [n, k]
  *                            (what the reference's entry points take);
