@@ -249,7 +249,9 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(E
 // MFMAs.  Work items (block, tile) follow prefill_item: groups of
 // consecutive blocks run tile by tile on one XCD, so a weight tile is
 // fetched once for the group and a block's token rows stay in that XCD's L2
-// across its tiles.
+// across its tiles.  Three workgroups per CU (at most 168 VGPRs: the
+// compiler spills a few setup values outside the K loops, none inside them);
+// the third workgroup hides more of the issue stalls than it costs.
 constexpr int kPfSlots = 64;
 
 // An expert whose group scales spread too widely for the running-sum scaling
@@ -260,7 +262,7 @@ __device__ __forceinline__ bool expert_needs_exact(const ExpertGemmParams& p, in
 }
 
 template <int STAGE>
-__global__ __launch_bounds__(256, 2) void expert_prefill_kernel(ExpertGemmParams p, int total_blocks) {
+__global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams p, int total_blocks) {
   constexpr int R = 4;
   // Per group, copied into LDS by buffer_load ... lds (double buffered):
   //  * token tile: 64 slots x 256 B, 16-byte part p of slot s stored at part

@@ -129,20 +129,44 @@ def test_mxfp4_prefill_reads_no_register_in_flight(tmp_path):
         assert inflight_register_reads(asm, name) == [], name
 
 
+def loop_instructions(asm: str, kernel: str) -> list[str]:
+    """The instructions of `kernel` inside loops: the blocks the compiler's
+    listing marks as a loop header or as in a loop."""
+
+    start = asm.index(kernel + ":")
+    lines = asm[start:asm.index(".Lfunc_end", start)].split("\n")
+    out, inloop = [], False
+    for line in lines:
+        s = line.strip()
+        if s.startswith(".LBB") or s.startswith("; %bb."):
+            inloop = "Loop" in s
+            continue
+        if inloop and s and not s.startswith((";", ".")):
+            out.append(s)
+    return out
+
+
 def test_int4_prefill_kernel_register_weights(tmp_path):
     """The int4 (W4A16) prefill kernel keeps its next weight group in
-    registers loaded by inline assembly as well: no spills, and nothing reads
-    those registers before the explicit wait."""
+    registers loaded by inline assembly as well, at three 256-thread
+    workgroups per CU (at most 168 VGPRs, a third of the LDS): nothing reads
+    those registers before the explicit wait (a spill of one would), and
+    nothing inside the K loops touches scratch.  A few values that live
+    across the loops (setup addresses) may be spilled outside them."""
 
     meta = kernel_metadata(CSRC / "experts.hip", tmp_path)
-    prefill = {k: v for k, v in meta.items() if "expert_prefill_kernel" in k}
+    prefill = {k: v for k, v in meta.items() if "expert_prefill_kernel" in k and "exact" not in k}
     assert len(prefill) == 2
     for name, m in prefill.items():
-        assert m["vgpr_spill_count"] == 0, name
+        assert m["vgpr_count"] <= 168, name
         assert m["sgpr_spill_count"] == 0, name
+        assert m["group_segment_fixed_size"] <= 160 * 1024 // 3, name
     asm = _device_asm(CSRC / "experts.hip", tmp_path)
     for name in prefill:
         assert inflight_register_reads(asm, name) == [], name
+        body = loop_instructions(asm, name)
+        assert sum(1 for s in body if s.startswith("v_mfma")) >= 64, name
+        assert [s for s in body if s.startswith("scratch_")] == [], name
 
 
 def _device_asm(src: Path, tmp_path: Path) -> str:
