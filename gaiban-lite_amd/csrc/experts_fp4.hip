@@ -197,18 +197,22 @@ __global__ __launch_bounds__(256, 4) void expert_fp4_decode_kernel(ExpertGemmPar
 // strip assignment and work order of the other prefill kernels.  Per group
 // the 64 x 128 B token tile (16-byte part q of slot s at q ^ swz128(s)),
 // each wavefront's 4 weight tiles and its two pairs' scale blocks are copied
-// into LDS by buffer_load ... lds in a three-buffer ring two groups ahead
-// (75 KiB per workgroup, two per CU).  Per group a wavefront issues 16 MFMAs
-// and no VALU work on the accumulators.
+// into LDS by buffer_load ... lds in a ring of RING buffers, RING - 1 groups
+// ahead: 25 KiB per buffer, so RING = 2 runs three workgroups per CU and
+// RING = 3 (copies two groups ahead) two.  Per group a wavefront issues 16
+// MFMAs and no VALU work on the accumulators.
 constexpr int kF4Slots = 64;
+constexpr int kF4Ring = 2;
 
-template <int STAGE>
-__global__ __launch_bounds__(256, 2) void expert_fp4_prefill_kernel(ExpertGemmParams p, int total_blocks) {
+template <int STAGE, int RING>
+__global__ __launch_bounds__(256, RING == 2 ? 3 : 2) void expert_fp4_prefill_kernel(ExpertGemmParams p,
+                                                                                   int total_blocks) {
+  static_assert(RING == 2 || RING == 3, "two or three buffers");
   constexpr int R = 4;
   constexpr int C = 4;
-  __shared__ __attribute__((aligned(16))) uint8_t xs[3][kF4Slots * 128];
-  __shared__ __attribute__((aligned(16))) uint8_t wts[3][4][R * kTileBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t scl[3][4][256];
+  __shared__ __attribute__((aligned(16))) uint8_t xs[RING][kF4Slots * 128];
+  __shared__ __attribute__((aligned(16))) uint8_t wts[RING][4][R * kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t scl[RING][4][256];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 
@@ -265,12 +269,13 @@ __global__ __launch_bounds__(256, 2) void expert_fp4_prefill_kernel(ExpertGemmPa
   const int sw = lane & 15;
   const int jg = lane >> 4;
   constexpr int kLoads = 2 + 4 + 1;  // copies one issue() makes per wavefront
-  // Step g: copy group g + 2 into buffer (u + 2) % 3 (released by step g - 1's
-  // barrier), compute group g from buffer u, wait for group g + 1.
+  // Step g: copy group g + RING - 1 into buffer (u + RING - 1) % RING
+  // (released by step g - 1's barrier), compute group g from buffer u, wait
+  // for group g + 1.
   auto step = [&](int g, auto u_c) {
     constexpr int u = decltype(u_c)::value;
-    const bool issue2 = g + 2 < groups;
-    if (issue2) issue(g + 2, (u + 2) % 3);
+    const bool issue2 = g + RING - 1 < groups;
+    if (issue2) issue(g + RING - 1, (u + RING - 1) % RING);
     i32x8 bfr[C];
 #pragma unroll
     for (int ct = 0; ct < C; ++ct) {
@@ -288,28 +293,31 @@ __global__ __launch_bounds__(256, 2) void expert_fp4_prefill_kernel(ExpertGemmPa
 #pragma unroll
       for (int ct = 0; ct < C; ++ct) acc[r][ct] = mfma_fp4_fp8(a, bfr[ct], sc, acc[r][ct]);
     }
-    if (issue2) lds_dma_wait_keep<kLoads>();  // this wavefront's copies of group g + 1 have landed
+    // this wavefront's copies of group g + 1 have landed (with three buffers
+    // the newest group's copies stay in flight)
+    if (RING == 3 && issue2) lds_dma_wait_keep<kLoads>();
     else lds_dma_wait_all();
-    __syncthreads();                          // ... and everyone's; buffer u is free again
+    __syncthreads();  // ... and everyone's; buffer u is free again
   };
   using U0 = std::integral_constant<int, 0>;
   using U1 = std::integral_constant<int, 1>;
   using U2 = std::integral_constant<int, 2>;
 
   issue(0, 0);
-  if (groups > 1) {
+  if (RING == 3 && groups > 1) {
     issue(1, 1);
     lds_dma_wait_keep<kLoads>();
   } else {
     lds_dma_wait_all();
   }
   __syncthreads();
-  // the last two steps copy nothing and the last waits for everything, so no
-  // copy is outstanding at exit
-  for (int g = 0; g < groups; g += 3) {
+  // the last RING - 1 steps copy nothing and the last waits for everything,
+  // so no copy is outstanding at exit
+  for (int g = 0; g < groups; g += RING) {
     step(g, U0{});
     if (g + 1 < groups) step(g + 1, U1{});
-    if (g + 2 < groups) step(g + 2, U2{});
+    if constexpr (RING == 3)
+      if (g + 2 < groups) step(g + 2, U2{});
   }
 
 #pragma unroll
@@ -376,8 +384,10 @@ static void launch_fp4_stage(const ExpertGemmParams& p, bool decode, int stage, 
     }
   } else {
     const dim3 grid((unsigned)prefill_grid(blocks, p.n_tiles));
-    if (stage == 1) hipLaunchKernelGGL(expert_fp4_prefill_kernel<1>, grid, dim3(256), 0, stream, p, blocks);
-    else hipLaunchKernelGGL(expert_fp4_prefill_kernel<2>, grid, dim3(256), 0, stream, p, blocks);
+    if (stage == 1)
+      hipLaunchKernelGGL((expert_fp4_prefill_kernel<1, kF4Ring>), grid, dim3(256), 0, stream, p, blocks);
+    else
+      hipLaunchKernelGGL((expert_fp4_prefill_kernel<2, kF4Ring>), grid, dim3(256), 0, stream, p, blocks);
   }
 }
 
