@@ -618,7 +618,7 @@ def main() -> int:
         "ms_per_step_fixed_routing": round(ms_fixed, 5),
         "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
         "roofline": {
-            "kernel": "expert_decode_kernel<1, 8> (w13 + SwiGLU), decode T=64",
+            "kernel": "expert_decode_kernel<1, 8, false> (w13 + SwiGLU), decode T=64",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

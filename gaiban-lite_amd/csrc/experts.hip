@@ -59,9 +59,20 @@ struct DecodeItem {
   int64_t rowid;       // lane: row id of its slot, -1 if padded
   int n0;
   float wmul;          // 1, or NaN when the block names no valid expert (stage-2 multiplier)
+  bool skip;           // PAIR: the block is the second of a pair, computed by the first
 };
 
-template <int STAGE>
+// Pairing of 8-slot blocks (PAIR, chosen at launch for block size 8 and on
+// average at least 4 slots per expert): consecutive blocks of one expert
+// pair up from the start of the expert's run of blocks, and the first block
+// of a pair takes both blocks' 16 slots as one item, so the expert's weights
+// stream once for them; the second block's items are skipped.  The position
+// in the run is counted back over at most kPairScan blocks; blocks further
+// into a long run stay unpaired, which keeps the pairs consistent (a block
+// pairs with the next only while both positions are below kPairScan).
+constexpr int kPairScan = 16;
+
+template <int STAGE, bool PAIR>
 __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int item, int routed, int64_t tk) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -72,16 +83,28 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
   DecodeItem it;
+  it.skip = false;
+  int span = p.block_size;
+  if (PAIR && bi < routed) {
+    const int e = p.expert_ids[blk];
+    int pos = 0;
+    while (pos < kPairScan && pos < blk && p.expert_ids[blk - pos - 1] == e) ++pos;
+    if (pos < kPairScan && (pos & 1)) {
+      it.skip = true;
+      return it;
+    }
+    if (pos + 1 < kPairScan && blk + 1 < routed && p.expert_ids[blk + 1] == e) span = 2 * p.block_size;
+  }
   it.n0 = STAGE == 1 ? tile * 64 : tile * 128;
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
   it.ws = p.ws + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 32 + 8 * (lane >> 4);
   it.wmul = b.poison ? __builtin_nanf("") : 1.0f;
-  it.rowid = slot_rowid(p, b, lane & 15, tk);
+  it.rowid = slot_rowid_span(p, b, lane & 15, tk, span);
   const int64_t arow = act_row_of<STAGE>(it.rowid, tk, p.topk);
   it.sum_base = arow >= 0 ? (uint32_t)(arow * sums_per_row * 4) : kOobOffset;
   const int ld_slot = threadIdx.x >> 4;
-  const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
+  const int64_t ld_row = act_row_of<STAGE>(slot_rowid_span(p, b, ld_slot, tk, span), tk, p.topk);
   it.ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + (threadIdx.x & 15) * 16) : kOobOffset;
   return it;
 }
@@ -92,7 +115,7 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
 // the deeper ring at every T measured; stage 2 (128 KiB items) keeps RING = 4
 // unless its items fit one wave of resident workgroups (T ~ 1), where the
 // bytes in flight per workgroup, not the workgroup count, bound the stream.
-template <int STAGE, int RING>
+template <int STAGE, int RING, bool PAIR>
 __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(ExpertGemmParams p) {
   constexpr int R = 2;
   constexpr int kAhead = RING - 2;
@@ -120,9 +143,21 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(E
 #pragma unroll
   for (int d = 0; d < 4; ++d) rd_lds[d] = (lane & 15) * 256 + (((4 * d + (lane >> 4)) ^ (lane & 15)) * 16);
 
-  DecodeItem cur = decode_item<STAGE>(p, item, routed, tk);
-  int next = item + stride;
-  DecodeItem nxt = next < n_items ? decode_item<STAGE>(p, next, routed, tk) : cur;
+  // this workgroup's next item from index i on (n_items when none is left),
+  // passing over the items of paired second blocks
+  auto fetch = [&](int i, DecodeItem& it) {
+    for (; i < n_items; i += stride) {
+      it = decode_item<STAGE, PAIR>(p, i, routed, tk);
+      if (!it.skip) return i;
+    }
+    return n_items;
+  };
+  DecodeItem cur;
+  item = fetch(item, cur);
+  if (item >= n_items) return;  // uniform per workgroup
+  DecodeItem nxt;
+  int next = fetch(item + stride, nxt);
+  if (next >= n_items) nxt = cur;
 
   // Weights kAhead groups ahead (ring RING), activations + sums one group
   // ahead (ring 2).  At the end of an item the prefetches continue with the
@@ -230,8 +265,8 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(E
     if (next >= n_items) break;  // uniform per workgroup; the last prefetches re-read cur
     item = next;
     cur = nxt;
-    next = item + stride;
-    nxt = next < n_items ? decode_item<STAGE>(p, next, routed, tk) : cur;
+    next = fetch(item + stride, nxt);
+    if (next >= n_items) nxt = cur;
   }
 }
 
@@ -779,7 +814,7 @@ using namespace dsv4;
 
 // Resident workgroups of a decode kernel on the current device (CUs x
 // occupancy), cached per device: the persistent grid size.
-template <int STAGE, int RING>
+template <int STAGE, int RING, bool PAIR>
 static int decode_resident_grid() {
   static int cache[64] = {0};
   int dev = 0;
@@ -787,7 +822,7 @@ static int decode_resident_grid() {
   if (cache[dev] == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, expert_decode_kernel<STAGE, RING>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, expert_decode_kernel<STAGE, RING, PAIR>, 256, 0) !=
             hipSuccess ||
         per_cu <= 0)
       per_cu = 1;
@@ -801,16 +836,29 @@ static int decode_resident_grid() {
 // blocks, T ~ 1), when K allows it; else the four-workgroups-per-CU kernel.
 // Either grid is at most one wave of resident workgroups (persistent items).  `blocks` bounds the active blocks
 // (the kernel reads the real count from the alignment on the device).
+template <int STAGE, bool PAIR>
+static void launch_decode_as(const ExpertGemmParams& p, int blocks, hipStream_t stream) {
+  const int items = p.n_tiles * blocks;
+  if ((p.k_dim / kGroup) % 8 == 0 && (STAGE == 1 || items <= decode_resident_grid<STAGE, 8, PAIR>())) {
+    const int grid = std::min(items, decode_resident_grid<STAGE, 8, PAIR>());
+    hipLaunchKernelGGL((expert_decode_kernel<STAGE, 8, PAIR>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  } else {
+    const int grid = std::min(items, decode_resident_grid<STAGE, 4, PAIR>());
+    hipLaunchKernelGGL((expert_decode_kernel<STAGE, 4, PAIR>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  }
+}
+
+// Pairs of 8-slot blocks pay off once an expert often holds more than one
+// block (on average at least 4 of its slots per 8-slot block); below that the
+// extra expert-id reads per item cost more than they save.
+static bool decode_pairs(const ExpertGemmParams& p) {
+  return p.block_size == 8 && p.tokens * p.topk >= 4 * (int64_t)p.experts;
+}
+
 template <int STAGE>
 static void launch_decode(const ExpertGemmParams& p, int blocks, hipStream_t stream) {
-  const int items = p.n_tiles * blocks;
-  if ((p.k_dim / kGroup) % 8 == 0 && (STAGE == 1 || items <= decode_resident_grid<STAGE, 8>())) {
-    const int grid = std::min(items, decode_resident_grid<STAGE, 8>());
-    hipLaunchKernelGGL((expert_decode_kernel<STAGE, 8>), dim3((unsigned)grid), dim3(256), 0, stream, p);
-  } else {
-    const int grid = std::min(items, decode_resident_grid<STAGE, 4>());
-    hipLaunchKernelGGL((expert_decode_kernel<STAGE, 4>), dim3((unsigned)grid), dim3(256), 0, stream, p);
-  }
+  if (decode_pairs(p)) launch_decode_as<STAGE, true>(p, blocks, stream);
+  else launch_decode_as<STAGE, false>(p, blocks, stream);
 }
 
 size_t dsv4_experts_workspace_bytes(int64_t tokens, int topk, int hidden, int inter,

@@ -96,6 +96,17 @@ __device__ __forceinline__ int64_t slot_rowid(const ExpertGemmParams& p, const B
   return t < p.tokens ? tk + t : -1;
 }
 
+// As slot_rowid for a routed block taken together with the next block of the
+// same expert (`routed_slots` = twice the block size; the two blocks' slots
+// are contiguous in sorted_token_ids).
+__device__ __forceinline__ int64_t slot_rowid_span(const ExpertGemmParams& p, const BlockInfo& b, int col,
+                                                   int64_t tk, int routed_slots) {
+  if (b.shared) return slot_rowid(p, b, col, tk);
+  if (col >= routed_slots) return -1;
+  const int32_t f = p.sorted[b.slot_base + col];
+  return (f >= 0 && f < tk) ? (int64_t)f : -1;
+}
+
 template <int STAGE>
 __device__ __forceinline__ int64_t act_row_of(int64_t rowid, int64_t tk, int topk) {
   if (rowid < 0) return -1;

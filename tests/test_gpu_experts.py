@@ -297,3 +297,27 @@ def test_extreme_scale_spread_takes_the_exact_path():
     assert_moe_close(outs[64], outs[16], what="prefill (exact path) vs decode")
     assert_moe_close(outs[64], ref, what="prefill (exact path) vs oracle")
     assert_moe_close(outs[16], ref, what="decode vs oracle")
+
+
+@pytest.mark.parametrize("t,zipf", [(40, False), (600, False), (300, True)])
+def test_paired_8_slot_blocks_equal_16_slot_blocks(t, zipf):
+    """Decode blocks of 8 slots pair up (two consecutive blocks of one expert
+    taken as one 16-slot item) once the experts average at least 4 slots per
+    block: the output equals, bit for bit, the same routing aligned in blocks
+    of 16 (a slot's result does not depend on how slots are grouped),
+    including runs longer than the 16-block position scan (T=600: about 19
+    blocks per expert) and Zipf routing, and matches the fp32 oracle."""
+
+    shape = S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True)
+    print(f"[experts] paired 8-slot blocks T={t} zipf={zipf}", flush=True)
+    x = S.make_hidden(t, shape.hidden, seed=61, device=DEV)
+    r = route_from_logits(S.make_logits(t, shape.experts, seed=62, device=DEV), topk=shape.topk)
+    ids = S.zipf_ids(t, shape.experts, shape.topk, seed=63, device=DEV) if zipf else r.routing_ids
+    out8 = run_experts(shape, x, ids, r.routing_weights, block_size=8)
+    out16 = run_experts(shape, x, ids, r.routing_weights, block_size=16)
+    assert torch.equal(out8, out16)
+    _, src = layer(shape)
+    rows = np.arange(t) if t <= 64 else np.sort(np.random.default_rng(t).choice(t, 64, replace=False))
+    ref = O.moe_fp32(to_np_f32(x), ids.cpu().numpy(), r.routing_weights.cpu().numpy(), src,
+                     shared_index=shape.experts, rows=rows)
+    assert_moe_close(to_np_f32(out8)[rows], ref, what=f"paired T={t}")
