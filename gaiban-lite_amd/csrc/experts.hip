@@ -62,16 +62,6 @@ struct DecodeItem {
   bool skip;           // PAIR: the block is the second of a pair, computed by the first
 };
 
-// Pairing of 8-slot blocks (PAIR, chosen at launch for block size 8 and on
-// average at least 4 slots per expert): consecutive blocks of one expert
-// pair up from the start of the expert's run of blocks, and the first block
-// of a pair takes both blocks' 16 slots as one item, so the expert's weights
-// stream once for them; the second block's items are skipped.  The position
-// in the run is counted back over at most kPairScan blocks; blocks further
-// into a long run stay unpaired, which keeps the pairs consistent (a block
-// pairs with the next only while both positions are below kPairScan).
-constexpr int kPairScan = 16;
-
 template <int STAGE, bool PAIR>
 __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int item, int routed, int64_t tk) {
   const int lane = threadIdx.x & 63;
@@ -83,18 +73,9 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
   const int groups = p.k_dim / kGroup;
   const int sums_per_row = p.k_dim / kSumChunk;
   DecodeItem it;
-  it.skip = false;
-  int span = p.block_size;
-  if (PAIR && bi < routed) {
-    const int e = p.expert_ids[blk];
-    int pos = 0;
-    while (pos < kPairScan && pos < blk && p.expert_ids[blk - pos - 1] == e) ++pos;
-    if (pos < kPairScan && (pos & 1)) {
-      it.skip = true;
-      return it;
-    }
-    if (pos + 1 < kPairScan && blk + 1 < routed && p.expert_ids[blk + 1] == e) span = 2 * p.block_size;
-  }
+  const int span = decode_block_span<PAIR>(p, bi, routed);
+  it.skip = span == 0;
+  if (it.skip) return it;
   it.n0 = STAGE == 1 ? tile * 64 : tile * 128;
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
@@ -846,13 +827,6 @@ static void launch_decode_as(const ExpertGemmParams& p, int blocks, hipStream_t 
     const int grid = std::min(items, decode_resident_grid<STAGE, 4, PAIR>());
     hipLaunchKernelGGL((expert_decode_kernel<STAGE, 4, PAIR>), dim3((unsigned)grid), dim3(256), 0, stream, p);
   }
-}
-
-// Pairs of 8-slot blocks pay off once an expert often holds more than one
-// block (on average at least 4 of its slots per 8-slot block); below that the
-// extra expert-id reads per item cost more than they save.
-static bool decode_pairs(const ExpertGemmParams& p) {
-  return p.block_size == 8 && p.tokens * p.topk >= 4 * (int64_t)p.experts;
 }
 
 template <int STAGE>

@@ -107,6 +107,37 @@ __device__ __forceinline__ int64_t slot_rowid_span(const ExpertGemmParams& p, co
   return (f >= 0 && f < tk) ? (int64_t)f : -1;
 }
 
+// Pairing of 8-slot decode blocks (PAIR, chosen at launch by decode_pairs):
+// consecutive blocks of one expert pair up from the start of the expert's run
+// of blocks, and the first block of a pair takes both blocks' 16 slots as one
+// item, so the expert's weights stream once for them; the second block's
+// items are skipped.  The position in the run is counted back over at most
+// kPairScan blocks; blocks further into a long run stay unpaired, which keeps
+// the pairs consistent (a block pairs with the next only while both
+// positions are below kPairScan).
+constexpr int kPairScan = 16;
+
+// Routed slots of decode block `bi` (< routed: a routed block): the block
+// size, twice it when the block leads a pair, 0 when it is a pair's second
+// block; shared-expert blocks (bi >= routed) keep their own size.
+template <bool PAIR>
+__device__ __forceinline__ int decode_block_span(const ExpertGemmParams& p, int bi, int routed) {
+  if (!PAIR || bi >= routed) return p.block_size;
+  const int e = p.expert_ids[bi];
+  int pos = 0;
+  while (pos < kPairScan && pos < bi && p.expert_ids[bi - pos - 1] == e) ++pos;
+  if (pos < kPairScan && (pos & 1)) return 0;
+  if (pos + 1 < kPairScan && bi + 1 < routed && p.expert_ids[bi + 1] == e) return 2 * p.block_size;
+  return p.block_size;
+}
+
+// Pairs of 8-slot blocks pay off once an expert often holds more than one
+// block (on average at least 4 of its slots per 8-slot block); below that the
+// extra expert-id reads per item cost more than they save.
+inline bool decode_pairs(const ExpertGemmParams& p) {
+  return p.block_size == 8 && p.tokens * p.topk >= 4 * (int64_t)p.experts;
+}
+
 template <int STAGE>
 __device__ __forceinline__ int64_t act_row_of(int64_t rowid, int64_t tk, int topk) {
   if (rowid < 0) return -1;

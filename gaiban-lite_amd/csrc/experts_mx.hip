@@ -59,9 +59,10 @@ struct MxItem {
   int64_t rowid;       // lane: row id of its slot, -1 if padded
   int n0;
   float wmul;          // 1, or NaN when the block names no valid expert (stage-2 multiplier)
+  bool skip;           // PAIR: the block is the second of a pair, computed by the first
 };
 
-template <int STAGE>
+template <int STAGE, bool PAIR>
 __device__ __forceinline__ MxItem mx_item(const ExpertGemmParams& p, int item, int routed, int64_t tk) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -71,19 +72,22 @@ __device__ __forceinline__ MxItem mx_item(const ExpertGemmParams& p, int item, i
   const BlockInfo b = block_info(p, blk);
   const int groups = p.k_dim / kGroup;
   MxItem it;
+  const int span = decode_block_span<PAIR>(p, bi, routed);
+  it.skip = span == 0;
+  if (it.skip) return it;
   it.n0 = STAGE == 1 ? tile * 64 : tile * 128;
   const int pair = tile * 4 + wave;
   it.wq = p.wq + (int64_t)b.expert * p.wq_stride + (int64_t)pair * groups * 2048 + lane * 16;
   it.ws = p.ws8 + (int64_t)b.expert * p.ws_stride + (int64_t)pair * groups * 128 + (lane & 15) * 8;
   it.wmul = b.poison ? __builtin_nanf("") : 1.0f;
-  it.rowid = slot_rowid(p, b, lane & 15, tk);
+  it.rowid = slot_rowid_span(p, b, lane & 15, tk, span);
   const int ld_slot = threadIdx.x >> 4;
-  const int64_t ld_row = act_row_of<STAGE>(slot_rowid(p, b, ld_slot, tk), tk, p.topk);
+  const int64_t ld_row = act_row_of<STAGE>(slot_rowid_span(p, b, ld_slot, tk, span), tk, p.topk);
   it.ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + (threadIdx.x & 15) * 16) : kOobOffset;
   return it;
 }
 
-template <int STAGE>
+template <int STAGE, bool PAIR>
 __global__ __launch_bounds__(256, 4) void mx_decode_kernel(ExpertGemmParams p) {
   constexpr int R = 2;
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * 256];  // part q of slot s at q ^ s
@@ -105,9 +109,21 @@ __global__ __launch_bounds__(256, 4) void mx_decode_kernel(ExpertGemmParams p) {
 #pragma unroll
   for (int d = 0; d < 4; ++d) rd_lds[d] = (lane & 15) * 256 + (((4 * d + (lane >> 4)) ^ (lane & 15)) * 16);
 
-  MxItem cur = mx_item<STAGE>(p, item, routed, tk);
-  int next = item + stride;
-  MxItem nxt = next < n_items ? mx_item<STAGE>(p, next, routed, tk) : cur;
+  // this workgroup's next item from index i on (n_items when none is left),
+  // passing over the items of paired second blocks
+  auto fetch = [&](int i, MxItem& it) {
+    for (; i < n_items; i += stride) {
+      it = mx_item<STAGE, PAIR>(p, i, routed, tk);
+      if (!it.skip) return i;
+    }
+    return n_items;
+  };
+  MxItem cur;
+  item = fetch(item, cur);
+  if (item >= n_items) return;  // uniform per workgroup
+  MxItem nxt;
+  int next = fetch(item + stride, nxt);
+  if (next >= n_items) nxt = cur;
 
   // Weights two groups ahead (ring 4), activations one group ahead (ring 2);
   // at the end of an item the prefetches continue with the next item (or
@@ -188,8 +204,8 @@ __global__ __launch_bounds__(256, 4) void mx_decode_kernel(ExpertGemmParams p) {
     if (next >= n_items) break;  // uniform per workgroup; the last prefetches re-read cur
     item = next;
     cur = nxt;
-    next = item + stride;
-    nxt = next < n_items ? mx_item<STAGE>(p, next, routed, tk) : cur;
+    next = fetch(item + stride, nxt);
+    if (next >= n_items) nxt = cur;
   }
 }
 
@@ -385,7 +401,7 @@ using namespace dsv4;
 
 // Resident workgroups of an MXFP4 decode kernel on the current device,
 // cached per device: the persistent grid size.
-template <int STAGE>
+template <int STAGE, bool PAIR>
 static int mx_decode_resident_grid() {
   static int cache[64] = {0};
   int dev = 0;
@@ -393,12 +409,25 @@ static int mx_decode_resident_grid() {
   if (cache[dev] == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mx_decode_kernel<STAGE>, 256, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mx_decode_kernel<STAGE, PAIR>, 256, 0) != hipSuccess ||
         per_cu <= 0)
       per_cu = 1;
     cache[dev] = cus * per_cu;
   }
   return cache[dev];
+}
+
+// One decode stage: persistent over at most one wave of resident
+// workgroups, with pairs of 8-slot blocks when decode_pairs says so.
+template <int STAGE>
+static void launch_mx_decode(const ExpertGemmParams& p, int blocks, hipStream_t stream) {
+  if (decode_pairs(p)) {
+    const int grid = std::min(p.n_tiles * blocks, mx_decode_resident_grid<STAGE, true>());
+    hipLaunchKernelGGL((mx_decode_kernel<STAGE, true>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  } else {
+    const int grid = std::min(p.n_tiles * blocks, mx_decode_resident_grid<STAGE, false>());
+    hipLaunchKernelGGL((mx_decode_kernel<STAGE, false>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  }
 }
 
 int dsv4_launch_experts_mxfp4(const uint16_t* x, int64_t tokens, int hidden, int inter, int experts, int topk,
@@ -442,8 +471,7 @@ int dsv4_launch_experts_mxfp4(const uint16_t* x, int64_t tokens, int hidden, int
   p.h_out = ws.h;
   if (decode) {
     p.n_tiles = inter / 64;
-    const int grid = std::min(p.n_tiles * blocks, mx_decode_resident_grid<1>());
-    hipLaunchKernelGGL(mx_decode_kernel<1>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    launch_mx_decode<1>(p, blocks, stream);
   } else {
     p.n_tiles = inter / 128;
     hipLaunchKernelGGL(mx_prefill_kernel<1>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)), dim3(256), 0,
@@ -465,8 +493,7 @@ int dsv4_launch_experts_mxfp4(const uint16_t* x, int64_t tokens, int hidden, int
   p.out_cols = hidden;
   if (decode) {
     p.n_tiles = hidden / 128;
-    const int grid = std::min(p.n_tiles * blocks, mx_decode_resident_grid<2>());
-    hipLaunchKernelGGL(mx_decode_kernel<2>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    launch_mx_decode<2>(p, blocks, stream);
   } else {
     p.n_tiles = hidden / 256;
     hipLaunchKernelGGL(mx_prefill_kernel<2>, dim3((unsigned)prefill_grid(blocks, p.n_tiles)), dim3(256), 0,

@@ -183,3 +183,37 @@ def test_fused_layer_entry_equals_staged_chain(t):
     ref = O.moe_fp32(to_np_f32(x.view(t, -1)), ref_route.ids, ref_route.weights, src, shared_index=shape.experts,
                      clamp_limit=10.0, rows=rows)
     assert_moe_close(to_np_f32(fused.view(t, -1))[rows], ref, what=f"fused mxfp4 T={t}")
+
+
+@pytest.mark.parametrize("t,zipf", [(40, False), (600, False), (300, True)])
+def test_paired_8_slot_blocks_equal_16_slot_blocks(t, zipf):
+    """MXFP4 decode blocks of 8 slots pair up (two consecutive blocks of one
+    expert as one 16-slot item) once the experts average at least 4 slots per
+    block: bit-identical to the same routing aligned in blocks of 16, runs
+    beyond the 16-block position scan and Zipf routing included, and within
+    the bar of the fp32 oracle."""
+
+    print(f"[mxfp4] paired 8-slot blocks T={t} zipf={zipf}", flush=True)
+    res, src = layer(SMALL)
+    x = S.make_hidden(t, SMALL.hidden, seed=71, device=DEV)
+    r = route_from_logits(S.make_logits(t, SMALL.experts, seed=72, device=DEV), topk=SMALL.topk)
+    ids = S.zipf_ids(t, SMALL.experts, SMALL.topk, seed=73, device=DEV) if zipf else r.routing_ids
+    outs = []
+    for bs in (8, 16):
+        a = deterministic_moe_align_block_size(ids, block_size=bs, num_experts=SMALL.experts)
+        out = torch.empty((t, SMALL.hidden), dtype=torch.bfloat16, device=DEV)
+        ws = torch.empty(ops.experts_workspace_bytes(t, SMALL.topk, SMALL.hidden, SMALL.inter, True),
+                         dtype=torch.uint8, device=DEV)
+        ops.experts_mxfp4_into(
+            x, w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, experts=SMALL.experts,
+            inter=SMALL.inter, has_shared=True, route_weights=r.routing_weights,
+            sorted_token_ids=a.sorted_token_ids, expert_ids=a.expert_ids,
+            num_tokens_post_padded=a.num_tokens_post_padded, block_size=bs, clamp_limit=0.0,
+            out=out, workspace=ws)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    rows = np.arange(t) if t <= 64 else np.sort(np.random.default_rng(t).choice(t, 64, replace=False))
+    ref = O.moe_fp32(to_np_f32(x), ids.cpu().numpy(), r.routing_weights.cpu().numpy(), src,
+                     shared_index=SMALL.experts, rows=rows)
+    assert_moe_close(to_np_f32(outs[0])[rows], ref, what=f"mxfp4 paired T={t}")
