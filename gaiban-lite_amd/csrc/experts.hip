@@ -378,9 +378,11 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
   };
 
   // Token columns that hold a valid slot: the alignment pads each expert's
-  // run at its end, so a block's valid slots come first.  A block with at
-  // most 32 of them runs the loop over two 16-slot column tiles instead of
-  // four (the MFMAs and scale FMAs of the empty tiles are skipped).
+  // run at its end, so a block's valid slots come first.  The loop runs over
+  // ceil(valid / 16) of the four 16-slot column tiles, at least two (the
+  // MFMAs and scale FMAs of the empty tiles are skipped: partial blocks are
+  // the last block of every expert, and most blocks when experts average
+  // under 64 slots).
   const uint64_t valid = __ballot(slot_rowid(p, b, lane, tk) >= 0);
   const int used = valid ? 64 - __builtin_clzll(valid) : 0;
 
@@ -535,8 +537,10 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
       }
     }
   };
-  if (used > 32)
+  if (used > 48)
     body(std::integral_constant<int, 4>{});
+  else if (used > 32)
+    body(std::integral_constant<int, 3>{});
   else
     body(std::integral_constant<int, 2>{});
 }

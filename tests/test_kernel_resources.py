@@ -65,9 +65,12 @@ def test_w8a8_prefill_kernel_fits_one_workgroup_per_cu(tmp_path):
 
 def inflight_register_reads(asm: str, kernel: str) -> list[str]:
     """Instructions of `kernel` that read or overwrite a VGPR whose
-    (non-LDS) buffer load may still be in flight, in program order: vector
-    memory operations complete in issue order and `s_waitcnt vmcnt(n)` leaves
-    only the newest n outstanding.  A read at the end of a loop body is seen
+    (non-LDS) inline-assembly load may still be in flight, in program order:
+    vector memory operations complete in issue order and `s_waitcnt vmcnt(n)`
+    leaves only the newest n outstanding.  The compiler's own loads (spill
+    reloads included) count toward vmcnt but are not tracked as registers:
+    the compiler waits for them itself on every path, whereas it knows nothing
+    of the inline-assembly loads.  A read at the end of a loop body is seen
     with the loads the body left in flight, which is where a copy at the loop's
     back edge would sit."""
 
@@ -84,7 +87,15 @@ def inflight_register_reads(asm: str, kernel: str) -> list[str]:
 
     outstanding: list[set[int]] = []  # destination VGPRs of each vector memory op, in issue order
     bad = []
+    inasm = False
     for line in body:
+        raw = line.strip()
+        if raw.startswith(";;#ASMSTART"):
+            inasm = True
+            continue
+        if raw.startswith(";;#ASMEND"):
+            inasm = False
+            continue
         ins = line.split(";")[0].strip()
         if not ins or ins.startswith(".") or ins.endswith(":"):
             continue
@@ -99,7 +110,7 @@ def inflight_register_reads(asm: str, kernel: str) -> list[str]:
         if op.startswith(("buffer_load", "global_load", "scratch_load")):
             if touched - regs(args[0]) & pending:
                 bad.append(ins)
-            outstanding.append(set() if ins.endswith("lds") else regs(args[0]))
+            outstanding.append(regs(args[0]) if inasm and not ins.endswith("lds") else set())
         elif op.startswith(("buffer_store", "global_store", "scratch_store", "buffer_atomic", "global_atomic")):
             if touched & pending:
                 bad.append(ins)
@@ -231,3 +242,32 @@ def test_w8a8_gemm256_k_loop_is_one_block_with_only_its_own_copy_waits(tmp_path)
         assert [s for s, a in body if not a and s.startswith("s_waitcnt") and "vmcnt" in s] == [], name
         branches = [s for s, _ in body if s.startswith(("s_cbranch", "s_branch"))]
         assert len(branches) == 1, (name, branches)  # the back edge only
+
+
+def test_inflight_analysis_on_planted_code():
+    """The in-flight check itself: a read of an inline-assembly load's
+    destination before its wait is reported, the same read after
+    `s_waitcnt vmcnt(0)` is not, and a compiler reload (waited for by the
+    compiler) is not tracked; vmcnt(n) keeps only the newest n loads."""
+
+    asm = "\n".join([
+        "k:",
+        "\t;;#ASMSTART",
+        "\tbuffer_load_dwordx4 v[10:13], v2, s[4:7], s8 offen",
+        "\t;;#ASMEND",
+        "\tscratch_load_dword v5, off, off offset:8",
+        "\tv_mov_b32_e32 v1, v5",
+        "\tv_mov_b32_e32 v1, v11",
+        "\ts_waitcnt vmcnt(1)",
+        "\tv_mov_b32_e32 v1, v12",
+        "\t;;#ASMSTART",
+        "\tbuffer_load_dwordx4 v[20:23], v2, s[4:7], s8 offen",
+        "\t;;#ASMEND",
+        "\tglobal_load_dword v6, v[2:3], off",
+        "\ts_waitcnt vmcnt(1)",
+        "\tv_add_u32_e32 v1, v20, v1",
+        "\ts_waitcnt vmcnt(0)",
+        "\tv_add_u32_e32 v1, v21, v1",
+        ".Lfunc_end0:",
+    ])
+    assert inflight_register_reads(asm, "k") == ["v_mov_b32_e32 v1, v11"]
