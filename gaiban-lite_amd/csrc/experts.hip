@@ -66,8 +66,8 @@ template <int STAGE, bool PAIR>
 __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int item, int routed, int64_t tk) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int bi = item / p.n_tiles;
-  const int tile = item - bi * p.n_tiles;
+  int bi, tile;
+  decode_item_block(p, item, routed, bi, tile);
   const int blk = bi < routed ? bi : p.max_blocks + (bi - routed);
   const BlockInfo b = block_info(p, blk);
   const int groups = p.k_dim / kGroup;
@@ -91,13 +91,14 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
 }
 
 // RING = 4: weights two groups ahead, four workgroups per CU.
-// RING = 8: weights six groups ahead, two workgroups per CU; K must be a
-// multiple of 8 groups.  Stage 1 (w13, 256 KiB per item) streams faster with
+// RING = 8: weights six groups ahead, three workgroups per CU (at most 168
+// VGPRs; at 169 the occupancy drops to two and T=64 stage 1 takes 6% longer);
+// K must be a multiple of 8 groups.  Stage 1 (w13, 256 KiB per item) streams faster with
 // the deeper ring at every T measured; stage 2 (128 KiB items) keeps RING = 4
 // unless its items fit one wave of resident workgroups (T ~ 1), where the
 // bytes in flight per workgroup, not the workgroup count, bound the stream.
 template <int STAGE, int RING, bool PAIR>
-__global__ __launch_bounds__(256, RING == 4 ? 4 : 2) void expert_decode_kernel(ExpertGemmParams p) {
+__global__ __launch_bounds__(256, RING == 4 ? 4 : 3) void expert_decode_kernel(ExpertGemmParams p) {
   constexpr int R = 2;
   constexpr int kAhead = RING - 2;
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][16 * 256];  // part q of slot s at q ^ s

@@ -152,18 +152,37 @@ __device__ __forceinline__ void scale4(u32x2 sv, float (&sc)[4]) {
   sc[3] = __uint_as_float(sv[1] & 0xFFFF0000u);
 }
 
-// Persistent decode kernels: active items (block, tile) are the routed blocks
-// below ceil(ntpp / block_size) followed by the shared-expert blocks, times the
-// N tiles.
+// Persistent decode kernels: active items (block, tile) are the shared-expert
+// blocks and the routed blocks below ceil(ntpp / block_size), times the N
+// tiles (order: decode_item_block).
 __device__ __forceinline__ int decode_routed_blocks(const ExpertGemmParams& p) {
   const int total = p.ntpp[0];
   const int blocks = total > 0 ? (total + p.block_size - 1) / p.block_size : 0;
   return blocks < p.full_blocks ? blocks : p.full_blocks;
 }
 
+__device__ __forceinline__ int decode_shared_blocks(const ExpertGemmParams& p) {
+  return p.shared_expert >= 0 ? (int)((p.tokens + p.shared_block_size - 1) / p.shared_block_size) : 0;
+}
+
 __device__ __forceinline__ int decode_items(const ExpertGemmParams& p, int routed) {
-  const int shared = p.shared_expert >= 0 ? (int)((p.tokens + p.shared_block_size - 1) / p.shared_block_size) : 0;
-  return (routed + shared) * p.n_tiles;
+  return (routed + decode_shared_blocks(p)) * p.n_tiles;
+}
+
+// Block index bi (< routed: a routed block; routed + s: shared-expert block s)
+// and N tile of decode item `item`: the S shared-expert blocks' items first,
+// then the routed blocks', each block's n_tiles items in tile order.  The
+// dispatcher sends workgroup i to XCD i % 8 and the persistent grid is a
+// multiple of 8 (or covers every item), so item i runs on XCD i % 8; with
+// n_tiles a multiple of 8 the S items of one shared-expert tile run on one
+// XCD, in the first round of the persistent loop when S * n_tiles fits the
+// grid, and stream that tile's weights through the XCD's L2 together.
+__device__ __forceinline__ void decode_item_block(const ExpertGemmParams& p, int item, int routed, int& bi,
+                                                  int& tile) {
+  const int S = decode_shared_blocks(p);
+  const int b = item / p.n_tiles;
+  tile = item - b * p.n_tiles;
+  bi = b < S ? routed + b : b - S;
 }
 
 // Workgroup stride over the items: the whole grid.  (Shrinking the grid so

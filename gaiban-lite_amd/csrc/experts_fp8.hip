@@ -92,8 +92,8 @@ __device__ __forceinline__ Fp8DecodeItem fp8_decode_item(const ExpertGemmParams&
                                                          int64_t tk) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int bi = item / p.n_tiles;
-  const int tile = item - bi * p.n_tiles;
+  int bi, tile;
+  decode_item_block(p, item, routed, bi, tile);
   const int blk = bi < routed ? bi : p.max_blocks + (bi - routed);
   const BlockInfo b = block_info(p, blk);
   const int groups = p.k_dim / kGroup;

@@ -66,8 +66,8 @@ template <int STAGE, bool PAIR>
 __device__ __forceinline__ MxItem mx_item(const ExpertGemmParams& p, int item, int routed, int64_t tk) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int bi = item / p.n_tiles;
-  const int tile = item - bi * p.n_tiles;
+  int bi, tile;
+  decode_item_block(p, item, routed, bi, tile);
   const int blk = bi < routed ? bi : p.max_blocks + (bi - routed);
   const BlockInfo b = block_info(p, blk);
   const int groups = p.k_dim / kGroup;

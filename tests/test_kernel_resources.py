@@ -271,3 +271,18 @@ def test_inflight_analysis_on_planted_code():
         ".Lfunc_end0:",
     ])
     assert inflight_register_reads(asm, "k") == ["v_mov_b32_e32 v1, v11"]
+
+
+def test_decode_kernels_keep_their_occupancy(tmp_path):
+    """The persistent W4A16 decode kernels stream weights at a rate set by the
+    resident workgroups: the deep-ring instances (RING 8) must fit three
+    256-thread workgroups per CU (at most 168 VGPRs), the 4-deep ones four (at
+    most 128), without scratch."""
+
+    meta = kernel_metadata(CSRC / "experts.hip", tmp_path)
+    dec = {k: v for k, v in meta.items() if "expert_decode_kernel" in k}
+    assert len(dec) == 8
+    for name, m in dec.items():
+        ring = int(re.search(r"expert_decode_kernelILi\dELi(\d)E", name).group(1))
+        assert m["vgpr_count"] <= {8: 168, 4: 128}[ring], (name, m["vgpr_count"])
+        assert m["vgpr_spill_count"] == 0 and m["sgpr_spill_count"] == 0, name
