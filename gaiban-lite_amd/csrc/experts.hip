@@ -62,10 +62,12 @@ struct DecodeItem {
   bool skip;           // PAIR: the block is the second of a pair, computed by the first
 };
 
+// `tid`: the thread's index in the 256 threads that compute the item.
 template <int STAGE, bool PAIR>
-__device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int item, int routed, int64_t tk) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+__device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int item, int routed, int64_t tk,
+                                                  int tid) {
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   int bi, tile;
   decode_item_block(p, item, routed, bi, tile);
   const int blk = bi < routed ? bi : p.max_blocks + (bi - routed);
@@ -84,9 +86,9 @@ __device__ __forceinline__ DecodeItem decode_item(const ExpertGemmParams& p, int
   it.rowid = slot_rowid_span(p, b, lane & 15, tk, span);
   const int64_t arow = act_row_of<STAGE>(it.rowid, tk, p.topk);
   it.sum_base = arow >= 0 ? (uint32_t)(arow * sums_per_row * 4) : kOobOffset;
-  const int ld_slot = threadIdx.x >> 4;
+  const int ld_slot = tid >> 4;
   const int64_t ld_row = act_row_of<STAGE>(slot_rowid_span(p, b, ld_slot, tk, span), tk, p.topk);
-  it.ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + (threadIdx.x & 15) * 16) : kOobOffset;
+  it.ld_base = ld_row >= 0 ? (uint32_t)(ld_row * p.k_dim * 2 + (tid & 15) * 16) : kOobOffset;
   return it;
 }
 
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 3) void expert_decode_kernel(E
   // passing over the items of paired second blocks
   auto fetch = [&](int i, DecodeItem& it) {
     for (; i < n_items; i += stride) {
-      it = decode_item<STAGE, PAIR>(p, i, routed, tk);
+      it = decode_item<STAGE, PAIR>(p, i, routed, tk, threadIdx.x);
       if (!it.skip) return i;
     }
     return n_items;
@@ -249,6 +251,165 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 3) void expert_decode_kernel(E
     cur = nxt;
     next = fetch(item + stride, nxt);
     if (next >= n_items) nxt = cur;
+  }
+}
+
+// ------------------------------------------------------- decode, K split
+// For launches with at most one decode item per CU (T = 1: 7 blocks x 32 N
+// tiles = 224 items on 256 CUs).  There each item's four wavefronts walk the
+// K groups of their strip pairs in sequence, one barrier per group, and that
+// serial chain, not the memory system, bounds the stream (stage 1 at T = 1
+// moved 59 MB in 21 us: 12-14 GB/s per CU).  Here eight wavefronts share an
+// item: wavefronts w and w + 4 take the same strip pair, w the lower half of
+// K and w + 4 the upper half, each with the deep ring of
+// expert_decode_kernel (weights six groups ahead) and its own activation
+// tile in LDS.  At the end the upper half's accumulators pass through LDS,
+// the lower half adds them, and the epilogue is expert_decode_kernel's.  Each
+// group's arithmetic is expert_decode_kernel's; the sum over groups is
+// formed as (lower half) + (upper half), so the results can differ from
+// that kernel's in the last bits.
+template <int STAGE>
+__global__ __launch_bounds__(512, 1) void expert_decode_ksplit_kernel(ExpertGemmParams p) {
+  constexpr int R = 2;
+  constexpr int RING = 8;
+  constexpr int kAhead = RING - 2;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][2][16 * 256];  // [half][buffer], part q of slot s at q ^ s
+  __shared__ f32x4 upper[4][R][64];
+  __shared__ float red[4][16];
+  const int tid = threadIdx.x & 255;
+  const int half = threadIdx.x >> 8;  // wavefront-uniform
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t tk = p.tokens * p.topk;
+  const int routed = decode_routed_blocks(p);
+  const int n_items = decode_items(p, routed);
+  const int item = blockIdx.x;
+  if (item >= n_items) return;  // uniform per workgroup
+  const DecodeItem cur = decode_item<STAGE, false>(p, item, routed, tk, tid);
+  const int hg = p.k_dim / kGroup / 2;  // groups per half: a multiple of RING (checked on the host)
+  const int gb = half * hg;             // this half's first group
+  const int sums_per_row = p.k_dim / kSumChunk;
+
+  const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act, (short)0, (int)(p.act_rows * p.k_dim * 2), kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act_sum, (short)0, (int)(p.act_rows * sums_per_row * 4), kRsrcFlags);
+  const int ld_slot = tid >> 4;
+  const int ld_lds = ld_slot * 256 + (((tid & 15) ^ ld_slot) * 16);
+  int rd_lds[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) rd_lds[d] = (lane & 15) * 256 + (((4 * d + (lane >> 4)) ^ (lane & 15)) * 16);
+
+  u32x4 W[RING][R];
+  u32x4 S[RING];
+  float CS[2][2];
+  u32x4 xr;
+  auto issue_w = [&](int g, u32x4 (&w)[R], u32x4& sv) {
+    w[0] = load16_nt(cur.wq + g * 2048);
+    w[1] = load16_nt(cur.wq + g * 2048 + 1024);
+    sv = load16(cur.ws + g * 32);
+  };
+  auto issue_x = [&](int g, float (&cs)[2]) {
+    xr = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, cur.ld_base + (uint32_t)(g * 256), 0, 0);
+    cs[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, cur.sum_base + (uint32_t)(g * 8), 0, 0));
+    cs[1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sum_rsrc, cur.sum_base + (uint32_t)(g * 8 + 4), 0, 0));
+  };
+
+  const uint32_t magic = dequant_magic();
+  issue_x(gb, CS[0]);
+#pragma unroll
+  for (int a = 0; a < kAhead; ++a) issue_w(gb + a, W[a], S[a]);
+  *reinterpret_cast<u32x4*>(&xs[half][0][ld_lds]) = xr;
+  __syncthreads();
+
+  f32x4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g0 = 0; g0 < hg; g0 += RING) {
+#pragma unroll
+    for (int u = 0; u < RING; ++u) {
+      const int g = g0 + u;
+      // prefetches past the half's end re-read its last group (unused), so
+      // every load is unconditional and the compiler's vmcnt waits stay exact
+      issue_x(gb + min(g + 1, hg - 1), CS[(u + 1) & 1]);
+      issue_w(gb + min(g + kAhead, hg - 1), W[(u + kAhead) % RING], S[(u + kAhead) % RING]);
+      const float nc = -kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
+      const f32x4 init = {nc, nc, nc, nc};
+      f32x4 tmp[R];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xs[half][u & 1][rd_lds[d]]));
+#pragma unroll
+        for (int r = 0; r < R; ++r) tmp[r] = mfma_bf16(dequant_biased(W[u][r][d], magic), bfr, d == 0 ? init : tmp[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float sc[4];
+        scale4(u32x2{S[u][2 * r], S[u][2 * r + 1]}, sc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * tmp[r][i];
+      }
+      *reinterpret_cast<u32x4*>(&xs[half][(u + 1) & 1][ld_lds]) = xr;
+      __syncthreads();
+    }
+  }
+
+  if (half == 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) upper[wave][r][lane] = acc[r];
+  }
+  __syncthreads();
+  if (half == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const f32x4 hi = upper[wave][r][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[r][i] += hi[i];
+    }
+  }
+
+  const int64_t rowid = cur.rowid;
+  if constexpr (STAGE == 1) {
+    if (half == 0) {
+      const float lim = p.clamp_limit;
+      uint32_t bits[4];
+      float part = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float gt = acc[0][i];
+        float up = acc[1][i];
+        if (lim > 0.0f) {
+          gt = fminf(gt, lim);
+          up = fminf(fmaxf(up, -lim), lim);
+        }
+        bits[i] = float_to_bf16_bits(silu_f(gt) * up);
+        part += __uint_as_float(bits[i] << 16);
+      }
+      if (rowid >= 0) {
+        const int n = cur.n0 + 16 * wave + 4 * (lane >> 4);
+        u32x2 packed = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+        *reinterpret_cast<u32x2*>(p.h_out + rowid * p.inter + n) = packed;
+      }
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      if (lane < 16) red[wave][lane] = part;
+    }
+    __syncthreads();
+    if (threadIdx.x < 16 && rowid >= 0) {
+      const float total = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+      p.hsum_out[rowid * (p.inter / kSumChunk) + cur.n0 / kSumChunk] = total;
+    }
+  } else {
+    if (half == 0 && rowid >= 0) {
+      const float wr = (rowid < tk ? p.route_w[rowid] : 1.0f) * cur.wmul;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int n = cur.n0 + 32 * wave + 16 * r + 4 * (lane >> 4);
+        f32x4 v = acc[r];
+        v[0] *= wr; v[1] *= wr; v[2] *= wr; v[3] *= wr;
+        *reinterpret_cast<f32x4*>(p.contrib + rowid * p.out_cols + n) = v;
+      }
+    }
   }
 }
 
@@ -817,14 +978,34 @@ static int decode_resident_grid() {
   return cache[dev];
 }
 
-// The decode launch of one stage: the deep-ring kernel for stage 1, and for
-// stage 2 when every item fits in one wave of resident workgroups (few
-// blocks, T ~ 1), when K allows it; else the four-workgroups-per-CU kernel.
-// Either grid is at most one wave of resident workgroups (persistent items).  `blocks` bounds the active blocks
-// (the kernel reads the real count from the alignment on the device).
+// The decode launch of one stage: with at most one item per CU the K-split
+// kernel (one item per workgroup); else the deep-ring kernel for stage 1,
+// and for stage 2 when every item fits in one wave of resident workgroups,
+// when K allows it; else the four-workgroups-per-CU kernel.  Either
+// persistent grid is at most one wave of resident workgroups.  `blocks`
+// bounds the active blocks (the kernels read the real count from the
+// alignment on the device).
+// Compute units of the current device, cached per device.
+static int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
 template <int STAGE, bool PAIR>
 static void launch_decode_as(const ExpertGemmParams& p, int blocks, hipStream_t stream) {
   const int items = p.n_tiles * blocks;
+  if (!PAIR && (p.k_dim / kGroup) % 16 == 0 && items <= device_cus()) {
+    // at most one item per CU: eight wavefronts per item, K split in two
+    hipLaunchKernelGGL((expert_decode_ksplit_kernel<STAGE>), dim3((unsigned)items), dim3(512), 0, stream, p);
+    return;
+  }
   if ((p.k_dim / kGroup) % 8 == 0 && (STAGE == 1 || items <= decode_resident_grid<STAGE, 8, PAIR>())) {
     const int grid = std::min(items, decode_resident_grid<STAGE, 8, PAIR>());
     hipLaunchKernelGGL((expert_decode_kernel<STAGE, 8, PAIR>), dim3((unsigned)grid), dim3(256), 0, stream, p);
