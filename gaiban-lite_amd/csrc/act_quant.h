@@ -100,18 +100,27 @@ __device__ __forceinline__ void act_quant_row(const uint16_t* __restrict__ x, in
 // with the activations beside the alignment.
 enum ActPrepMode : int {
   kPrepNone = 0,
-  kPrepRowSums = 1,      // 64-column row sums of x (the W4A16 kernels)
+  kPrepRowSums = 1,      // 64-column row sums of x (the W4A16 decode kernels)
   kPrepQuantInt4 = 2,    // act_quant_row<false> (the int4 W4A8 kernels)
-  kPrepQuantNatural = 3  // act_quant_row<true> (the MXFP4 W4A8 kernels)
+  kPrepQuantNatural = 3, // act_quant_row<true> (the MXFP4 W4A8 kernels)
+  kPrepRowNc = 4         // per 128-column group, -136 * (sum of 64 + sum of 64) (the W4A16 prefill kernels)
 };
 
 struct ActPrep {
   int mode;
   const uint16_t* x;  // [tokens][hidden]
   int hidden;
-  float* sums;        // row sums [tokens][hidden / 64], or e4m3 group sums [tokens][hidden / 128]
+  float* sums;        // row sums [tokens][hidden / 64], or per-group values [tokens][hidden / 128]
   uint8_t* q;         // e4m3 codes [tokens][hidden]
   float* qscale;      // [tokens]
 };
+
+// The W4A16 experts launcher takes the decode kernels for alignment blocks
+// of at most 16 slots (H and I multiples of 512), else the prefill kernels;
+// the two read the activation sums in different forms (kPrepRowSums /
+// kPrepRowNc), so the producers choose by the same rule.
+inline bool w4a16_decode_path(int block_size, int hidden, int inter) {
+  return block_size <= 16 && hidden % 512 == 0 && inter % 512 == 0;
+}
 
 }  // namespace dsv4

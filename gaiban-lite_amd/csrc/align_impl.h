@@ -221,12 +221,46 @@ __device__ __forceinline__ void row_sums_part(const uint16_t* __restrict__ x, in
   }
 }
 
+// The prefill form: per 128-column group g of row r, the two 64-column sums
+// (each summed as in row_sums_part) combined into the start value of the
+// group's MFMA chain, -136 * (s_lo + s_hi), stored at nc[r * (hidden / 128) + g].
+__device__ __forceinline__ void row_nc_part(const uint16_t* __restrict__ x, int64_t tokens, int hidden,
+                                           float* __restrict__ nc, int part, int parts) {
+  const int groups = hidden / 128;
+  const int64_t n = tokens * groups;
+  for (int64_t idx = (int64_t)part * kAlignThreads + threadIdx.x; idx < n; idx += (int64_t)parts * kAlignThreads) {
+    const int64_t r = idx / groups;
+    const int g = (int)(idx % groups);
+    const uint16_t* src = x + r * hidden + g * 128;
+    float half[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 64; e += 8) {
+        const u32x4 v = load16(src + 64 * h + e);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          sum += __uint_as_float(v[q] << 16);
+          sum += __uint_as_float(v[q] & 0xFFFF0000u);
+        }
+      }
+      half[h] = sum;
+    }
+    nc[idx] = -kDequantBias * (half[0] + half[1]);
+  }
+}
+
 // Share `part` of `parts` workgroups of kAlignThreads threads of the
-// activation work of a prologue launch: the row sums above, or the W4A8
-// quantiser with one wavefront per row (act_quant.h).
+// activation work of a prologue launch: the row sums above (either form),
+// or the W4A8 quantiser with one wavefront per row (act_quant.h).
 __device__ __forceinline__ void act_prep_part(const ActPrep& a, int64_t tokens, int part, int parts) {
   if (a.mode == kPrepRowSums) {
     row_sums_part(a.x, tokens, a.hidden, a.sums, part, parts);
+    return;
+  }
+  if (a.mode == kPrepRowNc) {
+    row_nc_part(a.x, tokens, a.hidden, a.sums, part, parts);
     return;
   }
   if (a.mode != kPrepQuantInt4 && a.mode != kPrepQuantNatural) return;
@@ -244,6 +278,7 @@ __device__ __forceinline__ void act_prep_part(const ActPrep& a, int64_t tokens, 
 inline int64_t act_prep_workgroups(const ActPrep& a, int64_t tokens, int64_t cap) {
   int64_t n = 0;
   if (a.mode == kPrepRowSums) n = (tokens * (a.hidden / 64) + kAlignThreads - 1) / kAlignThreads;
+  else if (a.mode == kPrepRowNc) n = (tokens * (a.hidden / 128) + kAlignThreads - 1) / kAlignThreads;
   else if (a.mode == kPrepQuantInt4 || a.mode == kPrepQuantNatural) n = (tokens + kAlignWaves - 1) / kAlignWaves;
   return n < cap ? n : cap;
 }

@@ -608,9 +608,9 @@ int dsv4moe_layer_w4a16(const uint16_t* x, const float* logits, const float* bia
   dsv4host::prof_stamp(dsv4host::kStampBegin, s);
   size_t room = 0;
   int32_t* scratch = dsv4_experts_align_scratch(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0, &room);
-  const dsv4::ActPrep prep{dsv4::kPrepRowSums, x, hidden,
-                           dsv4_experts_xsum(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0), nullptr,
-                           nullptr};
+  const dsv4::ActPrep prep{dsv4::w4a16_decode_path(block_size, hidden, inter) ? dsv4::kPrepRowSums : dsv4::kPrepRowNc,
+                           x, hidden, dsv4_experts_xsum(workspace, tokens, topk, hidden, inter, has_shared ? 1 : 0),
+                           nullptr, nullptr};
   rc = layer_route_align("layer_w4a16", prep, scratch, room, logits, bias, tokens, experts, topk, score_func,
                          route_scale, block_size, ids, weights, margin, sorted_token_ids, capacity, expert_ids,
                          num_tokens_post_padded, s);

@@ -31,6 +31,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "act_quant.h"
 #include "experts_common.h"
 #include "../../include/dsv4moe.h"
 
@@ -445,14 +446,15 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
   // Per group, copied into LDS by buffer_load ... lds (double buffered):
   //  * token tile: 64 slots x 256 B, 16-byte part p of slot s stored at part
   //    p ^ (s & 15) (conflict-free ds_read_b128 of the B fragments);
-  //  * the 64 slots' two 64-wide activation sums;
+  //  * the 64 slots' start values -136 * sum_g(x) (the prefill form of the
+  //    activation sums: row_nc_part, the stage-1 epilogues);
   //  * each wavefront's 16-row scale ratios (fp32, 256 B).
   // Padded slots read zeros (out-of-range buffer offsets).
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kPfSlots * 256];
   // 64 lanes x 4 B per ratio DMA: lanes 0..31 carry pair p0's 128-byte block,
   // lanes 32..63 pair p0 + 1's.
   __shared__ __attribute__((aligned(16))) uint8_t scl[2][4][256];
-  __shared__ float xsum[2][2][kPfSlots];
+  __shared__ float xnc[2][kPfSlots];
   __shared__ float red[4][kPfSlots];  // stage-1 epilogue: per-wavefront column sums
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -465,7 +467,6 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
   if (expert_needs_exact(p, b.expert)) return;  // expert_prefill_exact_kernel computes it
 
   const int groups = p.k_dim / kGroup;
-  const int sums_per_row = p.k_dim / kSumChunk;
 
   // wavefront w streams strip pairs p0 = tile*8 + 2w and p0 + 1; its strips
   // r = 2j + m are member m of pair p0 + j.  Stage 1: gate (m = 0) and up
@@ -475,8 +476,8 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
 
   const __amdgpu_buffer_rsrc_t act_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)p.act, (short)0, (int)(p.act_rows * p.k_dim * 2), kRsrcFlags);
-  const __amdgpu_buffer_rsrc_t sum_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)p.act_sum, (short)0, (int)(p.act_rows * sums_per_row * 4), kRsrcFlags);
+  const __amdgpu_buffer_rsrc_t nc_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)p.act_sum, (short)0, (int)(p.act_rows * groups * 4), kRsrcFlags);
   const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(p.wq + (int64_t)b.expert * p.wq_stride), (short)0, (int)p.wq_stride, kRsrcFlags);
   const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -493,10 +494,10 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
     const int part = (lane & 15) ^ (row & 15);
     dma_off[q] = ar >= 0 ? (uint32_t)(ar * p.k_dim * 2 + part * 16) : kOobOffset;
   }
-  uint32_t sum_off = kOobOffset;
+  uint32_t nc_off = kOobOffset;
   if (wave == 0) {
     const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, lane, tk), tk, p.topk);
-    if (ar >= 0) sum_off = (uint32_t)(ar * sums_per_row * 4);
+    if (ar >= 0) nc_off = (uint32_t)(ar * groups * 4);
   }
   // weight tiles: pair p, group g, member m at byte ((p*groups + g)*2 + m) * 1 KiB
   const uint32_t w_off0 = (uint32_t)(p0 * groups) * 2048 + lane * 16;
@@ -509,10 +510,7 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
     for (int q = 0; q < 4; ++q)
       lds_copy16(act_rsrc, lds_addr(&xs[buf][(16 * wave + 4 * q) * 256]), dma_off[q], g * 256);
     lds_copy4(r_rsrc, lds_addr(&scl[buf][wave][0]), r_off, g * 128);
-    if (wave == 0) {
-      lds_copy4(sum_rsrc, lds_addr(&xsum[buf][0][0]), sum_off, g * 8);
-      lds_copy4(sum_rsrc, lds_addr(&xsum[buf][1][0]), sum_off, g * 8 + 4);
-    }
+    if (wave == 0) lds_copy4(nc_rsrc, lds_addr(&xnc[buf][0]), nc_off, g * 4);
   };
   // The weight tiles are private to the wavefront: loaded straight into
   // registers, one group ahead, as inline asm -- the compiler neither counts
@@ -577,8 +575,7 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
       }
       float nc[C];
 #pragma unroll
-      for (int ct = 0; ct < C; ++ct)
-        nc[ct] = -kDequantBias * (xsum[u][0][ct * 16 + sw] + xsum[u][1][ct * 16 + sw]);
+      for (int ct = 0; ct < C; ++ct) nc[ct] = xnc[u][ct * 16 + sw];
       // ratios of strip r = 2j + m: pair j's block, element (quad * 2 + m) * 4 + i
       f32x4 ratio[R];
 #pragma unroll
@@ -675,12 +672,14 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
       }
       __syncthreads();
       if (threadIdx.x < C * 16) {
+        // stage 2's start value for K group `tile` (its 128 columns are this
+        // workgroup's h columns): -136 * (sum of the two 64-column halves)
         const int col = threadIdx.x;
         const int64_t rid = slot_rowid(p, b, col, tk);
         if (rid >= 0) {
-          float* dst = p.hsum_out + rid * (p.inter / kSumChunk) + n0 / kSumChunk;
-          dst[0] = red[0][col] + red[1][col];
-          dst[1] = red[2][col] + red[3][col];
+          const float lo = red[0][col] + red[1][col];
+          const float hi = red[2][col] + red[3][col];
+          p.hsum_out[rid * (p.inter / kGroup) + tile] = -kDequantBias * (lo + hi);
         }
       }
     } else {
@@ -735,7 +734,6 @@ __global__ __launch_bounds__(256, 1) void expert_prefill_exact_kernel(ExpertGemm
   const int sw = lane & 15;
   const int64_t tk = p.tokens * p.topk;
   const int groups = p.k_dim / kGroup;
-  const int sums_per_row = p.k_dim / kSumChunk;
   const uint32_t magic = dequant_magic();
   // element 1 of the stack's ratios: 1.0 when any expert of it is marked
   if (__builtin_nontemporal_load(p.wr + 1) == 0.0f) return;
@@ -776,14 +774,13 @@ __global__ __launch_bounds__(256, 1) void expert_prefill_exact_kernel(ExpertGemm
           }
           if (threadIdx.x < kPfSlots) {
             const int64_t ar = act_row_of<STAGE>(slot_rowid(p, b, (int)threadIdx.x, tk), tk, p.topk);
-            xsum_s[threadIdx.x] = ar >= 0 ? p.act_sum[ar * sums_per_row + 2 * g] + p.act_sum[ar * sums_per_row + 2 * g + 1]
-                                          : 0.0f;
+            xsum_s[threadIdx.x] = ar >= 0 ? p.act_sum[ar * groups + g] : 0.0f;
           }
           __syncthreads();
           f32x4 part[R][C];
 #pragma unroll
           for (int ct = 0; ct < C; ++ct) {
-            const float nc = -kDequantBias * xsum_s[ct * 16 + sw];
+            const float nc = xsum_s[ct * 16 + sw];
 #pragma unroll
             for (int r = 0; r < R; ++r) part[r][ct] = f32x4{nc, nc, nc, nc};
           }
@@ -853,9 +850,9 @@ __global__ __launch_bounds__(256, 1) void expert_prefill_exact_kernel(ExpertGemm
             const int col = (int)threadIdx.x;
             const int64_t rid = slot_rowid(p, b, col, tk);
             if (rid >= 0) {
-              float* dst = p.hsum_out + rid * (p.inter / kSumChunk) + n0 / kSumChunk;
-              dst[0] = red[0][col] + red[1][col];
-              dst[1] = red[2][col] + red[3][col];
+              const float lo = red[0][col] + red[1][col];
+              const float hi = red[2][col] + red[3][col];
+              p.hsum_out[rid * (p.inter / kGroup) + n0 / kGroup] = -kDequantBias * (lo + hi);
             }
           }
         } else {
@@ -881,26 +878,40 @@ __global__ __launch_bounds__(256, 1) void expert_prefill_exact_kernel(ExpertGemm
 
 // Per-row fp32 sums of bf16 activations over each 64-wide K chunk, summed in
 // ascending k order.
+// NC = false: out[r][c] = sum of x[r][64c .. 64c+63] (the decode kernels'
+// form); NC = true: out[r][g] = -136 * (sum of the first 64 + sum of the last
+// 64 columns of group g), each half summed as in the first form (the
+// prefill kernels' form, as row_nc_part).
+template <bool NC>
 __global__ __launch_bounds__(256) void row_chunk_sum_kernel(const uint16_t* __restrict__ x,
                                                             int64_t rows, int k_dim,
                                                             float* __restrict__ out) {
-  const int chunks = k_dim / kSumChunk;
+  constexpr int kHalves = NC ? 2 : 1;
+  const int chunks = k_dim / (kSumChunk * kHalves);
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= rows * chunks) return;
   const int64_t r = idx / chunks;
   const int c = (int)(idx % chunks);
-  const uint16_t* src = x + r * k_dim + c * kSumChunk;
-  float s = 0.0f;
+  const uint16_t* src = x + r * k_dim + c * kSumChunk * kHalves;
+  float half[kHalves];
 #pragma unroll
-  for (int e = 0; e < kSumChunk; e += 8) {
-    const u32x4 v = load16(src + e);
+  for (int h = 0; h < kHalves; ++h) {
+    float s = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      s += __uint_as_float(v[q] << 16);
-      s += __uint_as_float(v[q] & 0xFFFF0000u);
+    for (int e = 0; e < kSumChunk; e += 8) {
+      const u32x4 v = load16(src + h * kSumChunk + e);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        s += __uint_as_float(v[q] << 16);
+        s += __uint_as_float(v[q] & 0xFFFF0000u);
+      }
     }
+    half[h] = s;
   }
-  out[idx] = s;
+  if constexpr (NC)
+    out[idx] = -kDequantBias * (half[0] + half[1]);
+  else
+    out[idx] = half[0];
 }
 
 // out[t][n] = bf16( sum_{j<k} contrib[t*k+j][n] + contrib[T*k+t][n] ).  The
@@ -1054,16 +1065,21 @@ int dsv4_launch_experts_w4a16(const uint16_t* x, int64_t tokens, int hidden, int
   ExpertWorkspace ws = carve_workspace(workspace, tokens, topk, hidden, inter, has_shared);
   const int max_blocks = (int)((capacity + block_size - 1) / block_size);
   // decode kernel: blocks of <= 16 slots and K groups in multiples of 4
-  const bool decode = block_size <= 16 && hidden % 512 == 0 && inter % 512 == 0;
+  const bool decode = w4a16_decode_path(block_size, hidden, inter);
   const int shared_bs = decode ? 16 : block_size;
   const int shared_blocks = has_shared ? (int)((tokens + shared_bs - 1) / shared_bs) : 0;
   const int blocks = max_blocks + shared_blocks;
   const int64_t rows = tokens * topk + (has_shared ? tokens : 0);
 
   if (!rowsums_ready) {
-    const int64_t n = tokens * (hidden / kSumChunk);
-    hipLaunchKernelGGL(row_chunk_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                       stream, x, tokens, hidden, ws.xsum);
+    // the activation sums in the form the chosen kernels read
+    const int64_t n = tokens * (hidden / (decode ? kSumChunk : kGroup));
+    if (decode)
+      hipLaunchKernelGGL(row_chunk_sum_kernel<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                         stream, x, tokens, hidden, ws.xsum);
+    else
+      hipLaunchKernelGGL(row_chunk_sum_kernel<true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                         stream, x, tokens, hidden, ws.xsum);
     DSV4_CHECK_LAUNCH("row_chunk_sum_kernel");
   }
   dsv4host::prof_stamp(dsv4host::kStampRowSum, stream);

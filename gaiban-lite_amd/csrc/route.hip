@@ -278,8 +278,9 @@ __global__ __launch_bounds__(256) void route_topk_kernel(
 // Layer prologue in one launch: workgroup 0 routes every token when `route`
 // is set (wavefront w takes tokens w, w + 16, ...; used for T <= 16, since
 // routing is VALU-bound and one workgroup runs on one CU) and then runs the
-// alignment over the ids; workgroups 1.. compute the per-64-column row sums
-// of the activations (summed in ascending k, as row_chunk_sum_kernel).
+// alignment over the ids; workgroups 1.. do the activation work of `prep`
+// (act_prep_part: the row sums in the decode or the prefill form, summed in
+// ascending k as row_chunk_sum_kernel, or the W4A8 quantisation).
 // Replaces the route, align and row-sum launches (or the last two).
 struct PrologueArgs {
   const float* logits;
