@@ -286,3 +286,136 @@ def test_decode_kernels_keep_their_occupancy(tmp_path):
         ring = int(re.search(r"expert_decode_kernelILi\dELi(\d)E", name).group(1))
         assert m["vgpr_count"] <= {8: 168, 4: 128}[ring], (name, m["vgpr_count"])
         assert m["vgpr_spill_count"] == 0 and m["sgpr_spill_count"] == 0, name
+
+
+_LABEL = re.compile(r"^(\.LBB\d+_\d+):")
+_BB = re.compile(r"^; %bb\.\d+:")
+
+
+def mfmas_under_lane_mask(lines: list[str]) -> list[tuple[str, str]]:
+    """MFMAs of one kernel's listing that can execute while EXEC holds only
+    some lanes: a forward walk over the basic blocks (labels, fall-through and
+    branch edges) that tracks the open `if` regions -- `s_and_saveexec_b64
+    s[k]` (or `s_mov_b64 s[k], exec` then `s_mov_b64 exec, ...`) opens one
+    keyed by the saved mask, `s_xor_b64 s[j], exec, s[k]` renames it (an
+    if/else), `s_or_b64 exec, exec, s[k]` closes it.  Returns (block, MFMA)
+    pairs reached with a region open."""
+
+    blocks, cur = [], ["entry", []]
+    for line in lines:
+        s = line.strip()
+        m = _LABEL.match(s)
+        if m or _BB.match(s):
+            blocks.append(cur)
+            cur = [m.group(1) if m else s, []]
+            continue
+        if s and not s.startswith((";", ".")):
+            cur[1].append(s)
+    blocks.append(cur)
+    index = {name: i for i, (name, _) in enumerate(blocks)}
+    states, work, visits, bad = {0: ()}, [0], {}, set()
+    while work:
+        i = work.pop()
+        open_, saved, succ, ends = list(states[i]), None, [], False
+        for s in blocks[i][1]:
+            t = s.replace(",", " ").split()
+            op = t[0]
+            if op == "s_and_saveexec_b64":
+                open_.append(t[1])
+            elif op == "s_xor_b64" and len(t) > 3 and t[2] == "exec" and open_ and open_[-1] == t[3]:
+                open_[-1] = t[1]
+            elif op == "s_mov_b64" and len(t) > 2 and t[2] == "exec":
+                saved = t[1]
+            elif op == "s_mov_b64" and t[1] == "exec":
+                open_.append(saved or "?")
+            elif op == "s_or_b64" and t[1] == "exec":
+                key = t[3] if t[2] == "exec" else t[2]
+                if key in open_:
+                    while open_[-1] != key:
+                        open_.pop()
+                    open_.pop()
+            elif op.startswith("v_mfma") and open_:
+                bad.add((blocks[i][0], s))
+            elif op.startswith("s_cbranch"):
+                succ.append(t[1])
+            elif op == "s_branch":
+                succ.append(t[1])
+                ends = True
+            elif op == "s_endpgm":
+                ends = True
+        if not ends and i + 1 < len(blocks):
+            succ.append(blocks[i + 1][0])
+        for name in succ:
+            j = index.get(name)
+            if j is None:
+                continue
+            new = tuple(open_)
+            if j in states and (states[j] == new or len(new) <= len(states[j])):
+                continue
+            states[j] = new
+            visits[j] = visits.get(j, 0) + 1
+            if visits[j] < 20:
+                work.append(j)
+    return sorted(bad)
+
+
+def test_lane_mask_analysis_on_planted_code():
+    """The EXEC-region walk itself: an MFMA inside `if` (saveexec ... or
+    exec) is reported, one after the join is not, an if/else renamed by
+    s_xor_b64 closes at its own join, and a region closed on a branch path
+    laid out earlier (a loop latch) does not leak into later blocks."""
+
+    inside = ["k:", "\tv_cmp_gt_i32_e32 vcc, s4, v0", "\ts_and_saveexec_b64 s[2:3], vcc",
+              "\ts_cbranch_execz .LBB0_2", "; %bb.1:", "\tv_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], v[0:3]",
+              ".LBB0_2:", "\ts_or_b64 exec, exec, s[2:3]", "\ts_endpgm"]
+    assert [m for _, m in mfmas_under_lane_mask(inside)] == ["v_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], v[0:3]"]
+    after = inside[:5] + ["\tv_mov_b32_e32 v1, 0"] + inside[6:8] + \
+        ["\tv_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], v[0:3]", "\ts_endpgm"]
+    assert mfmas_under_lane_mask(after) == []
+    if_else = ["k:", "\ts_and_saveexec_b64 s[4:5], vcc", "\ts_xor_b64 s[6:7], exec, s[4:5]",
+               "\ts_cbranch_execz .LBB0_2", "; %bb.1:", "\tv_mov_b32_e32 v1, 0", ".LBB0_2:",
+               "\ts_andn2_saveexec_b64 s[6:7], s[6:7]", "\tv_mov_b32_e32 v1, 1",
+               "\ts_or_b64 exec, exec, s[6:7]", "\tv_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], v[0:3]",
+               "\ts_endpgm"]
+    assert mfmas_under_lane_mask(if_else) == []
+    latch = ["k:", "\ts_branch .LBB0_2", ".LBB0_1:", "\ts_or_b64 exec, exec, s[2:3]",
+             "\tv_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], v[0:3]", "\ts_cbranch_scc1 .LBB0_3",
+             ".LBB0_2:", "\ts_and_saveexec_b64 s[2:3], vcc", "\tv_mov_b32_e32 v1, 0", "\ts_branch .LBB0_1",
+             ".LBB0_3:", "\tv_mfma_f32_16x16x32_bf16 v[0:3], v[4:7], v[8:11], v[0:3]", "\ts_endpgm"]
+    assert mfmas_under_lane_mask(latch) == []
+
+
+# Kernels whose whole K loops run under an EXEC mask the compiler cannot
+# prove uniform but that is uniform per wavefront at run time: the exact-
+# scaling prefill kernel loops over a marked-block count read from LDS, the
+# split gate GEMM over a per-wavefront K range.
+_UNIFORM_MASKED_LOOPS = ("expert_prefill_exact_kernel", "gate_logits_split_kernel")
+
+
+@pytest.mark.parametrize("src", ["experts.hip", "experts_mx.hip", "experts_fp8.hip", "experts_fp4.hip",
+                                 "linear.hip", "gate.hip"])
+def test_mfmas_never_run_under_a_lane_mask(src, tmp_path):
+    """An MFMA is a cross-lane operation: its A and B operands and its result
+    spread over all 64 lanes.  Executed under a partial EXEC mask (inside a
+    per-lane `if`), lanes outside the mask contribute stale operand registers
+    (a spill reload under that mask loads only the active lanes) and the
+    products are wrong.  The compiler may sink the MFMAs of a peeled K loop's
+    last groups into the epilogue's per-slot `rowid >= 0` branches, since
+    their results feed only that epilogue; the W4A8-over-MXFP4 prefill kernel
+    with register weights was built that way once and gave wrong rows for
+    padded blocks.  No MFMA of these kernels may be reachable with an `if`
+    region open."""
+
+    asm = _device_asm(CSRC / src, tmp_path)
+    names = re.findall(r"^(_Z\S+):", asm, re.M)
+    checked = 0
+    for name in names:
+        start = asm.index(f"\n{name}:")
+        body = asm[start: asm.index(".Lfunc_end", start)].splitlines()
+        if not any(line.strip().startswith("v_mfma") for line in body):
+            continue
+        if any(k in name for k in _UNIFORM_MASKED_LOOPS):
+            continue
+        checked += 1
+        assert mfmas_under_lane_mask(body) == [], name
+    assert checked > 0
