@@ -303,6 +303,51 @@ struct PrologueArgs {
   int route;           // route in workgroup 0 (else ids are given)
 };
 
+// The alignment of one token's k distinct, valid expert ids in closed form
+// (what align_block computes when every count is 0 or 1): the experts in
+// ascending order each own one block, whose first slot holds the flat index
+// j of the id and whose other slots, like every position past k blocks,
+// hold the sentinel k; expert_ids[b] is the b-th smallest id, then -1; the
+// padded total is k * block_size.  Returns false (nothing written) when an id
+// is outside [0, experts) or repeats, which align_block handles.  Every
+// thread of the workgroup calls it after the ids are visible to it.
+__device__ __forceinline__ bool align_one_token(const int32_t* __restrict__ ids, int topk, int experts,
+                                                int block_size, int32_t* __restrict__ sorted_ids, int64_t capacity,
+                                                int32_t* __restrict__ expert_ids, int64_t num_blocks,
+                                                int32_t* __restrict__ ntpp) {
+  __shared__ int32_t order_flat[64];  // flat index j of the id of rank b
+  __shared__ int32_t order_expert[64];
+  __shared__ int ok;
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x < 64) {
+    const int id = lane < topk ? ids[lane] : 0;
+    const bool in_range = lane >= topk || (id >= 0 && id < experts);
+    int rank = 0;
+    bool repeat = false;
+    for (int i = 0; i < topk; ++i) {
+      const int other = __shfl(id, i, 64);
+      rank += other < id;
+      repeat |= i != lane && other == id;
+    }
+    const bool lane_ok = lane >= topk || (in_range && !repeat);
+    const uint64_t bad = __ballot(!lane_ok);
+    if (lane < topk) {
+      order_flat[rank] = lane;
+      order_expert[rank] = id;
+    }
+    if (lane == 0) ok = bad == 0;
+  }
+  __syncthreads();
+  if (!ok) return false;
+  for (int64_t pos = threadIdx.x; pos < capacity; pos += blockDim.x) {
+    const int64_t b = pos / block_size;
+    sorted_ids[pos] = (pos % block_size == 0 && b < topk) ? order_flat[b] : topk;
+  }
+  for (int64_t b = threadIdx.x; b < num_blocks; b += blockDim.x) expert_ids[b] = b < topk ? order_expert[b] : -1;
+  if (threadIdx.x == 0) ntpp[0] = topk * block_size;
+  return true;
+}
+
 template <int SCORE, int EPL>
 __global__ __launch_bounds__(kAlignThreads) void prologue_kernel(PrologueArgs a) {
   if (blockIdx.x == 0) {
@@ -311,6 +356,12 @@ __global__ __launch_bounds__(kAlignThreads) void prologue_kernel(PrologueArgs a)
         route_tokens<SCORE, EPL, 1>(a.logits, a.bias, t, 0, a.tokens, a.experts, a.topk, a.route_scale, a.ids,
                                     a.weights, a.margin, nullptr, nullptr);
       __syncthreads();  // every id is written (workgroup-scope visibility)
+      // one routed token (single-token decode): its k ids are distinct
+      // experts, and their alignment needs none of align_block's phases
+      if (a.tokens == 1 && a.topk <= 64 &&
+          align_one_token(a.ids, a.topk, a.experts, a.block_size, a.sorted_ids, a.capacity, a.expert_ids,
+                          a.num_blocks, a.ntpp))
+        return;
     }
     align_block(a.ids, a.tokens * a.topk, a.experts, a.expert_bits, a.block_size, a.sorted_ids, a.capacity,
                 a.expert_ids, a.num_blocks, a.ntpp);

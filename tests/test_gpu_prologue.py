@@ -107,7 +107,7 @@ def test_layer_entry_256_experts(tokens):
     check(*run_layer(shape, tokens, "sqrtsoftplus", seed=200 + tokens, route_scale=2.5, clamp=10.0))
 
 
-@pytest.mark.parametrize("tokens", [3, 16, 64])
+@pytest.mark.parametrize("tokens", [1, 3, 16, 64])
 def test_layer_entry_1024_experts(tokens):
     shape = S.LayerShape(experts=1024, hidden=512, inter=512, topk=8, has_shared=True)
     print(f"[prologue] E=1024 k=8 T={tokens}", flush=True)
@@ -126,3 +126,53 @@ def test_layer_entry_split_alignment(shape, tokens):
 
     print(f"[prologue] split align E={shape.experts} k={shape.topk} T={tokens}", flush=True)
     check(*run_layer(shape, tokens, "sqrtsoftplus", seed=400 + tokens, route_scale=2.5, clamp=10.0))
+
+
+@pytest.mark.parametrize("nan_cols", [[3], list(range(8))])
+def test_layer_entry_one_token_nan_logits_matches_staged(nan_cols):
+    """One routed token aligns in closed form when its k ids are distinct and
+    in range; logits with NaN entries may give the router other ids, and
+    whatever they are, the fused call must write exactly what the staged
+    route + align + experts launches write (the closed form, or align_block
+    when the ids repeat or leave the expert range)."""
+
+    shape = S.LayerShape(experts=8, hidden=1024, inter=512, topk=2, has_shared=True)
+    res = resident(shape)
+    E, H, I, k = shape.experts, shape.hidden, shape.inter, shape.topk
+    x = S.make_hidden(1, H, seed=7, device=DEV)
+    logits = torch.randn((1, E), device=DEV, generator=torch.Generator(DEV).manual_seed(8))
+    logits[0, nan_cols] = float("nan")
+    bs = ops.block_size_m(1, k, E)
+    cap = O.max_padded_tokens(k, E, bs)
+    nblocks = (cap + bs - 1) // bs
+    ws = torch.empty(ops.experts_workspace_bytes(1, k, H, I, True), dtype=torch.uint8, device=DEV)
+
+    def bufs():
+        return dict(ids=torch.full((1, k), -7, dtype=torch.int32, device=DEV),
+                    weights=torch.full((1, k), -7.0, dtype=torch.float32, device=DEV),
+                    sorted=torch.full((cap,), -7, dtype=torch.int32, device=DEV),
+                    expert_ids=torch.full((nblocks,), -7, dtype=torch.int32, device=DEV),
+                    ntpp=torch.full((1,), -7, dtype=torch.int32, device=DEV))
+
+    print(f"[prologue] T=1 NaN logits at {nan_cols}", flush=True)
+    f, st = bufs(), bufs()
+    out_f = torch.zeros((1, H), dtype=torch.bfloat16, device=DEV)
+    out_s = torch.zeros((1, H), dtype=torch.bfloat16, device=DEV)
+    common = dict(w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, w13r=res.w13_r, w2r=res.w2_r,
+                  experts=E, inter=I, has_shared=True, clamp_limit=0.0, block_size=bs)
+    ops.layer_w4a16_into(x, logits, None, topk=k, score_func="sigmoid", route_scale=1.0, ids=f["ids"],
+                         weights=f["weights"], margin=None, sorted_token_ids=f["sorted"],
+                         expert_ids=f["expert_ids"], num_tokens_post_padded=f["ntpp"], out=out_f,
+                         workspace=ws, **common)
+    ops.route_topk_into(logits, None, topk=k, score_func="sigmoid", route_scale=1.0, ids=st["ids"],
+                        weights=st["weights"], margin=None)
+    ops.align_into(st["ids"], block_size=bs, num_experts=E, sorted_token_ids=st["sorted"],
+                   expert_ids=st["expert_ids"], num_tokens_post_padded=st["ntpp"])
+    ops.experts_w4a16_into(x, route_weights=st["weights"], sorted_token_ids=st["sorted"],
+                           expert_ids=st["expert_ids"], num_tokens_post_padded=st["ntpp"], out=out_s,
+                           workspace=ws, **common)
+    torch.cuda.synchronize()
+    for name in ("ids", "sorted", "expert_ids", "ntpp"):
+        assert torch.equal(f[name], st[name]), name
+    assert torch.equal(f["weights"].view(torch.int32), st["weights"].view(torch.int32))
+    assert torch.equal(out_f.view(torch.int16), out_s.view(torch.int16))
