@@ -100,7 +100,7 @@ def test_layer_entry_small_layer(score, tokens):
     check(*run_layer(shape, tokens, score, seed=100 + tokens))
 
 
-@pytest.mark.parametrize("tokens", [1, 17, 64, 96])
+@pytest.mark.parametrize("tokens", [1, 8, 10, 11, 17, 64, 96])
 def test_layer_entry_256_experts(tokens):
     shape = S.LayerShape(experts=256, hidden=512, inter=512, topk=6, has_shared=True)
     print(f"[prologue] E=256 k=6 T={tokens}", flush=True)
