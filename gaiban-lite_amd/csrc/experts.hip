@@ -505,12 +505,17 @@ __global__ __launch_bounds__(256, 3) void expert_prefill_kernel(ExpertGemmParams
   // ratios: 128 bytes per (pair, group), 32 lanes x 4 bytes per pair
   const uint32_t r_off = (uint32_t)((p0 + (lane >> 5)) * groups) * 128 + (lane & 31) * 4;
 
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // here, plus constant offsets (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][16 * wave * 256]));
+  const uint32_t scl_lds = __builtin_amdgcn_readfirstlane(lds_addr(&scl[0][wave][0]));
+  const uint32_t xnc_lds = lds_addr(&xnc[0][0]);
   auto issue = [&](int g, int buf) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      lds_copy16(act_rsrc, lds_addr(&xs[buf][(16 * wave + 4 * q) * 256]), dma_off[q], g * 256);
-    lds_copy4(r_rsrc, lds_addr(&scl[buf][wave][0]), r_off, g * 128);
-    if (wave == 0) lds_copy4(nc_rsrc, lds_addr(&xnc[buf][0]), nc_off, g * 4);
+      lds_copy16(act_rsrc, xs_lds + buf * (uint32_t)sizeof(xs[0]) + q * 1024, dma_off[q], g * 256);
+    lds_copy4(r_rsrc, scl_lds + buf * (uint32_t)sizeof(scl[0]), r_off, g * 128);
+    if (wave == 0) lds_copy4(nc_rsrc, xnc_lds + buf * (uint32_t)sizeof(xnc[0]), nc_off, g * 4);
   };
   // The weight tiles are private to the wavefront: loaded straight into
   // registers, one group ahead, as inline asm -- the compiler neither counts

@@ -249,15 +249,20 @@ __global__ __launch_bounds__(256, RING == 2 ? 3 : 2) void expert_fp4_prefill_ker
   // lanes 32..63 pair p0 + 1's
   const uint32_t s_off = (uint32_t)((p0 + (lane >> 5)) * groups) * 128 + (lane & 31) * 4;
 
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // here, plus constant offsets (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][16 * wave * 128]));
+  const uint32_t wts_lds = __builtin_amdgcn_readfirstlane(lds_addr(&wts[0][wave][0]));
+  const uint32_t scl_lds = __builtin_amdgcn_readfirstlane(lds_addr(&scl[0][wave][0]));
   auto issue = [&](int g, int buf) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
-      lds_copy16(act_rsrc, lds_addr(&xs[buf][(16 * wave + 8 * q) * 128]), dma_off[q], g * 128);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][0]), w_off0, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][kTileBytes]), w_off0 + kTileBytes, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][2 * kTileBytes]), w_off1, g * 2048);
-    lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][3 * kTileBytes]), w_off1 + kTileBytes, g * 2048);
-    lds_copy4(s_rsrc, lds_addr(&scl[buf][wave][0]), s_off, g * 128);
+      lds_copy16(act_rsrc, xs_lds + buf * (uint32_t)sizeof(xs[0]) + q * 1024, dma_off[q], g * 128);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      lds_copy16(w_rsrc, wts_lds + buf * (uint32_t)sizeof(wts[0]) + t * kTileBytes,
+                 (t < 2 ? w_off0 : w_off1) + (t & 1) * kTileBytes, g * 2048);
+    lds_copy4(s_rsrc, scl_lds + buf * (uint32_t)sizeof(scl[0]), s_off, g * 128);
   };
 
   f32x4 acc[R][C];

@@ -262,10 +262,12 @@ __global__ __launch_bounds__(256, 2) void mx_prefill_kernel(ExpertGemmParams p, 
   const uint32_t s_off0 = (uint32_t)(p0 * groups) * 128 + (lane & 15) * 8;
   const uint32_t s_off1 = (uint32_t)((p0 + 1) * groups) * 128 + (lane & 15) * 8;
 
+  // copy destinations: this wavefront's buffer-0 address, made scalar once
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][16 * wave * 256]));
   auto issue = [&](int g, int buf) {
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      lds_copy16(act_rsrc, lds_addr(&xs[buf][(16 * wave + 4 * q) * 256]), dma_off[q], g * 256);
+      lds_copy16(act_rsrc, xs_lds + buf * (uint32_t)sizeof(xs[0]) + q * 1024, dma_off[q], g * 256);
   };
   // The weight tiles and scales are private to the wavefront: loaded straight
   // into registers, one group ahead (no LDS traffic for them).
