@@ -735,12 +735,17 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel3(LinearParams p) {
 
   static_assert(kActDma % 4 == 0, "every wavefront issues the same number of copies");
   constexpr int kStepLoads = kActPerWave + R;
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][wave * 1024]));
+  const uint32_t wts_lds = __builtin_amdgcn_readfirstlane(lds_addr(&wts[0][wave][0]));
   auto issue = [&](int win, int buf) {
 #pragma unroll
     for (int i = 0; i < kActPerWave; ++i)
-      lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + 4 * i) * 1024]), a_off[i], win * 128);
+      lds_copy16(a_rsrc, xs_lds + buf * (uint32_t)sizeof(xs[0]) + i * 4096, a_off[i], win * 128);
 #pragma unroll
-    for (int r = 0; r < R; ++r) lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 1024]), w_off[r], win * wstep);
+    for (int r = 0; r < R; ++r)
+      lds_copy16(w_rsrc, wts_lds + buf * (uint32_t)sizeof(wts[0]) + r * 1024, w_off[r], win * wstep);
   };
 
   f32x4 acc[R][C];
@@ -910,14 +915,19 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel_w3(LinearParams p) {
   }
 
   static_assert(kActDma % 4 == 0, "every wavefront issues the same number of copies");
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][wave * 1024]));
+  const uint32_t wts_lds = __builtin_amdgcn_readfirstlane(lds_addr(&wts[0][wave][0]));
   auto issue_tok = [&](int win, int buf) {
 #pragma unroll
     for (int i = 0; i < kActPerWave; ++i)
-      lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + 4 * i) * 1024]), a_off[i], win * 128);
+      lds_copy16(a_rsrc, xs_lds + buf * (uint32_t)sizeof(xs[0]) + i * 4096, a_off[i], win * 128);
   };
   auto issue_w = [&](int win, int buf) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) lds_copy16(w_rsrc, lds_addr(&wts[buf][wave][r * 1024]), w_off[r], win * wstep);
+    for (int r = 0; r < R; ++r)
+      lds_copy16(w_rsrc, wts_lds + buf * (uint32_t)sizeof(wts[0]) + r * 1024, w_off[r], win * wstep);
   };
 
   f32x4 acc[R][C];
@@ -1585,18 +1595,24 @@ __global__ __launch_bounds__(256 * H, 1) void w8a8_block_prefill_kernel(BlockFp8
 
   constexpr int kStepLoads = kActPerWave + 2 * R / H + 1;
   static_assert(kStepLoads < 64, "vmcnt range");
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][wave * 1024]));
+  const uint32_t wts_lds = __builtin_amdgcn_readfirstlane(lds_addr(&wts[0][sg][0]));
+  const uint32_t scs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&scs[0][wave][0]));
   auto issue = [&](int kb, int buf) {
 #pragma unroll
     for (int i = 0; i < kActPerWave; ++i)
-      lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + kWaves * i) * 1024]), a_off[i], kb * 128);
+      lds_copy16(a_rsrc, xs_lds + buf * (uint32_t)sizeof(xs[0]) + i * kWaves * 1024, a_off[i], kb * 128);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
         if (H == 1 || t == half)
-          lds_copy16(w_rsrc, lds_addr(&wts[buf][sg][r * 2048 + t * 1024]), w_off[r], (2 * kb + t) * wstep);
+          lds_copy16(w_rsrc, wts_lds + buf * (uint32_t)sizeof(wts[0]) + r * 2048 + t * 1024, w_off[r],
+                     (2 * kb + t) * wstep);
     }
-    lds_copy4(as_rsrc, lds_addr(&scs[buf][wave][0]), s_off, kb & ~3);
+    lds_copy4(as_rsrc, scs_lds + buf * (uint32_t)sizeof(scs[0]), s_off, kb & ~3);
   };
 
   f32x4 acc[R][C];
@@ -1798,22 +1814,28 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void w8a8_gemm256_kernel(BlockFp8P
   const int n16 = lane & 15;
   const int j = lane >> 4;
 
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][wave * 1024]));
+  const uint32_t wts_lds =
+      __builtin_amdgcn_readfirstlane(lds_addr(&wts[0][RM ? wave * 1024 : wave * kSpw * 2048]));
+  const uint32_t scs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&scs[0][64 * (wave & 3)]));
   auto issue = [&](int kb, int buf) {
 #pragma unroll
     for (int i = 0; i < kActPerWave; ++i)
-      lds_copy16(a_rsrc, lds_addr(&xs[buf][(wave + kWaves * i) * 1024]), a_off[i], kb * 128);
+      lds_copy16(a_rsrc, xs_lds + buf * (uint32_t)sizeof(xs[0]) + i * kWaves * 1024, a_off[i], kb * 128);
 #pragma unroll
     for (int s = 0; s < (RM ? kWCopies : kSpw); ++s) {
       if constexpr (RM) {
-        lds_copy16(w_rsrc, lds_addr(&wts[buf][(wave + kWaves * s) * 1024]), w_off[s], kb * 128);
+        lds_copy16(w_rsrc, wts_lds + buf * (uint32_t)sizeof(wts[0]) + s * kWaves * 1024, w_off[s], kb * 128);
       } else {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-          lds_copy16(w_rsrc, lds_addr(&wts[buf][(wave * kSpw + s) * 2048 + t * 1024]), w_off[s],
+          lds_copy16(w_rsrc, wts_lds + buf * (uint32_t)sizeof(wts[0]) + s * 2048 + t * 1024, w_off[s],
                      (2 * kb + t) * wstep);
       }
     }
-    lds_copy4(as_rsrc, lds_addr(&scs[buf][64 * (wave & 3)]), s_off, kb & ~3);
+    lds_copy4(as_rsrc, scs_lds + buf * (uint32_t)sizeof(scs[0]), s_off, kb & ~3);
   };
 
   f32x4 acc[TN][TM];
