@@ -135,6 +135,8 @@ template <typename T>
 __device__ __forceinline__ uint32_t lds_addr(T* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)p;
 }
+// The LDS pointer of byte address `a` (a wavefront-uniform value stays scalar).
+__device__ __forceinline__ lds_void_ptr lds_ptr(uint32_t a) { return (lds_void_ptr)(uintptr_t)a; }
 
 // SiLU with the hardware reciprocal (v_rcp_f32, within an ulp) instead of
 // the IEEE division: the prefill epilogues (32 per lane per work item, about

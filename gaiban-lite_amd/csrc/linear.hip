@@ -180,14 +180,20 @@ __global__ __launch_bounds__(256, 2) void w8a16_kernel(LinearParams p) {
       if (64 * q + lane < p.kblocks) srow[q] = row[64 * q + lane];
   }
 
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][wave * 1024]));
+  const uint32_t wts_lds = __builtin_amdgcn_readfirstlane(lds_addr(&wts[0][wave][0]));
   auto issue = [&](int win, int buf) {
 #pragma unroll
     for (int i = 0; i < kActPerWave; ++i) {
       const int q = wave + 4 * i;
-      if (q < kActDma) lds_dma16(a_rsrc, (lds_void_ptr)&xs[buf][q * 1024], a_off[i], win * 128);
+      if (q < kActDma)
+        lds_dma16(a_rsrc, lds_ptr(xs_lds + buf * (uint32_t)sizeof(xs[0]) + i * 4096), a_off[i], win * 128);
     }
 #pragma unroll
-    for (int r = 0; r < R; ++r) lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 1024], w_off[r], win * wstep);
+    for (int r = 0; r < R; ++r)
+      lds_dma16(w_rsrc, lds_ptr(wts_lds + buf * (uint32_t)sizeof(wts[0]) + r * 1024), w_off[r], win * wstep);
   };
 
   f32x4 acc[R][C];
@@ -1267,16 +1273,22 @@ __global__ __launch_bounds__(256, 2) void w8a8_block_kernel(BlockFp8Params p) {
     srow_t[c] = tok < p.m ? p.as + tok * p.kblocks : nullptr;
   }
 
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][wave * 1024]));
+  const uint32_t wts_lds = __builtin_amdgcn_readfirstlane(lds_addr(&wts[0][wave][0]));
   auto issue = [&](int kb, int buf) {
 #pragma unroll
     for (int i = 0; i < kActPerWave; ++i) {
       const int q = wave + 4 * i;
-      if (q < kActDma) lds_dma16(a_rsrc, (lds_void_ptr)&xs[buf][q * 1024], a_off[i], kb * 128);
+      if (q < kActDma)
+        lds_dma16(a_rsrc, lds_ptr(xs_lds + buf * (uint32_t)sizeof(xs[0]) + i * 4096), a_off[i], kb * 128);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 2048], w_off[r], (2 * kb) * wstep);
-      lds_dma16(w_rsrc, (lds_void_ptr)&wts[buf][wave][r * 2048 + 1024], w_off[r], (2 * kb + 1) * wstep);
+      const uint32_t wb = wts_lds + buf * (uint32_t)sizeof(wts[0]) + r * 2048;
+      lds_dma16(w_rsrc, lds_ptr(wb), w_off[r], (2 * kb) * wstep);
+      lds_dma16(w_rsrc, lds_ptr(wb + 1024), w_off[r], (2 * kb + 1) * wstep);
     }
   };
 
