@@ -112,11 +112,15 @@ __global__ __launch_bounds__(256, 2) void gate_logits_tile_kernel(const uint16_t
     xoff[q] = t < tokens ? (uint32_t)(t * hidden * 2 + part * 16) : kOobOffset;
     woff[q] = e < experts ? (uint32_t)((int64_t)e * hidden * 2 + part * 16) : kOobOffset;
   }
+  // copy destinations: this wavefront's buffer-0 addresses, made scalar once
+  // (the K loop sets M0 with scalar adds only)
+  const uint32_t xs_lds = __builtin_amdgcn_readfirstlane(lds_addr(&xs[0][16 * wave * 256]));
+  const uint32_t ws_lds = __builtin_amdgcn_readfirstlane(lds_addr(&ws[0][16 * wave * 256]));
   auto issue = [&](int c, int buf) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      lds_copy16(x_rsrc, lds_addr(&xs[buf][(16 * wave + 4 * q) * 256]), xoff[q], c * kGateChunk * 2);
-      lds_copy16(w_rsrc, lds_addr(&ws[buf][(16 * wave + 4 * q) * 256]), woff[q], c * kGateChunk * 2);
+      lds_copy16(x_rsrc, xs_lds + buf * (uint32_t)sizeof(xs[0]) + q * 1024, xoff[q], c * kGateChunk * 2);
+      lds_copy16(w_rsrc, ws_lds + buf * (uint32_t)sizeof(ws[0]) + q * 1024, woff[q], c * kGateChunk * 2);
     }
   };
   const int sw = lane & 15;
