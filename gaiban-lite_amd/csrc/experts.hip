@@ -269,12 +269,27 @@ __global__ __launch_bounds__(256, RING == 4 ? 4 : 3) void expert_decode_kernel(E
 // group's arithmetic is expert_decode_kernel's; the sum over groups is
 // formed as (lower half) + (upper half), so the results can differ from
 // that kernel's in the last bits.
-template <int STAGE>
+// RESIDENT (K <= 4096: at most kKsplitResidentGroups groups per half): each
+// half's activation rows (16 slots x its K range, 64 KiB) and their 64-column
+// sums are copied into LDS once, before the K loop, so the loop holds only
+// the weight ring and the MFMAs: no activation load, no LDS store and no
+// barrier per group.  With a group's copy one group ahead and a barrier per
+// group, the four wavefronts of a half waited on that copy every group (8
+// MFMAs of work per group at one token), and the CU kept about 33 L1 -> L2
+// requests in flight against ~90 in the persistent kernel at T = 64.  The
+// same operations in the same order on every value: the same bits.
+constexpr int kKsplitResidentGroups = 16;
+
+template <int STAGE, bool RESIDENT>
 __global__ __launch_bounds__(512, 1) void expert_decode_ksplit_kernel(ExpertGemmParams p) {
   constexpr int R = 2;
   constexpr int RING = 8;
   constexpr int kAhead = RING - 2;
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][2][16 * 256];  // [half][buffer], part q of slot s at q ^ s
+  constexpr int kXsGroups = RESIDENT ? kKsplitResidentGroups : 2;
+  // [half][group (RESIDENT) or buffer][slot x 256 B], part q of slot s at q ^ s
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kXsGroups][16 * 256];
+  // RESIDENT: [half][64-column chunk of the half][slot] activation sums
+  __shared__ float xsum[RESIDENT ? 2 : 1][RESIDENT ? 2 * kKsplitResidentGroups : 1][16];
   __shared__ f32x4 upper[4][R][64];
   __shared__ float red[4][16];
   const int tid = threadIdx.x & 255;
@@ -317,10 +332,33 @@ __global__ __launch_bounds__(512, 1) void expert_decode_ksplit_kernel(ExpertGemm
   };
 
   const uint32_t magic = dequant_magic();
-  issue_x(gb, CS[0]);
+  if constexpr (RESIDENT) {
+    // the half's activation groups (padded slots read zeros) and sums, once
+    u32x4 rows[kKsplitResidentGroups];
 #pragma unroll
-  for (int a = 0; a < kAhead; ++a) issue_w(gb + a, W[a], S[a]);
-  *reinterpret_cast<u32x4*>(&xs[half][0][ld_lds]) = xr;
+    for (int g = 0; g < kKsplitResidentGroups; ++g)
+      if (g < hg) rows[g] = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc, cur.ld_base + (uint32_t)((gb + g) * 256), 0, 0);
+    const int chunk = tid >> 4;  // 0..15, and 16 + that
+    float cs_lo = 0.0f, cs_hi = 0.0f;
+    if (chunk < 2 * hg)
+      cs_lo = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            sum_rsrc, cur.sum_base + (uint32_t)((2 * gb + chunk) * 4), 0, 0));
+    if (chunk + 16 < 2 * hg)
+      cs_hi = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            sum_rsrc, cur.sum_base + (uint32_t)((2 * gb + chunk + 16) * 4), 0, 0));
+#pragma unroll
+    for (int a = 0; a < kAhead; ++a) issue_w(gb + a, W[a], S[a]);
+#pragma unroll
+    for (int g = 0; g < kKsplitResidentGroups; ++g)
+      if (g < hg) *reinterpret_cast<u32x4*>(&xs[half][g][ld_lds]) = rows[g];
+    if (chunk < 2 * hg) xsum[half][chunk][tid & 15] = cs_lo;
+    if (chunk + 16 < 2 * hg) xsum[half][chunk + 16][tid & 15] = cs_hi;
+  } else {
+    issue_x(gb, CS[0]);
+#pragma unroll
+    for (int a = 0; a < kAhead; ++a) issue_w(gb + a, W[a], S[a]);
+    *reinterpret_cast<u32x4*>(&xs[half][0][ld_lds]) = xr;
+  }
   __syncthreads();
 
   f32x4 acc[R];
@@ -332,14 +370,19 @@ __global__ __launch_bounds__(512, 1) void expert_decode_ksplit_kernel(ExpertGemm
       const int g = g0 + u;
       // prefetches past the half's end re-read its last group (unused), so
       // every load is unconditional and the compiler's vmcnt waits stay exact
-      issue_x(gb + min(g + 1, hg - 1), CS[(u + 1) & 1]);
+      if constexpr (!RESIDENT) issue_x(gb + min(g + 1, hg - 1), CS[(u + 1) & 1]);
       issue_w(gb + min(g + kAhead, hg - 1), W[(u + kAhead) % RING], S[(u + kAhead) % RING]);
-      const float nc = -kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
+      float nc;
+      if constexpr (RESIDENT)
+        nc = -kDequantBias * (xsum[half][2 * g][lane & 15] + xsum[half][2 * g + 1][lane & 15]);
+      else
+        nc = -kDequantBias * (CS[u & 1][0] + CS[u & 1][1]);
       const f32x4 init = {nc, nc, nc, nc};
+      const uint8_t* xg = RESIDENT ? &xs[half][min(g, kXsGroups - 1)][0] : &xs[half][u & 1][0];
       f32x4 tmp[R];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xs[half][u & 1][rd_lds[d]]));
+        const bf16x8 bfr = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&xg[rd_lds[d]]));
 #pragma unroll
         for (int r = 0; r < R; ++r) tmp[r] = mfma_bf16(dequant_biased(W[u][r][d], magic), bfr, d == 0 ? init : tmp[r]);
       }
@@ -350,8 +393,10 @@ __global__ __launch_bounds__(512, 1) void expert_decode_ksplit_kernel(ExpertGemm
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[r][i] += sc[i] * tmp[r][i];
       }
-      *reinterpret_cast<u32x4*>(&xs[half][(u + 1) & 1][ld_lds]) = xr;
-      __syncthreads();
+      if constexpr (!RESIDENT) {
+        *reinterpret_cast<u32x4*>(&xs[half][(u + 1) & 1][ld_lds]) = xr;
+        __syncthreads();
+      }
     }
   }
 
@@ -1018,8 +1063,12 @@ template <int STAGE, bool PAIR>
 static void launch_decode_as(const ExpertGemmParams& p, int blocks, hipStream_t stream) {
   const int items = p.n_tiles * blocks;
   if (!PAIR && (p.k_dim / kGroup) % 16 == 0 && items <= device_cus()) {
-    // at most one item per CU: eight wavefronts per item, K split in two
-    hipLaunchKernelGGL((expert_decode_ksplit_kernel<STAGE>), dim3((unsigned)items), dim3(512), 0, stream, p);
+    // at most one item per CU: eight wavefronts per item, K split in two,
+    // each half's activations resident in LDS when they fit
+    if (p.k_dim / kGroup / 2 <= kKsplitResidentGroups)
+      hipLaunchKernelGGL((expert_decode_ksplit_kernel<STAGE, true>), dim3((unsigned)items), dim3(512), 0, stream, p);
+    else
+      hipLaunchKernelGGL((expert_decode_ksplit_kernel<STAGE, false>), dim3((unsigned)items), dim3(512), 0, stream, p);
     return;
   }
   if ((p.k_dim / kGroup) % 8 == 0 && (STAGE == 1 || items <= decode_resident_grid<STAGE, 8, PAIR>())) {
