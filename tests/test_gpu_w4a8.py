@@ -147,6 +147,50 @@ def test_flash_prefill_zipf_subset():
     check(S.FLASH, 8192, rows=rows, zipf=True)
 
 
+def test_extreme_scale_spread():
+    """Gate rows whose group scales alternate 2^100 / 2^-100 (beyond any
+    running-sum ratio in fp32) and a 2^40 spread in w2: the W4A8 kernels
+    scale every group exactly, so the prefill output (blocks of 64) equals
+    the decode kernels' (blocks of 16) and the fp32 W4A8 oracle."""
+
+    shape = TINY_SHARED
+    print("[w4a8] extreme scale spread", flush=True)
+    w13, s13, w2, s2 = S.make_checkpoint_experts(shape, seed=31, device=DEV)
+    g = torch.arange(s13.shape[-1], device=DEV)
+    wild = torch.where(g % 2 == 0, torch.tensor(2.0 ** 100, device=DEV), torch.tensor(2.0 ** -100, device=DEV))
+    s13[3, :shape.inter] = (wild * 1e-2).to(torch.bfloat16)
+    s2[5] = (s2[5].float() * torch.where(torch.arange(s2.shape[-1], device=DEV) % 2 == 0, 2.0 ** 20,
+                                        2.0 ** -20)).to(torch.bfloat16)
+    res = ResidentInt4MoEWeights.from_checkpoint_layout(w13, s13, w2, s2, experts=shape.experts, has_shared=True,
+                                                        marlin_input_dtype=torch.float8_e4m3fn)
+    src = DeviceExpertSource(w13, s13, w2, s2)
+    t = 256
+    x = S.make_hidden(t, shape.hidden, seed=32, device=DEV)
+    ids = torch.stack([torch.full((t,), 3, device=DEV), (torch.arange(t, device=DEV) % 7 + 4) % 8], dim=1)
+    ids[::5, 1] = 5
+    ids = ids.to(torch.int32)
+    w = torch.full((t, 2), 0.5, device=DEV, dtype=torch.float32)
+    outs = {}
+    for bs in (16, 64):
+        align = deterministic_moe_align_block_size(ids, block_size=bs, num_experts=shape.experts)
+        out = torch.empty((t, shape.hidden), dtype=torch.bfloat16, device=DEV)
+        ws = torch.empty(ops.experts_w4a8_workspace_bytes(t, 2, shape.hidden, shape.inter, True),
+                         dtype=torch.uint8, device=DEV)
+        ops.experts_w4a8_into(
+            x, w13q=res.w13_q, w13s=res.w13_s, w2q=res.w2_q, w2s=res.w2_s, experts=shape.experts,
+            inter=shape.inter, has_shared=True, route_weights=w, sorted_token_ids=align.sorted_token_ids,
+            expert_ids=align.expert_ids, num_tokens_post_padded=align.num_tokens_post_padded, block_size=bs,
+            clamp_limit=0.0, out=out, workspace=ws)
+        torch.cuda.synchronize()
+        outs[bs] = to_np_f32(out)
+        assert np.isfinite(outs[bs]).all(), bs
+    ref = O.moe_w4a8_f32(to_np_f32(x), ids.cpu().numpy(), w.cpu().numpy(), src, shared_index=shape.experts)
+    assert np.abs(ref).max() > 1e25  # the 2^100 groups dominate
+    assert_moe_close(outs[64], outs[16], what="prefill vs decode")
+    assert_moe_close(outs[64], ref, what="prefill vs oracle")
+    assert_moe_close(outs[16], ref, what="decode vs oracle")
+
+
 def test_layer_w4a8_dropin():
     res, src = layer(TINY_SHARED)
     cfg = TP4MoEConfig(hidden_size=1024, intermediate_size=512, experts=8, topk=2, route_scale=1.0,
